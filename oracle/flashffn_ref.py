@@ -1,0 +1,434 @@
+"""torch-CPU restatement of the FlashFFN v3 autograd Function (CPU oracle).
+
+TEST INFRASTRUCTURE ONLY -- imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline, never by the product.
+
+Contents
+  kernel contracts with the reference's wrapper names and torch in/out:
+    triton_silu_mul (flashffn.py:205-220), triton_swiglu_backward (:223-239),
+    triton_swiglu_backward_glu (:259-293), v3_quantize_group_absmax
+    (:1055-1088), v3_dequantize_group_absmax (:1091-1110),
+    triton_silu_mul_quant (:1314-1340), triton_dequant_swiglu_backward
+    (:1343-1373); all computed by oracle/codec.py.
+  OracleFlashFFNv3Function: FlashFFNv3Function.forward/backward
+    (:1395-1602) in the reference's op order, on CPU tensors of any float dtype.
+  ref_grads_fp32: the fp32 plain-autograd reference of the same factored
+    computation (src/verify_flashffn_v3.py:294-327).
+  count_saved_bytes / int4_saved_bytes_closed_form: the reference's
+    saved-activation accounting (src/verify_flashffn_v3.py:523-543,594-600).
+
+Parity status: OracleFlashFFNv3Function is pinned against ref_grads_fp32 (in
+'recompute' and 'bf16' cache modes the two agree to float32 rounding in fp32,
+which fails on any dropped term, wrong transpose or wrong scale in the
+reassociated backward) and against the reference's own V2 cosine thresholds in
+the quantised modes (tests/test_oracle_function.py).  GEMM outputs are not
+bit-pinnable against the reference (cuBLAS), as in the reference's own gates.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+from . import codec
+
+# ---------------------------------------------------------------------------
+# torch <-> numpy with exact bf16 handling
+# ---------------------------------------------------------------------------
+
+
+def to_f32(t: torch.Tensor) -> np.ndarray:
+    """Exact widening of a bf16/fp16/fp32 tensor to a float32 numpy array."""
+    return t.detach().cpu().to(torch.float32).contiguous().numpy()
+
+
+def from_f32(a: np.ndarray, dtype: torch.dtype) -> torch.Tensor:
+    """Round a float32 array to `dtype` with round-to-nearest-even."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    if dtype == torch.bfloat16:
+        return torch.from_numpy(codec.f32_to_bf16_bits(a).view(np.int16)).view(torch.bfloat16)
+    if dtype == torch.float16:
+        return torch.from_numpy(a.astype(np.float16))
+    if dtype == torch.float32:
+        return torch.from_numpy(a.copy())
+    raise TypeError(f"unsupported dtype {dtype}")
+
+
+def bf16_bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+# ---------------------------------------------------------------------------
+# kernel contracts (torch in / torch out)
+# ---------------------------------------------------------------------------
+
+
+def v3_quantize_group_absmax(t: torch.Tensor, bits: int, group_size: int = 64):
+    """flashffn.py:1055-1088 -> (payload uint8 [N,D/2] | int8 [N,D], scales fp16 [N,G])."""
+    q, s = codec.quantize_group_absmax(to_f32(t), bits, group_size)
+    return torch.from_numpy(q), torch.from_numpy(s)
+
+
+def v3_dequantize_group_absmax(payload, scales, bits, group_size=64, dtype=torch.bfloat16):
+    """flashffn.py:1091-1110."""
+    f = codec.dequantize_group_absmax_f32(payload.cpu().numpy(), scales.cpu().numpy(),
+                                          bits, group_size)
+    return from_f32(f, dtype)
+
+
+def triton_silu_mul(h_gate, h_up):
+    """flashffn.py:205-220: output in the input dtype."""
+    return from_f32(codec.silu_mul(to_f32(h_gate), to_f32(h_up)), h_gate.dtype).reshape(h_gate.shape)
+
+
+def triton_swiglu_backward(grad_h_mid, h_gate, h_up):
+    """flashffn.py:223-239 -> (grad_h_gate, grad_h_up) in h_gate's dtype."""
+    dg, du = codec.swiglu_backward(to_f32(grad_h_mid), to_f32(h_gate), to_f32(h_up))
+    dt = h_gate.dtype
+    return from_f32(dg, dt).reshape(h_gate.shape), from_f32(du, dt).reshape(h_gate.shape)
+
+
+def triton_swiglu_backward_glu(grad_h_mid, h_gate, h_up, want_h_mid):
+    """flashffn.py:259-293 values (aliasing is a memory property, not a value one)."""
+    dg, du = triton_swiglu_backward(grad_h_mid, h_gate, h_up)
+    hm = triton_silu_mul(h_gate, h_up) if want_h_mid else None
+    return dg, du, hm
+
+
+def triton_silu_mul_quant(h_gate, h_up, bits, group_size=64):
+    """flashffn.py:1314-1340 contract -> (h_mid, q_gate, s_gate, q_up, s_up)."""
+    g, u = to_f32(h_gate), to_f32(h_up)
+    hm, qg, sg, qu, su = codec.silu_mul_quant(g, u, bits, group_size)
+    return (from_f32(hm, h_gate.dtype), torch.from_numpy(qg), torch.from_numpy(sg),
+            torch.from_numpy(qu), torch.from_numpy(su))
+
+
+def triton_dequant_swiglu_backward(grad_h_mid, q_gate, s_gate, q_up, s_up, bits,
+                                   group_size=64, want_h_mid=False):
+    """flashffn.py:1343-1373 contract -> (grad_h_gate, grad_h_up, h_mid_hat | None)."""
+    dg, du, hm = codec.dequant_swiglu_backward(
+        to_f32(grad_h_mid), q_gate.numpy(), s_gate.numpy(), q_up.numpy(), s_up.numpy(),
+        bits, group_size, want_h_mid)
+    dt = grad_h_mid.dtype
+    return from_f32(dg, dt), from_f32(du, dt), (from_f32(hm, dt) if want_h_mid else None)
+
+
+# ---------------------------------------------------------------------------
+# FlashFFNv3Function restated
+# ---------------------------------------------------------------------------
+
+
+class OracleFlashFFNv3Function(torch.autograd.Function):
+    """CPU restatement of FlashFFNv3Function (flashffn.py:1376-1602).
+
+    Same argument list:
+      apply(x, w_gate, a_gate, b_gate, w_up, a_up, b_up, w_down, a_down, b_down,
+            s_gate, s_up, s_down, cache_mode, group_size, use_triton)
+    The Triton kernels are replaced by their oracle contracts; the GEMMs are
+    torch CPU F.linear/@ in the tensors' dtype, as the reference runs them.
+    """
+
+    @staticmethod
+    def forward(ctx, x, w_gate, a_gate, b_gate, w_up, a_up, b_up, w_down, a_down, b_down,
+                s_gate=0.0, s_up=0.0, s_down=0.0, cache_mode="int4", group_size=64,
+                use_triton=True):
+        assert cache_mode in ("int4", "int8", "bf16", "recompute"), cache_mode
+        orig_shape = x.shape
+        hidden_dim = x.shape[-1]
+        x_2d = x.reshape(-1, hidden_dim)
+
+        h_gate = F.linear(x_2d, w_gate)                                  # :1410
+        xa_g = None
+        if a_gate is not None:
+            xa_g = F.linear(x_2d, a_gate)                                # :1413
+            h_gate = h_gate + s_gate * F.linear(xa_g, b_gate)            # :1414
+        h_up = F.linear(x_2d, w_up)                                      # :1416
+        xa_u = None
+        if a_up is not None:
+            xa_u = F.linear(x_2d, a_up)
+            h_up = h_up + s_up * F.linear(xa_u, b_up)                    # :1420
+
+        c_gate = qs_gate = c_up = qs_up = None
+        fused_quant = (cache_mode in ("int4", "int8") and use_triton
+                       and h_gate.dtype == torch.bfloat16)               # :1424-1426
+        if fused_quant:
+            bits = 4 if cache_mode == "int4" else 8
+            h_mid, c_gate, qs_gate, c_up, qs_up = triton_silu_mul_quant(
+                h_gate, h_up, bits, group_size)                          # :1429
+        else:
+            h_mid = triton_silu_mul(h_gate, h_up)                        # :1433
+
+        y = F.linear(h_mid, w_down)                                      # :1435
+        ha_d = None
+        if a_down is not None:
+            ha_d = F.linear(h_mid, a_down)                               # :1438
+            y = y + s_down * F.linear(ha_d, b_down)                      # :1439
+
+        if not fused_quant:
+            if cache_mode in ("int4", "int8"):
+                bits = 4 if cache_mode == "int4" else 8
+                c_gate, qs_gate = v3_quantize_group_absmax(h_gate, bits, group_size)
+                c_up, qs_up = v3_quantize_group_absmax(h_up, bits, group_size)
+            elif cache_mode == "bf16":
+                c_gate, c_up = h_gate, h_up
+        ctx.save_for_backward(x, w_gate, a_gate, b_gate, w_up, a_up, b_up,
+                              w_down, a_down, b_down, xa_g, xa_u, ha_d,
+                              c_gate, qs_gate, c_up, qs_up)              # :1454-1458
+        ctx.s = (s_gate, s_up, s_down)
+        ctx.cache_mode = cache_mode
+        ctx.group_size = group_size
+        ctx.use_triton = fused_quant
+        ctx.orig_shape = orig_shape
+        ctx.in_dtype = x.dtype
+        if len(orig_shape) == 3:
+            y = y.view(orig_shape[0], orig_shape[1], hidden_dim)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        (x, w_gate, a_gate, b_gate, w_up, a_up, b_up, w_down, a_down, b_down,
+         xa_g, xa_u, ha_d, c_gate, qs_gate, c_up, qs_up) = ctx.saved_tensors
+        s_gate, s_up, s_down = ctx.s
+        mode = ctx.cache_mode
+        hidden_dim = ctx.orig_shape[-1]
+        (need_x, need_wg, need_ag, need_bg, need_wu, need_au, need_bu,
+         need_wd, need_ad, need_bd) = ctx.needs_input_grad[:10]
+        gy = grad_y.reshape(-1, hidden_dim)
+        x_2d = x.reshape(-1, hidden_dim)
+
+        need_gate_path = (need_x or need_wg or need_ag or need_bg
+                          or need_wu or need_au or need_bu)              # :1488-1489
+        need_h_mid = need_wd or (a_down is not None and need_ad)         # :1490
+        need_recon = need_gate_path or need_h_mid
+        use_k2 = mode in ("int4", "int8") and ctx.use_triton and need_gate_path
+
+        hg = hu = None
+        if need_recon and not use_k2:                                    # :1500-1516
+            if mode == "recompute":
+                hg = F.linear(x_2d, w_gate)
+                if a_gate is not None:
+                    hg = hg + s_gate * F.linear(xa_g, b_gate)
+                hu = F.linear(x_2d, w_up)
+                if a_up is not None:
+                    hu = hu + s_up * F.linear(xa_u, b_up)
+            elif mode == "bf16":
+                hg, hu = c_gate, c_up
+            else:
+                bits = 4 if mode == "int4" else 8
+                hg = v3_dequantize_group_absmax(c_gate, qs_gate, bits, ctx.group_size,
+                                                ctx.in_dtype)
+                hu = v3_dequantize_group_absmax(c_up, qs_up, bits, ctx.group_size,
+                                                ctx.in_dtype)
+
+        grad_w_down = grad_a_down = grad_b_down = None
+        gyB_d = None
+        if a_down is not None and (need_gate_path or need_ad):
+            gyB_d = gy @ b_down                                          # :1521
+
+        grad_h_gate = grad_h_up = h_mid_hat = None
+        if use_k2:                                                       # :1525-1533
+            bits = 4 if mode == "int4" else 8
+            grad_h_mid = gy @ w_down
+            if a_down is not None:
+                grad_h_mid = grad_h_mid + s_down * (gyB_d @ a_down)
+            grad_h_gate, grad_h_up, h_mid_hat = triton_dequant_swiglu_backward(
+                grad_h_mid, c_gate, qs_gate, c_up, qs_up, bits, ctx.group_size,
+                want_h_mid=need_h_mid)
+
+        if need_h_mid:                                                   # :1536-1543
+            if h_mid_hat is None:
+                h_mid_hat = triton_silu_mul(hg, hu)
+            if need_wd:
+                grad_w_down = gy.t() @ h_mid_hat
+            if need_ad:
+                grad_a_down = s_down * (gyB_d.t() @ h_mid_hat)
+        if need_bd:
+            grad_b_down = s_down * (gy.t() @ ha_d)                       # :1545
+
+        grad_x = None
+        grad_w_gate = grad_a_gate = grad_b_gate = None
+        grad_w_up = grad_a_up = grad_b_up = None
+        if need_gate_path:                                               # :1551-1587
+            if grad_h_gate is None:
+                grad_h_mid = gy @ w_down
+                if a_down is not None:
+                    grad_h_mid = grad_h_mid + s_down * (gyB_d @ a_down)
+                grad_h_gate, grad_h_up = triton_swiglu_backward(grad_h_mid, hg, hu)
+            ghgB = None
+            if a_gate is not None and (need_x or need_ag):
+                ghgB = grad_h_gate @ b_gate
+            ghuB = None
+            if a_up is not None and (need_x or need_au):
+                ghuB = grad_h_up @ b_up
+            if need_x:
+                grad_x = grad_h_gate @ w_gate
+                if a_gate is not None:
+                    grad_x = grad_x + s_gate * (ghgB @ a_gate)
+                grad_x = grad_x + grad_h_up @ w_up
+                if a_up is not None:
+                    grad_x = grad_x + s_up * (ghuB @ a_up)
+            if need_bg:
+                grad_b_gate = s_gate * (grad_h_gate.t() @ xa_g)
+            if need_ag:
+                grad_a_gate = s_gate * (ghgB.t() @ x_2d)
+            if need_bu:
+                grad_b_up = s_up * (grad_h_up.t() @ xa_u)
+            if need_au:
+                grad_a_up = s_up * (ghuB.t() @ x_2d)
+            if need_wg:
+                grad_w_gate = grad_h_gate.t() @ x_2d
+            if need_wu:
+                grad_w_up = grad_h_up.t() @ x_2d
+
+        if need_x and len(ctx.orig_shape) == 3:
+            grad_x = grad_x.view(ctx.orig_shape)
+        return (grad_x, grad_w_gate, grad_a_gate, grad_b_gate,
+                grad_w_up, grad_a_up, grad_b_up,
+                grad_w_down, grad_a_down, grad_b_down) + (None,) * (len(ctx.needs_input_grad) - 10)
+
+
+# ---------------------------------------------------------------------------
+# fp32 plain-autograd reference and test helpers
+# ---------------------------------------------------------------------------
+
+PROJ = ("gate", "up", "down")
+
+
+def ref_grads_fp32(ps: dict, x: torch.Tensor, gy: torch.Tensor):
+    """src/verify_flashffn_v3.py:294-327: plain autograd in float32 of the SAME
+    factored computation, from the SAME (possibly bf16) inputs upcast.
+    Returns ({name: grad}, y)."""
+    def leaf(t, rg):
+        return None if t is None else t.detach().float().requires_grad_(rg)
+
+    xl = x.detach().float().requires_grad_(True)
+    t = {}
+    for key in PROJ:
+        t[f"w_{key}"] = leaf(ps[f"w_{key}"], ps["train_w"])
+        has = ps[f"a_{key}"] is not None
+        t[f"a_{key}"] = leaf(ps[f"a_{key}"], has)
+        t[f"b_{key}"] = leaf(ps[f"b_{key}"], has)
+
+    def proj(z, key):
+        out = F.linear(z, t[f"w_{key}"])
+        if t[f"a_{key}"] is not None:
+            out = out + ps[f"s_{key}"] * F.linear(F.linear(z, t[f"a_{key}"]), t[f"b_{key}"])
+        return out
+
+    h_mid = F.silu(proj(xl, "gate")) * proj(xl, "up")
+    y = proj(h_mid, "down")
+    y.backward(gy.detach().float())
+    grads = {"grad_x": xl.grad}
+    for k, tt in t.items():
+        if tt is not None and tt.requires_grad:
+            grads[k] = tt.grad
+    return grads, y.detach()
+
+
+def run_function_grads(fn_apply, ps: dict, x, gy, mode: str, group_size: int,
+                       use_triton: bool = True):
+    """Run an FFN v3 Function (oracle or product) on leaf clones of `ps`.
+    Mirrors src/verify_flashffn_v3.py:259-291.  Returns ({name: grad}, y)."""
+    def leaf(t, rg):
+        return None if t is None else t.detach().clone().requires_grad_(rg)
+
+    xl = x.detach().clone().requires_grad_(True)
+    t = {}
+    for key in PROJ:
+        t[f"w_{key}"] = leaf(ps[f"w_{key}"], ps["train_w"])
+        has = ps[f"a_{key}"] is not None
+        t[f"a_{key}"] = leaf(ps[f"a_{key}"], has)
+        t[f"b_{key}"] = leaf(ps[f"b_{key}"], has)
+    y = fn_apply(xl, t["w_gate"], t["a_gate"], t["b_gate"],
+                 t["w_up"], t["a_up"], t["b_up"],
+                 t["w_down"], t["a_down"], t["b_down"],
+                 ps["s_gate"], ps["s_up"], ps["s_down"], mode, group_size, use_triton)
+    y.backward(gy)
+    grads = {"grad_x": xl.grad}
+    for k, tt in t.items():
+        if tt is not None and tt.requires_grad:
+            grads[k] = tt.grad
+    return grads, y.detach()
+
+
+def synthetic_param_set(config: str, h: int, d: int, rank: int, scaling: float,
+                        seed: int, dtype=torch.bfloat16, device="cpu",
+                        b_std: float = 0.02, peft_init: bool = False):
+    """Seeded parameters after src/verify_flashffn_v3.py:150-182.
+
+    config: 'all' (LoRA on gate/up/down) | 'gateup' | 'none' | 'fullft'.
+    W ~ N(0, 0.02).  Adapters: A ~ randn/sqrt(in) (reference gate) or, with
+    peft_init, kaiming-uniform(a=sqrt(5)) as nn.Linear/PEFT initialise it;
+    B ~ N(0, b_std)."""
+    g = torch.Generator().manual_seed(seed)
+    ps = {"train_w": config == "fullft"}
+    ps["w_gate"] = (torch.randn(d, h, generator=g) * 0.02).to(device, dtype)
+    ps["w_up"] = (torch.randn(d, h, generator=g) * 0.02).to(device, dtype)
+    ps["w_down"] = (torch.randn(h, d, generator=g) * 0.02).to(device, dtype)
+    has = {"gate": config in ("all", "gateup"), "up": config in ("all", "gateup"),
+           "down": config == "all"}
+    for key, d_in, d_out in (("gate", h, d), ("up", h, d), ("down", d, h)):
+        if has[key]:
+            if peft_init:
+                bound = 1.0 / np.sqrt(d_in)     # kaiming_uniform_(a=sqrt(5)) on [r, in]
+                a = (torch.rand(rank, d_in, generator=g) * 2 - 1) * bound
+            else:
+                a = torch.randn(rank, d_in, generator=g) / np.sqrt(d_in)
+            ps[f"a_{key}"] = a.to(device, dtype)
+            ps[f"b_{key}"] = (torch.randn(d_out, rank, generator=g) * b_std).to(device, dtype)
+            ps[f"s_{key}"] = scaling
+        else:
+            ps[f"a_{key}"] = ps[f"b_{key}"] = None
+            ps[f"s_{key}"] = 0.0
+    return ps
+
+
+def tensor_cos(a, b) -> float:
+    return float(F.cosine_similarity(a.double().flatten(), b.double().flatten(), dim=0))
+
+
+def rel_frob(a, b) -> float:
+    b64 = b.double()
+    den = b64.norm()
+    return float((a.double() - b64).norm() / den) if den > 0 else float((a.double()).norm())
+
+
+def count_saved_bytes(forward_fn, param_ptrs):
+    """src/verify_flashffn_v3.py:523-543: non-parameter bytes saved for
+    backward, deduplicated by (data_ptr, nbytes).  Returns (total, entries)."""
+    seen = set()
+    entries = []
+    total = 0
+
+    def pack(t):
+        nonlocal total
+        key = (t.data_ptr(), t.nbytes)
+        if t.data_ptr() in param_ptrs or key in seen:
+            return t
+        seen.add(key)
+        total += t.nbytes
+        entries.append({"shape": list(t.shape), "dtype": str(t.dtype), "bytes": t.nbytes})
+        return t
+
+    with torch.autograd.graph.saved_tensors_hooks(pack, lambda t: t):
+        y = forward_fn()
+    del y
+    return total, entries
+
+
+def int4_saved_bytes_closed_form(n: int, h: int, d: int, rank: int, group: int = 64,
+                                 n_thin: int = 3, x_bytes_per: int = 2):
+    """src/verify_flashffn_v3.py:598-600: x + 2*N*D/2 + 2*N*(D/g)*2 + 3*N*r*2."""
+    return (n * h * x_bytes_per + 2 * (n * d // 2) + 2 * (n * (d // group) * 2)
+            + n_thin * (n * rank * 2))
+
+
+def saved_bytes_closed_form(n: int, h: int, d: int, bits: int, group: int,
+                            n_thin: int = 0, rank: int = 0, x_bytes_per: int = 2,
+                            n_outlier: int = 0):
+    """Generalisation of the int4 closed form to int8 and outlier channels:
+    x + 2 payloads + 2 fp16 scale arrays + thin [N,r] + 2 bf16 outlier blocks."""
+    payload = n * d // 2 if bits == 4 else n * d
+    return (n * h * x_bytes_per + 2 * payload + 2 * n * (d // group) * 2
+            + n_thin * n * rank * 2 + 2 * n * n_outlier * 2)
