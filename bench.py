@@ -1,0 +1,197 @@
+"""Benchmark: FlashFFN v3 SwiGLU FFN fwd+bwd tokens/s + saved-activation MB on
+one MI355X (BASELINE.json metric), workload C2: Llama-7B FFN dims
+d_model=4096, d_ff=11008, 8x1024 tokens, bf16, int8 per-group(128) GLU cache,
+full fine-tune (dense weight grads), synthetic seeded inputs.
+
+  python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Prints ONE JSON line.  A step is one forward + backward of the FFN block on
+the same resident inputs.  `roofline` is for the dominant HIP kernel of this
+build, timed live with HIP events on its launch stream inside the timed steps;
+`kernels` lists every timed kernel.  `cpu_baseline` times the CPU oracle (the
+restatement of the reference's FlashFFNv3Function; the reference itself
+cannot run on a CPU) on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+# workload C2
+N_TOK, HID, INTER, GROUP, BITS = 8 * 1024, 4096, 11008, 128, 8
+MODE = "int8"
+
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, published
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
+
+
+def codec_bytes(n, d, bits, group, want_h_mid=True):
+    """Algorithmic HBM bytes of the standalone codec kernels (per launch).
+    K1: read g,u bf16; write h_mid bf16, 2 payloads, 2 fp16 scale arrays.
+    K2: read dh bf16, 2 payloads, 2 scale arrays; write dg, du (+ h_mid^) bf16."""
+    payload = n * d // 2 if bits == 4 else n * d
+    scales = n * (d // group) * 2
+    k1 = 2 * n * d * 2 + n * d * 2 + 2 * payload + 2 * scales
+    k2 = n * d * 2 + 2 * payload + 2 * scales + 2 * n * d * 2 + (n * d * 2 if want_h_mid else 0)
+    return k1, k2
+
+
+def gemm_flops_fwd_bwd(n, h, d, full_ft=True):
+    """3 GEMMs forward, 6 backward (full-FT) of 2*N*H*D FLOPs each."""
+    return (18 if full_ft else 12) * n * h * d
+
+
+def saved_bytes(fn, exclude_ptrs):
+    """Saved-for-backward bytes, deduplicated by storage, parameters and x
+    excluded (the reference's accounting, src/verify_flashffn_v3.py:523-543)."""
+    import torch
+    seen, total = set(), 0
+
+    def pack(t):
+        nonlocal total
+        key = (t.data_ptr(), t.nbytes)
+        if t.data_ptr() not in exclude_ptrs and key not in seen:
+            seen.add(key)
+            total += t.nbytes
+        return t
+
+    with torch.autograd.graph.saved_tensors_hooks(pack, lambda t: t):
+        y = fn()
+    del y
+    return total
+
+
+def cpu_baseline(budget_tokens=512):
+    """Times the CPU oracle's FlashFFNv3Function (fp32, int8 g128, full-FT)
+    on `budget_tokens` tokens of the C2 shape: 1 warmup + 3 reps, median."""
+    import torch
+    from oracle import flashffn_ref as R
+    torch.set_num_threads(os.cpu_count() or 1)
+    ps = R.synthetic_param_set("fullft", HID, INTER, 0, 0.0, seed=0, dtype=torch.float32)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(budget_tokens, HID, generator=g)
+    gy = torch.randn(budget_tokens, HID, generator=g)
+    times = []
+    for rep in range(4):
+        t0 = time.perf_counter()
+        R.run_function_grads(R.OracleFlashFFNv3Function.apply, ps, x, gy, MODE, GROUP)
+        dt = time.perf_counter() - t0
+        if rep:
+            times.append(dt)
+    times.sort()
+    med = times[len(times) // 2]
+    return {"value": budget_tokens / med, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{budget_tokens} tokens of C2 (H={HID}, D={INTER}), fp32, int8 g{GROUP}, "
+                      f"full-FT fwd+bwd; oracle FlashFFNv3Function on CPU, median of 3",
+            "median_s": med}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--tokens", type=int, default=N_TOK)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=512)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(multi-GPU sharding is a design note, not a code path)"}))
+        sys.exit(2)
+
+    import torch
+    import compact_amd as cpt
+    from compact_amd.kernels import KernelTimer
+
+    dev = torch.device("cuda:0")
+    n, h, d = args.tokens, HID, INTER
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(n, h, device=dev, generator=g).to(torch.bfloat16)
+    gy = torch.randn(n, h, device=dev, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(d, h, device=dev, generator=g) * 0.02).to(torch.bfloat16).requires_grad_()
+    wu = (torch.randn(d, h, device=dev, generator=g) * 0.02).to(torch.bfloat16).requires_grad_()
+    wd = (torch.randn(h, d, device=dev, generator=g) * 0.02).to(torch.bfloat16).requires_grad_()
+    x.requires_grad_()
+    params = (wg, wu, wd)
+
+    def fwd():
+        return cpt.FlashFFNv3Function.apply(x, wg, None, None, wu, None, None, wd, None, None,
+                                            0.0, 0.0, 0.0, MODE, GROUP, True)
+
+    def step():
+        for p in params + (x,):
+            p.grad = None
+        y = fwd()
+        y.backward(gy)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    cpt.v3_reset_counters()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with KernelTimer() as kt:
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(args.steps):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    total_ms = e0.elapsed_time(e1)
+    ms = total_ms / args.steps
+    assert cpt._V3_COUNTERS["triton_quant_fwd"] == args.steps, "fused K1 did not run"
+    assert cpt._V3_COUNTERS["triton_dequant_bwd"] == args.steps, "fused K2 did not run"
+    kern = kt.avg_ms()
+
+    sb = saved_bytes(fwd, {p.data_ptr() for p in params} | {x.data_ptr()}) + x.nbytes
+
+    k1_bytes, k2_bytes = codec_bytes(n, d, BITS, GROUP)
+    algo = {"silu_mul_quant": (k1_bytes, "hbm"), "dequant_swiglu_backward": (k2_bytes, "hbm")}
+    kernels = {}
+    for name, st in kern.items():
+        entry = dict(st)
+        if name in algo:
+            b, bound = algo[name]
+            entry["gbs"] = b / (st["avg_ms"] * 1e-3) / 1e9
+            entry["frac_hbm"] = entry["gbs"] / HBM_PEAK_GBS
+        kernels[name] = entry
+    # dominant HIP kernel of this build by total time
+    dom = max(kern, key=lambda k: kern[k]["total_ms"])
+    b, bound = algo[dom]
+    ach = b / (kern[dom]["avg_ms"] * 1e-3) / 1e9
+    roofline = {"kernel": dom, "bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": ach / HBM_PEAK_GBS, "traffic": None,
+                "algorithmic_bytes": b}
+    flops = gemm_flops_fwd_bwd(n, h, d)
+    out = {
+        "metric": "FFN fwd+bwd tokens/sec + saved-activation MB, Llama-7B FFN shape, 1 MI355X",
+        "value": n / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seed 0, X~N(0,1), W~N(0,0.02))",
+        "config": {"workload": "C2: SwiGLU FFN fwd+bwd, d_model=4096, d_ff=11008, "
+                               "8x1024 tokens, bf16, int8 per-group(128) cache, full-FT",
+                   "tokens": n, "d_model": h, "d_ff": d, "cache_mode": MODE,
+                   "group_size": GROUP, "parallelism": "none (1 GPU)"},
+        "saved_activation_mb": sb / 1e6,
+        "step_tflops": flops / (ms * 1e-3) / 1e12,
+        "step_frac_mfma_bf16": flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+        "roofline": roofline,
+        "kernels": kernels,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(args.cpu_tokens)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,677 @@
+// Memory-bound kernels of the FlashFFN v3 hot path for gfx950:
+//   * per-group absmax codec (quantise / dequantise)           ref src/flashffn.py:1055-1110
+//   * K1: SiLU(g)*u + codec of both g and u in one pass         ref src/flashffn.py:1149-1225
+//   * K2: dequantise + SwiGLU backward (+ h_mid^)              ref src/flashffn.py:1228-1300
+//   * plain GLU forward / backward / in-place backward         ref src/flashffn.py:50-198
+//
+// Layout: every tensor is row-major and contiguous.  Because D is a multiple
+// of the group size, a group never straddles a row, so the kernels treat an
+// [N, D] tensor as a flat array and a group as group_size consecutive
+// elements; scales are the flat [N * D / group_size] array.
+//
+// Fast path: one thread owns 8 consecutive elements (one 128-bit load of a
+// bf16 tensor), a group of 8..512 elements is owned by group_size/8
+// consecutive lanes of one wavefront, and the group absmax is reduced with
+// lane shuffles.  The absmax is taken as an unsigned max over the bit
+// patterns with the sign cleared: for non-negative floats that order is the
+// float order, so the reduction is exact and order independent.
+// Generic path (any dtype / alignment / group size): one thread per group.
+
+#include "common.h"
+#include "compact_amd.h"
+
+namespace cpt {
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ float sigmoid_f32(float x) {
+  // tl.sigmoid: 1 / (1 + exp(-x)), float32
+  return 1.0f / (1.0f + expf(-x));
+}
+
+template <int BITS> struct QMax;
+template <> struct QMax<4> { static constexpr float v = 7.0f; };
+template <> struct QMax<8> { static constexpr float v = 127.0f; };
+
+// fp16 scale of a group from its absmax (bits of |x|), exactly as
+// src/flashffn.py:1076-1080: scale = fp16(absmax / qmax); safe = scale>0 ? scale : 1.
+template <int BITS>
+__device__ __forceinline__ uint16_t scale_bits(uint32_t absmax_bits) {
+  const float s32 = __uint_as_float(absmax_bits) / QMax<BITS>::v;
+  return f32_to_f16_bits(s32);
+}
+__device__ __forceinline__ float safe_scale(uint16_t sh) {
+  const float s = f16_bits_to_f32(sh);
+  return s > 0.0f ? s : 1.0f;
+}
+
+// code = clamp(rint(v / safe), -qmax, qmax)   (src/flashffn.py:1080)
+template <int BITS>
+__device__ __forceinline__ int quant_code(float v, float safe) {
+  float q = __builtin_rintf(v / safe);
+  q = fminf(fmaxf(q, -QMax<BITS>::v), QMax<BITS>::v);
+  return (int)q;
+}
+
+// Codes of 8 consecutive elements packed as stored: int8 -> 8 bytes,
+// int4 -> 4 bytes of (code+8) nibbles, even column low (src/flashffn.py:1081-1085).
+template <int BITS>
+__device__ __forceinline__ void store_codes8(uint8_t* q, int64_t c, const float v[8], float safe) {
+  if (BITS == 8) {
+    uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      w0 |= ((uint32_t)quant_code<8>(v[j], safe) & 0xFFu) << (8 * j);
+      w1 |= ((uint32_t)quant_code<8>(v[4 + j], safe) & 0xFFu) << (8 * j);
+    }
+    reinterpret_cast<uint2*>(q)[c] = make_uint2(w0, w1);
+  } else {
+    uint32_t w = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) w |= (uint32_t)(quant_code<4>(v[j], safe) + 8) << (4 * j);
+    reinterpret_cast<uint32_t*>(q)[c] = w;
+  }
+}
+
+// Codes of 8 consecutive elements as floats.
+template <int BITS>
+__device__ __forceinline__ void load_codes8(const uint8_t* q, int64_t c, float code[8]) {
+  if (BITS == 8) {
+    uint2 w = reinterpret_cast<const uint2*>(q)[c];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      code[j] = (float)(int8_t)((w.x >> (8 * j)) & 0xFFu);
+      code[4 + j] = (float)(int8_t)((w.y >> (8 * j)) & 0xFFu);
+    }
+  } else {
+    uint32_t w = reinterpret_cast<const uint32_t*>(q)[c];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) code[j] = (float)((w >> (4 * j)) & 0xFu) - 8.0f;
+  }
+}
+
+// Group absmax over LPG consecutive lanes (LPG a power of two <= 64).
+template <int LPG>
+__device__ __forceinline__ uint32_t group_absmax8(const float v[8]) {
+  uint32_t am = 0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) am = max(am, __float_as_uint(v[j]) & 0x7FFFFFFFu);
+#pragma unroll
+  for (int off = 1; off < LPG; off <<= 1) am = max(am, (uint32_t)__shfl_xor((int)am, off));
+  return am;
+}
+
+// Quantise the 8 elements this thread owns; lane 0 of each group writes the scale.
+template <int BITS, int LPG>
+__device__ __forceinline__ void quant_chunk(const float v[8], bool valid, int64_t c,
+                                            uint8_t* q, uint16_t* s) {
+  const uint32_t am = group_absmax8<LPG>(v);
+  const uint16_t sh = scale_bits<BITS>(am);
+  if (!valid) return;
+  if ((c & (LPG - 1)) == 0) s[c / LPG] = sh;
+  store_codes8<BITS>(q, c, v, safe_scale(sh));
+}
+
+// ---------------------------------------------------------------------------
+// standalone quantise, fast path (input dtype DT, group size 8*LPG)
+// ---------------------------------------------------------------------------
+template <int DT, int BITS, int LPG>
+__global__ __launch_bounds__(kBlock) void quantize_fast_kernel(
+    const void* __restrict__ t, uint8_t* __restrict__ q, uint16_t* __restrict__ s,
+    int64_t nchunk) {
+  const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const bool valid = c < nchunk;
+  float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (valid) Vec8<DT>::ld(t, c, v);
+  quant_chunk<BITS, LPG>(v, valid, c, q, s);
+}
+
+// ---------------------------------------------------------------------------
+// K1: h_mid = SiLU(g)*u (bf16) + codec of g and u, fast path
+// ---------------------------------------------------------------------------
+template <int BITS, int LPG>
+__global__ __launch_bounds__(kBlock) void silu_mul_quant_kernel(
+    const uint16_t* __restrict__ g, const uint16_t* __restrict__ u, uint16_t* __restrict__ hm,
+    uint8_t* __restrict__ qg, uint16_t* __restrict__ sg, uint8_t* __restrict__ qu,
+    uint16_t* __restrict__ su, int64_t nchunk) {
+  const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const bool valid = c < nchunk;
+  float gv[8] = {0, 0, 0, 0, 0, 0, 0, 0}, uv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (valid) {
+    Vec8<kBF16>::ld(g, c, gv);
+    Vec8<kBF16>::ld(u, c, uv);
+    float h[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float act = gv[j] * sigmoid_f32(gv[j]);  // src/flashffn.py:1212-1213
+      h[j] = act * uv[j];
+    }
+    Vec8<kBF16>::st(hm, c, h);
+  }
+  quant_chunk<BITS, LPG>(gv, valid, c, qg, sg);
+  quant_chunk<BITS, LPG>(uv, valid, c, qu, su);
+}
+
+// ---------------------------------------------------------------------------
+// generic path: one thread per span of `span` elements (a whole number of
+// groups, even so int4 bytes are never shared between threads)
+// ---------------------------------------------------------------------------
+template <int DT, int BITS, bool GLU>
+__global__ __launch_bounds__(kBlock) void quant_generic_kernel(
+    const void* __restrict__ tg, const void* __restrict__ tu, void* __restrict__ hm,
+    uint8_t* __restrict__ qg, uint16_t* __restrict__ sg, uint8_t* __restrict__ qu,
+    uint16_t* __restrict__ su, int64_t nspan, int64_t span, int64_t gs) {
+  using E = Elem<DT>;
+  const int64_t sp = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (sp >= nspan) return;
+  const typename E::T* pg = reinterpret_cast<const typename E::T*>(tg);
+  const typename E::T* pu = reinterpret_cast<const typename E::T*>(tu);
+  const int64_t e0 = sp * span;
+  if (GLU) {
+    typename E::T* ph = reinterpret_cast<typename E::T*>(hm);
+    for (int64_t e = e0; e < e0 + span; ++e) {
+      const float gv = E::ld(pg + e), uv = E::ld(pu + e);
+      const float act = gv * sigmoid_f32(gv);
+      E::st(ph + e, act * uv);
+    }
+  }
+  for (int pass = 0; pass < (GLU ? 2 : 1); ++pass) {
+    const typename E::T* p = pass == 0 ? pg : pu;
+    uint8_t* q = pass == 0 ? qg : qu;
+    uint16_t* s = pass == 0 ? sg : su;
+    for (int64_t g0 = e0; g0 < e0 + span; g0 += gs) {
+      uint32_t am = 0;
+      for (int64_t e = g0; e < g0 + gs; ++e) am = max(am, __float_as_uint(E::ld(p + e)) & 0x7FFFFFFFu);
+      const uint16_t sh = scale_bits<BITS>(am);
+      s[g0 / gs] = sh;
+      const float safe = safe_scale(sh);
+      for (int64_t e = g0; e < g0 + gs; ++e) {
+        const int code = quant_code<BITS>(E::ld(p + e), safe);
+        if (BITS == 8) {
+          q[e] = (uint8_t)(code & 0xFF);
+        } else if ((e & 1) == 0) {
+          q[e >> 1] = (uint8_t)((q[e >> 1] & 0xF0u) | (uint32_t)(code + 8));
+        } else {
+          q[e >> 1] = (uint8_t)((q[e >> 1] & 0x0Fu) | ((uint32_t)(code + 8) << 4));
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dequantise: out = dtype(fp32(code) * fp32(scale))   (src/flashffn.py:1099-1110)
+// ---------------------------------------------------------------------------
+template <int BITS, int OUT_DT>
+__global__ __launch_bounds__(kBlock) void dequantize_fast_kernel(
+    const uint8_t* __restrict__ q, const uint16_t* __restrict__ s, void* __restrict__ out,
+    int64_t nchunk, int gs_shift) {
+  const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (c >= nchunk) return;
+  float code[8], v[8];
+  load_codes8<BITS>(q, c, code);
+  const float sc = f16_bits_to_f32(s[(c * 8) >> gs_shift]);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = code[j] * sc;
+  Vec8<OUT_DT>::st(out, c, v);
+}
+
+template <int BITS, int OUT_DT>
+__global__ __launch_bounds__(kBlock) void dequantize_generic_kernel(
+    const uint8_t* __restrict__ q, const uint16_t* __restrict__ s, void* __restrict__ out,
+    int64_t n_el, int64_t gs) {
+  using E = Elem<OUT_DT>;
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= n_el) return;
+  float code;
+  if (BITS == 8) {
+    code = (float)(int8_t)q[e];
+  } else {
+    const uint32_t b = q[e >> 1];
+    code = (float)((e & 1) ? (b >> 4) : (b & 0xFu)) - 8.0f;
+  }
+  E::st(reinterpret_cast<typename E::T*>(out) + e, code * f16_bits_to_f32(s[e / gs]));
+}
+
+// ---------------------------------------------------------------------------
+// K2: dequantise through bf16, SwiGLU backward, optional h_mid^
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void swiglu_bwd1(float dh, float g, float u, float& dg, float& du,
+                                            float& hact) {
+  // src/flashffn.py:109-123, same op order
+  const float sig = sigmoid_f32(g);
+  hact = g * sig;
+  const float grad_h_act = dh * u;
+  du = dh * hact;
+  const float dsilu = sig * (1.0f + g * (1.0f - sig));
+  dg = grad_h_act * dsilu;
+}
+
+template <int BITS, bool WANT_HM>
+__global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_kernel(
+    const uint16_t* __restrict__ gmid, const uint8_t* __restrict__ qg,
+    const uint16_t* __restrict__ sg, const uint8_t* __restrict__ qu,
+    const uint16_t* __restrict__ su, uint16_t* __restrict__ dg, uint16_t* __restrict__ du,
+    uint16_t* __restrict__ hm, int64_t nchunk, int gs_shift) {
+  const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (c >= nchunk) return;
+  float cg[8], cu[8], dh[8], og[8], ou[8], oh[8];
+  load_codes8<BITS>(qg, c, cg);
+  load_codes8<BITS>(qu, c, cu);
+  Vec8<kBF16>::ld(gmid, c, dh);
+  const int64_t si = (c * 8) >> gs_shift;
+  const float scg = f16_bits_to_f32(sg[si]);
+  const float scu = f16_bits_to_f32(su[si]);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    // bf16 round trip of the dequantised cache (src/flashffn.py:1251-1253)
+    const float hg = bf16_to_f32(f32_to_bf16_bits(cg[j] * scg));
+    const float hu = bf16_to_f32(f32_to_bf16_bits(cu[j] * scu));
+    float hact;
+    swiglu_bwd1(dh[j], hg, hu, og[j], ou[j], hact);
+    oh[j] = hact * hu;  // src/flashffn.py:1298-1300
+  }
+  Vec8<kBF16>::st(dg, c, og);
+  Vec8<kBF16>::st(du, c, ou);
+  if (WANT_HM) Vec8<kBF16>::st(hm, c, oh);
+}
+
+// generic K2 (group sizes below 8, misaligned pointers): one thread per element
+template <int BITS, bool WANT_HM>
+__global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_generic_kernel(
+    const uint16_t* __restrict__ gmid, const uint8_t* __restrict__ qg,
+    const uint16_t* __restrict__ sg, const uint8_t* __restrict__ qu,
+    const uint16_t* __restrict__ su, uint16_t* __restrict__ dg, uint16_t* __restrict__ du,
+    uint16_t* __restrict__ hm, int64_t n_el, int64_t gs) {
+  const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (e >= n_el) return;
+  float code_g, code_u;
+  if (BITS == 8) {
+    code_g = (float)(int8_t)qg[e];
+    code_u = (float)(int8_t)qu[e];
+  } else {
+    const uint32_t bg = qg[e >> 1], bu = qu[e >> 1];
+    code_g = (float)((e & 1) ? (bg >> 4) : (bg & 0xFu)) - 8.0f;
+    code_u = (float)((e & 1) ? (bu >> 4) : (bu & 0xFu)) - 8.0f;
+  }
+  const float hg = bf16_to_f32(f32_to_bf16_bits(code_g * f16_bits_to_f32(sg[e / gs])));
+  const float hu = bf16_to_f32(f32_to_bf16_bits(code_u * f16_bits_to_f32(su[e / gs])));
+  float og, ou, hact;
+  swiglu_bwd1(bf16_to_f32(gmid[e]), hg, hu, og, ou, hact);
+  dg[e] = (uint16_t)f32_to_bf16_bits(og);
+  du[e] = (uint16_t)f32_to_bf16_bits(ou);
+  if (WANT_HM) hm[e] = (uint16_t)f32_to_bf16_bits(hact * hu);
+}
+
+// ---------------------------------------------------------------------------
+// plain GLU kernels (any float dtype).  Thread c owns elements [8c, 8c+8);
+// the last thread takes the ragged tail element by element.  VEC=false is
+// the path for pointers that are not 16-byte aligned.
+// ---------------------------------------------------------------------------
+template <int DT, bool VEC>
+__global__ __launch_bounds__(kBlock) void silu_mul_kernel(
+    const void* __restrict__ g, const void* __restrict__ u, void* __restrict__ out, int64_t n) {
+  using E = Elem<DT>;
+  const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t e0 = c * 8;
+  if (e0 >= n) return;
+  if (VEC && e0 + 8 <= n) {
+    float gv[8], uv[8], h[8];
+    Vec8<DT>::ld(g, c, gv);
+    Vec8<DT>::ld(u, c, uv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h[j] = (gv[j] * sigmoid_f32(gv[j])) * uv[j];
+    Vec8<DT>::st(out, c, h);
+    return;
+  }
+  const typename E::T* pg = reinterpret_cast<const typename E::T*>(g);
+  const typename E::T* pu = reinterpret_cast<const typename E::T*>(u);
+  typename E::T* po = reinterpret_cast<typename E::T*>(out);
+  for (int64_t e = e0; e < n && e < e0 + 8; ++e) {
+    const float gv = E::ld(pg + e);
+    E::st(po + e, (gv * sigmoid_f32(gv)) * E::ld(pu + e));
+  }
+}
+
+// Outputs may alias inputs (src/flashffn.py:129-198): every element is read
+// before anything is written, and no two threads share an element, so no
+// pointer here is __restrict__.
+template <int DT, bool VEC, bool WANT_HM>
+__global__ __launch_bounds__(kBlock) void swiglu_bwd_kernel(
+    const void* dh, const void* g, const void* u, void* dg, void* du, void* hm, int64_t n) {
+  using E = Elem<DT>;
+  const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t e0 = c * 8;
+  if (e0 >= n) return;
+  if (VEC && e0 + 8 <= n) {
+    float a[8], gv[8], uv[8], og[8], ou[8], oh[8];
+    Vec8<DT>::ld(dh, c, a);
+    Vec8<DT>::ld(g, c, gv);
+    Vec8<DT>::ld(u, c, uv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float hact;
+      swiglu_bwd1(a[j], gv[j], uv[j], og[j], ou[j], hact);
+      oh[j] = hact * uv[j];
+    }
+    if (WANT_HM) Vec8<DT>::st(hm, c, oh);
+    Vec8<DT>::st(dg, c, og);
+    Vec8<DT>::st(du, c, ou);
+    return;
+  }
+  const typename E::T* pdh = reinterpret_cast<const typename E::T*>(dh);
+  const typename E::T* pg = reinterpret_cast<const typename E::T*>(g);
+  const typename E::T* pu = reinterpret_cast<const typename E::T*>(u);
+  for (int64_t e = e0; e < n && e < e0 + 8; ++e) {
+    const float a = E::ld(pdh + e), gv = E::ld(pg + e), uv = E::ld(pu + e);
+    float og, ou, hact;
+    swiglu_bwd1(a, gv, uv, og, ou, hact);
+    if (WANT_HM) E::st(reinterpret_cast<typename E::T*>(hm) + e, hact * uv);
+    E::st(reinterpret_cast<typename E::T*>(dg) + e, og);
+    E::st(reinterpret_cast<typename E::T*>(du) + e, ou);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host-side dispatch helpers
+// ---------------------------------------------------------------------------
+inline unsigned grid_for(int64_t items) { return (unsigned)((items + kBlock - 1) / kBlock); }
+
+inline int launch_status() {
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+inline int log2_exact(int64_t v) {
+  int s = 0;
+  while ((int64_t(1) << s) < v) ++s;
+  return s;
+}
+
+// Argument contract of the codec (src/flashffn.py:1070-1072, 1303-1311).
+inline int check_codec(int64_t n, int64_t d, int bits, int64_t gs, bool need_pow2) {
+  if (bits != 4 && bits != 8) return kErrBits;
+  if (n < 0 || d < 0 || gs <= 0) return kErrShape;
+  if (d % gs != 0) return kErrRagged;
+  if (need_pow2 && !is_pow2(gs)) return kErrGroupPow2;
+  if (bits == 4 && (d & 1)) return kErrShape;
+  return kOk;
+}
+
+template <int BITS, int LPG>
+void launch_quant_fast(int dt, const void* t, uint8_t* q, uint16_t* s, int64_t nchunk,
+                       hipStream_t st) {
+  const unsigned grid = grid_for(nchunk);
+  if (dt == kBF16)
+    quantize_fast_kernel<kBF16, BITS, LPG><<<grid, kBlock, 0, st>>>(t, q, s, nchunk);
+  else if (dt == kF16)
+    quantize_fast_kernel<kF16, BITS, LPG><<<grid, kBlock, 0, st>>>(t, q, s, nchunk);
+  else
+    quantize_fast_kernel<kF32, BITS, LPG><<<grid, kBlock, 0, st>>>(t, q, s, nchunk);
+}
+
+template <int BITS>
+void launch_quant_fast_lpg(int dt, int lpg, const void* t, uint8_t* q, uint16_t* s,
+                           int64_t nchunk, hipStream_t st) {
+  switch (lpg) {
+    case 1: launch_quant_fast<BITS, 1>(dt, t, q, s, nchunk, st); break;
+    case 2: launch_quant_fast<BITS, 2>(dt, t, q, s, nchunk, st); break;
+    case 4: launch_quant_fast<BITS, 4>(dt, t, q, s, nchunk, st); break;
+    case 8: launch_quant_fast<BITS, 8>(dt, t, q, s, nchunk, st); break;
+    case 16: launch_quant_fast<BITS, 16>(dt, t, q, s, nchunk, st); break;
+    case 32: launch_quant_fast<BITS, 32>(dt, t, q, s, nchunk, st); break;
+    default: launch_quant_fast<BITS, 64>(dt, t, q, s, nchunk, st); break;
+  }
+}
+
+template <int BITS>
+void launch_quant_generic(int dt, bool glu, const void* g, const void* u, void* hm, uint8_t* qg,
+                          uint16_t* sg, uint8_t* qu, uint16_t* su, int64_t n_el, int64_t gs,
+                          hipStream_t st) {
+  // int4 packs two columns per byte: a span must hold an even number of elements
+  const int64_t span = (BITS == 4 && (gs & 1)) ? 2 * gs : gs;
+  const int64_t nspan = n_el / span;
+  const unsigned grid = grid_for(nspan);
+  if (glu) {
+    quant_generic_kernel<kBF16, BITS, true>
+        <<<grid, kBlock, 0, st>>>(g, u, hm, qg, sg, qu, su, nspan, span, gs);
+  } else if (dt == kBF16) {
+    quant_generic_kernel<kBF16, BITS, false>
+        <<<grid, kBlock, 0, st>>>(g, g, nullptr, qg, sg, qg, sg, nspan, span, gs);
+  } else if (dt == kF16) {
+    quant_generic_kernel<kF16, BITS, false>
+        <<<grid, kBlock, 0, st>>>(g, g, nullptr, qg, sg, qg, sg, nspan, span, gs);
+  } else {
+    quant_generic_kernel<kF32, BITS, false>
+        <<<grid, kBlock, 0, st>>>(g, g, nullptr, qg, sg, qg, sg, nspan, span, gs);
+  }
+}
+
+template <int BITS, int LPG>
+void launch_k1(const uint16_t* g, const uint16_t* u, uint16_t* hm, uint8_t* qg, uint16_t* sg,
+               uint8_t* qu, uint16_t* su, int64_t nchunk, hipStream_t st) {
+  silu_mul_quant_kernel<BITS, LPG>
+      <<<grid_for(nchunk), kBlock, 0, st>>>(g, u, hm, qg, sg, qu, su, nchunk);
+}
+
+template <int BITS>
+void launch_k1_lpg(int lpg, const uint16_t* g, const uint16_t* u, uint16_t* hm, uint8_t* qg,
+                   uint16_t* sg, uint8_t* qu, uint16_t* su, int64_t nchunk, hipStream_t st) {
+  switch (lpg) {
+    case 1: launch_k1<BITS, 1>(g, u, hm, qg, sg, qu, su, nchunk, st); break;
+    case 2: launch_k1<BITS, 2>(g, u, hm, qg, sg, qu, su, nchunk, st); break;
+    case 4: launch_k1<BITS, 4>(g, u, hm, qg, sg, qu, su, nchunk, st); break;
+    case 8: launch_k1<BITS, 8>(g, u, hm, qg, sg, qu, su, nchunk, st); break;
+    case 16: launch_k1<BITS, 16>(g, u, hm, qg, sg, qu, su, nchunk, st); break;
+    case 32: launch_k1<BITS, 32>(g, u, hm, qg, sg, qu, su, nchunk, st); break;
+    default: launch_k1<BITS, 64>(g, u, hm, qg, sg, qu, su, nchunk, st); break;
+  }
+}
+
+template <int DT>
+void launch_glu(int op, bool vec, const void* a, const void* g, const void* u, void* o1,
+                void* o2, void* o3, int64_t n, hipStream_t st) {
+  const unsigned grid = grid_for((n + 7) / 8);
+  if (op == 0) {
+    if (vec) silu_mul_kernel<DT, true><<<grid, kBlock, 0, st>>>(g, u, o1, n);
+    else silu_mul_kernel<DT, false><<<grid, kBlock, 0, st>>>(g, u, o1, n);
+  } else if (o3 == nullptr) {
+    if (vec) swiglu_bwd_kernel<DT, true, false><<<grid, kBlock, 0, st>>>(a, g, u, o1, o2, o3, n);
+    else swiglu_bwd_kernel<DT, false, false><<<grid, kBlock, 0, st>>>(a, g, u, o1, o2, o3, n);
+  } else {
+    if (vec) swiglu_bwd_kernel<DT, true, true><<<grid, kBlock, 0, st>>>(a, g, u, o1, o2, o3, n);
+    else swiglu_bwd_kernel<DT, false, true><<<grid, kBlock, 0, st>>>(a, g, u, o1, o2, o3, n);
+  }
+}
+
+inline int glu_dispatch(int op, int dt, const void* a, const void* g, const void* u, void* o1,
+                        void* o2, void* o3, int64_t n, hipStream_t st) {
+  if (n < 0) return kErrShape;
+  if (n == 0) return kOk;
+  if (!g || !u || !o1 || (op != 0 && (!a || !o2))) return kErrShape;
+  bool vec = aligned16(g) && aligned16(u) && aligned16(o1);
+  if (op != 0) vec = vec && aligned16(a) && aligned16(o2) && (o3 == nullptr || aligned16(o3));
+  switch (dt) {
+    case kF32: launch_glu<kF32>(op, vec, a, g, u, o1, o2, o3, n, st); break;
+    case kF16: launch_glu<kF16>(op, vec, a, g, u, o1, o2, o3, n, st); break;
+    case kBF16: launch_glu<kBF16>(op, vec, a, g, u, o1, o2, o3, n, st); break;
+    default: return kErrDType;
+  }
+  return launch_status();
+}
+
+}  // namespace cpt
+
+using namespace cpt;
+
+extern "C" {
+
+int cpt_v3_quantize_group_absmax(const void* t, int dtype, int64_t n, int64_t d, int bits,
+                                 int64_t group_size, void* payload, void* scales,
+                                 void* stream) {
+  int rc = check_codec(n, d, bits, group_size, false);
+  if (rc) return rc;
+  if (dtype != kF32 && dtype != kF16 && dtype != kBF16) return kErrDType;
+  const int64_t n_el = n * d;
+  if (n_el == 0) return kOk;
+  if (!t || !payload || !scales) return kErrShape;
+  hipStream_t st = (hipStream_t)stream;
+  uint8_t* q = (uint8_t*)payload;
+  uint16_t* s = (uint16_t*)scales;
+  const bool fast = is_pow2(group_size) && group_size >= 8 && group_size <= 512 &&
+                    aligned16(t) && ((uintptr_t)payload & 7u) == 0;
+  if (fast) {
+    const int lpg = (int)(group_size / 8);
+    if (bits == 4) launch_quant_fast_lpg<4>(dtype, lpg, t, q, s, n_el / 8, st);
+    else launch_quant_fast_lpg<8>(dtype, lpg, t, q, s, n_el / 8, st);
+  } else {
+    if (bits == 4) launch_quant_generic<4>(dtype, false, t, t, nullptr, q, s, q, s, n_el, group_size, st);
+    else launch_quant_generic<8>(dtype, false, t, t, nullptr, q, s, q, s, n_el, group_size, st);
+  }
+  return launch_status();
+}
+
+int cpt_v3_dequantize_group_absmax(const void* payload, const void* scales, int64_t n, int64_t d,
+                                   int bits, int64_t group_size, void* out, int out_dtype,
+                                   void* stream) {
+  int rc = check_codec(n, d, bits, group_size, false);
+  if (rc) return rc;
+  if (out_dtype != kF32 && out_dtype != kF16 && out_dtype != kBF16) return kErrDType;
+  const int64_t n_el = n * d;
+  if (n_el == 0) return kOk;
+  if (!payload || !scales || !out) return kErrShape;
+  hipStream_t st = (hipStream_t)stream;
+  const uint8_t* q = (const uint8_t*)payload;
+  const uint16_t* s = (const uint16_t*)scales;
+  const bool fast = is_pow2(group_size) && group_size >= 8 && aligned16(out) &&
+                    ((uintptr_t)payload & 7u) == 0;
+  if (fast) {
+    const int64_t nchunk = n_el / 8;
+    const int sh = log2_exact(group_size);
+    const unsigned grid = grid_for(nchunk);
+#define CPT_DQ(B, O) dequantize_fast_kernel<B, O><<<grid, kBlock, 0, st>>>(q, s, out, nchunk, sh)
+    if (bits == 4) {
+      if (out_dtype == kBF16) CPT_DQ(4, kBF16); else if (out_dtype == kF16) CPT_DQ(4, kF16); else CPT_DQ(4, kF32);
+    } else {
+      if (out_dtype == kBF16) CPT_DQ(8, kBF16); else if (out_dtype == kF16) CPT_DQ(8, kF16); else CPT_DQ(8, kF32);
+    }
+#undef CPT_DQ
+  } else {
+    const unsigned grid = grid_for(n_el);
+#define CPT_DQG(B, O) dequantize_generic_kernel<B, O><<<grid, kBlock, 0, st>>>(q, s, out, n_el, group_size)
+    if (bits == 4) {
+      if (out_dtype == kBF16) CPT_DQG(4, kBF16); else if (out_dtype == kF16) CPT_DQG(4, kF16); else CPT_DQG(4, kF32);
+    } else {
+      if (out_dtype == kBF16) CPT_DQG(8, kBF16); else if (out_dtype == kF16) CPT_DQG(8, kF16); else CPT_DQG(8, kF32);
+    }
+#undef CPT_DQG
+  }
+  return launch_status();
+}
+
+int cpt_silu_mul(const void* h_gate, const void* h_up, void* out, int64_t n_elements, int dtype,
+                 void* stream) {
+  return glu_dispatch(0, dtype, nullptr, h_gate, h_up, out, nullptr, nullptr, n_elements,
+                      (hipStream_t)stream);
+}
+
+int cpt_swiglu_backward(const void* grad_h_mid, const void* h_gate, const void* h_up,
+                        void* grad_h_gate, void* grad_h_up, int64_t n_elements, int dtype,
+                        void* stream) {
+  return glu_dispatch(1, dtype, grad_h_mid, h_gate, h_up, grad_h_gate, grad_h_up, nullptr,
+                      n_elements, (hipStream_t)stream);
+}
+
+int cpt_swiglu_backward_glu(const void* grad_h_mid, const void* h_gate, const void* h_up,
+                            void* grad_h_gate, void* grad_h_up, void* h_mid, int64_t n_elements,
+                            int dtype, void* stream) {
+  return glu_dispatch(1, dtype, grad_h_mid, h_gate, h_up, grad_h_gate, grad_h_up, h_mid,
+                      n_elements, (hipStream_t)stream);
+}
+
+int cpt_silu_mul_quant(const void* h_gate, const void* h_up, int64_t n, int64_t d, int bits,
+                       int64_t group_size, void* h_mid, void* q_gate, void* s_gate, void* q_up,
+                       void* s_up, void* stream) {
+  int rc = check_codec(n, d, bits, group_size, true);
+  if (rc) return rc;
+  const int64_t n_el = n * d;
+  if (n_el == 0) return kOk;
+  if (!h_gate || !h_up || !h_mid || !q_gate || !s_gate || !q_up || !s_up) return kErrShape;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* g = (const uint16_t*)h_gate;
+  const uint16_t* u = (const uint16_t*)h_up;
+  uint16_t* hm = (uint16_t*)h_mid;
+  uint8_t* qg = (uint8_t*)q_gate;
+  uint8_t* qu = (uint8_t*)q_up;
+  uint16_t* sg = (uint16_t*)s_gate;
+  uint16_t* su = (uint16_t*)s_up;
+  const bool fast = group_size >= 8 && group_size <= 512 && aligned16(g) && aligned16(u) &&
+                    aligned16(hm) && ((uintptr_t)qg & 7u) == 0 && ((uintptr_t)qu & 7u) == 0;
+  if (fast) {
+    const int lpg = (int)(group_size / 8);
+    if (bits == 4) launch_k1_lpg<4>(lpg, g, u, hm, qg, sg, qu, su, n_el / 8, st);
+    else launch_k1_lpg<8>(lpg, g, u, hm, qg, sg, qu, su, n_el / 8, st);
+  } else {
+    if (bits == 4) launch_quant_generic<4>(kBF16, true, g, u, hm, qg, sg, qu, su, n_el, group_size, st);
+    else launch_quant_generic<8>(kBF16, true, g, u, hm, qg, sg, qu, su, n_el, group_size, st);
+  }
+  return launch_status();
+}
+
+int cpt_dequant_swiglu_backward(const void* grad_h_mid, const void* q_gate, const void* s_gate,
+                                const void* q_up, const void* s_up, int64_t n, int64_t d,
+                                int bits, int64_t group_size, void* grad_h_gate,
+                                void* grad_h_up, void* h_mid_hat, void* stream) {
+  int rc = check_codec(n, d, bits, group_size, true);
+  if (rc) return rc;
+  const int64_t n_el = n * d;
+  if (n_el == 0) return kOk;
+  if (!grad_h_mid || !q_gate || !s_gate || !q_up || !s_up || !grad_h_gate || !grad_h_up)
+    return kErrShape;
+  hipStream_t st = (hipStream_t)stream;
+  const uint16_t* gm = (const uint16_t*)grad_h_mid;
+  const uint8_t* qg = (const uint8_t*)q_gate;
+  const uint8_t* qu = (const uint8_t*)q_up;
+  const uint16_t* sg = (const uint16_t*)s_gate;
+  const uint16_t* su = (const uint16_t*)s_up;
+  uint16_t* og = (uint16_t*)grad_h_gate;
+  uint16_t* ou = (uint16_t*)grad_h_up;
+  uint16_t* oh = (uint16_t*)h_mid_hat;
+  const bool fast = group_size >= 8 && aligned16(gm) && aligned16(og) && aligned16(ou) &&
+                    (oh == nullptr || aligned16(oh)) && ((uintptr_t)qg & 7u) == 0 &&
+                    ((uintptr_t)qu & 7u) == 0;
+  if (fast) {
+    const int64_t nchunk = n_el / 8;
+    const unsigned grid = grid_for(nchunk);
+    const int sh = log2_exact(group_size);
+#define CPT_K2(B, W) dequant_swiglu_bwd_kernel<B, W><<<grid, kBlock, 0, st>>>(gm, qg, sg, qu, su, og, ou, oh, nchunk, sh)
+    if (bits == 4) { if (oh) CPT_K2(4, true); else CPT_K2(4, false); }
+    else { if (oh) CPT_K2(8, true); else CPT_K2(8, false); }
+#undef CPT_K2
+  } else {
+    const unsigned grid = grid_for(n_el);
+#define CPT_K2G(B, W) dequant_swiglu_bwd_generic_kernel<B, W><<<grid, kBlock, 0, st>>>(gm, qg, sg, qu, su, og, ou, oh, n_el, group_size)
+    if (bits == 4) { if (oh) CPT_K2G(4, true); else CPT_K2G(4, false); }
+    else { if (oh) CPT_K2G(8, true); else CPT_K2G(8, false); }
+#undef CPT_K2G
+  }
+  return launch_status();
+}
+
+const char* cpt_status_string(int status) {
+  switch (status) {
+    case kOk: return "ok";
+    case kErrBits: return "unsupported bits (expected 4 or 8)";
+    case kErrRagged: return "D not divisible by group_size";
+    case kErrGroupPow2: return "group_size must be a power of two";
+    case kErrShape: return "bad shape or null pointer";
+    case kErrDType: return "unsupported dtype";
+    case kErrLaunch: return "kernel launch failed";
+    case kErrAlign: return "pointer alignment not met";
+    case kErrTooLarge: return "size beyond the supported maximum";
+    default: return "unknown status";
+  }
+}
+
+int cpt_abi_version(void) { return 1; }
+
+}  // extern "C"

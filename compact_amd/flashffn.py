@@ -1,0 +1,312 @@
+"""FlashFFN v3 on MI355X: LoRA-factored SwiGLU FFN whose backward cache is the
+per-group absmax int4/int8 code of h_gate and h_up.
+
+API kept from the reference (src/flashffn.py:1376-1694):
+  FlashFFNv3Function.apply(x, w_gate, a_gate, b_gate, w_up, a_up, b_up,
+                           w_down, a_down, b_down, s_gate=0.0, s_up=0.0,
+                           s_down=0.0, cache_mode="int4", group_size=64,
+                           use_triton=True)
+  make_v3_forward(mlp, cache_mode="int4", group_size=64, use_triton=True)
+  FlashFFNv3(mlp, cache_mode="int4", group_size=64, use_triton=True)
+
+  out_P = x @ W_P^T + s_P * (x @ A_P^T) @ B_P^T  for P in {gate, up, down}
+  h_mid = SiLU(h_gate) * h_up;  y = out_down(h_mid)
+
+cache_mode: 'int4' / 'int8' save x + codes + fp16 scales of h_gate and h_up;
+'bf16' saves h_gate and h_up; 'recompute' saves x only.  Adapters also save
+the thin [N, r] products xA_g, xA_u, h_mid A_d^T.  `use_triton` keeps the
+reference's name and meaning: use the fused device kernels (K1 forward, K2
+backward) for int4/int8 bf16 caches; False runs the standalone codec kernels.
+Every kernel is a HIP kernel of libcompact_amd.so; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+import warnings
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import kernels as K
+from .kernels import _V3_COUNTERS
+
+
+def _bits(mode: str) -> int:
+    return 4 if mode == "int4" else 8
+
+
+class FlashFFNv3Function(torch.autograd.Function):
+    """LoRA-factored SwiGLU FFN with a quantised GLU-cache backward
+    (src/flashffn.py:1376-1602).  a_*/b_* may be None (pass s_*=0.0)."""
+
+    @staticmethod
+    def forward(ctx, x, w_gate, a_gate, b_gate, w_up, a_up, b_up, w_down, a_down, b_down,
+                s_gate=0.0, s_up=0.0, s_down=0.0, cache_mode="int4", group_size=64,
+                use_triton=True):
+        assert cache_mode in ("int4", "int8", "bf16", "recompute"), cache_mode
+        _V3_COUNTERS["forward"] += 1
+        K._require_device(x)
+        orig_shape = x.shape
+        hidden_dim = x.shape[-1]
+        x_2d = x.reshape(-1, hidden_dim)
+
+        # factored forward in PEFT op order: base, then + s * B(A(x))  (:1410-1420)
+        h_gate = F.linear(x_2d, w_gate)
+        xa_g = None
+        if a_gate is not None:
+            xa_g = F.linear(x_2d, a_gate)
+            h_gate = h_gate + s_gate * F.linear(xa_g, b_gate)
+        h_up = F.linear(x_2d, w_up)
+        xa_u = None
+        if a_up is not None:
+            xa_u = F.linear(x_2d, a_up)
+            h_up = h_up + s_up * F.linear(xa_u, b_up)
+
+        c_gate = qs_gate = c_up = qs_up = None
+        fused_quant = (cache_mode in ("int4", "int8") and use_triton
+                       and h_gate.dtype == torch.bfloat16)                # :1424-1426
+        if fused_quant:
+            h_mid, c_gate, qs_gate, c_up, qs_up = K.silu_mul_quant(
+                h_gate, h_up, _bits(cache_mode), group_size)
+            del h_gate, h_up
+        else:
+            h_mid = K.silu_mul(h_gate, h_up)
+
+        y = F.linear(h_mid, w_down)                                       # :1435
+        ha_d = None
+        if a_down is not None:
+            ha_d = F.linear(h_mid, a_down)
+            y = y + s_down * F.linear(ha_d, b_down)
+
+        if not fused_quant:                                               # :1442-1451
+            if cache_mode in ("int4", "int8"):
+                c_gate, qs_gate = K.v3_quantize_group_absmax(h_gate, _bits(cache_mode),
+                                                             group_size)
+                c_up, qs_up = K.v3_quantize_group_absmax(h_up, _bits(cache_mode), group_size)
+                del h_gate, h_up
+            elif cache_mode == "bf16":
+                c_gate, c_up = h_gate, h_up
+            else:
+                del h_gate, h_up
+        del h_mid
+
+        ctx.save_for_backward(x, w_gate, a_gate, b_gate, w_up, a_up, b_up,
+                              w_down, a_down, b_down, xa_g, xa_u, ha_d,
+                              c_gate, qs_gate, c_up, qs_up)
+        ctx.s = (s_gate, s_up, s_down)
+        ctx.cache_mode = cache_mode
+        ctx.group_size = group_size
+        ctx.use_triton = fused_quant
+        ctx.orig_shape = orig_shape
+        ctx.in_dtype = x.dtype
+        if len(orig_shape) == 3:
+            y = y.view(orig_shape[0], orig_shape[1], hidden_dim)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        _V3_COUNTERS["backward"] += 1
+        (x, w_gate, a_gate, b_gate, w_up, a_up, b_up, w_down, a_down, b_down,
+         xa_g, xa_u, ha_d, c_gate, qs_gate, c_up, qs_up) = ctx.saved_tensors
+        s_gate, s_up, s_down = ctx.s
+        mode = ctx.cache_mode
+        hidden_dim = ctx.orig_shape[-1]
+        (need_x, need_wg, need_ag, need_bg, need_wu, need_au, need_bu,
+         need_wd, need_ad, need_bd) = ctx.needs_input_grad[:10]
+        gy = grad_y.reshape(-1, hidden_dim)
+        if not gy.is_contiguous():
+            gy = gy.contiguous()
+        x_2d = x.reshape(-1, hidden_dim)
+
+        need_gate_path = (need_x or need_wg or need_ag or need_bg
+                          or need_wu or need_au or need_bu)               # :1488-1489
+        need_h_mid = need_wd or (a_down is not None and need_ad)          # :1490
+        need_recon = need_gate_path or need_h_mid
+        use_k2 = mode in ("int4", "int8") and ctx.use_triton and need_gate_path
+
+        hg = hu = None
+        if need_recon and not use_k2:                                     # :1500-1516
+            if mode == "recompute":
+                hg = F.linear(x_2d, w_gate)
+                if a_gate is not None:
+                    hg = hg + s_gate * F.linear(xa_g, b_gate)
+                hu = F.linear(x_2d, w_up)
+                if a_up is not None:
+                    hu = hu + s_up * F.linear(xa_u, b_up)
+            elif mode == "bf16":
+                hg, hu = c_gate, c_up
+            else:
+                hg = K.v3_dequantize_group_absmax(c_gate, qs_gate, _bits(mode), ctx.group_size,
+                                                  ctx.in_dtype)
+                hu = K.v3_dequantize_group_absmax(c_up, qs_up, _bits(mode), ctx.group_size,
+                                                  ctx.in_dtype)
+
+        grad_w_down = grad_a_down = grad_b_down = None
+        gyB_d = None
+        if a_down is not None and (need_gate_path or need_ad):
+            gyB_d = gy @ b_down                                           # :1521
+
+        grad_h_gate = grad_h_up = h_mid_hat = None
+        if use_k2:                                                        # :1525-1533
+            grad_h_mid = gy @ w_down
+            if a_down is not None:
+                grad_h_mid = grad_h_mid + s_down * (gyB_d @ a_down)
+            grad_h_gate, grad_h_up, h_mid_hat = K.dequant_swiglu_backward(
+                grad_h_mid, c_gate, qs_gate, c_up, qs_up, _bits(mode), ctx.group_size,
+                want_h_mid=need_h_mid)
+            del grad_h_mid
+
+        if need_h_mid:                                                    # :1536-1543
+            if h_mid_hat is None:
+                h_mid_hat = K.silu_mul(hg, hu)
+            if need_wd:
+                grad_w_down = gy.t() @ h_mid_hat
+            if need_ad:
+                grad_a_down = s_down * (gyB_d.t() @ h_mid_hat)
+            del h_mid_hat
+        if need_bd:
+            grad_b_down = s_down * (gy.t() @ ha_d)                        # :1545
+
+        grad_x = None
+        grad_w_gate = grad_a_gate = grad_b_gate = None
+        grad_w_up = grad_a_up = grad_b_up = None
+        if need_gate_path:                                                # :1551-1587
+            if grad_h_gate is None:
+                grad_h_mid = gy @ w_down
+                if a_down is not None:
+                    grad_h_mid = grad_h_mid + s_down * (gyB_d @ a_down)
+                grad_h_gate, grad_h_up = K.swiglu_backward(grad_h_mid, hg, hu)
+                del grad_h_mid
+            ghgB = None
+            if a_gate is not None and (need_x or need_ag):
+                ghgB = grad_h_gate @ b_gate
+            ghuB = None
+            if a_up is not None and (need_x or need_au):
+                ghuB = grad_h_up @ b_up
+            if need_x:
+                grad_x = grad_h_gate @ w_gate
+                if a_gate is not None:
+                    grad_x = grad_x + s_gate * (ghgB @ a_gate)
+                grad_x = grad_x + grad_h_up @ w_up
+                if a_up is not None:
+                    grad_x = grad_x + s_up * (ghuB @ a_up)
+            if need_bg:
+                grad_b_gate = s_gate * (grad_h_gate.t() @ xa_g)
+            if need_ag:
+                grad_a_gate = s_gate * (ghgB.t() @ x_2d)
+            if need_bu:
+                grad_b_up = s_up * (grad_h_up.t() @ xa_u)
+            if need_au:
+                grad_a_up = s_up * (ghuB.t() @ x_2d)
+            if need_wg:
+                grad_w_gate = grad_h_gate.t() @ x_2d
+            if need_wu:
+                grad_w_up = grad_h_up.t() @ x_2d
+
+        # frozen weights => no dense [D_out, D_in] gradient was built (:1589-1593)
+        if not (need_wg or need_wu or need_wd):
+            assert grad_w_gate is None and grad_w_up is None and grad_w_down is None, \
+                "FlashFFNv3 invariant violated: dense weight grad with frozen weights"
+        if need_x and len(ctx.orig_shape) == 3:
+            grad_x = grad_x.view(ctx.orig_shape)
+        return (grad_x, grad_w_gate, grad_a_gate, grad_b_gate,
+                grad_w_up, grad_a_up, grad_b_up,
+                grad_w_down, grad_a_down, grad_b_down) + (None,) * (len(ctx.needs_input_grad) - 10)
+
+
+# ---------------------------------------------------------------------------
+# module-level API (src/flashffn.py:1605-1694)
+# ---------------------------------------------------------------------------
+
+def _is_lora(proj: nn.Module) -> bool:
+    return (hasattr(proj, "base_layer")
+            and isinstance(getattr(proj, "lora_A", None), nn.ModuleDict)
+            and len(proj.lora_A) > 0)
+
+
+def _v3_extract_proj(proj: nn.Module):
+    """(W, A, B, s) from a plain nn.Linear or a PEFT-LoRA-shaped wrapper
+    (src/flashffn.py:1605-1634).  Plain: (weight, None, None, 0.0).  Rejects
+    DoRA / AdaLoRA / several active adapters; warns that dropout is ignored."""
+    if not _is_lora(proj):
+        return proj.weight, None, None, 0.0
+    if len(getattr(proj, "lora_magnitude_vector", {}) or {}) > 0:
+        raise NotImplementedError("FlashFFNv3 fast path does not support DoRA")
+    if hasattr(proj, "lora_E"):
+        raise NotImplementedError("FlashFFNv3 fast path does not support AdaLoRA")
+    assert len(proj.active_adapters) == 1, "exactly one active adapter expected"
+    name = proj.active_adapters[0]
+    drop = proj.lora_dropout[name]
+    p = float(getattr(drop, "p", 0.0))
+    if p > 0.0:
+        warnings.warn(f"FlashFFNv3 ignores LoRA dropout (p={p}); results differ from PEFT "
+                      "forward when training with dropout.")
+    w = proj.get_base_layer().weight
+    return w, proj.lora_A[name].weight, proj.lora_B[name].weight, float(proj.scaling[name])
+
+
+def _v3_proj_kind(proj: nn.Module) -> str:
+    """Structural (duck-typed) classification of one MLP projection
+    (src/flashffn.py:1798-1821): 'dora' | 'adalora' | 'vera' | 'dylora' |
+    'lora' | 'plain' | 'unknown'."""
+    if hasattr(proj, "base_layer"):
+        if len(getattr(proj, "lora_magnitude_vector", None) or {}) > 0:
+            return "dora"
+        if len(getattr(proj, "lora_E", None) or {}) > 0:
+            return "adalora"
+        if len(getattr(proj, "vera_lambda_d", None) or {}) > 0:
+            return "vera"
+        if (isinstance(getattr(proj, "lora_A", None), nn.Parameter)
+                and isinstance(getattr(proj, "lora_B", None), nn.Parameter)
+                and hasattr(proj, "r") and hasattr(proj, "scaling")):
+            return "dylora"
+        if isinstance(getattr(proj, "lora_A", None), nn.ModuleDict) and len(proj.lora_A) > 0:
+            return "lora"
+        return "unknown"
+    if hasattr(proj, "weight"):
+        return "plain"
+    return "unknown"
+
+
+def make_v3_forward(mlp: nn.Module, cache_mode: str = "int4", group_size: int = 64,
+                    use_triton: bool = True):
+    """Drop-in replacement for a LLaMA-style MLP forward (src/flashffn.py:1637-1678).
+    `mlp` exposes gate_proj / up_proj / down_proj, each a plain nn.Linear or a
+    PEFT-LoRA-shaped wrapper; factors are re-extracted on every call and cast
+    to x's dtype through autograd.  Unknown wrappers raise NotImplementedError."""
+    kinds = tuple(_v3_proj_kind(getattr(mlp, p)) for p in ("gate_proj", "up_proj", "down_proj"))
+    if any(k == "unknown" for k in kinds):
+        raise NotImplementedError(f"FlashFFNv3: unsupported projection wrapper(s) on MLP: {kinds}")
+    if any(k not in ("plain", "lora") for k in kinds):
+        raise NotImplementedError(f"FlashFFNv3: adapter kinds {kinds} need the adapter Function")
+
+    def v3_forward(x):
+        wg, ag, bg, sg = _v3_extract_proj(mlp.gate_proj)
+        wu, au, bu, su = _v3_extract_proj(mlp.up_proj)
+        wd, ad, bd, sd = _v3_extract_proj(mlp.down_proj)
+        dt = x.dtype
+
+        def cast(t):
+            return t if (t is None or t.dtype == dt) else t.to(dt)
+
+        return FlashFFNv3Function.apply(x, cast(wg), cast(ag), cast(bg), cast(wu), cast(au),
+                                        cast(bu), cast(wd), cast(ad), cast(bd), sg, su, sd,
+                                        cache_mode, group_size, use_triton)
+    return v3_forward
+
+
+class FlashFFNv3(nn.Module):
+    """Module wrapper around make_v3_forward for an existing MLP (src/flashffn.py:1681-1694)."""
+
+    def __init__(self, mlp: nn.Module, cache_mode: str = "int4", group_size: int = 64,
+                 use_triton: bool = True):
+        super().__init__()
+        self.mlp = mlp
+        self.cache_mode = cache_mode
+        self.group_size = group_size
+        self.use_triton = use_triton
+        self._fwd = make_v3_forward(mlp, cache_mode, group_size, use_triton)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self._fwd(x)

@@ -1,0 +1,282 @@
+"""torch-facing wrappers of the HIP kernels, with the reference's names and
+argument contracts (src/flashffn.py:205-293, 1055-1110, 1303-1373).
+
+Each wrapper validates its arguments the way the reference does (assert),
+allocates its outputs with torch on the input's device (the C ABI never
+allocates), and launches on torch's current stream.  Inputs must be HIP
+device tensors: there is no CPU path.
+
+The reference's Triton-era names (`triton_silu_mul_quant`, ...) are kept as
+aliases so callers of the reference swap in unchanged; `use_triton` in the
+Function API keeps its meaning "use the fused device kernels".
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import check
+
+_DT = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}
+
+# Honesty counters (src/flashffn.py:1040-1042): prove which path ran.
+# quant_fwd / dequant_bwd count executions of the fused K1 / K2 kernels.
+_V3_COUNTERS = {"forward": 0, "backward": 0,
+                "triton_quant_fwd": 0, "triton_dequant_bwd": 0,
+                "adapter_forward": 0, "adapter_backward": 0}
+
+
+def v3_reset_counters():
+    for k in _V3_COUNTERS:
+        _V3_COUNTERS[k] = 0
+
+
+def _stream(t: torch.Tensor):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+class KernelTimer:
+    """Opt-in per-kernel timing with HIP events recorded on the stream each
+    kernel is launched on.  `with KernelTimer() as kt: ...` collects
+    (start, end) event pairs per kernel name; `kt.avg_ms()` reads them after
+    a synchronize.  Disabled (zero events) outside the context."""
+
+    active = None
+
+    def __init__(self):
+        self.events = {}
+
+    def __enter__(self):
+        KernelTimer.active = self
+        return self
+
+    def __exit__(self, *exc):
+        KernelTimer.active = None
+
+    def avg_ms(self):
+        out = {}
+        for name, pairs in self.events.items():
+            ts = [a.elapsed_time(b) for a, b in pairs]
+            out[name] = {"calls": len(ts), "avg_ms": sum(ts) / len(ts), "total_ms": sum(ts)}
+        return out
+
+
+class _timed:
+    __slots__ = ("name", "ev")
+
+    def __init__(self, name):
+        self.name = name
+        self.ev = None
+
+    def __enter__(self):
+        if KernelTimer.active is not None:
+            self.ev = torch.cuda.Event(enable_timing=True)
+            self.ev.record(torch.cuda.current_stream())
+        return self
+
+    def __exit__(self, *exc):
+        kt = KernelTimer.active
+        if self.ev is not None and kt is not None:
+            end = torch.cuda.Event(enable_timing=True)
+            end.record(torch.cuda.current_stream())
+            kt.events.setdefault(self.name, []).append((self.ev, end))
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _require_device(*ts):
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError("compact_amd kernels run on the HIP device only; got a CPU tensor")
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    if t.dtype not in _DT:
+        raise AssertionError(f"unsupported dtype {t.dtype}")
+    return _DT[t.dtype]
+
+
+# ---------------------------------------------------------------------------
+# GLU elementwise (src/flashffn.py:205-293)
+# ---------------------------------------------------------------------------
+
+def silu_mul(h_gate: torch.Tensor, h_up: torch.Tensor) -> torch.Tensor:
+    """SiLU(h_gate) * h_up in float32, stored in h_gate's dtype
+    (`triton_silu_mul`, src/flashffn.py:205-220)."""
+    _require_device(h_gate, h_up)
+    assert h_up.shape == h_gate.shape and h_up.dtype == h_gate.dtype
+    h_gate, h_up = h_gate.contiguous(), h_up.contiguous()
+    out = torch.empty_like(h_gate)
+    check(_lib.lib().cpt_silu_mul(h_gate.data_ptr(), h_up.data_ptr(), out.data_ptr(),
+                                  h_gate.numel(), _dtype_code(h_gate), _stream(h_gate)),
+          "silu_mul")
+    return out
+
+
+def swiglu_backward(grad_h_mid, h_gate, h_up):
+    """(grad_h_gate, grad_h_up) through h_mid = SiLU(h_gate)*h_up
+    (`triton_swiglu_backward`, src/flashffn.py:223-239)."""
+    _require_device(grad_h_mid, h_gate, h_up)
+    assert h_gate.shape == h_up.shape == grad_h_mid.shape
+    assert h_gate.dtype == h_up.dtype == grad_h_mid.dtype
+    grad_h_mid, h_gate, h_up = grad_h_mid.contiguous(), h_gate.contiguous(), h_up.contiguous()
+    dg = torch.empty_like(h_gate)
+    du = torch.empty_like(h_up)
+    check(_lib.lib().cpt_swiglu_backward(grad_h_mid.data_ptr(), h_gate.data_ptr(),
+                                         h_up.data_ptr(), dg.data_ptr(), du.data_ptr(),
+                                         h_gate.numel(), _dtype_code(h_gate), _stream(h_gate)),
+          "swiglu_backward")
+    return dg, du
+
+
+def swiglu_backward_glu(grad_h_mid, h_gate, h_up, want_h_mid, inplace=False):
+    """SwiGLU backward plus the h_mid rematerialisation in one pass
+    (`triton_swiglu_backward_glu`, src/flashffn.py:259-293).  `inplace=True`
+    writes grad_h_gate over h_gate, grad_h_up over h_up and h_mid over
+    grad_h_mid (inputs must be contiguous and private to the caller).
+    Returns (grad_h_gate, grad_h_up, h_mid | None)."""
+    _require_device(grad_h_mid, h_gate, h_up)
+    assert h_gate.shape == h_up.shape == grad_h_mid.shape
+    assert h_gate.dtype == h_up.dtype == grad_h_mid.dtype
+    if inplace:
+        assert grad_h_mid.is_contiguous() and h_gate.is_contiguous() and h_up.is_contiguous()
+        dg, du = h_gate, h_up
+        hm = grad_h_mid if want_h_mid else None
+    else:
+        grad_h_mid, h_gate, h_up = grad_h_mid.contiguous(), h_gate.contiguous(), h_up.contiguous()
+        dg = torch.empty_like(h_gate)
+        du = torch.empty_like(h_up)
+        hm = torch.empty_like(h_gate) if want_h_mid else None
+    check(_lib.lib().cpt_swiglu_backward_glu(grad_h_mid.data_ptr(), h_gate.data_ptr(),
+                                             h_up.data_ptr(), dg.data_ptr(), du.data_ptr(),
+                                             _ptr(hm), h_gate.numel(), _dtype_code(h_gate),
+                                             _stream(h_gate)),
+          "swiglu_backward_glu")
+    return dg, du, hm
+
+
+# ---------------------------------------------------------------------------
+# codec (src/flashffn.py:1055-1110)
+# ---------------------------------------------------------------------------
+
+def v3_quantize_group_absmax(t: torch.Tensor, bits: int, group_size: int = 64):
+    """Per-group absmax quantisation along the last dim
+    (src/flashffn.py:1055-1088).  t: [N, D] float tensor.  Returns
+    (payload uint8 [N, D/2] | int8 [N, D], scales fp16 [N, D/group_size])."""
+    assert bits in (4, 8), f"unsupported bits={bits}"
+    _require_device(t)
+    n, d = t.shape
+    assert d % group_size == 0, f"D={d} not divisible by group_size={group_size}"
+    t = t.contiguous()
+    g = d // group_size
+    if bits == 4:
+        payload = torch.empty((n, d // 2), dtype=torch.uint8, device=t.device)
+    else:
+        payload = torch.empty((n, d), dtype=torch.int8, device=t.device)
+    scales = torch.empty((n, g), dtype=torch.float16, device=t.device)
+    check(_lib.lib().cpt_v3_quantize_group_absmax(t.data_ptr(), _dtype_code(t), n, d, bits,
+                                                  group_size, payload.data_ptr(),
+                                                  scales.data_ptr(), _stream(t)),
+          "v3_quantize_group_absmax")
+    return payload, scales
+
+
+def v3_dequantize_group_absmax(payload, scales, bits, group_size=64, dtype=torch.bfloat16):
+    """Inverse of v3_quantize_group_absmax (src/flashffn.py:1091-1110):
+    out_dtype(fp32(code) * fp32(scale)), [N, D]."""
+    assert bits in (4, 8), f"unsupported bits={bits}"
+    _require_device(payload, scales)
+    n = payload.shape[0]
+    d = payload.shape[1] * (2 if bits == 4 else 1)
+    assert d % group_size == 0, f"D={d} not divisible by group_size={group_size}"
+    assert tuple(scales.shape) == (n, d // group_size) and scales.dtype == torch.float16
+    payload, scales = payload.contiguous(), scales.contiguous()
+    out = torch.empty((n, d), dtype=dtype, device=payload.device)
+    check(_lib.lib().cpt_v3_dequantize_group_absmax(payload.data_ptr(), scales.data_ptr(), n, d,
+                                                    bits, group_size, out.data_ptr(),
+                                                    _DT[dtype], _stream(payload)),
+          "v3_dequantize_group_absmax")
+    return out
+
+
+def _check_quant_shapes(t, bits, group_size):
+    """src/flashffn.py:1303-1311."""
+    assert bits in (4, 8), f"unsupported bits={bits}"
+    assert t.dim() == 2 and t.is_contiguous(), "expected contiguous [N, D]"
+    assert t.dtype == torch.bfloat16, f"fused v3 kernels are bf16-only, got {t.dtype}"
+    n, d = t.shape
+    assert d % group_size == 0, f"D={d} not divisible by group_size={group_size}"
+    assert group_size > 0 and (group_size & (group_size - 1)) == 0, \
+        f"group_size={group_size} must be a power of two"
+    return n, d, d // group_size
+
+
+def silu_mul_quant(h_gate, h_up, bits, group_size=64):
+    """K1 (src/flashffn.py:1314-1340): returns (h_mid, q_gate, s_gate, q_up, s_up);
+    h_mid equals silu_mul(h_gate, h_up) and payloads/scales equal
+    v3_quantize_group_absmax of each input, bit for bit."""
+    _require_device(h_gate, h_up)
+    n, d, g = _check_quant_shapes(h_gate, bits, group_size)
+    assert h_up.shape == h_gate.shape and h_up.is_contiguous() and h_up.dtype == h_gate.dtype
+    dev = h_gate.device
+    h_mid = torch.empty_like(h_gate)
+    s_gate = torch.empty((n, g), dtype=torch.float16, device=dev)
+    s_up = torch.empty((n, g), dtype=torch.float16, device=dev)
+    if bits == 4:
+        q_gate = torch.empty((n, d // 2), dtype=torch.uint8, device=dev)
+        q_up = torch.empty((n, d // 2), dtype=torch.uint8, device=dev)
+    else:
+        q_gate = torch.empty((n, d), dtype=torch.int8, device=dev)
+        q_up = torch.empty((n, d), dtype=torch.int8, device=dev)
+    with _timed("silu_mul_quant"):
+        rc = _lib.lib().cpt_silu_mul_quant(h_gate.data_ptr(), h_up.data_ptr(), n, d, bits,
+                                           group_size, h_mid.data_ptr(), q_gate.data_ptr(),
+                                           s_gate.data_ptr(), q_up.data_ptr(), s_up.data_ptr(),
+                                           _stream(h_gate))
+    check(rc, "silu_mul_quant")
+    _V3_COUNTERS["triton_quant_fwd"] += 1
+    return h_mid, q_gate, s_gate, q_up, s_up
+
+
+def dequant_swiglu_backward(grad_h_mid, q_gate, s_gate, q_up, s_up, bits, group_size=64,
+                            want_h_mid=False):
+    """K2 (src/flashffn.py:1343-1373): returns (grad_h_gate, grad_h_up,
+    h_mid_hat | None), equal to dequantise-through-bf16 + swiglu_backward
+    (+ silu_mul) without materialising the dequantised caches."""
+    _require_device(grad_h_mid, q_gate, s_gate, q_up, s_up)
+    assert grad_h_mid.dim() == 2 and grad_h_mid.is_contiguous()
+    assert grad_h_mid.dtype == torch.bfloat16, \
+        f"fused v3 kernels are bf16-only, got {grad_h_mid.dtype}"
+    assert bits in (4, 8), f"unsupported bits={bits}"
+    n, d = grad_h_mid.shape
+    assert d % group_size == 0, f"D={d} not divisible by group_size={group_size}"
+    assert group_size > 0 and (group_size & (group_size - 1)) == 0, \
+        f"group_size={group_size} must be a power of two"
+    g = d // group_size
+    assert tuple(s_gate.shape) == (n, g) and tuple(s_up.shape) == (n, g)
+    expect = (n, d // 2) if bits == 4 else (n, d)
+    assert tuple(q_gate.shape) == expect and tuple(q_up.shape) == expect, \
+        f"payload shape {tuple(q_gate.shape)} != expected {expect}"
+    q_gate, s_gate, q_up, s_up = (t.contiguous() for t in (q_gate, s_gate, q_up, s_up))
+    grad_h_gate = torch.empty_like(grad_h_mid)
+    grad_h_up = torch.empty_like(grad_h_mid)
+    h_mid_hat = torch.empty_like(grad_h_mid) if want_h_mid else None
+    with _timed("dequant_swiglu_backward"):
+        rc = _lib.lib().cpt_dequant_swiglu_backward(
+            grad_h_mid.data_ptr(), q_gate.data_ptr(), s_gate.data_ptr(), q_up.data_ptr(),
+            s_up.data_ptr(), n, d, bits, group_size, grad_h_gate.data_ptr(),
+            grad_h_up.data_ptr(), _ptr(h_mid_hat), _stream(grad_h_mid))
+    check(rc, "dequant_swiglu_backward")
+    _V3_COUNTERS["triton_dequant_bwd"] += 1
+    return grad_h_gate, grad_h_up, h_mid_hat
+
+
+# The reference's names (src/flashffn.py:205,223,259,1314,1343), kept for drop-in use.
+triton_silu_mul = silu_mul
+triton_swiglu_backward = swiglu_backward
+triton_swiglu_backward_glu = swiglu_backward_glu
+triton_silu_mul_quant = silu_mul_quant
+triton_dequant_swiglu_backward = dequant_swiglu_backward

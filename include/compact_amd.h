@@ -1,0 +1,94 @@
+/*
+ * compact_amd.h -- C ABI of libcompact_amd.so, the gfx950 (MI355X) kernels of
+ * the FlashFFN v3 hot path (SwiGLU FFN with a compressed GLU cache).
+ *
+ * Every entry point takes device pointers, sizes and a HIP stream (passed as
+ * void*; NULL is the legacy default stream), launches asynchronously on that
+ * stream, allocates nothing and returns a status code (0 = success, see
+ * CPT_* below; cpt_status_string() gives the text).  Tensors are row-major and
+ * contiguous.  dtype codes: 0 = float32, 1 = float16, 2 = bfloat16.
+ * References are file:line in the reference repository SDMuhsin/CompAct.
+ */
+#ifndef COMPACT_AMD_H
+#define COMPACT_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  CPT_OK = 0,
+  CPT_ERR_BITS = 1,        /* bits not in {4, 8} */
+  CPT_ERR_RAGGED = 2,      /* D % group_size != 0 (ragged last group) */
+  CPT_ERR_GROUP_POW2 = 3,  /* group_size not a power of two (fused kernels) */
+  CPT_ERR_SHAPE = 4,       /* negative / inconsistent size, null pointer */
+  CPT_ERR_DTYPE = 5,       /* dtype code not supported by this entry point */
+  CPT_ERR_LAUNCH = 6,      /* the HIP launch failed */
+  CPT_ERR_ALIGN = 7,       /* a pointer misses the alignment the kernel needs */
+  CPT_ERR_TOO_LARGE = 8    /* size beyond what the kernel indexes */
+};
+
+enum { CPT_F32 = 0, CPT_F16 = 1, CPT_BF16 = 2 };
+
+const char* cpt_status_string(int status);
+int cpt_abi_version(void);
+
+/* ---------------- per-group absmax codec ---------------- */
+
+/* Replaces v3_quantize_group_absmax (src/flashffn.py:1055-1088).
+ * t: [n, d] of `dtype`; payload: uint8 [n, d/2] (bits=4, code+8 nibbles, even
+ * column low) or int8 [n, d] (bits=8); scales: fp16 [n, d/group_size].
+ * scale = fp16(absmax/qmax); code = clamp(rint(v/safe), +-qmax).  Any
+ * group_size dividing d (the eager codec has no power-of-two requirement). */
+int cpt_v3_quantize_group_absmax(const void* t, int dtype, int64_t n, int64_t d, int bits,
+                                 int64_t group_size, void* payload, void* scales, void* stream);
+
+/* Replaces v3_dequantize_group_absmax (src/flashffn.py:1091-1110):
+ * out[n, d] (out_dtype) = out_dtype(fp32(code) * fp32(scale)). */
+int cpt_v3_dequantize_group_absmax(const void* payload, const void* scales, int64_t n, int64_t d,
+                                   int bits, int64_t group_size, void* out, int out_dtype,
+                                   void* stream);
+
+/* ---------------- GLU elementwise kernels ---------------- */
+
+/* Replaces triton_silu_mul / _silu_mul_fwd_kernel (src/flashffn.py:50-82,205-220):
+ * out = (g * sigmoid(g)) * u in float32, stored in `dtype`. */
+int cpt_silu_mul(const void* h_gate, const void* h_up, void* out, int64_t n_elements, int dtype,
+                 void* stream);
+
+/* Replaces triton_swiglu_backward / _swiglu_bwd_kernel (src/flashffn.py:85-126,223-239). */
+int cpt_swiglu_backward(const void* grad_h_mid, const void* h_gate, const void* h_up,
+                        void* grad_h_gate, void* grad_h_up, int64_t n_elements, int dtype,
+                        void* stream);
+
+/* Replaces triton_swiglu_backward_glu / _swiglu_bwd_glu_kernel
+ * (src/flashffn.py:129-198,259-293): the backward plus h_mid (NULL to skip);
+ * outputs may alias inputs (in-place mode). */
+int cpt_swiglu_backward_glu(const void* grad_h_mid, const void* h_gate, const void* h_up,
+                            void* grad_h_gate, void* grad_h_up, void* h_mid, int64_t n_elements,
+                            int dtype, void* stream);
+
+/* ---------------- fused codec kernels (bf16 only) ---------------- */
+
+/* Replaces triton_silu_mul_quant / K1 _v3_silu_mul_quant_fwd_kernel
+ * (src/flashffn.py:1188-1225,1314-1340): h_mid = SiLU(g)*u (bf16 [n,d]) and
+ * the codec of both g and u.  group_size must be a power of two. */
+int cpt_silu_mul_quant(const void* h_gate, const void* h_up, int64_t n, int64_t d, int bits,
+                       int64_t group_size, void* h_mid, void* q_gate, void* s_gate, void* q_up,
+                       void* s_up, void* stream);
+
+/* Replaces triton_dequant_swiglu_backward / K2 _v3_dequant_swiglu_bwd_kernel
+ * (src/flashffn.py:1256-1300,1343-1373): dequantise both caches through bf16,
+ * SwiGLU backward, and h_mid^ when h_mid_hat is not NULL. */
+int cpt_dequant_swiglu_backward(const void* grad_h_mid, const void* q_gate, const void* s_gate,
+                                const void* q_up, const void* s_up, int64_t n, int64_t d,
+                                int bits, int64_t group_size, void* grad_h_gate,
+                                void* grad_h_up, void* h_mid_hat, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* COMPACT_AMD_H */

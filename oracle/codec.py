@@ -64,15 +64,17 @@ def _qmax(bits: int) -> np.float32:
     return np.float32(2 ** (bits - 1) - 1)
 
 
-def check_codec_args(shape, bits: int, group_size: int):
-    """The reference's argument contract (flashffn.py:1070-1072,1303-1311):
-    bits in {4, 8}, D divisible by group_size, group_size a power of two."""
+def check_codec_args(shape, bits: int, group_size: int, need_pow2: bool = False):
+    """The reference's argument contract: the eager codec asserts bits in
+    {4, 8} and D divisible by group_size (flashffn.py:1070-1072); the fused
+    K1/K2 wrappers also require a power-of-two group_size (:1303-1311)."""
     assert bits in (4, 8), f"unsupported bits={bits}"
     assert len(shape) == 2, "expected [N, D]"
     n, d = shape
     assert d % group_size == 0, f"D={d} not divisible by group_size={group_size}"
-    assert group_size > 0 and (group_size & (group_size - 1)) == 0, \
-        f"group_size={group_size} must be a power of two"
+    if need_pow2:
+        assert group_size > 0 and (group_size & (group_size - 1)) == 0, \
+            f"group_size={group_size} must be a power of two"
     return n, d, d // group_size
 
 
@@ -193,6 +195,7 @@ def silu_mul_quant(g: np.ndarray, u: np.ndarray, bits: int, group_size: int = 64
     """K1 contract (flashffn.py:1116-1122,1314-1319): h_mid = silu_mul(g, u)
     plus the codec of BOTH g and u.  g, u: float32 values of the bf16 inputs.
     Returns (h_mid_f32, q_gate, s_gate, q_up, s_up); the caller rounds h_mid."""
+    check_codec_args(np.shape(g), bits, group_size, need_pow2=True)
     qg, sg = quantize_group_absmax(g, bits, group_size)
     qu, su = quantize_group_absmax(u, bits, group_size)
     return silu_mul(g, u), qg, sg, qu, su

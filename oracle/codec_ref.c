@@ -85,7 +85,7 @@ static float rint_even(float x) {          /* round half to even, exact in f32 *
  * scales: binary16 bits [n, d/group]. Returns 0, or -1 on a bad argument. */
 int oracle_quantize(const float* t, int64_t n, int64_t d, int bits, int group,
                     void* payload, uint16_t* scales) {
-    if ((bits != 4 && bits != 8) || group <= 0 || (group & (group - 1)) || d % group) return -1;
+    if ((bits != 4 && bits != 8) || group <= 0 || d % group) return -1;
     const float qmax = (float)((1 << (bits - 1)) - 1);
     const int64_t ng = d / group;
     volatile float qm = qmax;               /* keep the division a real f32 division */

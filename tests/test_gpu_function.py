@@ -1,0 +1,170 @@
+"""GPU parity of FlashFFNv3Function / make_v3_forward against the CPU oracle
+and the fp32 autograd reference, after the reference's gates
+(src/verify_flashffn_v3.py:376-625, src/verify_v3_kernels.py:260-350):
+  V1  y vs the oracle (rel 1e-2 in bf16) and identical across cache modes;
+  V2  grads vs fp32 plain autograd of the same bf16 inputs: cosine >= 0.999
+      (recompute / bf16 / int8), int4 adapter grads >= 0.98, grad_x >= 0.99;
+      grads vs the oracle Function (rel Frobenius 2e-2 in bf16, 1e-5 in fp32);
+  G3  fused-kernel grads == standalone-codec grads, bitwise; counters prove
+      which kernels ran;
+  V3  saved-for-backward bytes == the closed form.
+"""
+
+import pytest
+import torch
+
+from oracle import flashffn_ref as R
+from tests.peft_like import SwiGLUMLP, lora_wrap
+
+pytestmark = pytest.mark.gpu
+
+H, D, RANK, S, N = 256, 768, 16, 2.0, 256
+
+
+def _cpt():
+    import compact_amd
+    return compact_amd
+
+
+def _to(ps, device):
+    return {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in ps.items()}
+
+
+def _run(ps, x, gy, mode, group, use_triton=True):
+    return R.run_function_grads(_cpt().FlashFFNv3Function.apply, ps, x, gy, mode, group,
+                                use_triton)
+
+
+@pytest.mark.parametrize("config", ["all", "gateup", "none", "fullft"])
+@pytest.mark.parametrize("mode,group", [("int4", 64), ("int8", 128), ("bf16", 64),
+                                        ("recompute", 64)])
+def test_function_vs_oracle_bf16(device, config, mode, group):
+    ps = R.synthetic_param_set(config, H, D, RANK, S, seed=3, dtype=torch.bfloat16)
+    gen = torch.Generator().manual_seed(11)
+    x = torch.randn(N, H, generator=gen).to(torch.bfloat16)
+    gy = torch.randn(N, H, generator=gen).to(torch.bfloat16)
+    got, y = _run(_to(ps, device), x.to(device), gy.to(device), mode, group)
+    ora, y_o = R.run_function_grads(R.OracleFlashFFNv3Function.apply, ps, x, gy, mode, group)
+    ref, y_ref = R.ref_grads_fp32(ps, x, gy)
+    assert R.rel_frob(y.cpu(), y_o) < 1e-2
+    assert set(got) == set(ref)
+    for k in ref:
+        g = got[k].cpu()
+        assert R.rel_frob(g, ora[k]) < 2e-2, k
+        c = R.tensor_cos(g, ref[k])
+        if mode == "int4":
+            floor = 0.99 if k == "grad_x" else (0.98 if k.startswith(("a_", "b_")) else 0.98)
+        else:
+            floor = 0.999
+        assert c >= floor, (k, c)
+
+
+@pytest.mark.parametrize("config", ["all", "fullft"])
+@pytest.mark.parametrize("mode", ["int8", "recompute", "bf16"])
+def test_function_vs_oracle_fp32(device, config, mode):
+    """fp32 (config C1's dtype): the unfused device kernels, 1e-5."""
+    torch.backends.cuda.matmul.allow_tf32 = False
+    ps = R.synthetic_param_set(config, H, D, RANK, S, seed=4, dtype=torch.float32)
+    gen = torch.Generator().manual_seed(12)
+    x = torch.randn(N, H, generator=gen)
+    gy = torch.randn(N, H, generator=gen)
+    got, y = _run(_to(ps, device), x.to(device), gy.to(device), mode, 128)
+    ora, y_o = R.run_function_grads(R.OracleFlashFFNv3Function.apply, ps, x, gy, mode, 128)
+    assert R.rel_frob(y.cpu(), y_o) < 1e-5
+    # Unquantised modes: 1e-5.  int8 cache: the codes depend on h_gate/h_up,
+    # which CPU and GPU GEMMs round differently (~1e-7 relative); a value on a
+    # rounding tie flips one code, which moves grads by ~1e-4, so 1e-3 there.
+    tol = 1e-5 if mode != "int8" else 1e-3
+    for k in ora:
+        assert R.rel_frob(got[k].cpu(), ora[k]) < tol, k
+
+
+@pytest.mark.parametrize("mode", ["int4", "int8"])
+def test_fused_equals_unfused_bitwise(device, mode):
+    cpt = _cpt()
+    ps = _to(R.synthetic_param_set("all", H, D, RANK, S, seed=5), device)
+    gen = torch.Generator().manual_seed(13)
+    x = torch.randn(N, H, generator=gen).to(torch.bfloat16).to(device)
+    gy = torch.randn(N, H, generator=gen).to(torch.bfloat16).to(device)
+    cpt.v3_reset_counters()
+    fused, yf = _run(ps, x, gy, mode, 64, use_triton=True)
+    assert cpt._V3_COUNTERS["triton_quant_fwd"] == 1
+    assert cpt._V3_COUNTERS["triton_dequant_bwd"] == 1
+    cpt.v3_reset_counters()
+    eager, ye = _run(ps, x, gy, mode, 64, use_triton=False)
+    assert cpt._V3_COUNTERS["triton_quant_fwd"] == 0
+    assert cpt._V3_COUNTERS["triton_dequant_bwd"] == 0
+    assert cpt._V3_COUNTERS["forward"] == 1 and cpt._V3_COUNTERS["backward"] == 1
+    assert torch.equal(yf, ye)
+    for k in fused:
+        assert torch.equal(fused[k], eager[k]), k
+
+
+def test_forward_identical_across_cache_modes_3d(device):
+    cpt = _cpt()
+    ps = _to(R.synthetic_param_set("all", H, D, RANK, S, seed=6), device)
+    x = torch.randn(2, 64, H, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    x = x.to(device)
+    ys = []
+    with torch.no_grad():
+        for mode in ("int4", "int8", "bf16", "recompute"):
+            ys.append(cpt.FlashFFNv3Function.apply(
+                x, ps["w_gate"], ps["a_gate"], ps["b_gate"], ps["w_up"], ps["a_up"],
+                ps["b_up"], ps["w_down"], ps["a_down"], ps["b_down"], S, S, S, mode, 64, True))
+    assert ys[0].shape == x.shape
+    assert all(torch.equal(ys[0], y) for y in ys)
+
+
+@pytest.mark.parametrize("mode,bits", [("int4", 4), ("int8", 8)])
+def test_saved_bytes_closed_form(device, mode, bits):
+    cpt = _cpt()
+    ps = _to(R.synthetic_param_set("all", H, D, RANK, S, seed=7), device)
+    params = [v for v in ps.values() if isinstance(v, torch.Tensor)]
+    for p in params:
+        p.requires_grad_(True)
+    x = torch.randn(N, H, device=device).to(torch.bfloat16).requires_grad_(True)
+    ptrs = {p.data_ptr() for p in params} | {x.data_ptr()}
+    got, entries = R.count_saved_bytes(
+        lambda: cpt.FlashFFNv3Function.apply(
+            x, ps["w_gate"], ps["a_gate"], ps["b_gate"], ps["w_up"], ps["a_up"], ps["b_up"],
+            ps["w_down"], ps["a_down"], ps["b_down"], S, S, S, mode, 64, True), ptrs)
+    got += x.nbytes
+    assert got == R.saved_bytes_closed_form(N, H, D, bits, 64, n_thin=3, rank=RANK), entries
+
+
+@pytest.mark.parametrize("lora", [False, True])
+def test_make_v3_forward_matches_module(device, lora):
+    """The patched MLP forward equals the unpatched module within bf16
+    tolerance, and its grads reach the original parameters."""
+    cpt = _cpt()
+    torch.manual_seed(0)
+    mlp = SwiGLUMLP(H, D)
+    if lora:
+        lora_wrap(mlp, RANK, 32.0)
+    mlp = mlp.to(device=device, dtype=torch.bfloat16)
+    x = torch.randn(4, 32, H, device=device).to(torch.bfloat16)
+    y_ref = mlp(x).float()
+    fwd = cpt.make_v3_forward(mlp, "int8", 128)
+    y = fwd(x)
+    assert y.shape == x.shape
+    assert R.rel_frob(y.float(), y_ref) < 1e-2
+    y.float().pow(2).mean().backward()
+    trainable = [p for p in mlp.parameters() if p.requires_grad]
+    assert trainable and all(p.grad is not None for p in trainable)
+    mod = cpt.FlashFFNv3(mlp, "int4", 64)
+    assert R.rel_frob(mod(x).float(), y_ref) < 3e-2
+
+
+def test_unknown_wrapper_raises():
+    import torch.nn as nn
+    cpt = _cpt()
+    mlp = SwiGLUMLP(16, 32)
+
+    class Weird(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.base_layer = nn.Linear(16, 32)
+
+    mlp.gate_proj = Weird()
+    with pytest.raises(NotImplementedError):
+        cpt.make_v3_forward(mlp)

@@ -1,0 +1,235 @@
+"""GPU parity of the codec and GLU kernels (libcompact_amd.so) against the CPU
+oracle, following the reference's gates G1/G2/G4 (src/verify_v3_kernels.py:
+98-253, 357-414).
+
+Bar: codes and scales bit-exact; dequantised values bit-exact (no
+transcendental involved); h_mid / grad_h_gate / grad_h_up within
+REL = 1e-2 elementwise (plus 1e-5 of the tensor's max as absolute floor) in
+bf16 -- the only difference from the oracle is the float32 exp inside the
+sigmoid.  At full config sizes the oracle checks a seeded sample of rows
+(rows are independent: a group never straddles a row).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import codec
+from oracle.flashffn_ref import bf16_bits, to_f32
+from tests.inputs import KINDS, make_pair
+
+pytestmark = pytest.mark.gpu
+
+REL = 1e-2
+
+
+def _lib():
+    import compact_amd
+    return compact_amd
+
+
+def close(got: torch.Tensor, ref_f32: np.ndarray, rel=REL):
+    g = to_f32(got).astype(np.float64)
+    r = np.asarray(ref_f32, np.float64)
+    finite = np.isfinite(r)
+    assert np.array_equal(np.isfinite(g), finite)
+    floor = 1e-5 * (np.abs(r[finite]).max() if finite.any() else 0.0)
+    err = np.abs(g - r)[finite]
+    tol = (rel * np.abs(r) + floor)[finite]
+    bad = err > tol
+    assert not bad.any(), f"{bad.sum()} / {bad.size} beyond tol; worst {err.max():.3e}"
+
+
+def payload_equal(got: torch.Tensor, ref: np.ndarray):
+    assert np.array_equal(got.cpu().numpy().view(np.uint8), ref.view(np.uint8))
+
+
+def scales_equal(got: torch.Tensor, ref: np.ndarray):
+    assert np.array_equal(got.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+
+
+# --------------------------------------------------------------------------
+# G1: K1 vs the codec, bitwise
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("bits,group", [(4, 64), (8, 64), (8, 128), (4, 32), (4, 8), (8, 512),
+                                        (4, 4), (8, 1024)])
+def test_k1_bit_exact_vs_oracle(device, kind, bits, group):
+    cpt = _lib()
+    n, d = 96, 2048
+    a, b = make_pair(kind, n, d, group=min(group, 64), seed=41)
+    hm, qg, sg, qu, su = cpt.silu_mul_quant(a.to(device), b.to(device), bits, group)
+    g, u = to_f32(a), to_f32(b)
+    rhm, rqg, rsg, rqu, rsu = codec.silu_mul_quant(g, u, bits, group)
+    payload_equal(qg, rqg)
+    payload_equal(qu, rqu)
+    scales_equal(sg, rsg)
+    scales_equal(su, rsu)
+    close(hm, codec.round_bf16(rhm))
+
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("bits,group", [(4, 64), (8, 128), (8, 48), (4, 2)])
+def test_quantize_bit_exact_vs_oracle(device, kind, dtype, bits, group):
+    cpt = _lib()
+    n, d = 64, 1536
+    a, _ = make_pair(kind, n, d, group=16, seed=5, dtype=dtype)
+    q, s = cpt.v3_quantize_group_absmax(a.to(device), bits, group)
+    rq, rs = codec.quantize_group_absmax(to_f32(a), bits, group)
+    payload_equal(q, rq)
+    scales_equal(s, rs)
+    for out_dt in (torch.bfloat16, torch.float32, torch.float16):
+        deq = cpt.v3_dequantize_group_absmax(q, s, bits, group, dtype=out_dt)
+        ref = codec.dequantize_group_absmax_f32(rq, rs, bits, group)
+        if out_dt == torch.bfloat16:
+            rb = codec.f32_to_bf16_bits(ref)
+            gb = bf16_bits(deq)
+            nan = (rb & 0x7FFF) > 0x7F80
+            assert np.array_equal(nan, (gb & 0x7FFF) > 0x7F80)
+            assert np.array_equal(gb[~nan], rb[~nan])
+        else:
+            want = ref.astype(np.float16) if out_dt == torch.float16 else ref
+            got = deq.cpu().numpy()
+            assert np.array_equal(np.isnan(got), np.isnan(want))
+            m = ~np.isnan(want)
+            assert np.array_equal(got[m].view(np.uint8), want[m].view(np.uint8))
+
+
+def test_quantize_misaligned_view_uses_generic_path(device):
+    cpt = _lib()
+    base, _ = make_pair("random", 33, 256, seed=3)
+    flat = base.to(device).flatten()
+    view = flat[1:1 + 32 * 256].view(32, 256)       # 2-byte offset: not 16-byte aligned
+    q, s = cpt.v3_quantize_group_absmax(view, 4, 64)
+    rq, rs = codec.quantize_group_absmax(to_f32(view), 4, 64)
+    payload_equal(q, rq)
+    scales_equal(s, rs)
+
+
+# --------------------------------------------------------------------------
+# G2: K2 vs dequantise + swiglu_backward (+ silu_mul)
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("kind", KINDS)
+@pytest.mark.parametrize("bits,group", [(4, 64), (8, 128), (4, 4)])
+def test_k2_vs_oracle_and_unfused(device, kind, bits, group):
+    cpt = _lib()
+    n, d = 96, 2048
+    a, b = make_pair(kind, n, d, group=min(group, 64), seed=43)
+    gm = torch.randn(n, d, generator=torch.Generator().manual_seed(44)).to(torch.bfloat16)
+    _, qg, sg, qu, su = cpt.silu_mul_quant(a.to(device), b.to(device), bits, group)
+    gmd = gm.to(device)
+    dg, du, hm = cpt.dequant_swiglu_backward(gmd, qg, sg, qu, su, bits, group, want_h_mid=True)
+    dg2, du2, hm2 = cpt.dequant_swiglu_backward(gmd, qg, sg, qu, su, bits, group,
+                                                want_h_mid=False)
+    assert hm2 is None
+    assert torch.equal(dg.view(torch.int16), dg2.view(torch.int16))
+    assert torch.equal(du.view(torch.int16), du2.view(torch.int16))
+    # unfused device path: bitwise equal (same sigmoid, same op order)
+    hg = cpt.v3_dequantize_group_absmax(qg, sg, bits, group)
+    hu = cpt.v3_dequantize_group_absmax(qu, su, bits, group)
+    ug, uu = cpt.swiglu_backward(gmd, hg, hu)
+    uh = cpt.silu_mul(hg, hu)
+    for x, y in ((dg, ug), (du, uu), (hm, uh)):
+        assert torch.equal(x.view(torch.int16), y.view(torch.int16))
+    # oracle, tolerance
+    rdg, rdu, rhm = codec.dequant_swiglu_backward(
+        to_f32(gm), qg.cpu().numpy(), sg.cpu().numpy(), qu.cpu().numpy(), su.cpu().numpy(),
+        bits, group, want_h_mid=True)
+    close(dg, codec.round_bf16(rdg))
+    close(du, codec.round_bf16(rdu))
+    close(hm, codec.round_bf16(rhm))
+
+
+# --------------------------------------------------------------------------
+# G4: shape sweep, ragged groups
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n", [1, 7, 512, 2048, 8192])
+@pytest.mark.parametrize("d", [5632, 11008, 14336])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_shape_sweep(device, n, d, bits):
+    cpt = _lib()
+    group = 64
+    gen = torch.Generator(device=device).manual_seed(n * 7 + d + bits)
+    a = (torch.randn(n, d, device=device, generator=gen) * 3).to(torch.bfloat16)
+    b = (torch.randn(n, d, device=device, generator=gen) * 2).to(torch.bfloat16)
+    hm, qg, sg, qu, su = cpt.silu_mul_quant(a, b, bits, group)
+    q2, s2 = cpt.v3_quantize_group_absmax(a, bits, group)
+    assert torch.equal(qg.view(torch.uint8), q2.view(torch.uint8))
+    assert torch.equal(sg.view(torch.int16), s2.view(torch.int16))
+    assert torch.equal(hm.view(torch.int16), cpt.silu_mul(a, b).view(torch.int16))
+    rows = torch.randperm(n, generator=torch.Generator().manual_seed(1))[:16]
+    ra, rb = to_f32(a.cpu()[rows]), to_f32(b.cpu()[rows])
+    rq, rs = codec.quantize_group_absmax(rb, bits, group)
+    payload_equal(qu.cpu()[rows], rq)
+    scales_equal(su.cpu()[rows], rs)
+    close(hm.cpu()[rows], codec.round_bf16(codec.silu_mul(ra, rb)))
+
+
+def test_ragged_group_raises(device):
+    cpt = _lib()
+    a = torch.zeros(4, 5664, dtype=torch.bfloat16, device=device)
+    with pytest.raises(AssertionError):
+        cpt.silu_mul_quant(a, a, 4, 64)
+    with pytest.raises(AssertionError):
+        cpt.v3_quantize_group_absmax(a, 4, 64)
+    q = torch.zeros(4, 5664 // 2, dtype=torch.uint8, device=device)
+    s = torch.zeros(4, 5664 // 64, dtype=torch.float16, device=device)
+    with pytest.raises(AssertionError):
+        cpt.dequant_swiglu_backward(a, q, s, q, s, 4, 64)
+    with pytest.raises(AssertionError):
+        cpt.silu_mul_quant(torch.zeros(4, 96, dtype=torch.bfloat16, device=device),
+                           torch.zeros(4, 96, dtype=torch.bfloat16, device=device), 4, 48)
+    with pytest.raises(AssertionError):
+        cpt.silu_mul_quant(a.float(), a.float(), 4, 64)
+
+
+def test_empty_inputs(device):
+    cpt = _lib()
+    a = torch.zeros(0, 1024, dtype=torch.bfloat16, device=device)
+    hm, qg, sg, qu, su = cpt.silu_mul_quant(a, a, 4, 64)
+    assert hm.shape == (0, 1024) and qg.shape == (0, 512) and sg.shape == (0, 16)
+    dg, du, h = cpt.dequant_swiglu_backward(a, qg, sg, qu, su, 4, 64, want_h_mid=True)
+    assert dg.shape == (0, 1024) and h.shape == (0, 1024)
+
+
+# --------------------------------------------------------------------------
+# plain GLU kernels, all dtypes, ragged tails, misaligned views, in place
+# --------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("numel", [1, 7, 8, 1000, 4099, 65536])
+def test_glu_kernels_vs_oracle(device, dtype, numel):
+    cpt = _lib()
+    gen = torch.Generator().manual_seed(numel)
+    g = (torch.randn(numel, generator=gen) * 4).to(dtype)
+    u = (torch.randn(numel, generator=gen) * 3).to(dtype)
+    dh = torch.randn(numel, generator=gen).to(dtype)
+    gd, ud, dhd = g.to(device), u.to(device), dh.to(device)
+    rel = 1e-5 if dtype == torch.float32 else REL
+    rnd = {torch.bfloat16: codec.round_bf16, torch.float32: lambda v: v,
+           torch.float16: lambda v: v.astype(np.float16).astype(np.float32)}[dtype]
+    close(cpt.silu_mul(gd, ud), rnd(codec.silu_mul(to_f32(g), to_f32(u))), rel)
+    dg, du = cpt.swiglu_backward(dhd, gd, ud)
+    rdg, rdu = codec.swiglu_backward(to_f32(dh), to_f32(g), to_f32(u))
+    close(dg, rnd(rdg), rel)
+    close(du, rnd(rdu), rel)
+    dg2, du2, hm2 = cpt.swiglu_backward_glu(dhd, gd, ud, True)
+    assert torch.equal(dg2, dg) and torch.equal(du2, du)
+    assert torch.equal(hm2, cpt.silu_mul(gd, ud))
+    # in place: outputs over inputs, same values
+    g3, u3, dh3 = gd.clone(), ud.clone(), dhd.clone()
+    a, b, c = cpt.swiglu_backward_glu(dh3, g3, u3, True, inplace=True)
+    assert a.data_ptr() == g3.data_ptr() and c.data_ptr() == dh3.data_ptr()
+    assert torch.equal(a, dg) and torch.equal(b, du) and torch.equal(c, hm2)
+
+
+def test_glu_misaligned_view(device):
+    cpt = _lib()
+    g = torch.randn(1001, device=device).to(torch.bfloat16)
+    u = torch.randn(1001, device=device).to(torch.bfloat16)
+    out = cpt.silu_mul(g[1:], u[1:])
+    assert torch.equal(out, cpt.silu_mul(g[1:].clone(), u[1:].clone()))

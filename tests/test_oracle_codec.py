@@ -89,8 +89,10 @@ def test_ragged_and_bad_args_assert():
     t = np.zeros((2, 96), np.float32)
     with pytest.raises(AssertionError):
         codec.quantize_group_absmax(t, 4, 64)           # ragged last group
-    with pytest.raises(AssertionError):
-        codec.quantize_group_absmax(t, 4, 48)           # not a power of two
+    with pytest.raises(AssertionError):               # fused path: power of two only
+        codec.silu_mul_quant(t, t, 4, 48)
+    q, s = codec.quantize_group_absmax(t, 4, 48)       # eager codec accepts 48
+    assert q.shape == (2, 48) and s.shape == (2, 2)
     with pytest.raises(AssertionError):
         codec.quantize_group_absmax(np.zeros((2, 64), np.float32), 3, 64)
 
@@ -134,9 +136,10 @@ def test_brute_force_ties_and_boundaries():
 # --------------------------------------------------------------------------
 
 @pytest.mark.parametrize("kind", KINDS)
-@pytest.mark.parametrize("bits,group", [(4, 64), (8, 128), (8, 64), (4, 32)])
+@pytest.mark.parametrize("bits,group", [(4, 64), (8, 128), (8, 64), (4, 32), (8, 48)])
 def test_c_restatement_bit_exact(kind, bits, group):
-    a, b = make_pair(kind, 64, 1024, group=group, seed=11)
+    d = 1024 if 1024 % group == 0 else 960
+    a, b = make_pair(kind, 64, d, group=group, seed=11)
     for t in (a, b):
         vals = to_f32(t)
         q_np, s_np = codec.quantize_group_absmax(vals, bits, group)
