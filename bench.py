@@ -44,6 +44,25 @@ def codec_bytes(n, d, bits, group, want_h_mid=True):
     return k1, k2
 
 
+def algorithmic_work(n, h, d):
+    """Per-launch algorithmic work of every timed kernel: (amount, bound),
+    FLOPs for the MFMA-bound GEMMs (2*M*N*K per product), bytes for the
+    HBM-bound standalone codec kernels."""
+    k1_bytes, k2_bytes = codec_bytes(n, d, BITS, GROUP)
+    gemm = 2 * n * h * d
+    return {
+        "ffn_gate_up": (2 * gemm, "mfma"),          # x @ [Wg; Wu]^T (+ GLU + codec)
+        "gemm_fwd_down": (gemm, "mfma"),            # h_mid @ Wd^T
+        "ffn_down_dgrad": (gemm, "mfma"),           # gy @ Wd (+ dequant + SwiGLU bwd)
+        "gemm_wgrad_down": (gemm, "mfma"),          # gy^T @ h_mid^
+        "gemm_dgrad_x": (2 * gemm, "mfma"),         # dg @ Wg + du @ Wu
+        "gemm_wgrad_gate": (gemm, "mfma"),          # dg^T @ x
+        "gemm_wgrad_up": (gemm, "mfma"),            # du^T @ x
+        "silu_mul_quant": (k1_bytes, "hbm"),
+        "dequant_swiglu_backward": (k2_bytes, "hbm"),
+    }
+
+
 def gemm_flops_fwd_bwd(n, h, d, full_ft=True):
     """3 GEMMs forward, 6 backward (full-FT) of 2*N*H*D FLOPs each."""
     return (18 if full_ft else 12) * n * h * d
@@ -149,29 +168,39 @@ def main():
         torch.cuda.synchronize()
     total_ms = e0.elapsed_time(e1)
     ms = total_ms / args.steps
-    assert cpt._V3_COUNTERS["triton_quant_fwd"] == args.steps, "fused K1 did not run"
-    assert cpt._V3_COUNTERS["triton_dequant_bwd"] == args.steps, "fused K2 did not run"
+    assert cpt._V3_COUNTERS["triton_quant_fwd"] == args.steps, "fused codec (K1) did not run"
+    assert cpt._V3_COUNTERS["triton_dequant_bwd"] == args.steps, "fused dequant (K2) did not run"
     kern = kt.avg_ms()
 
     sb = saved_bytes(fwd, {p.data_ptr() for p in params} | {x.data_ptr()}) + x.nbytes
 
-    k1_bytes, k2_bytes = codec_bytes(n, d, BITS, GROUP)
-    algo = {"silu_mul_quant": (k1_bytes, "hbm"), "dequant_swiglu_backward": (k2_bytes, "hbm")}
+    algo = algorithmic_work(n, h, d)
     kernels = {}
     for name, st in kern.items():
         entry = dict(st)
         if name in algo:
-            b, bound = algo[name]
-            entry["gbs"] = b / (st["avg_ms"] * 1e-3) / 1e9
-            entry["frac_hbm"] = entry["gbs"] / HBM_PEAK_GBS
+            amount, bound = algo[name]
+            rate = amount / (st["avg_ms"] * 1e-3)
+            if bound == "hbm":
+                entry["gbs"] = rate / 1e9
+                entry["frac_hbm"] = entry["gbs"] / HBM_PEAK_GBS
+            else:
+                entry["tflops"] = rate / 1e12
+                entry["frac_mfma_bf16"] = entry["tflops"] / MFMA_BF16_PEAK_TFLOPS
         kernels[name] = entry
-    # dominant HIP kernel of this build by total time
+    # dominant HIP kernel of this build by total time in the timed steps
     dom = max(kern, key=lambda k: kern[k]["total_ms"])
-    b, bound = algo[dom]
-    ach = b / (kern[dom]["avg_ms"] * 1e-3) / 1e9
-    roofline = {"kernel": dom, "bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": ach / HBM_PEAK_GBS, "traffic": None,
-                "algorithmic_bytes": b}
+    amount, bound = algo[dom]
+    rate = amount / (kern[dom]["avg_ms"] * 1e-3)
+    if bound == "hbm":
+        roofline = {"kernel": dom, "bound": "hbm", "achieved": rate / 1e9, "peak": HBM_PEAK_GBS,
+                    "unit": "GB/s", "frac": rate / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                    "algorithmic_bytes": amount}
+    else:
+        roofline = {"kernel": dom, "bound": "mfma", "achieved": rate / 1e12,
+                    "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                    "frac": rate / 1e12 / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
+                    "algorithmic_flops": amount}
     flops = gemm_flops_fwd_bwd(n, h, d)
     out = {
         "metric": "FFN fwd+bwd tokens/sec + saved-activation MB, Llama-7B FFN shape, 1 MI355X",

@@ -28,7 +28,12 @@ SIGNATURES = {
     "cpt_swiglu_backward_glu": [_P, _P, _P, _P, _P, _P, _L, _I, _P],
     "cpt_silu_mul_quant": [_P, _P, _L, _L, _I, _L, _P, _P, _P, _P, _P, _P],
     "cpt_dequant_swiglu_backward": [_P, _P, _P, _P, _P, _L, _L, _I, _L, _P, _P, _P, _P],
+    "cpt_gemm_bf16": [_P, _L, _I, _P, _L, _I, _P, _L, _P, _L, _L, _P, _L, _L, _L, _L, _P],
+    "cpt_ffn_gate_up": [_P, _P, _P, _L, _L, _L, _I, _L, _P, _P, _P, _P, _P, _P, _P, _P],
+    "cpt_ffn_down_dgrad": [_P, _P, _L, _L, _L, _I, _L, _P, _P, _P, _P, _P, _P, _P, _P],
 }
+
+CACHE_NONE, CACHE_BF16, CACHE_INT4, CACHE_INT8 = 0, 1, 4, 8
 
 _lib = None
 

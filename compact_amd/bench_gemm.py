@@ -1,0 +1,79 @@
+"""Per-GEMM comparison on the C2 FFN shapes: this build's MFMA engine (and
+its fused FlashFFN kernels) against the library GEMM torch calls (hipBLASLt)
+with the standalone codec kernels.
+
+    python -m compact_amd.bench_gemm [--iters 20] [--json out.json]
+
+Prints one line per GEMM of a C2 fwd+bwd step (8192 tokens, d_model 4096,
+d_ff 11008, bf16), timed with HIP events on the current stream.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+
+import torch
+
+from . import gemm as G
+from . import kernels as K
+
+
+def _time(fn, iters):
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(iters):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--iters", type=int, default=20)
+    ap.add_argument("--json", default=None)
+    args = ap.parse_args()
+    n, h, d, gs = 8192, 4096, 11008, 128
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randn(n, h, device=dev, generator=g).bfloat16()
+    gy = torch.randn(n, h, device=dev, generator=g).bfloat16()
+    wg = (torch.randn(d, h, device=dev, generator=g) * .02).bfloat16()
+    wu = (torch.randn(d, h, device=dev, generator=g) * .02).bfloat16()
+    wd = (torch.randn(h, d, device=dev, generator=g) * .02).bfloat16()
+    hm = torch.randn(n, d, device=dev, generator=g).bfloat16()
+    _, qg, sg, qu, su = K.silu_mul_quant(hm, hm, 8, gs)
+    fl = 2 * n * h * d
+
+    def lib_gate_up():
+        a, b = x @ wg.t(), x @ wu.t()
+        return K.silu_mul_quant(a, b, 8, gs)
+
+    def lib_dgrad():
+        return K.dequant_swiglu_backward(gy @ wd, qg, sg, qu, su, 8, gs, want_h_mid=True)
+
+    cases = [
+        ("fwd gate/up + GLU + int8 codec", lambda: G.ffn_gate_up(x, wg, wu, 8, gs), lib_gate_up, 2 * fl),
+        ("fwd down  h_mid @ Wd^T", lambda: G.linear(hm, wd), lambda: hm @ wd.t(), fl),
+        ("bwd gy @ Wd + dequant + SwiGLU bwd", lambda: G.ffn_down_dgrad(gy, wd, 8, gs, qg, sg, qu, su, True), lib_dgrad, fl),
+        ("bwd dWd = gy^T @ h_mid", lambda: G.mm(gy.t(), hm), lambda: gy.t() @ hm, fl),
+        ("bwd dx = dg @ Wg + du @ Wu", lambda: G.mm2(hm, wg, hm, wu), lambda: hm @ wg + hm @ wu, 2 * fl),
+        ("bwd dWg = dg^T @ x", lambda: G.mm(hm.t(), x), lambda: hm.t() @ x, fl),
+    ]
+    out = {}
+    for name, mine, lib, flops in cases:
+        a, b = _time(mine, args.iters), _time(lib, args.iters)
+        out[name] = {"engine_ms": a, "library_ms": b, "engine_tflops": flops / a / 1e9,
+                     "library_tflops": flops / b / 1e9}
+        print(f"{name:38s} engine {a:7.3f} ms {flops / a / 1e9:7.1f} TF/s | "
+              f"library {b:7.3f} ms {flops / b / 1e9:7.1f} TF/s", flush=True)
+    if args.json:
+        json.dump(out, open(args.json, "w"), indent=1)
+
+
+if __name__ == "__main__":
+    main()

@@ -31,7 +31,7 @@ COMMON = [
     "-Wall", "-Wno-unused-function",
     f"-I{CSRC}", f"-I{os.path.join(ROOT, 'include')}",
 ]
-PER_FILE = {"codec.hip": ["-ffp-contract=off"]}
+PER_FILE = {"codec.hip": ["-ffp-contract=off"], "gemm.hip": ["-ffp-contract=off"]}
 
 
 def hipcc() -> str:

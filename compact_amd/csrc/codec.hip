@@ -19,56 +19,29 @@
 
 #include "common.h"
 #include "compact_amd.h"
+#include "glu_math.h"
 
 namespace cpt {
 
 constexpr int kBlock = 256;
 
-__device__ __forceinline__ float sigmoid_f32(float x) {
-  // tl.sigmoid: 1 / (1 + exp(-x)), float32
-  return 1.0f / (1.0f + expf(-x));
-}
-
-template <int BITS> struct QMax;
-template <> struct QMax<4> { static constexpr float v = 7.0f; };
-template <> struct QMax<8> { static constexpr float v = 127.0f; };
-
-// fp16 scale of a group from its absmax (bits of |x|), exactly as
-// src/flashffn.py:1076-1080: scale = fp16(absmax / qmax); safe = scale>0 ? scale : 1.
-template <int BITS>
-__device__ __forceinline__ uint16_t scale_bits(uint32_t absmax_bits) {
-  const float s32 = __uint_as_float(absmax_bits) / QMax<BITS>::v;
-  return f32_to_f16_bits(s32);
-}
-__device__ __forceinline__ float safe_scale(uint16_t sh) {
-  const float s = f16_bits_to_f32(sh);
-  return s > 0.0f ? s : 1.0f;
-}
-
-// code = clamp(rint(v / safe), -qmax, qmax)   (src/flashffn.py:1080)
-template <int BITS>
-__device__ __forceinline__ int quant_code(float v, float safe) {
-  float q = __builtin_rintf(v / safe);
-  q = fminf(fmaxf(q, -QMax<BITS>::v), QMax<BITS>::v);
-  return (int)q;
-}
-
 // Codes of 8 consecutive elements packed as stored: int8 -> 8 bytes,
 // int4 -> 4 bytes of (code+8) nibbles, even column low (src/flashffn.py:1081-1085).
 template <int BITS>
 __device__ __forceinline__ void store_codes8(uint8_t* q, int64_t c, const float v[8], float safe) {
+  const float rs = __builtin_amdgcn_rcpf(safe);
   if (BITS == 8) {
     uint32_t w0 = 0, w1 = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      w0 |= ((uint32_t)quant_code<8>(v[j], safe) & 0xFFu) << (8 * j);
-      w1 |= ((uint32_t)quant_code<8>(v[4 + j], safe) & 0xFFu) << (8 * j);
+      w0 |= ((uint32_t)quant_code<8>(v[j], safe, rs) & 0xFFu) << (8 * j);
+      w1 |= ((uint32_t)quant_code<8>(v[4 + j], safe, rs) & 0xFFu) << (8 * j);
     }
     reinterpret_cast<uint2*>(q)[c] = make_uint2(w0, w1);
   } else {
     uint32_t w = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) w |= (uint32_t)(quant_code<4>(v[j], safe) + 8) << (4 * j);
+    for (int j = 0; j < 8; ++j) w |= (uint32_t)(quant_code<4>(v[j], safe, rs) + 8) << (4 * j);
     reinterpret_cast<uint32_t*>(q)[c] = w;
   }
 }
@@ -142,10 +115,7 @@ __global__ __launch_bounds__(kBlock) void silu_mul_quant_kernel(
     Vec8<kBF16>::ld(u, c, uv);
     float h[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float act = gv[j] * sigmoid_f32(gv[j]);  // src/flashffn.py:1212-1213
-      h[j] = act * uv[j];
-    }
+    for (int j = 0; j < 8; ++j) h[j] = silu_mul1(gv[j], uv[j]);  // src/flashffn.py:1212-1215
     Vec8<kBF16>::st(hm, c, h);
   }
   quant_chunk<BITS, LPG>(gv, valid, c, qg, sg);
@@ -170,9 +140,7 @@ __global__ __launch_bounds__(kBlock) void quant_generic_kernel(
   if (GLU) {
     typename E::T* ph = reinterpret_cast<typename E::T*>(hm);
     for (int64_t e = e0; e < e0 + span; ++e) {
-      const float gv = E::ld(pg + e), uv = E::ld(pu + e);
-      const float act = gv * sigmoid_f32(gv);
-      E::st(ph + e, act * uv);
+      E::st(ph + e, silu_mul1(E::ld(pg + e), E::ld(pu + e)));
     }
   }
   for (int pass = 0; pass < (GLU ? 2 : 1); ++pass) {
@@ -185,8 +153,9 @@ __global__ __launch_bounds__(kBlock) void quant_generic_kernel(
       const uint16_t sh = scale_bits<BITS>(am);
       s[g0 / gs] = sh;
       const float safe = safe_scale(sh);
+      const float rs = __builtin_amdgcn_rcpf(safe);
       for (int64_t e = g0; e < g0 + gs; ++e) {
-        const int code = quant_code<BITS>(E::ld(p + e), safe);
+        const int code = quant_code<BITS>(E::ld(p + e), safe, rs);
         if (BITS == 8) {
           q[e] = (uint8_t)(code & 0xFF);
         } else if ((e & 1) == 0) {
@@ -236,17 +205,6 @@ __global__ __launch_bounds__(kBlock) void dequantize_generic_kernel(
 // ---------------------------------------------------------------------------
 // K2: dequantise through bf16, SwiGLU backward, optional h_mid^
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void swiglu_bwd1(float dh, float g, float u, float& dg, float& du,
-                                            float& hact) {
-  // src/flashffn.py:109-123, same op order
-  const float sig = sigmoid_f32(g);
-  hact = g * sig;
-  const float grad_h_act = dh * u;
-  du = dh * hact;
-  const float dsilu = sig * (1.0f + g * (1.0f - sig));
-  dg = grad_h_act * dsilu;
-}
-
 template <int BITS, bool WANT_HM>
 __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_kernel(
     const uint16_t* __restrict__ gmid, const uint8_t* __restrict__ qg,
@@ -265,8 +223,8 @@ __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_kernel(
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     // bf16 round trip of the dequantised cache (src/flashffn.py:1251-1253)
-    const float hg = bf16_to_f32(f32_to_bf16_bits(cg[j] * scg));
-    const float hu = bf16_to_f32(f32_to_bf16_bits(cu[j] * scu));
+    const float hg = round_bf16(cg[j] * scg);
+    const float hu = round_bf16(cu[j] * scu);
     float hact;
     swiglu_bwd1(dh[j], hg, hu, og[j], ou[j], hact);
     oh[j] = hact * hu;  // src/flashffn.py:1298-1300
@@ -294,8 +252,8 @@ __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_generic_kernel(
     code_g = (float)((e & 1) ? (bg >> 4) : (bg & 0xFu)) - 8.0f;
     code_u = (float)((e & 1) ? (bu >> 4) : (bu & 0xFu)) - 8.0f;
   }
-  const float hg = bf16_to_f32(f32_to_bf16_bits(code_g * f16_bits_to_f32(sg[e / gs])));
-  const float hu = bf16_to_f32(f32_to_bf16_bits(code_u * f16_bits_to_f32(su[e / gs])));
+  const float hg = round_bf16(code_g * f16_bits_to_f32(sg[e / gs]));
+  const float hu = round_bf16(code_u * f16_bits_to_f32(su[e / gs]));
   float og, ou, hact;
   swiglu_bwd1(bf16_to_f32(gmid[e]), hg, hu, og, ou, hact);
   dg[e] = (uint16_t)f32_to_bf16_bits(og);
@@ -320,7 +278,7 @@ __global__ __launch_bounds__(kBlock) void silu_mul_kernel(
     Vec8<DT>::ld(g, c, gv);
     Vec8<DT>::ld(u, c, uv);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) h[j] = (gv[j] * sigmoid_f32(gv[j])) * uv[j];
+    for (int j = 0; j < 8; ++j) h[j] = silu_mul1(gv[j], uv[j]);
     Vec8<DT>::st(out, c, h);
     return;
   }
@@ -329,7 +287,7 @@ __global__ __launch_bounds__(kBlock) void silu_mul_kernel(
   typename E::T* po = reinterpret_cast<typename E::T*>(out);
   for (int64_t e = e0; e < n && e < e0 + 8; ++e) {
     const float gv = E::ld(pg + e);
-    E::st(po + e, (gv * sigmoid_f32(gv)) * E::ld(pu + e));
+    E::st(po + e, silu_mul1(gv, E::ld(pu + e)));
   }
 }
 

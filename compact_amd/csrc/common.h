@@ -9,8 +9,8 @@
 //   * no FMA contraction in the codec/GLU file (-ffp-contract=off);
 //   * rint is v_rndne_f32 (round half to even), fp16 conversion is
 //     v_cvt_f16_f32 in the default round-to-nearest-even mode;
-//   * bf16 rounding is done in integer arithmetic below (RNE, NaN -> 0x7FC0,
-//     the convention of c10::BFloat16).
+//   * bf16 rounding is v_cvt_pk_bf16_f32 (round to nearest even, like
+//     c10::BFloat16 for every non-NaN value).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -38,12 +38,15 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t b16) {
   return __uint_as_float(b16 << 16);
 }
 
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return u >> 16;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// bf16 round-to-nearest-even of two floats, packed (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  bf16x2_t v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
 }
+
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) { return pack_bf16x2(f, 0.0f) & 0xFFFFu; }
 
 __device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
@@ -106,15 +109,11 @@ template <int DT> struct Vec8Half {  // 16-bit formats
     uint32_t ws[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      uint32_t lo, hi;
       if (DT == kBF16) {
-        lo = f32_to_bf16_bits(v[2 * j]);
-        hi = f32_to_bf16_bits(v[2 * j + 1]);
+        ws[j] = pack_bf16x2(v[2 * j], v[2 * j + 1]);
       } else {
-        lo = f32_to_f16_bits(v[2 * j]);
-        hi = f32_to_f16_bits(v[2 * j + 1]);
+        ws[j] = (uint32_t)f32_to_f16_bits(v[2 * j]) | ((uint32_t)f32_to_f16_bits(v[2 * j + 1]) << 16);
       }
-      ws[j] = lo | (hi << 16);
     }
     reinterpret_cast<uint4*>(base)[i8] = make_uint4(ws[0], ws[1], ws[2], ws[3]);
   }

@@ -1,0 +1,931 @@
+// MFMA bf16 GEMM engine for gfx950 with the FlashFFN epilogues fused in.
+//
+// C[M, N] = sum over pairs p of  A_p[M, K_p] . B_p[K_p, N]   (fp32 accumulation)
+//
+// Operands are bf16.  Each operand is either K-major (K contiguous: A stored
+// [M][lda], B stored [N][ldb] -- the nn.Linear weight layout) or MN-major
+// (A stored [K][lda], B stored [K][ldb]).  Tiles are staged in LDS K-major
+// so every MFMA fragment is one 128-bit LDS read; MN-major operands are
+// transposed 8x8 in registers on their way into LDS.
+//
+// Block tile 256 (m) x 256 (n) x 64 (k), 256 threads = 4 wavefronts in a
+// 2 x 2 arrangement, each owning 128 x 128 outputs as 4 x 4 tiles of
+// v_mfma_f32_32x32x16_bf16.  The MFMA "A" slot is fed from the n-side operand
+// and the "B" slot from the m-side operand, so a lane ends up holding, for one
+// output row m, runs of 4 consecutive output columns n: the layout the fused
+// epilogues want (a quantisation group is a run of columns of one row).
+//   acc[i][j][r] -> n = nw + 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4
+//                   m = mw + 32 j + lane % 32
+// LDS: two stages x two operands x 256 rows x 64 bf16 in padded rows
+// (146 KiB; see lds_row), conflict-free for the fragment reads (32
+// consecutive rows, one chunk) and for the transposed stores (rows 8 apart).
+// Grid: one block per output tile, block ids remapped so each XCD works on a
+// contiguous range of tiles, grouped 8 tile-rows deep for L2 reuse.
+
+#include <type_traits>
+
+#include "common.h"
+#include "compact_amd.h"
+#include "glu_math.h"
+
+namespace cpt {
+namespace gemm {
+
+// Compile-time loop: f(std::integral_constant<int, I>) for I in [B, E), so
+// accumulator indices in the epilogues are constants and stay in registers.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 256, BN = 256, BK = 64, NTHR = 256;
+constexpr int TILE_ELEMS = 256 * 72 + 32 * 8;  // one operand stage in LDS (padded rows)
+constexpr int LDS_BYTES = 4 * TILE_ELEMS * 2;   // 2 stages x 2 operands (146 KiB)
+constexpr int GROUP_ROWS = 8;                  // tile-rows per L2 group
+
+// Padded rows: row r starts at r * 72 + (r / 8) * 8 elements (144 bytes per
+// row plus 16 bytes per 8 rows).  8 consecutive rows fall on distinct 16-byte
+// bank groups (36-dword stride), and so do 8 rows spaced 8 apart (292-dword
+// stride), which keeps fragment reads and transposed stores conflict-free
+// while the address stays affine in the chunk.
+constexpr int ROW_ELEMS = 72;
+__device__ __forceinline__ int lds_row(int row) { return row * ROW_ELEMS + ((row >> 3) << 3); }
+__device__ __forceinline__ int lds_off(int row, int chunk) { return lds_row(row) + (chunk << 3); }
+
+// ---------------------------------------------------------------------------
+// global -> registers -> LDS
+// ---------------------------------------------------------------------------
+
+// K-major tile: rows r0..r0+255, k0..k0+63 of p[row * ld + k]; thread owns 8
+// 16-byte chunks, 8 consecutive threads cover one 128-byte row slice.
+__device__ __forceinline__ void gload_kmajor(const uint16_t* p, int64_t ld, int64_t rows, int64_t K,
+                                             int64_t r0, int64_t k0, int tid, uint4 (&reg)[8]) {
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int q = tid + NTHR * it;
+    const int row = q >> 3, c = q & 7;
+    const int64_t gr = r0 + row, gk = k0 + c * 8;
+    if (gr < rows && gk < K)
+      reg[it] = *reinterpret_cast<const uint4*>(p + gr * ld + gk);
+    else
+      reg[it] = make_uint4(0, 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ void sstore_kmajor(uint16_t* lds, int tid, const uint4 (&reg)[8]) {
+#pragma unroll
+  for (int it = 0; it < 8; ++it) {
+    const int q = tid + NTHR * it;
+    *reinterpret_cast<uint4*>(lds + lds_off(q >> 3, q & 7)) = reg[it];
+  }
+}
+
+// MN-major tile: thread owns an 8 (k) x 8 (mn) block: k = k0 + 8 (tid / 32) + r,
+// mn = r0 + 8 (tid % 32) + 0..7 of p[k * ld + mn].  Requires rows % 8 == 0.
+__device__ __forceinline__ void gload_mnmajor(const uint16_t* p, int64_t ld, int64_t rows, int64_t K,
+                                              int64_t r0, int64_t k0, int tid, uint4 (&reg)[8]) {
+  const int mb = tid & 31, kb = tid >> 5;
+  const int64_t gmn = r0 + mb * 8;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) {
+    const int64_t gk = k0 + kb * 8 + r;
+    if (gmn < rows && gk < K)
+      reg[r] = *reinterpret_cast<const uint4*>(p + gk * ld + gmn);
+    else
+      reg[r] = make_uint4(0, 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ uint32_t dword_of(const uint4& v, int i) {
+  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+
+// 8x8 transpose of 16-bit elements: LDS row (mn) i gets element i of reg[0..7] (k).
+__device__ __forceinline__ void sstore_mnmajor(uint16_t* lds, int tid, const uint4 (&reg)[8]) {
+  const int mb = tid & 31, kb = tid >> 5;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    uint32_t o[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const uint32_t lo = dword_of(reg[2 * w], i >> 1), hi = dword_of(reg[2 * w + 1], i >> 1);
+      o[w] = (i & 1) ? ((lo >> 16) | (hi & 0xFFFF0000u)) : ((lo & 0xFFFFu) | (hi << 16));
+    }
+    *reinterpret_cast<uint4*>(lds + lds_off(mb * 8 + i, kb)) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// arguments
+// ---------------------------------------------------------------------------
+struct Operand {
+  const uint16_t* p;
+  int64_t ld;
+};
+
+// C = sum_p A_p . B_p ; A_p logical [M, K_p] (m-side), B_p logical [K_p, N] (n-side)
+struct KArgs {
+  Operand a[2], b[2];
+  int64_t K[2];
+  int npairs;
+  const uint16_t* b_up;    // dual gate/up GEMM: up weight (layout of b[0])
+  int64_t M, N;            // output extent; dual: N = 2 * D (virtual columns)
+  int tiles_m, tiles_n;
+  // plain output
+  uint16_t* C;
+  int64_t ldc;
+  // FlashFFN epilogues
+  int64_t D;               // d_ff (inter)
+  uint16_t* h_mid;         // F1 out (may be null)
+  uint16_t* h_gate;        // F1 out (bf16 cache) / B1 in (bf16 cache)
+  uint16_t* h_up;
+  uint8_t* q_gate;         // F1 out / B1 in (codes)
+  uint16_t* s_gate;
+  uint8_t* q_up;
+  uint16_t* s_up;
+  uint16_t* grad_gate;     // B1 out
+  uint16_t* grad_up;
+  uint16_t* h_mid_hat;     // B1 out (may be null)
+};
+
+enum Epi { EPI_STORE = 0, EPI_GLU = 1, EPI_DGLU = 2 };
+enum Cache { CACHE_NONE = 0, CACHE_BF16 = 1, CACHE_INT4 = 4, CACHE_INT8 = 8 };
+
+// ---------------------------------------------------------------------------
+// tile scheduling
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int nb = gridDim.x;
+  const int b = blockIdx.x;
+  // blocks are dispatched round-robin over the 8 XCDs: give each XCD a
+  // contiguous range of logical tiles so co-resident tiles share L2 panels
+  const int xcd = b & 7, idx = b >> 3;
+  const int base = nb >> 3, extra = nb & 7;
+  const int logical = xcd * base + min(xcd, extra) + idx;
+  const int per_group = GROUP_ROWS * tiles_n;
+  const int g = logical / per_group;
+  const int first = g * GROUP_ROWS;
+  const int rows = min(GROUP_ROWS, tiles_m - first);
+  const int in = logical - g * per_group;
+  tm = first + in % rows;
+  tn = in / rows;
+}
+
+// ---------------------------------------------------------------------------
+// main loop
+// ---------------------------------------------------------------------------
+struct Acc {
+  f32x16 v[4][4];
+};
+
+// ---------------------------------------------------------------------------
+// Branch-free tile loads with buffer instructions.  Every operand gets a
+// buffer resource whose num_records ends at the operand's last valid byte in
+// the strided direction (rows for K-major, k for MN-major), so rows past the
+// edge read as zero in hardware; the remaining edge (k for K-major, mn for
+// MN-major) is handled by pushing the offset past num_records (kOOB).
+// Offsets are 32-bit: each operand must span < 2 GiB (checked on the host).
+// ---------------------------------------------------------------------------
+constexpr uint32_t kOOB = 0x80000000u;
+constexpr int kRsrcWord3 = 0x00020000;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
+  const uint32_t n = bytes > 0x7FFFFFFF ? 0x7FFFFFFFu : (uint32_t)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)n, kRsrcWord3);
+}
+
+__device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return *reinterpret_cast<uint4*>(&v);
+}
+
+template <bool AK, bool BKM, bool DUAL>
+struct Loader {
+  __amdgpu_buffer_rsrc_t ra[2], rb[2], rup;
+  uint32_t oa[8], ob[8];   // per-thread byte offsets at k = 0 (kOOB if the row/mn is out)
+  int64_t K[2];
+  int nk0;
+  int64_t lda, ldb;
+  uint32_t ka_ok_shift;    // unused placeholder for alignment of the struct
+
+  __device__ __forceinline__ void init(const KArgs& A, int64_t m0, int64_t n0, int tid) {
+    lda = A.a[0].ld;
+    ldb = A.b[0].ld;
+    K[0] = A.K[0];
+    K[1] = A.npairs > 1 ? A.K[1] : 0;
+    nk0 = (int)((A.K[0] + BK - 1) / BK);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      if (p == 1 && A.npairs < 2) { ra[1] = ra[0]; rb[1] = rb[0]; continue; }
+      // m-side: K-major spans M rows; MN-major spans K rows
+      ra[p] = make_rsrc(A.a[p].p, (AK ? A.M : A.K[p]) * lda * 2);
+      rb[p] = make_rsrc(A.b[p].p, (DUAL ? A.D : (BKM ? A.N : A.K[p])) * ldb * 2);
+    }
+    rup = DUAL ? make_rsrc(A.b_up, A.D * ldb * 2) : rb[0];
+    if (AK) {
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int64_t row = m0 + (tid >> 3) + 32 * it;
+        oa[it] = (uint32_t)((row * lda + (tid & 7) * 8) * 2);
+      }
+    } else {
+      const int64_t mn = m0 + (tid & 31) * 8;
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+        oa[r] = mn < A.M ? (uint32_t)((((tid >> 5) * 8 + r) * lda + mn) * 2) : kOOB;
+    }
+    if (DUAL) {
+      const int64_t d0 = n0 >> 1;
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int blk = it >> 1;
+        const int64_t d = d0 + ((blk >> 1) << 6) + (tid >> 3) + 32 * (it & 1);
+        ob[it] = (uint32_t)((d * ldb + (tid & 7) * 8) * 2);
+      }
+    } else if (BKM) {
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int64_t row = n0 + (tid >> 3) + 32 * it;
+        ob[it] = (uint32_t)((row * ldb + (tid & 7) * 8) * 2);
+      }
+    } else {
+      const int64_t mn = n0 + (tid & 31) * 8;
+#pragma unroll
+      for (int r = 0; r < 8; ++r)
+        ob[r] = mn < A.N ? (uint32_t)((((tid >> 5) * 8 + r) * ldb + mn) * 2) : kOOB;
+    }
+  }
+
+  // global loads of k-tile kt into registers (16 x 128-bit, no branches)
+  __device__ __forceinline__ void issue(int kt, int tid, uint4 (&va)[8], uint4 (&vb)[8]) const {
+    const int p = kt >= nk0 ? 1 : 0;
+    const int64_t k0 = (int64_t)(kt - p * nk0) * BK;
+    const int64_t Kp = p ? K[1] : K[0];
+    const __amdgpu_buffer_rsrc_t rA = p ? ra[1] : ra[0];
+    const __amdgpu_buffer_rsrc_t rB = p ? rb[1] : rb[0];
+    const bool kok = k0 + (tid & 7) * 8 < Kp;   // K-major chunk inside K
+    if (AK) {
+      const uint32_t adv = (uint32_t)(k0 * 2);
+#pragma unroll
+      for (int it = 0; it < 8; ++it) va[it] = bload(rA, kok ? oa[it] + adv : kOOB);
+    } else {
+      const uint32_t adv = (uint32_t)(k0 * lda * 2);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) va[r] = bload(rA, oa[r] == kOOB ? kOOB : oa[r] + adv);
+    }
+    if (DUAL || BKM) {
+      const uint32_t adv = (uint32_t)(k0 * 2);
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const __amdgpu_buffer_rsrc_t r = (DUAL && ((it >> 1) & 1)) ? rup : rB;
+        vb[it] = bload(r, kok ? ob[it] + adv : kOOB);
+      }
+    } else {
+      const uint32_t adv = (uint32_t)(k0 * ldb * 2);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) vb[r] = bload(rB, ob[r] == kOOB ? kOOB : ob[r] + adv);
+    }
+  }
+};
+
+struct Frags {
+  bf16x8 n[4];   // n-side fragments (MFMA A slot)
+  bf16x8 m[4];   // m-side fragments (MFMA B slot)
+};
+
+__device__ __forceinline__ void read_frags(const uint16_t* stage_base, int wn, int wm, int lane,
+                                           int s, Frags& f) {
+  const uint16_t* sa = stage_base;
+  const uint16_t* sb = stage_base + TILE_ELEMS;
+  const int chunk = s * 2 + (lane >> 5);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    f.n[i] = *reinterpret_cast<const bf16x8*>(sb + lds_off(wn * 128 + i * 32 + (lane & 31), chunk));
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    f.m[j] = *reinterpret_cast<const bf16x8*>(sa + lds_off(wm * 128 + j * 32 + (lane & 31), chunk));
+}
+
+template <int I0, int I1>
+__device__ __forceinline__ void mfma_range(const Frags& f, Acc& acc) {
+#pragma unroll
+  for (int t = I0; t < I1; ++t) {
+    const int i = t >> 2, j = t & 3;
+    acc.v[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.n[i], f.m[j], acc.v[i][j], 0, 0, 0);
+  }
+}
+
+// scheduling-group masks (LLVM AMDGPU sched_group_barrier)
+constexpr int SG_MFMA = 0x008, SG_VMEM_R = 0x020, SG_DS_R = 0x100, SG_DS_W = 0x200;
+
+template <int N, int MASK, int PER = 1>
+__device__ __forceinline__ void sched_interleave() {
+  // N times: one MFMA, then PER instructions of MASK
+#pragma unroll
+  for (int t = 0; t < N; ++t) {
+    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(MASK, PER, 0);
+  }
+}
+
+template <int N>
+__device__ __forceinline__ void sched_interleave_load_read() {
+  // N times: one MFMA, one global load, one LDS read
+#pragma unroll
+  for (int t = 0; t < N; ++t) {
+    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(SG_VMEM_R, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(SG_DS_R, 1, 0);
+  }
+}
+
+// Software-pipelined main loop.  Per k-tile (4 sub-steps of k16, fragment
+// register sets f0/f1 alternating):
+//   s0: 16 MFMAs interleaved with the 16 global loads of tile kt+1 and the
+//       8 LDS reads of s1;  s1, s2: 16 MFMAs with the 8 LDS reads of s+1;
+//   s3: 8 MFMAs interleaved with the 16 LDS writes of tile kt+1 (other
+//       stage), one barrier, then 8 MFMAs with the 8 LDS reads of (kt+1, s0).
+// The other stage was last read during tile kt-1, before the barrier that
+// ended it, so one barrier per k-tile suffices.
+template <bool AK, bool BKM, bool DUAL>
+__device__ __forceinline__ void mainloop(const KArgs& A, int64_t m0, int64_t n0, uint16_t* lds,
+                                         Acc& acc) {
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wn = wave & 1, wm = wave >> 1;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc.v[i][j][r] = 0.0f;
+
+  Loader<AK, BKM, DUAL> L;
+  L.init(A, m0, n0, tid);
+  int nk = L.nk0;
+  if (A.npairs > 1) nk += (int)((A.K[1] + BK - 1) / BK);
+
+  uint4 va[8], vb[8];
+  auto store = [&](int stage) {
+    uint16_t* sa = lds + stage * 2 * TILE_ELEMS;
+    uint16_t* sb = sa + TILE_ELEMS;
+    if (AK) sstore_kmajor(sa, tid, va); else sstore_mnmajor(sa, tid, va);
+    if (BKM || DUAL) sstore_kmajor(sb, tid, vb); else sstore_mnmajor(sb, tid, vb);
+  };
+
+  L.issue(0, tid, va, vb);
+  store(0);
+  __syncthreads();
+  Frags f0, f1;
+  read_frags(lds, wn, wm, lane, 0, f0);
+  for (int kt = 0; kt + 1 < nk; ++kt) {
+    const int stage = kt & 1;
+    const uint16_t* base = lds + stage * 2 * TILE_ELEMS;
+    L.issue(kt + 1, tid, va, vb);
+    read_frags(base, wn, wm, lane, 1, f1);
+    mfma_range<0, 16>(f0, acc);
+    sched_interleave_load_read<8>();
+    sched_interleave<8, SG_VMEM_R>();
+    read_frags(base, wn, wm, lane, 2, f0);
+    mfma_range<0, 16>(f1, acc);
+    sched_interleave<8, SG_DS_R>();
+    read_frags(base, wn, wm, lane, 3, f1);
+    mfma_range<0, 16>(f0, acc);
+    sched_interleave<8, SG_DS_R>();
+    store(stage ^ 1);
+    mfma_range<0, 8>(f1, acc);
+    sched_interleave<8, SG_DS_W, 2>();
+    __syncthreads();
+    read_frags(lds + (stage ^ 1) * 2 * TILE_ELEMS, wn, wm, lane, 0, f0);
+    mfma_range<8, 16>(f1, acc);
+    sched_interleave<8, SG_DS_R>();
+  }
+  {
+    // last k-tile: no loads, no stores
+    const uint16_t* base = lds + ((nk - 1) & 1) * 2 * TILE_ELEMS;
+    read_frags(base, wn, wm, lane, 1, f1);
+    mfma_range<0, 16>(f0, acc);
+    read_frags(base, wn, wm, lane, 2, f0);
+    mfma_range<0, 16>(f1, acc);
+    read_frags(base, wn, wm, lane, 3, f1);
+    mfma_range<0, 16>(f0, acc);
+    mfma_range<0, 16>(f1, acc);
+  }
+  __syncthreads();   // the epilogue may reuse LDS
+}
+
+__device__ __forceinline__ uint32_t absbits(float x) { return __float_as_uint(x) & 0x7FFFFFFFu; }
+
+// ---------------------------------------------------------------------------
+// epilogue: plain bf16 store
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void epi_store(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wn = wave & 1, wm = wave >> 1;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t n = n0 + wn * 128 + i * 32 + g * 8 + (lane >> 5) * 4;
+        const f32x16& a = acc.v[i][j];
+        if (m >= A.M) continue;
+        if (n + 3 < A.N) {
+          *reinterpret_cast<uint2*>(A.C + m * A.ldc + n) =
+              make_uint2(pack_bf16x2(a[g * 4 + 0], a[g * 4 + 1]),
+                         pack_bf16x2(a[g * 4 + 2], a[g * 4 + 3]));
+        } else {
+          for (int e = 0; e < 4; ++e)
+            if (n + e < A.N) A.C[m * A.ldc + n + e] = (uint16_t)f32_to_bf16_bits(a[g * 4 + e]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// epilogue F1: h_gate/h_up rounded to bf16 -> h_mid = SiLU(g)*u, and the
+// per-group absmax codec of g and u (or their bf16 copies).
+// Wave (wn, wm) holds gate in acc[0..1][j] and up in acc[2..3][j] for
+// d = d0 + 64 wn + 32 i + 8 q + 4 (lane/32) + e, m = m0 + 128 wm + 32 j + lane%32.
+// ---------------------------------------------------------------------------
+template <int CACHE, int GS>
+__device__ __forceinline__ void epi_glu(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0,
+                                        uint16_t* lds) {
+  constexpr int BITS = CACHE == CACHE_INT4 ? 4 : 8;
+  constexpr bool QUANT = CACHE == CACHE_INT4 || CACHE == CACHE_INT8;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wn = wave & 1, wm = wave >> 1;
+  const int half = lane >> 5;
+  const int64_t D = A.D;
+  const int64_t dw0 = (n0 >> 1) + wn * 64;   // first d of this wave
+  const int64_t G = D / GS;
+
+  // per-run absmax (bits of |bf16(acc)|), [t = gate/up][j][i][q]
+  uint32_t am[2][4][2][4];
+  if (QUANT) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x16& a = acc.v[i + 2 * t][j];
+            uint32_t v = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v = max(v, absbits(round_bf16(a[q * 4 + e])));
+            am[t][j][i][q] = v;
+          }
+    // combine runs of one group inside the lane
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (GS >= 16) {
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            am[t][j][i][0] = am[t][j][i][1] = max(am[t][j][i][0], am[t][j][i][1]);
+            am[t][j][i][2] = am[t][j][i][3] = max(am[t][j][i][2], am[t][j][i][3]);
+          }
+        }
+        if (GS >= 32) {
+#pragma unroll
+          for (int i = 0; i < 2; ++i) {
+            const uint32_t v = max(am[t][j][i][0], am[t][j][i][2]);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) am[t][j][i][q] = v;
+          }
+        }
+        if (GS >= 64) {
+          const uint32_t v = max(am[t][j][0][0], am[t][j][1][0]);
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) am[t][j][i][q] = v;
+        }
+      }
+    // the other half of each run-pair lives in lane ^ 32
+    if (GS >= 8) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              am[t][j][i][q] = max(am[t][j][i][q], (uint32_t)__shfl_xor((int)am[t][j][i][q], 32));
+    }
+    if (GS == 128) {
+      // a group spans both waves of a wave-row: exchange through LDS
+      uint32_t* sm = reinterpret_cast<uint32_t*>(lds);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int ml = wm * 128 + j * 32 + (lane & 31);
+          if (half == 0) sm[((t * 256 + ml) << 1) + wn] = am[t][j][0][0];
+        }
+      __syncthreads();
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int ml = wm * 128 + j * 32 + (lane & 31);
+          const uint32_t v = max(am[t][j][0][0], sm[((t * 256 + ml) << 1) + (wn ^ 1)]);
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) am[t][j][i][q] = v;
+        }
+    }
+  }
+
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int64_t d = dw0 + i * 32 + q * 8 + half * 4;
+        if (m >= A.M || d >= D) continue;
+        const f32x16& ag = acc.v[i][j];
+        const f32x16& au = acc.v[i + 2][j];
+        float g[4], u[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          g[e] = round_bf16(ag[q * 4 + e]);
+          u[e] = round_bf16(au[q * 4 + e]);
+        }
+        if (A.h_mid) {
+          float h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) h[e] = silu_mul1(g[e], u[e]);
+          *reinterpret_cast<uint2*>(A.h_mid + m * D + d) =
+              make_uint2(pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]));
+        }
+        if (CACHE == CACHE_BF16) {
+          *reinterpret_cast<uint2*>(A.h_gate + m * D + d) =
+              make_uint2(pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3]));
+          *reinterpret_cast<uint2*>(A.h_up + m * D + d) =
+              make_uint2(pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3]));
+        }
+        if (QUANT) {
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const float* v = t ? u : g;
+            const uint16_t sh = scale_bits<BITS>(am[t][j][i][q]);
+            const float safe = safe_scale(sh);
+            const float rs = __builtin_amdgcn_rcpf(safe);
+            uint16_t* sp = t ? A.s_up : A.s_gate;
+            uint8_t* qp = t ? A.q_up : A.q_gate;
+            const bool first_of_group = GS <= 4 ? true : (half == 0 && ((d & (GS - 1)) == 0));
+            if (first_of_group) sp[m * G + d / GS] = sh;
+            if (BITS == 8) {
+              uint32_t w = 0;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) w |= ((uint32_t)quant_code<8>(v[e], safe, rs) & 0xFFu) << (8 * e);
+              *reinterpret_cast<uint32_t*>(qp + m * D + d) = w;
+            } else {
+              uint32_t w = 0;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) w |= (uint32_t)(quant_code<4>(v[e], safe, rs) + 8) << (4 * e);
+              *reinterpret_cast<uint16_t*>(qp + m * (D >> 1) + (d >> 1)) = (uint16_t)w;
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// epilogue B1: grad_h_mid = bf16(acc); dequantise the cache through bf16 (or
+// read the bf16 cache); SwiGLU backward -> grad_h_gate, grad_h_up, h_mid^.
+// n-side = d: d = n0 + 128 wn + 32 i + 8 q + 4 (lane/32) + e.
+// ---------------------------------------------------------------------------
+template <int CACHE, int GS>
+__device__ __forceinline__ void epi_dglu(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0) {
+  constexpr int BITS = CACHE == CACHE_INT4 ? 4 : 8;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wn = wave & 1, wm = wave >> 1;
+  const int64_t D = A.D;
+  const int64_t G = D / GS;
+  const uint8_t* __restrict__ qg = A.q_gate;
+  const uint8_t* __restrict__ qu = A.q_up;
+  const uint16_t* __restrict__ sgp = A.s_gate;
+  const uint16_t* __restrict__ sup = A.s_up;
+  const uint16_t* __restrict__ hgp = A.h_gate;
+  const uint16_t* __restrict__ hup = A.h_up;
+  uint16_t* __restrict__ og_p = A.grad_gate;
+  uint16_t* __restrict__ ou_p = A.grad_up;
+  uint16_t* __restrict__ oh_p = A.h_mid_hat;
+  static_for<0, 4>([&](auto j) {
+    const int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
+    const bool mok = m < A.M;
+    // 1) gather this row's cache words for all 16 runs (independent loads)
+    uint2 cw[4][4];     // [i][q]: .x gate, .y up (codes) or packed bf16 pairs
+    uint2 cw2[4][4];    // bf16 cache: second half of the 4 values
+    float sc[4][4][2];  // scales
+    static_for<0, 4>([&](auto i) {
+      static_for<0, 4>([&](auto q) {
+        const int64_t d = n0 + wn * 128 + i * 32 + q * 8 + (lane >> 5) * 4;
+        const bool ok = mok && d < D;
+        if constexpr (CACHE == CACHE_BF16) {
+          const uint2 wg = ok ? *reinterpret_cast<const uint2*>(hgp + m * D + d) : make_uint2(0, 0);
+          const uint2 wu = ok ? *reinterpret_cast<const uint2*>(hup + m * D + d) : make_uint2(0, 0);
+          cw[i][q] = wg;
+          cw2[i][q] = wu;
+        } else {
+          sc[i][q][0] = ok ? f16_bits_to_f32(sgp[m * G + d / GS]) : 0.0f;
+          sc[i][q][1] = ok ? f16_bits_to_f32(sup[m * G + d / GS]) : 0.0f;
+          if constexpr (BITS == 8) {
+            cw[i][q].x = ok ? *reinterpret_cast<const uint32_t*>(qg + m * D + d) : 0u;
+            cw[i][q].y = ok ? *reinterpret_cast<const uint32_t*>(qu + m * D + d) : 0u;
+          } else {
+            cw[i][q].x = ok ? *reinterpret_cast<const uint16_t*>(qg + m * (D >> 1) + (d >> 1)) : 0u;
+            cw[i][q].y = ok ? *reinterpret_cast<const uint16_t*>(qu + m * (D >> 1) + (d >> 1)) : 0u;
+          }
+        }
+      });
+    });
+    // 2) dequantise, SwiGLU backward, store
+    static_for<0, 4>([&](auto i) {
+      static_for<0, 4>([&](auto q) {
+        const int64_t d = n0 + wn * 128 + i * 32 + q * 8 + (lane >> 5) * 4;
+        if (!mok || d >= D) return;
+        float hg[4], hu[4];
+        if constexpr (CACHE == CACHE_BF16) {
+          const uint2 wg = cw[i][q], wu = cw2[i][q];
+          hg[0] = __uint_as_float(wg.x << 16); hg[1] = __uint_as_float(wg.x & 0xFFFF0000u);
+          hg[2] = __uint_as_float(wg.y << 16); hg[3] = __uint_as_float(wg.y & 0xFFFF0000u);
+          hu[0] = __uint_as_float(wu.x << 16); hu[1] = __uint_as_float(wu.x & 0xFFFF0000u);
+          hu[2] = __uint_as_float(wu.y << 16); hu[3] = __uint_as_float(wu.y & 0xFFFF0000u);
+        } else if constexpr (BITS == 8) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            hg[e] = round_bf16((float)(int8_t)((cw[i][q].x >> (8 * e)) & 0xFFu) * sc[i][q][0]);
+            hu[e] = round_bf16((float)(int8_t)((cw[i][q].y >> (8 * e)) & 0xFFu) * sc[i][q][1]);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            hg[e] = round_bf16(((float)((cw[i][q].x >> (4 * e)) & 0xFu) - 8.0f) * sc[i][q][0]);
+            hu[e] = round_bf16(((float)((cw[i][q].y >> (4 * e)) & 0xFu) - 8.0f) * sc[i][q][1]);
+          }
+        }
+        float og[4], ou[4], oh[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float hact;
+          swiglu_bwd1(round_bf16(acc.v[i][j][q * 4 + e]), hg[e], hu[e], og[e], ou[e], hact);
+          oh[e] = hact * hu[e];
+        }
+        *reinterpret_cast<uint2*>(og_p + m * D + d) =
+            make_uint2(pack_bf16x2(og[0], og[1]), pack_bf16x2(og[2], og[3]));
+        *reinterpret_cast<uint2*>(ou_p + m * D + d) =
+            make_uint2(pack_bf16x2(ou[0], ou[1]), pack_bf16x2(ou[2], ou[3]));
+        if (oh_p)
+          *reinterpret_cast<uint2*>(oh_p + m * D + d) =
+              make_uint2(pack_bf16x2(oh[0], oh[1]), pack_bf16x2(oh[2], oh[3]));
+      });
+    });
+  });
+}
+
+// ---------------------------------------------------------------------------
+// kernel
+// ---------------------------------------------------------------------------
+template <bool AK, bool BKM, int EPI, int CACHE, int GS>
+__global__ __launch_bounds__(NTHR, 1) void gemm_kernel(KArgs A) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  int tm, tn;
+  tile_coords(A.tiles_m, A.tiles_n, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  Acc acc;
+  mainloop<AK, BKM, EPI == EPI_GLU>(A, m0, n0, lds, acc);
+  if constexpr (EPI == EPI_STORE) epi_store(A, acc, m0, n0);
+  else if constexpr (EPI == EPI_GLU) epi_glu<CACHE, GS>(A, acc, m0, n0, lds);
+  else epi_dglu<CACHE, GS>(A, acc, m0, n0);
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+template <bool AK, bool BKM, int EPI, int CACHE, int GS>
+int launch(KArgs& A, hipStream_t st) {
+  auto kern = gemm_kernel<AK, BKM, EPI, CACHE, GS>;
+  static bool attr_set = false;   // per instantiation
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            LDS_BYTES) != hipSuccess)
+      return kErrLaunch;
+    attr_set = true;
+  }
+  const int64_t tiles = (int64_t)A.tiles_m * A.tiles_n;
+  if (tiles <= 0) return kOk;
+  if (tiles > 0x7FFFFFFF) return kErrTooLarge;
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(NTHR), LDS_BYTES, st, A);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+// layout checks for one operand: 16-byte aligned rows and vectors
+inline bool operand_ok(const void* p, int64_t ld, bool kmajor, int64_t mn, int64_t K) {
+  if (!p || !al16(p) || (ld & 7)) return false;
+  if (kmajor) return (K & 7) == 0 && ld >= K;
+  return (mn & 7) == 0 && ld >= mn;
+}
+
+// 32-bit buffer offsets: the strided extent plus one tile of overhang must
+// stay below 2 GiB.
+inline bool operand_fits(int64_t ld, bool kmajor, int64_t mn, int64_t K) {
+  const int64_t rows = (kmajor ? mn : K) + 256;
+  return rows * ld * 2 < ((int64_t)1 << 31);
+}
+
+template <int EPI, int CACHE>
+int dispatch_gs(int64_t gs, KArgs& A, hipStream_t st, bool ak, bool bk) {
+  // fused epilogues exist for a/b layouts used by the FFN: F1 (k, k), B1 (k, mn)
+  (void)ak; (void)bk;
+  if constexpr (EPI == EPI_GLU) {
+    switch (gs) {
+      case 32: return launch<true, true, EPI, CACHE, 32>(A, st);
+      case 64: return launch<true, true, EPI, CACHE, 64>(A, st);
+      case 128: return launch<true, true, EPI, CACHE, 128>(A, st);
+      default: return kErrGroupPow2;
+    }
+  } else {
+    switch (gs) {
+      case 32: return launch<true, false, EPI, CACHE, 32>(A, st);
+      case 64: return launch<true, false, EPI, CACHE, 64>(A, st);
+      case 128: return launch<true, false, EPI, CACHE, 128>(A, st);
+      default: return kErrGroupPow2;
+    }
+  }
+}
+
+}  // namespace gemm
+}  // namespace cpt
+
+using namespace cpt;
+using namespace cpt::gemm;
+
+extern "C" {
+
+int cpt_gemm_bf16(const void* a, int64_t lda, int a_kmajor, const void* b, int64_t ldb,
+                  int b_kmajor, const void* a2, int64_t lda2, const void* b2, int64_t ldb2,
+                  int64_t K2, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                  void* stream) {
+  if (M < 0 || N < 0 || K < 0 || K2 < 0) return kErrShape;
+  if (M == 0 || N == 0) return kOk;
+  if (!c || !al16(c) || (ldc & 3) || ldc < N) return kErrAlign;
+  if (K > 0 && (!operand_ok(a, lda, a_kmajor, M, K) || !operand_ok(b, ldb, b_kmajor, N, K)))
+    return kErrAlign;
+  if (!operand_fits(lda, a_kmajor, M, K) || !operand_fits(ldb, b_kmajor, N, K))
+    return kErrTooLarge;
+  const bool two = a2 != nullptr;
+  if (two && (!operand_ok(a2, lda2, a_kmajor, M, K2) || !operand_ok(b2, ldb2, b_kmajor, N, K2)))
+    return kErrAlign;
+  // the second pair shares the first pair's per-thread offsets
+  if (two && (lda2 != lda || ldb2 != ldb)) return kErrShape;
+  if (two && (!operand_fits(lda, a_kmajor, M, K2) || !operand_fits(ldb, b_kmajor, N, K2)))
+    return kErrTooLarge;
+  KArgs A{};
+  A.a[0] = {(const uint16_t*)a, lda};
+  A.b[0] = {(const uint16_t*)b, ldb};
+  A.K[0] = K;
+  A.npairs = 1;
+  if (two) {
+    A.a[1] = {(const uint16_t*)a2, lda2};
+    A.b[1] = {(const uint16_t*)b2, ldb2};
+    A.K[1] = K2;
+    A.npairs = 2;
+  }
+  A.M = M; A.N = N;
+  A.tiles_m = (int)((M + BM - 1) / BM);
+  A.tiles_n = (int)((N + BN - 1) / BN);
+  A.C = (uint16_t*)c;
+  A.ldc = ldc;
+  hipStream_t st = (hipStream_t)stream;
+  if (a_kmajor && b_kmajor) return launch<true, true, EPI_STORE, 0, 0>(A, st);
+  if (a_kmajor && !b_kmajor) return launch<true, false, EPI_STORE, 0, 0>(A, st);
+  if (!a_kmajor && !b_kmajor) return launch<false, false, EPI_STORE, 0, 0>(A, st);
+  return launch<false, true, EPI_STORE, 0, 0>(A, st);
+}
+
+int cpt_ffn_gate_up(const void* x, const void* w_gate, const void* w_up, int64_t n_tok,
+                    int64_t hidden, int64_t inter, int cache, int64_t group_size, void* h_mid,
+                    void* h_gate, void* h_up, void* q_gate, void* s_gate, void* q_up,
+                    void* s_up, void* stream) {
+  if (n_tok < 0 || hidden < 0 || inter < 0) return kErrShape;
+  if (cache != CACHE_NONE && cache != CACHE_BF16 && cache != CACHE_INT4 && cache != CACHE_INT8)
+    return kErrBits;
+  const bool quant = cache == CACHE_INT4 || cache == CACHE_INT8;
+  if (quant) {
+    if (group_size <= 0 || inter % group_size) return kErrRagged;
+    if (!is_pow2(group_size)) return kErrGroupPow2;
+    if (group_size != 32 && group_size != 64 && group_size != 128) return kErrGroupPow2;
+    if (!q_gate || !s_gate || !q_up || !s_up) return kErrShape;
+  }
+  if (cache == CACHE_BF16 && (!h_gate || !h_up || !al16(h_gate) || !al16(h_up))) return kErrShape;
+  if (!quant && cache != CACHE_BF16 && !h_mid) return kErrShape;
+  if (n_tok == 0 || inter == 0) return kOk;
+  if ((inter & 7) || !operand_ok(x, hidden, true, n_tok, hidden) ||
+      !operand_ok(w_gate, hidden, true, inter, hidden) ||
+      !operand_ok(w_up, hidden, true, inter, hidden) || (h_mid && !al16(h_mid)))
+    return kErrAlign;
+  if (quant && ((uintptr_t)q_gate & 3 || (uintptr_t)q_up & 3)) return kErrAlign;
+  if (!operand_fits(hidden, true, n_tok, hidden) || !operand_fits(hidden, true, inter, hidden))
+    return kErrTooLarge;
+  KArgs A{};
+  A.a[0] = {(const uint16_t*)x, hidden};
+  A.b[0] = {(const uint16_t*)w_gate, hidden};
+  A.K[0] = hidden;
+  A.npairs = 1;
+  A.b_up = (const uint16_t*)w_up;
+  A.M = n_tok;
+  A.N = 2 * inter;
+  A.D = inter;
+  A.tiles_m = (int)((n_tok + BM - 1) / BM);
+  A.tiles_n = (int)((inter + 127) / 128);
+  A.h_mid = (uint16_t*)h_mid;
+  A.h_gate = (uint16_t*)h_gate;
+  A.h_up = (uint16_t*)h_up;
+  A.q_gate = (uint8_t*)q_gate;
+  A.s_gate = (uint16_t*)s_gate;
+  A.q_up = (uint8_t*)q_up;
+  A.s_up = (uint16_t*)s_up;
+  hipStream_t st = (hipStream_t)stream;
+  switch (cache) {
+    case CACHE_NONE: return launch<true, true, EPI_GLU, CACHE_NONE, 64>(A, st);
+    case CACHE_BF16: return launch<true, true, EPI_GLU, CACHE_BF16, 64>(A, st);
+    case CACHE_INT4: return dispatch_gs<EPI_GLU, CACHE_INT4>(group_size, A, st, true, true);
+    default: return dispatch_gs<EPI_GLU, CACHE_INT8>(group_size, A, st, true, true);
+  }
+}
+
+int cpt_ffn_down_dgrad(const void* grad_y, const void* w_down, int64_t n_tok, int64_t hidden,
+                       int64_t inter, int cache, int64_t group_size, const void* c_gate,
+                       const void* s_gate, const void* c_up, const void* s_up, void* grad_h_gate,
+                       void* grad_h_up, void* h_mid_hat, void* stream) {
+  if (n_tok < 0 || hidden < 0 || inter < 0) return kErrShape;
+  if (cache != CACHE_BF16 && cache != CACHE_INT4 && cache != CACHE_INT8) return kErrBits;
+  const bool quant = cache != CACHE_BF16;
+  if (quant) {
+    if (group_size <= 0 || inter % group_size) return kErrRagged;
+    if (!is_pow2(group_size)) return kErrGroupPow2;
+    if (group_size != 32 && group_size != 64 && group_size != 128) return kErrGroupPow2;
+    if (!s_gate || !s_up) return kErrShape;
+  }
+  if (!c_gate || !c_up || !grad_h_gate || !grad_h_up) return kErrShape;
+  if (n_tok == 0 || inter == 0) return kOk;
+  if ((inter & 7) || !operand_ok(grad_y, hidden, true, n_tok, hidden) ||
+      !operand_ok(w_down, inter, false, inter, hidden) || !al16(grad_h_gate) ||
+      !al16(grad_h_up) || (h_mid_hat && !al16(h_mid_hat)))
+    return kErrAlign;
+  if (!operand_fits(hidden, true, n_tok, hidden) || !operand_fits(inter, false, inter, hidden))
+    return kErrTooLarge;
+  KArgs A{};
+  A.a[0] = {(const uint16_t*)grad_y, hidden};
+  A.b[0] = {(const uint16_t*)w_down, inter};   // W_d [H, D]: n-side d, k = h, MN-major
+  A.K[0] = hidden;
+  A.npairs = 1;
+  A.M = n_tok;
+  A.N = inter;
+  A.D = inter;
+  A.tiles_m = (int)((n_tok + BM - 1) / BM);
+  A.tiles_n = (int)((inter + BN - 1) / BN);
+  if (quant) {
+    A.q_gate = (uint8_t*)c_gate;
+    A.q_up = (uint8_t*)c_up;
+    A.s_gate = (uint16_t*)s_gate;
+    A.s_up = (uint16_t*)s_up;
+  } else {
+    A.h_gate = (uint16_t*)c_gate;
+    A.h_up = (uint16_t*)c_up;
+  }
+  A.grad_gate = (uint16_t*)grad_h_gate;
+  A.grad_up = (uint16_t*)grad_h_up;
+  A.h_mid_hat = (uint16_t*)h_mid_hat;
+  hipStream_t st = (hipStream_t)stream;
+  switch (cache) {
+    case CACHE_BF16: return launch<true, false, EPI_DGLU, CACHE_BF16, 64>(A, st);
+    case CACHE_INT4: return dispatch_gs<EPI_DGLU, CACHE_INT4>(group_size, A, st, true, false);
+    default: return dispatch_gs<EPI_DGLU, CACHE_INT8>(group_size, A, st, true, false);
+  }
+}
+
+}  // extern "C"

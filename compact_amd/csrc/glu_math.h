@@ -1,0 +1,71 @@
+// Elementwise math shared by the standalone codec/GLU kernels (codec.hip) and
+// the fused GEMM epilogues (gemm.hip).  Both include this one definition, so a
+// fused kernel and its unfused composition agree bit for bit.
+//
+// References (SDMuhsin/CompAct): GLU forward src/flashffn.py:71-76, backward
+// :109-123, codec :1071-1088 (quantise) and :1099-1110 (dequantise), the
+// bf16 round trip of the dequantised cache :1251-1253.
+#pragma once
+
+#include "common.h"
+
+namespace cpt {
+
+// sigmoid(x) = 1 / (1 + e^-x) on the transcendental unit: v_exp_f32 (2^x) and
+// v_rcp_f32, each about 1 ulp.  Large |x| saturate to exactly 0 or 1.
+__device__ __forceinline__ float sigmoid_f32(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(x * -1.4426950408889634f));
+}
+
+// float -> bf16 -> float
+__device__ __forceinline__ float round_bf16(float x) {
+  return __uint_as_float(pack_bf16x2(x, 0.0f) << 16);
+}
+
+// GLU forward of one element: (g * sigmoid(g)) * u
+__device__ __forceinline__ float silu_mul1(float g, float u) { return (g * sigmoid_f32(g)) * u; }
+
+// GLU backward of one element (op order of the reference's _swiglu_bwd_kernel).
+__device__ __forceinline__ void swiglu_bwd1(float dh, float g, float u, float& dg, float& du,
+                                            float& hact) {
+  const float sig = sigmoid_f32(g);
+  hact = g * sig;
+  const float grad_h_act = dh * u;
+  du = dh * hact;
+  const float dsilu = sig * (1.0f + g * (1.0f - sig));
+  dg = grad_h_act * dsilu;
+}
+
+template <int BITS> struct QMax;
+template <> struct QMax<4> { static constexpr float v = 7.0f; };
+template <> struct QMax<8> { static constexpr float v = 127.0f; };
+
+// scale = fp16(fp32(absmax / qmax))  (absmax given as the bits of |x|)
+template <int BITS>
+__device__ __forceinline__ uint16_t scale_bits(uint32_t absmax_bits) {
+  return f32_to_f16_bits(__uint_as_float(absmax_bits) / QMax<BITS>::v);
+}
+
+// safe = scale > 0 ? scale : 1
+__device__ __forceinline__ float safe_scale(uint16_t sh) {
+  const float s = f16_bits_to_f32(sh);
+  return s > 0.0f ? s : 1.0f;
+}
+
+// code = clamp(rint(fp32(v / safe)), -qmax, qmax), the reference's definition.
+// Fast path: q = v * rcp(safe).  Every quotient here has |v / safe| < 256
+// (at most qmax * 1.5, reached with fp16-subnormal scales), where
+// |q - v/safe| <= 2^-14 and |fp32(v/safe) - v/safe| <= 2^-17.  So whenever q
+// is farther than 2^-12 from a half-integer, rint(q) == rint(fp32(v/safe)).
+// Otherwise (rare) the correctly rounded division decides.  safe = inf gives
+// rcp = 0 and code 0, as v / inf does.
+template <int BITS>
+__device__ __forceinline__ int quant_code(float v, float safe, float rsafe) {
+  const float q = v * rsafe;
+  float r = __builtin_rintf(q);
+  if (__builtin_fabsf(q - r) > 0.5f - 0.000244140625f) r = __builtin_rintf(v / safe);
+  r = fminf(fmaxf(r, -QMax<BITS>::v), QMax<BITS>::v);
+  return (int)r;
+}
+
+}  // namespace cpt

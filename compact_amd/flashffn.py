@@ -28,6 +28,8 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import _lib
+from . import gemm as G
 from . import kernels as K
 from .kernels import _V3_COUNTERS
 
@@ -36,9 +38,43 @@ def _bits(mode: str) -> int:
     return 4 if mode == "int4" else 8
 
 
+_CACHE_CODE = {"int4": _lib.CACHE_INT4, "int8": _lib.CACHE_INT8, "bf16": _lib.CACHE_BF16,
+               "recompute": _lib.CACHE_NONE}
+_FUSED_GROUPS = (32, 64, 128)
+
+
+def _mfma(*ts) -> bool:
+    """The MFMA engine runs bf16 operands whose dims are multiples of 8."""
+    for t in ts:
+        if t is None:
+            continue
+        if t.dtype != torch.bfloat16 or any(d % 8 for d in t.shape):
+            return False
+    return True
+
+
+def _mm(a, b, name):
+    """a @ b: the MFMA engine for bf16, the library GEMM otherwise."""
+    if _mfma(a, b) and a.shape[0] > 0:
+        return G.mm(a, b, name)
+    return a @ b
+
+
+def _linear(x, w, name):
+    if _mfma(x, w) and x.shape[0] > 0:
+        return G.linear(x, w, name)
+    return F.linear(x, w)
+
+
 class FlashFFNv3Function(torch.autograd.Function):
     """LoRA-factored SwiGLU FFN with a quantised GLU-cache backward
-    (src/flashffn.py:1376-1602).  a_*/b_* may be None (pass s_*=0.0)."""
+    (src/flashffn.py:1376-1602).  a_*/b_* may be None (pass s_*=0.0).
+
+    bf16 without gate/up adapters runs the fused MFMA kernels: the forward
+    gate/up GEMM carries SiLU*mul and the codec in its epilogue, the backward
+    down-projection GEMM carries the dequantisation and the SwiGLU backward.
+    Other cases compose the GEMM engine (or the library GEMM for non-bf16
+    dtypes) with the standalone elementwise kernels in the reference's order."""
 
     @staticmethod
     def forward(ctx, x, w_gate, a_gate, b_gate, w_up, a_up, b_up, w_down, a_down, b_down,
@@ -50,46 +86,60 @@ class FlashFFNv3Function(torch.autograd.Function):
         orig_shape = x.shape
         hidden_dim = x.shape[-1]
         x_2d = x.reshape(-1, hidden_dim)
-
-        # factored forward in PEFT op order: base, then + s * B(A(x))  (:1410-1420)
-        h_gate = F.linear(x_2d, w_gate)
-        xa_g = None
-        if a_gate is not None:
-            xa_g = F.linear(x_2d, a_gate)
-            h_gate = h_gate + s_gate * F.linear(xa_g, b_gate)
-        h_up = F.linear(x_2d, w_up)
-        xa_u = None
-        if a_up is not None:
-            xa_u = F.linear(x_2d, a_up)
-            h_up = h_up + s_up * F.linear(xa_u, b_up)
+        if not x_2d.is_contiguous():
+            x_2d = x_2d.contiguous()
+        quant = cache_mode in ("int4", "int8")
+        fusable = (a_gate is None and a_up is None and _mfma(x_2d, w_gate, w_up)
+                   and x_2d.shape[0] > 0)
 
         c_gate = qs_gate = c_up = qs_up = None
-        fused_quant = (cache_mode in ("int4", "int8") and use_triton
-                       and h_gate.dtype == torch.bfloat16)                # :1424-1426
-        if fused_quant:
-            h_mid, c_gate, qs_gate, c_up, qs_up = K.silu_mul_quant(
-                h_gate, h_up, _bits(cache_mode), group_size)
-            del h_gate, h_up
+        h_gate = h_up = None
+        fused_quant = (quant and use_triton and x.dtype == torch.bfloat16)   # :1424-1426
+        if fusable and fused_quant and group_size in _FUSED_GROUPS:
+            # dual GEMM + GLU + codec in one kernel (K1 fused into the epilogue)
+            h_mid, _, _, c_gate, qs_gate, c_up, qs_up = G.ffn_gate_up(
+                x_2d, w_gate, w_up, _CACHE_CODE[cache_mode], group_size)
+            _V3_COUNTERS["triton_quant_fwd"] += 1
+            xa_g = xa_u = None
+        elif fusable and not fused_quant:
+            # h_gate/h_up are needed (bf16 cache, eager codec) or not (recompute)
+            keep = cache_mode != "recompute"
+            h_mid, h_gate, h_up, *_ = G.ffn_gate_up(
+                x_2d, w_gate, w_up, _lib.CACHE_BF16 if keep else _lib.CACHE_NONE, group_size)
+            xa_g = xa_u = None
         else:
-            h_mid = K.silu_mul(h_gate, h_up)
+            # factored forward in PEFT op order: base, then + s * B(A(x))  (:1410-1420)
+            h_gate = _linear(x_2d, w_gate, "gemm_fwd_gate")
+            xa_g = None
+            if a_gate is not None:
+                xa_g = F.linear(x_2d, a_gate)
+                h_gate = h_gate + s_gate * F.linear(xa_g, b_gate)
+            h_up = _linear(x_2d, w_up, "gemm_fwd_up")
+            xa_u = None
+            if a_up is not None:
+                xa_u = F.linear(x_2d, a_up)
+                h_up = h_up + s_up * F.linear(xa_u, b_up)
+            if fused_quant:
+                h_mid, c_gate, qs_gate, c_up, qs_up = K.silu_mul_quant(
+                    h_gate, h_up, _bits(cache_mode), group_size)
+                h_gate = h_up = None
+            else:
+                h_mid = K.silu_mul(h_gate, h_up)
 
-        y = F.linear(h_mid, w_down)                                       # :1435
+        y = _linear(h_mid, w_down, "gemm_fwd_down")                         # :1435
         ha_d = None
         if a_down is not None:
             ha_d = F.linear(h_mid, a_down)
             y = y + s_down * F.linear(ha_d, b_down)
 
-        if not fused_quant:                                               # :1442-1451
-            if cache_mode in ("int4", "int8"):
+        if not fused_quant:                                                # :1442-1451
+            if quant:
                 c_gate, qs_gate = K.v3_quantize_group_absmax(h_gate, _bits(cache_mode),
                                                              group_size)
                 c_up, qs_up = K.v3_quantize_group_absmax(h_up, _bits(cache_mode), group_size)
-                del h_gate, h_up
             elif cache_mode == "bf16":
                 c_gate, c_up = h_gate, h_up
-            else:
-                del h_gate, h_up
-        del h_mid
+        del h_gate, h_up, h_mid
 
         ctx.save_for_backward(x, w_gate, a_gate, b_gate, w_up, a_up, b_up,
                               w_down, a_down, b_down, xa_g, xa_u, ha_d,
@@ -111,6 +161,7 @@ class FlashFFNv3Function(torch.autograd.Function):
          xa_g, xa_u, ha_d, c_gate, qs_gate, c_up, qs_up) = ctx.saved_tensors
         s_gate, s_up, s_down = ctx.s
         mode = ctx.cache_mode
+        gs = ctx.group_size
         hidden_dim = ctx.orig_shape[-1]
         (need_x, need_wg, need_ag, need_bg, need_wu, need_au, need_bu,
          need_wd, need_ad, need_bd) = ctx.needs_input_grad[:10]
@@ -118,29 +169,36 @@ class FlashFFNv3Function(torch.autograd.Function):
         if not gy.is_contiguous():
             gy = gy.contiguous()
         x_2d = x.reshape(-1, hidden_dim)
+        if not x_2d.is_contiguous():
+            x_2d = x_2d.contiguous()
 
         need_gate_path = (need_x or need_wg or need_ag or need_bg
                           or need_wu or need_au or need_bu)               # :1488-1489
         need_h_mid = need_wd or (a_down is not None and need_ad)          # :1490
         need_recon = need_gate_path or need_h_mid
         use_k2 = mode in ("int4", "int8") and ctx.use_triton and need_gate_path
+        fusable = (a_down is None and _mfma(gy, w_down) and gy.shape[0] > 0)
+        fusable_gu = (a_gate is None and a_up is None and _mfma(x_2d, w_gate, w_up)
+                      and x_2d.shape[0] > 0)
 
         hg = hu = None
         if need_recon and not use_k2:                                     # :1500-1516
             if mode == "recompute":
-                hg = F.linear(x_2d, w_gate)
-                if a_gate is not None:
-                    hg = hg + s_gate * F.linear(xa_g, b_gate)
-                hu = F.linear(x_2d, w_up)
-                if a_up is not None:
-                    hu = hu + s_up * F.linear(xa_u, b_up)
+                if fusable_gu:
+                    _, hg, hu, *_ = G.ffn_gate_up(x_2d, w_gate, w_up, _lib.CACHE_BF16, gs,
+                                                  want_h_mid=False)
+                else:
+                    hg = _linear(x_2d, w_gate, "gemm_recompute_gate")
+                    if a_gate is not None:
+                        hg = hg + s_gate * F.linear(xa_g, b_gate)
+                    hu = _linear(x_2d, w_up, "gemm_recompute_up")
+                    if a_up is not None:
+                        hu = hu + s_up * F.linear(xa_u, b_up)
             elif mode == "bf16":
                 hg, hu = c_gate, c_up
             else:
-                hg = K.v3_dequantize_group_absmax(c_gate, qs_gate, _bits(mode), ctx.group_size,
-                                                  ctx.in_dtype)
-                hu = K.v3_dequantize_group_absmax(c_up, qs_up, _bits(mode), ctx.group_size,
-                                                  ctx.in_dtype)
+                hg = K.v3_dequantize_group_absmax(c_gate, qs_gate, _bits(mode), gs, ctx.in_dtype)
+                hu = K.v3_dequantize_group_absmax(c_up, qs_up, _bits(mode), gs, ctx.in_dtype)
 
         grad_w_down = grad_a_down = grad_b_down = None
         gyB_d = None
@@ -148,20 +206,34 @@ class FlashFFNv3Function(torch.autograd.Function):
             gyB_d = gy @ b_down                                           # :1521
 
         grad_h_gate = grad_h_up = h_mid_hat = None
-        if use_k2:                                                        # :1525-1533
-            grad_h_mid = gy @ w_down
-            if a_down is not None:
-                grad_h_mid = grad_h_mid + s_down * (gyB_d @ a_down)
-            grad_h_gate, grad_h_up, h_mid_hat = K.dequant_swiglu_backward(
-                grad_h_mid, c_gate, qs_gate, c_up, qs_up, _bits(mode), ctx.group_size,
-                want_h_mid=need_h_mid)
-            del grad_h_mid
+        if need_gate_path:
+            if use_k2 and fusable and gs in _FUSED_GROUPS:                # :1525-1533
+                # dgrad GEMM with dequantise + SwiGLU backward in its epilogue
+                grad_h_gate, grad_h_up, h_mid_hat = G.ffn_down_dgrad(
+                    gy, w_down, _CACHE_CODE[mode], gs, c_gate, qs_gate, c_up, qs_up,
+                    need_h_mid)
+                _V3_COUNTERS["triton_dequant_bwd"] += 1
+            elif (not use_k2) and fusable and hg is not None and _mfma(hg, hu):
+                grad_h_gate, grad_h_up, h_mid_hat = G.ffn_down_dgrad(
+                    gy, w_down, _lib.CACHE_BF16, gs, hg, None, hu, None, need_h_mid)
+            else:
+                grad_h_mid = _mm(gy, w_down, "gemm_dgrad_down")
+                if a_down is not None:
+                    grad_h_mid = grad_h_mid + s_down * (gyB_d @ a_down)
+                if use_k2:
+                    grad_h_gate, grad_h_up, h_mid_hat = K.dequant_swiglu_backward(
+                        grad_h_mid, c_gate, qs_gate, c_up, qs_up, _bits(mode), gs,
+                        want_h_mid=need_h_mid)
+                else:
+                    grad_h_gate, grad_h_up, h_mid_hat = K.swiglu_backward_glu(
+                        grad_h_mid, hg, hu, need_h_mid)
+                del grad_h_mid
 
         if need_h_mid:                                                    # :1536-1543
             if h_mid_hat is None:
                 h_mid_hat = K.silu_mul(hg, hu)
             if need_wd:
-                grad_w_down = gy.t() @ h_mid_hat
+                grad_w_down = _mm(gy.t(), h_mid_hat, "gemm_wgrad_down")
             if need_ad:
                 grad_a_down = s_down * (gyB_d.t() @ h_mid_hat)
             del h_mid_hat
@@ -172,12 +244,6 @@ class FlashFFNv3Function(torch.autograd.Function):
         grad_w_gate = grad_a_gate = grad_b_gate = None
         grad_w_up = grad_a_up = grad_b_up = None
         if need_gate_path:                                                # :1551-1587
-            if grad_h_gate is None:
-                grad_h_mid = gy @ w_down
-                if a_down is not None:
-                    grad_h_mid = grad_h_mid + s_down * (gyB_d @ a_down)
-                grad_h_gate, grad_h_up = K.swiglu_backward(grad_h_mid, hg, hu)
-                del grad_h_mid
             ghgB = None
             if a_gate is not None and (need_x or need_ag):
                 ghgB = grad_h_gate @ b_gate
@@ -185,10 +251,13 @@ class FlashFFNv3Function(torch.autograd.Function):
             if a_up is not None and (need_x or need_au):
                 ghuB = grad_h_up @ b_up
             if need_x:
-                grad_x = grad_h_gate @ w_gate
+                if _mfma(grad_h_gate, w_gate, grad_h_up, w_up):
+                    # dg @ W_g + du @ W_u as one K-concatenated GEMM
+                    grad_x = G.mm2(grad_h_gate, w_gate, grad_h_up, w_up, "gemm_dgrad_x")
+                else:
+                    grad_x = grad_h_gate @ w_gate + grad_h_up @ w_up
                 if a_gate is not None:
                     grad_x = grad_x + s_gate * (ghgB @ a_gate)
-                grad_x = grad_x + grad_h_up @ w_up
                 if a_up is not None:
                     grad_x = grad_x + s_up * (ghuB @ a_up)
             if need_bg:
@@ -200,9 +269,9 @@ class FlashFFNv3Function(torch.autograd.Function):
             if need_au:
                 grad_a_up = s_up * (ghuB.t() @ x_2d)
             if need_wg:
-                grad_w_gate = grad_h_gate.t() @ x_2d
+                grad_w_gate = _mm(grad_h_gate.t(), x_2d, "gemm_wgrad_gate")
             if need_wu:
-                grad_w_up = grad_h_up.t() @ x_2d
+                grad_w_up = _mm(grad_h_up.t(), x_2d, "gemm_wgrad_up")
 
         # frozen weights => no dense [D_out, D_in] gradient was built (:1589-1593)
         if not (need_wg or need_wu or need_wd):

@@ -1,0 +1,180 @@
+"""torch-facing wrappers of the MFMA GEMM engine (libcompact_amd.so).
+
+mm(a, b)        a @ b for 2-D bf16 tensors; each operand may be row-major or
+                a transposed view (K-major / MN-major on the device side).
+mm2(a, b, a2, b2)  a @ b + a2 @ b2 in one fp32 accumulation.
+linear(x, w)    x @ w.T (F.linear without bias).
+ffn_gate_up     fused dual GEMM + GLU + codec (forward of gate/up + K1).
+ffn_down_dgrad  fused grad_y @ w_down + dequantise + SwiGLU backward (+ K2).
+
+These replace the cuBLAS GEMMs the reference issues through F.linear / @
+(src/flashffn.py:1410-1439,1503-1587).  bf16 only: the MFMA path.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import check
+from .kernels import _require_device, _stream, _timed
+
+
+def _layout_a(a: torch.Tensor):
+    """(tensor, ld, kmajor) for a logical [M, K] operand."""
+    if a.stride(1) == 1 and a.stride(0) % 8 == 0 and a.stride(0) >= a.shape[1]:
+        return a, a.stride(0), 1
+    if a.stride(0) == 1 and a.stride(1) % 8 == 0 and a.stride(1) >= a.shape[0]:
+        return a, a.stride(1), 0
+    a = a.contiguous()
+    return a, a.stride(0), 1
+
+
+def _layout_b(b: torch.Tensor):
+    """(tensor, ld, kmajor) for a logical [K, N] operand (kmajor: stored [N][ld])."""
+    if b.stride(0) == 1 and b.stride(1) % 8 == 0 and b.stride(1) >= b.shape[0]:
+        return b, b.stride(1), 1
+    if b.stride(1) == 1 and b.stride(0) % 8 == 0 and b.stride(0) >= b.shape[1]:
+        return b, b.stride(0), 0
+    b = b.contiguous()
+    return b, b.stride(0), 0
+
+
+def _with_ld(t: torch.Tensor, ld: int, rows_dim: int) -> torch.Tensor:
+    """Copy of 2-D `t` whose storage rows (along `rows_dim`) are `ld` apart."""
+    if rows_dim == 0:
+        buf = torch.zeros((t.shape[0], ld), dtype=t.dtype, device=t.device)
+        buf[:, :t.shape[1]] = t
+        return buf[:, :t.shape[1]]
+    buf = torch.zeros((t.shape[1], ld), dtype=t.dtype, device=t.device)
+    buf[:, :t.shape[0]] = t.t()
+    return buf[:, :t.shape[0]].t()
+
+
+def _common_ld(x, x2, kmajor: int, is_b: bool):
+    """The two pairs of mm2 share per-thread offsets, so their operands need
+    one leading dimension: re-lay both with the larger one."""
+    # storage row axis: A K-major [M][ld] -> dim 0; A MN-major [K][ld] -> dim 1;
+    # B K-major [N][ld] -> dim 1; B MN-major [K][ld] -> dim 0
+    rows_dim = (0 if kmajor else 1) if not is_b else (1 if kmajor else 0)
+    extent = lambda t: t.shape[1 - rows_dim]
+    ld = max((extent(x) + 7) // 8 * 8, (extent(x2) + 7) // 8 * 8)
+    return _with_ld(x, ld, rows_dim), _with_ld(x2, ld, rows_dim), ld
+
+
+def _check_bf16(*ts):
+    for t in ts:
+        assert t.dtype == torch.bfloat16, f"MFMA GEMM path is bf16-only, got {t.dtype}"
+        assert t.dim() == 2
+
+
+def mm(a: torch.Tensor, b: torch.Tensor, name: str = "gemm") -> torch.Tensor:
+    """a [M, K] @ b [K, N] -> bf16 [M, N] on the MFMA engine."""
+    return mm2(a, b, None, None, name)
+
+
+def mm2(a, b, a2=None, b2=None, name: str = "gemm") -> torch.Tensor:
+    """a @ b (+ a2 @ b2) in one fp32 accumulation -> bf16 [M, N]."""
+    _require_device(a, b)
+    _check_bf16(a, b)
+    M, K = a.shape
+    K_, N = b.shape
+    assert K == K_, f"inner dims differ: {tuple(a.shape)} @ {tuple(b.shape)}"
+    a, lda, ak = _layout_a(a)
+    b, ldb, bk = _layout_b(b)
+    p_a2 = p_b2 = None
+    lda2 = ldb2 = K2 = 0
+    if a2 is not None:
+        _check_bf16(a2, b2)
+        assert a2.shape[0] == M and b2.shape[1] == N and a2.shape[1] == b2.shape[0]
+        K2 = a2.shape[1]
+        a2, lda2, ak2 = _layout_a(a2)
+        b2, ldb2, bk2 = _layout_b(b2)
+        if ak2 != ak:
+            a2 = a2.t().contiguous().t() if ak == 0 else a2.contiguous()
+            a2, lda2, ak2 = _layout_a(a2)
+        if bk2 != bk:
+            b2 = b2.t().contiguous().t() if bk == 1 else b2.contiguous()
+            b2, ldb2, bk2 = _layout_b(b2)
+        assert ak2 == ak and bk2 == bk
+        if lda2 != lda:
+            a, a2, lda = _common_ld(a, a2, ak, is_b=False)
+            lda2 = lda
+        if ldb2 != ldb:
+            b, b2, ldb = _common_ld(b, b2, bk, is_b=True)
+            ldb2 = ldb
+        p_a2, p_b2 = a2.data_ptr(), b2.data_ptr()
+    ldc = (N + 7) // 8 * 8
+    c = torch.empty((M, ldc), dtype=torch.bfloat16, device=a.device)
+    with _timed(name):
+        rc = _lib.lib().cpt_gemm_bf16(a.data_ptr(), lda, ak, b.data_ptr(), ldb, bk, p_a2, lda2,
+                                      p_b2, ldb2, K2, c.data_ptr(), ldc, M, N, K, _stream(a))
+    check(rc, name)
+    return c if ldc == N else c[:, :N]
+
+
+def linear(x: torch.Tensor, w: torch.Tensor, name: str = "gemm") -> torch.Tensor:
+    """x [M, K] @ w[N, K].T -> [M, N] (F.linear without bias)."""
+    return mm(x, w.t(), name)
+
+
+def ffn_gate_up(x, w_gate, w_up, cache: int, group_size: int, want_h_mid: bool = True):
+    """Fused dual GEMM + GLU + codec.  Returns (h_mid | None, h_gate | None,
+    h_up | None, q_gate | None, s_gate | None, q_up | None, s_up | None)."""
+    _require_device(x, w_gate, w_up)
+    _check_bf16(x, w_gate, w_up)
+    n, hdim = x.shape
+    d = w_gate.shape[0]
+    assert w_gate.shape == (d, hdim) and w_up.shape == (d, hdim)
+    x, w_gate, w_up = x.contiguous(), w_gate.contiguous(), w_up.contiguous()
+    dev = x.device
+    h_mid = torch.empty((n, d), dtype=torch.bfloat16, device=dev) if want_h_mid else None
+    hg = hu = qg = sg = qu = su = None
+    if cache == _lib.CACHE_BF16:
+        hg = torch.empty((n, d), dtype=torch.bfloat16, device=dev)
+        hu = torch.empty((n, d), dtype=torch.bfloat16, device=dev)
+    elif cache in (_lib.CACHE_INT4, _lib.CACHE_INT8):
+        g = d // group_size
+        shape = (n, d // 2) if cache == _lib.CACHE_INT4 else (n, d)
+        qdt = torch.uint8 if cache == _lib.CACHE_INT4 else torch.int8
+        qg = torch.empty(shape, dtype=qdt, device=dev)
+        qu = torch.empty(shape, dtype=qdt, device=dev)
+        sg = torch.empty((n, g), dtype=torch.float16, device=dev)
+        su = torch.empty((n, g), dtype=torch.float16, device=dev)
+
+    def p(t):
+        return None if t is None else t.data_ptr()
+
+    with _timed("ffn_gate_up"):
+        rc = _lib.lib().cpt_ffn_gate_up(x.data_ptr(), w_gate.data_ptr(), w_up.data_ptr(), n,
+                                        hdim, d, cache, group_size, p(h_mid), p(hg), p(hu),
+                                        p(qg), p(sg), p(qu), p(su), _stream(x))
+    check(rc, "ffn_gate_up")
+    return h_mid, hg, hu, qg, sg, qu, su
+
+
+def ffn_down_dgrad(grad_y, w_down, cache: int, group_size: int, c_gate, s_gate, c_up, s_up,
+                   want_h_mid: bool):
+    """Fused grad_y @ w_down + dequantise + SwiGLU backward.
+    Returns (grad_h_gate, grad_h_up, h_mid_hat | None)."""
+    _require_device(grad_y, w_down)
+    _check_bf16(grad_y, w_down)
+    n, hdim = grad_y.shape
+    d = w_down.shape[1]
+    assert w_down.shape == (hdim, d)
+    grad_y, w_down = grad_y.contiguous(), w_down.contiguous()
+    dev = grad_y.device
+    dg = torch.empty((n, d), dtype=torch.bfloat16, device=dev)
+    du = torch.empty((n, d), dtype=torch.bfloat16, device=dev)
+    hm = torch.empty((n, d), dtype=torch.bfloat16, device=dev) if want_h_mid else None
+
+    def p(t):
+        return None if t is None else t.contiguous().data_ptr()
+
+    with _timed("ffn_down_dgrad"):
+        rc = _lib.lib().cpt_ffn_down_dgrad(grad_y.data_ptr(), w_down.data_ptr(), n, hdim, d,
+                                           cache, group_size, p(c_gate), p(s_gate), p(c_up),
+                                           p(s_up), dg.data_ptr(), du.data_ptr(), p(hm),
+                                           _stream(grad_y))
+    check(rc, "ffn_down_dgrad")
+    return dg, du, hm

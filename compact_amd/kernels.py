@@ -274,9 +274,27 @@ def dequant_swiglu_backward(grad_h_mid, q_gate, s_gate, q_up, s_up, bits, group_
     return grad_h_gate, grad_h_up, h_mid_hat
 
 
-# The reference's names (src/flashffn.py:205,223,259,1314,1343), kept for drop-in use.
-triton_silu_mul = silu_mul
+# The reference's names and signatures (src/flashffn.py:205,223,259,1314,1343),
+# kept for drop-in use.  `digest` belongs to the fused decoder block's
+# rematerialisation certificate, which is outside this path.
+
+def triton_silu_mul(h_gate, h_up, digest=False):
+    """src/flashffn.py:205-220."""
+    if digest:
+        raise NotImplementedError("digest witnesses belong to the fused decoder block")
+    return silu_mul(h_gate, h_up)
+
+
 triton_swiglu_backward = swiglu_backward
-triton_swiglu_backward_glu = swiglu_backward_glu
+
+
+def triton_swiglu_backward_glu(grad_h_mid, h_gate, h_up, want_h_mid, inplace, digest=False):
+    """src/flashffn.py:259-293: returns (grad_h_gate, grad_h_up, h_mid | None, None)."""
+    if digest:
+        raise NotImplementedError("digest witnesses belong to the fused decoder block")
+    dg, du, hm = swiglu_backward_glu(grad_h_mid, h_gate, h_up, want_h_mid, inplace)
+    return dg, du, hm, None
+
+
 triton_silu_mul_quant = silu_mul_quant
 triton_dequant_swiglu_backward = dequant_swiglu_backward

@@ -87,6 +87,46 @@ int cpt_dequant_swiglu_backward(const void* grad_h_mid, const void* q_gate, cons
                                 int bits, int64_t group_size, void* grad_h_gate,
                                 void* grad_h_up, void* h_mid_hat, void* stream);
 
+/* ---------------- MFMA bf16 GEMMs (gfx950) ---------------- */
+
+/* Replaces the cuBLAS GEMMs the reference issues through F.linear / @
+ * (src/flashffn.py:1410-1439,1503-1587):  C[M, N] = A[M, K] . B[K, N]
+ * (+ A2[M, K2] . B2[K2, N] when a2 != NULL, same layouts), fp32 accumulate,
+ * bf16 in and out.  a_kmajor: A stored [M][lda] (1) or [K][lda] (0);
+ * b_kmajor: B stored [N][ldb] (1, the nn.Linear weight) or [K][ldb] (0).
+ * Pointers 16-byte aligned, leading dims multiples of 8, the contiguous
+ * extent of each operand a multiple of 8, N and ldc multiples of 4. */
+int cpt_gemm_bf16(const void* a, int64_t lda, int a_kmajor, const void* b, int64_t ldb,
+                  int b_kmajor, const void* a2, int64_t lda2, const void* b2, int64_t ldb2,
+                  int64_t K2, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Cache kinds of the fused FFN kernels. */
+enum { CPT_CACHE_NONE = 0, CPT_CACHE_BF16 = 1, CPT_CACHE_INT4 = 4, CPT_CACHE_INT8 = 8 };
+
+/* Fused forward of the gate/up projections (replaces F.linear(x, w_gate),
+ * F.linear(x, w_up) and K1, src/flashffn.py:1410-1433): one dual MFMA GEMM
+ * over x [n_tok, hidden] and w_gate, w_up [inter, hidden] whose epilogue
+ * rounds h_gate/h_up to bf16 and writes h_mid = SiLU(h_gate)*h_up (if
+ * h_mid != NULL) plus, by `cache`: nothing (NONE), h_gate/h_up bf16 (BF16),
+ * or the int4/int8 per-group absmax codes and fp16 scales of both (bit-equal
+ * to cpt_silu_mul_quant on the same bf16 values).  group_size in {32,64,128}. */
+int cpt_ffn_gate_up(const void* x, const void* w_gate, const void* w_up, int64_t n_tok,
+                    int64_t hidden, int64_t inter, int cache, int64_t group_size, void* h_mid,
+                    void* h_gate, void* h_up, void* q_gate, void* s_gate, void* q_up,
+                    void* s_up, void* stream);
+
+/* Fused backward of the down projection into the GLU (replaces gy @ w_down
+ * and K2, src/flashffn.py:1525-1533): grad_h_mid = bf16(grad_y @ w_down)
+ * with grad_y [n_tok, hidden], w_down [hidden, inter]; the epilogue reads the
+ * cache (BF16: c_gate/c_up are h_gate/h_up bf16; INT4/INT8: codes + fp16
+ * scales, dequantised through bf16) and writes grad_h_gate, grad_h_up and,
+ * if h_mid_hat != NULL, h_mid^ = SiLU(hg^)*hu^ (bit-equal to
+ * cpt_dequant_swiglu_backward on the same bf16 grad_h_mid). */
+int cpt_ffn_down_dgrad(const void* grad_y, const void* w_down, int64_t n_tok, int64_t hidden,
+                       int64_t inter, int cache, int64_t group_size, const void* c_gate,
+                       const void* s_gate, const void* c_up, const void* s_up, void* grad_h_gate,
+                       void* grad_h_up, void* h_mid_hat, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -79,10 +79,14 @@ def test_function_vs_oracle_fp32(device, config, mode):
         assert R.rel_frob(got[k].cpu(), ora[k]) < tol, k
 
 
+@pytest.mark.parametrize("config", ["all", "fullft", "none"])
 @pytest.mark.parametrize("mode", ["int4", "int8"])
-def test_fused_equals_unfused_bitwise(device, mode):
+def test_fused_equals_unfused_bitwise(device, mode, config):
+    """G3: with use_triton the codec runs fused (into the GEMM epilogues when
+    there are no gate/up adapters, else as the K1/K2 kernels); without it the
+    standalone quantise/dequantise kernels run.  Grads must be bitwise equal."""
     cpt = _cpt()
-    ps = _to(R.synthetic_param_set("all", H, D, RANK, S, seed=5), device)
+    ps = _to(R.synthetic_param_set(config, H, D, RANK, S, seed=5), device)
     gen = torch.Generator().manual_seed(13)
     x = torch.randn(N, H, generator=gen).to(torch.bfloat16).to(device)
     gy = torch.randn(N, H, generator=gen).to(torch.bfloat16).to(device)

@@ -1,0 +1,145 @@
+"""GPU tests of the MFMA GEMM engine and its fused FlashFFN epilogues.
+
+GEMM numerics are compared with a float32 reference of the same bf16 inputs
+(fp32 GEMMs run on the CPU: torch's bf16 batched products are avoided as a
+reference); the bar is the bf16 rounding of the output: elementwise
+|got - ref| <= 1e-2 |ref| + 1e-3 max|ref|.  Fused kernels must equal their
+unfused composition (the same GEMM engine with a plain bf16 store, then the
+standalone K1 / K2 kernel) bit for bit: the accumulation order is the same.
+"""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _cpt():
+    import compact_amd
+    from compact_amd import gemm
+    return compact_amd, gemm
+
+
+def ref_mm(a, b):
+    return a.float().cpu() @ b.float().cpu()
+
+
+def assert_gemm_close(got, ref):
+    got = got.float().cpu()
+    tol = 1e-2 * ref.abs() + 1e-3 * ref.abs().max()
+    bad = (got - ref).abs() > tol
+    assert not bad.any(), f"{int(bad.sum())} elements off; max err {(got - ref).abs().max():.3e}"
+
+
+def rnd(shape, seed, device, scale=1.0):
+    g = torch.Generator(device=device).manual_seed(seed)
+    return (torch.randn(*shape, device=device, generator=g) * scale).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("ak", [True, False])
+@pytest.mark.parametrize("bk", [True, False])
+@pytest.mark.parametrize("mnk", [(256, 256, 64), (300, 264, 136), (8, 512, 512),
+                                 (1000, 96, 1024), (512, 1024, 8)])
+def test_mm_layouts(device, ak, bk, mnk):
+    _, G = _cpt()
+    m, n, k = mnk
+    a = rnd((m, k), 1, device) if ak else rnd((k, m), 1, device).t()
+    b = rnd((n, k), 2, device).t() if bk else rnd((k, n), 2, device)
+    got = G.mm(a, b)
+    assert got.shape == (m, n)
+    assert_gemm_close(got, ref_mm(a, b))
+
+
+def test_mm_two_pairs(device):
+    _, G = _cpt()
+    a, b = rnd((384, 256), 3, device), rnd((256, 520), 4, device)
+    a2, b2 = rnd((384, 128), 5, device), rnd((128, 520), 6, device)
+    got = G.mm2(a, b, a2, b2)
+    assert_gemm_close(got, ref_mm(a, b) + ref_mm(a2, b2))
+
+
+def test_mm_deterministic_and_k_tail(device):
+    _, G = _cpt()
+    a, b = rnd((512, 200), 7, device), rnd((200, 256), 8, device)
+    c1, c2 = G.mm(a, b), G.mm(a, b)
+    assert torch.equal(c1, c2)
+    assert_gemm_close(c1, ref_mm(a, b))
+
+
+@pytest.mark.parametrize("cache,bits,group", [("int4", 4, 64), ("int8", 8, 128), ("int8", 8, 64),
+                                              ("int4", 4, 32), ("bf16", 0, 64),
+                                              ("none", 0, 64)])
+@pytest.mark.parametrize("n_tok,hid,inter", [(512, 256, 512), (300, 128, 384), (7, 64, 256)])
+def test_gate_up_fused_equals_unfused(device, cache, bits, group, n_tok, hid, inter):
+    cpt, G = _cpt()
+    from compact_amd import _lib
+    code = {"int4": _lib.CACHE_INT4, "int8": _lib.CACHE_INT8, "bf16": _lib.CACHE_BF16,
+            "none": _lib.CACHE_NONE}[cache]
+    x = rnd((n_tok, hid), 10, device)
+    wg = rnd((inter, hid), 11, device, 0.05)
+    wu = rnd((inter, hid), 12, device, 0.05)
+    hm, hg, hu, qg, sg, qu, su = G.ffn_gate_up(x, wg, wu, code, group)
+    hg_ref = G.linear(x, wg)
+    hu_ref = G.linear(x, wu)
+    assert_gemm_close(hg_ref, ref_mm(x, wg.t()))
+    hm_ref = cpt.silu_mul(hg_ref, hu_ref)
+    assert torch.equal(hm.view(torch.int16), hm_ref.view(torch.int16))
+    if cache == "bf16":
+        assert torch.equal(hg.view(torch.int16), hg_ref.view(torch.int16))
+        assert torch.equal(hu.view(torch.int16), hu_ref.view(torch.int16))
+    if bits:
+        _, rqg, rsg, rqu, rsu = cpt.silu_mul_quant(hg_ref, hu_ref, bits, group)
+        assert torch.equal(qg.view(torch.uint8), rqg.view(torch.uint8))
+        assert torch.equal(qu.view(torch.uint8), rqu.view(torch.uint8))
+        assert torch.equal(sg.view(torch.int16), rsg.view(torch.int16))
+        assert torch.equal(su.view(torch.int16), rsu.view(torch.int16))
+
+
+@pytest.mark.parametrize("cache,bits,group", [("int4", 4, 64), ("int8", 8, 128), ("int4", 4, 32),
+                                              ("bf16", 0, 64)])
+@pytest.mark.parametrize("want_h_mid", [True, False])
+@pytest.mark.parametrize("n_tok,hid,inter", [(512, 256, 512), (300, 128, 384)])
+def test_down_dgrad_fused_equals_unfused(device, cache, bits, group, want_h_mid, n_tok, hid,
+                                         inter):
+    cpt, G = _cpt()
+    from compact_amd import _lib
+    code = {"int4": _lib.CACHE_INT4, "int8": _lib.CACHE_INT8, "bf16": _lib.CACHE_BF16}[cache]
+    hg = rnd((n_tok, inter), 20, device, 3.0)
+    hu = rnd((n_tok, inter), 21, device, 2.0)
+    gy = rnd((n_tok, hid), 22, device)
+    wd = rnd((hid, inter), 23, device, 0.05)
+    if bits:
+        _, qg, sg, qu, su = cpt.silu_mul_quant(hg, hu, bits, group)
+        dg, du, hm = G.ffn_down_dgrad(gy, wd, code, group, qg, sg, qu, su, want_h_mid)
+        gmid = G.mm(gy, wd)
+        rdg, rdu, rhm = cpt.dequant_swiglu_backward(gmid, qg, sg, qu, su, bits, group,
+                                                    want_h_mid=want_h_mid)
+    else:
+        dg, du, hm = G.ffn_down_dgrad(gy, wd, code, group, hg, None, hu, None, want_h_mid)
+        gmid = G.mm(gy, wd)
+        rdg, rdu, rhm = cpt.swiglu_backward_glu(gmid, hg, hu, want_h_mid)
+    assert_gemm_close(gmid, ref_mm(gy, wd))
+    assert torch.equal(dg.view(torch.int16), rdg.view(torch.int16))
+    assert torch.equal(du.view(torch.int16), rdu.view(torch.int16))
+    if want_h_mid:
+        assert torch.equal(hm.view(torch.int16), rhm.view(torch.int16))
+    else:
+        assert hm is None
+
+
+def test_c2_shapes_gemm_numerics(device):
+    """The C2 GEMM shapes (8192 x 4096 x 11008), checked on sampled rows
+    against an fp32 product of the same bf16 operands."""
+    _, G = _cpt()
+    n, h, d = 8192, 4096, 11008
+    x = rnd((n, h), 30, device)
+    w = rnd((d, h), 31, device, 0.02)
+    y = G.linear(x, w)
+    rows = torch.arange(0, n, 997, device=device)
+    ref = x[rows].float() @ w.float().t()
+    assert_gemm_close(y[rows], ref.cpu())
+    gy = rnd((n, h), 32, device)
+    dw = G.mm(gy.t(), y)            # TN: [H, D] = gy^T @ y, both token-major
+    cols = torch.arange(0, d, 1009, device=device)
+    ref2 = gy.float().t() @ y[:, cols].float()
+    assert_gemm_close(dw[:, cols], ref2.cpu())

@@ -227,6 +227,19 @@ def test_glu_kernels_vs_oracle(device, dtype, numel):
     assert torch.equal(a, dg) and torch.equal(b, du) and torch.equal(c, hm2)
 
 
+def test_reference_named_wrappers(device):
+    """The reference-named entry points keep the reference's signatures."""
+    cpt = _lib()
+    g = torch.randn(64, 128, device=device).to(torch.bfloat16)
+    u = torch.randn(64, 128, device=device).to(torch.bfloat16)
+    dh = torch.randn(64, 128, device=device).to(torch.bfloat16)
+    assert torch.equal(cpt.triton_silu_mul(g, u), cpt.silu_mul(g, u))
+    out = cpt.triton_swiglu_backward_glu(dh, g, u, True, False)
+    assert len(out) == 4 and out[3] is None
+    with pytest.raises(NotImplementedError):
+        cpt.triton_silu_mul(g, u, digest=True)
+
+
 def test_glu_misaligned_view(device):
     cpt = _lib()
     g = torch.randn(1001, device=device).to(torch.bfloat16)
