@@ -12,6 +12,8 @@ from .kernels import (  # noqa: F401
     v3_quantize_group_absmax, v3_dequantize_group_absmax,
     triton_silu_mul, triton_swiglu_backward, triton_swiglu_backward_glu,
     triton_silu_mul_quant, triton_dequant_swiglu_backward,
+    outlier_select, v3_quantize_outlier, v3_dequantize_outlier, silu_mul_quant_outlier,
+    dequant_swiglu_backward_outlier,
 )
 from .flashffn import (  # noqa: F401
     FlashFFNv3Function, FlashFFNv3, make_v3_forward, _v3_extract_proj, _v3_proj_kind,

@@ -28,7 +28,15 @@ SIGNATURES = {
     "cpt_swiglu_backward_glu": [_P, _P, _P, _P, _P, _P, _L, _I, _P],
     "cpt_silu_mul_quant": [_P, _P, _L, _L, _I, _L, _P, _P, _P, _P, _P, _P],
     "cpt_dequant_swiglu_backward": [_P, _P, _P, _P, _P, _L, _L, _I, _L, _P, _P, _P, _P],
+    "cpt_outlier_select": [_P, _I, _L, _L, _L, _P, _P, _P, _P, _P],
+    "cpt_v3_quantize_outlier": [_P, _I, _L, _L, _I, _L, _P, _L, _P, _P, _P, _P],
+    "cpt_v3_dequantize_outlier": [_P, _P, _P, _L, _P, _L, _L, _I, _L, _P, _P],
+    "cpt_silu_mul_quant_outlier": [_P, _P, _L, _L, _I, _L, _P, _P, _L, _P, _P, _P, _P, _P, _P,
+                                   _P, _P],
+    "cpt_dequant_swiglu_backward_outlier": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _I,
+                                            _L, _P, _P, _P, _P],
     "cpt_gemm_bf16": [_P, _L, _I, _P, _L, _I, _P, _L, _P, _L, _L, _P, _L, _L, _L, _L, _P],
+    "cpt_gemm_bf16_ex": [_P, _L, _I, _P, _L, _I, _P, _L, _L, _L, _L, ctypes.c_float, _I, _I, _P, _P],
     "cpt_ffn_gate_up": [_P, _P, _P, _L, _L, _L, _I, _L, _P, _P, _P, _P, _P, _P, _P, _P],
     "cpt_ffn_down_dgrad": [_P, _P, _L, _L, _L, _I, _L, _P, _P, _P, _P, _P, _P, _P, _P],
 }

@@ -85,28 +85,71 @@ __device__ __forceinline__ void quant_chunk(const float v[8], bool valid, int64_
   store_codes8<BITS>(q, c, v, safe_scale(sh));
 }
 
+// Outlier channels (zero-and-store): columns with slot[col] >= 0 are copied
+// out as bf16 into out[row * k + slot] and zeroed before the codec sees them
+// (HyC-LoRA's outlier extraction, hyclora/operators/compress_function.py:111-143,
+// on the v3 per-group codec).  v holds 8 consecutive elements of one row.
+struct Outliers {
+  const int16_t* slot;   // [D], -1 for ordinary columns
+  uint16_t* out;         // [N, k] bf16
+  int64_t k;
+};
+
+__device__ __forceinline__ void extract_outliers8(float v[8], int64_t c, int64_t d,
+                                                  const Outliers& o, bool valid) {
+  if (!valid) return;
+  const int64_t e0 = c * 8;
+  const int64_t row = e0 / d, col = e0 - row * d;
+  const uint4 w = *reinterpret_cast<const uint4*>(o.slot + col);   // 8 x int16
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int sl = (int16_t)((ws[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+    if (sl >= 0) {
+      o.out[row * o.k + sl] = (uint16_t)f32_to_bf16_bits(v[j]);
+      v[j] = 0.0f;
+    }
+  }
+}
+
+// Overwrite dequantised values of outlier columns with the stored bf16 values
+// (compress_function.py:147-174).
+__device__ __forceinline__ void restore_outliers8(float v[8], int64_t c, int64_t d,
+                                                  const Outliers& o) {
+  const int64_t e0 = c * 8;
+  const int64_t row = e0 / d, col = e0 - row * d;
+  const uint4 w = *reinterpret_cast<const uint4*>(o.slot + col);
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int sl = (int16_t)((ws[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+    if (sl >= 0) v[j] = bf16_to_f32(o.out[row * o.k + sl]);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // standalone quantise, fast path (input dtype DT, group size 8*LPG)
 // ---------------------------------------------------------------------------
-template <int DT, int BITS, int LPG>
+template <int DT, int BITS, int LPG, bool OUTL>
 __global__ __launch_bounds__(kBlock) void quantize_fast_kernel(
     const void* __restrict__ t, uint8_t* __restrict__ q, uint16_t* __restrict__ s,
-    int64_t nchunk) {
+    int64_t nchunk, int64_t d, Outliers o) {
   const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   const bool valid = c < nchunk;
   float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   if (valid) Vec8<DT>::ld(t, c, v);
+  if (OUTL) extract_outliers8(v, c, d, o, valid);
   quant_chunk<BITS, LPG>(v, valid, c, q, s);
 }
 
 // ---------------------------------------------------------------------------
 // K1: h_mid = SiLU(g)*u (bf16) + codec of g and u, fast path
 // ---------------------------------------------------------------------------
-template <int BITS, int LPG>
+template <int BITS, int LPG, bool OUTL>
 __global__ __launch_bounds__(kBlock) void silu_mul_quant_kernel(
     const uint16_t* __restrict__ g, const uint16_t* __restrict__ u, uint16_t* __restrict__ hm,
     uint8_t* __restrict__ qg, uint16_t* __restrict__ sg, uint8_t* __restrict__ qu,
-    uint16_t* __restrict__ su, int64_t nchunk) {
+    uint16_t* __restrict__ su, int64_t nchunk, int64_t d, Outliers og, Outliers ou) {
   const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   const bool valid = c < nchunk;
   float gv[8] = {0, 0, 0, 0, 0, 0, 0, 0}, uv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
@@ -117,6 +160,10 @@ __global__ __launch_bounds__(kBlock) void silu_mul_quant_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) h[j] = silu_mul1(gv[j], uv[j]);  // src/flashffn.py:1212-1215
     Vec8<kBF16>::st(hm, c, h);
+  }
+  if (OUTL) {
+    extract_outliers8(gv, c, d, og, valid);
+    extract_outliers8(uv, c, d, ou, valid);
   }
   quant_chunk<BITS, LPG>(gv, valid, c, qg, sg);
   quant_chunk<BITS, LPG>(uv, valid, c, qu, su);
@@ -171,10 +218,10 @@ __global__ __launch_bounds__(kBlock) void quant_generic_kernel(
 // ---------------------------------------------------------------------------
 // dequantise: out = dtype(fp32(code) * fp32(scale))   (src/flashffn.py:1099-1110)
 // ---------------------------------------------------------------------------
-template <int BITS, int OUT_DT>
+template <int BITS, int OUT_DT, bool OUTL>
 __global__ __launch_bounds__(kBlock) void dequantize_fast_kernel(
     const uint8_t* __restrict__ q, const uint16_t* __restrict__ s, void* __restrict__ out,
-    int64_t nchunk, int gs_shift) {
+    int64_t nchunk, int gs_shift, int64_t d, Outliers o) {
   const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (c >= nchunk) return;
   float code[8], v[8];
@@ -182,6 +229,11 @@ __global__ __launch_bounds__(kBlock) void dequantize_fast_kernel(
   const float sc = f16_bits_to_f32(s[(c * 8) >> gs_shift]);
 #pragma unroll
   for (int j = 0; j < 8; ++j) v[j] = code[j] * sc;
+  if (OUTL) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = round_bf16(v[j]);
+    restore_outliers8(v, c, d, o);
+  }
   Vec8<OUT_DT>::st(out, c, v);
 }
 
@@ -205,15 +257,16 @@ __global__ __launch_bounds__(kBlock) void dequantize_generic_kernel(
 // ---------------------------------------------------------------------------
 // K2: dequantise through bf16, SwiGLU backward, optional h_mid^
 // ---------------------------------------------------------------------------
-template <int BITS, bool WANT_HM>
+template <int BITS, bool WANT_HM, bool OUTL>
 __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_kernel(
     const uint16_t* __restrict__ gmid, const uint8_t* __restrict__ qg,
     const uint16_t* __restrict__ sg, const uint8_t* __restrict__ qu,
     const uint16_t* __restrict__ su, uint16_t* __restrict__ dg, uint16_t* __restrict__ du,
-    uint16_t* __restrict__ hm, int64_t nchunk, int gs_shift) {
+    uint16_t* __restrict__ hm, int64_t nchunk, int gs_shift, int64_t d, Outliers outg,
+    Outliers outu) {
   const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (c >= nchunk) return;
-  float cg[8], cu[8], dh[8], og[8], ou[8], oh[8];
+  float cg[8], cu[8], dh[8], og[8], ou[8], oh[8], hg[8], hu[8];
   load_codes8<BITS>(qg, c, cg);
   load_codes8<BITS>(qu, c, cu);
   Vec8<kBF16>::ld(gmid, c, dh);
@@ -223,11 +276,18 @@ __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_kernel(
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     // bf16 round trip of the dequantised cache (src/flashffn.py:1251-1253)
-    const float hg = round_bf16(cg[j] * scg);
-    const float hu = round_bf16(cu[j] * scu);
+    hg[j] = round_bf16(cg[j] * scg);
+    hu[j] = round_bf16(cu[j] * scu);
+  }
+  if (OUTL) {
+    restore_outliers8(hg, c, d, outg);
+    restore_outliers8(hu, c, d, outu);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
     float hact;
-    swiglu_bwd1(dh[j], hg, hu, og[j], ou[j], hact);
-    oh[j] = hact * hu;  // src/flashffn.py:1298-1300
+    swiglu_bwd1(dh[j], hg[j], hu[j], og[j], ou[j], hact);
+    oh[j] = hact * hu[j];  // src/flashffn.py:1298-1300
   }
   Vec8<kBF16>::st(dg, c, og);
   Vec8<kBF16>::st(du, c, ou);
@@ -355,29 +415,29 @@ inline int check_codec(int64_t n, int64_t d, int bits, int64_t gs, bool need_pow
   return kOk;
 }
 
-template <int BITS, int LPG>
-void launch_quant_fast(int dt, const void* t, uint8_t* q, uint16_t* s, int64_t nchunk,
-                       hipStream_t st) {
+template <int BITS, int LPG, bool OUTL>
+void launch_quant_fast(int dt, const void* t, uint8_t* q, uint16_t* s, int64_t nchunk, int64_t d,
+                       Outliers o, hipStream_t st) {
   const unsigned grid = grid_for(nchunk);
   if (dt == kBF16)
-    quantize_fast_kernel<kBF16, BITS, LPG><<<grid, kBlock, 0, st>>>(t, q, s, nchunk);
+    quantize_fast_kernel<kBF16, BITS, LPG, OUTL><<<grid, kBlock, 0, st>>>(t, q, s, nchunk, d, o);
   else if (dt == kF16)
-    quantize_fast_kernel<kF16, BITS, LPG><<<grid, kBlock, 0, st>>>(t, q, s, nchunk);
+    quantize_fast_kernel<kF16, BITS, LPG, OUTL><<<grid, kBlock, 0, st>>>(t, q, s, nchunk, d, o);
   else
-    quantize_fast_kernel<kF32, BITS, LPG><<<grid, kBlock, 0, st>>>(t, q, s, nchunk);
+    quantize_fast_kernel<kF32, BITS, LPG, OUTL><<<grid, kBlock, 0, st>>>(t, q, s, nchunk, d, o);
 }
 
-template <int BITS>
+template <int BITS, bool OUTL>
 void launch_quant_fast_lpg(int dt, int lpg, const void* t, uint8_t* q, uint16_t* s,
-                           int64_t nchunk, hipStream_t st) {
+                           int64_t nchunk, int64_t d, Outliers o, hipStream_t st) {
   switch (lpg) {
-    case 1: launch_quant_fast<BITS, 1>(dt, t, q, s, nchunk, st); break;
-    case 2: launch_quant_fast<BITS, 2>(dt, t, q, s, nchunk, st); break;
-    case 4: launch_quant_fast<BITS, 4>(dt, t, q, s, nchunk, st); break;
-    case 8: launch_quant_fast<BITS, 8>(dt, t, q, s, nchunk, st); break;
-    case 16: launch_quant_fast<BITS, 16>(dt, t, q, s, nchunk, st); break;
-    case 32: launch_quant_fast<BITS, 32>(dt, t, q, s, nchunk, st); break;
-    default: launch_quant_fast<BITS, 64>(dt, t, q, s, nchunk, st); break;
+    case 1: launch_quant_fast<BITS, 1, OUTL>(dt, t, q, s, nchunk, d, o, st); break;
+    case 2: launch_quant_fast<BITS, 2, OUTL>(dt, t, q, s, nchunk, d, o, st); break;
+    case 4: launch_quant_fast<BITS, 4, OUTL>(dt, t, q, s, nchunk, d, o, st); break;
+    case 8: launch_quant_fast<BITS, 8, OUTL>(dt, t, q, s, nchunk, d, o, st); break;
+    case 16: launch_quant_fast<BITS, 16, OUTL>(dt, t, q, s, nchunk, d, o, st); break;
+    case 32: launch_quant_fast<BITS, 32, OUTL>(dt, t, q, s, nchunk, d, o, st); break;
+    default: launch_quant_fast<BITS, 64, OUTL>(dt, t, q, s, nchunk, d, o, st); break;
   }
 }
 
@@ -404,24 +464,26 @@ void launch_quant_generic(int dt, bool glu, const void* g, const void* u, void* 
   }
 }
 
-template <int BITS, int LPG>
+template <int BITS, int LPG, bool OUTL>
 void launch_k1(const uint16_t* g, const uint16_t* u, uint16_t* hm, uint8_t* qg, uint16_t* sg,
-               uint8_t* qu, uint16_t* su, int64_t nchunk, hipStream_t st) {
-  silu_mul_quant_kernel<BITS, LPG>
-      <<<grid_for(nchunk), kBlock, 0, st>>>(g, u, hm, qg, sg, qu, su, nchunk);
+               uint8_t* qu, uint16_t* su, int64_t nchunk, int64_t d, Outliers og, Outliers ou,
+               hipStream_t st) {
+  silu_mul_quant_kernel<BITS, LPG, OUTL>
+      <<<grid_for(nchunk), kBlock, 0, st>>>(g, u, hm, qg, sg, qu, su, nchunk, d, og, ou);
 }
 
-template <int BITS>
+template <int BITS, bool OUTL>
 void launch_k1_lpg(int lpg, const uint16_t* g, const uint16_t* u, uint16_t* hm, uint8_t* qg,
-                   uint16_t* sg, uint8_t* qu, uint16_t* su, int64_t nchunk, hipStream_t st) {
+                   uint16_t* sg, uint8_t* qu, uint16_t* su, int64_t nchunk, int64_t d,
+                   Outliers og, Outliers ou, hipStream_t st) {
   switch (lpg) {
-    case 1: launch_k1<BITS, 1>(g, u, hm, qg, sg, qu, su, nchunk, st); break;
-    case 2: launch_k1<BITS, 2>(g, u, hm, qg, sg, qu, su, nchunk, st); break;
-    case 4: launch_k1<BITS, 4>(g, u, hm, qg, sg, qu, su, nchunk, st); break;
-    case 8: launch_k1<BITS, 8>(g, u, hm, qg, sg, qu, su, nchunk, st); break;
-    case 16: launch_k1<BITS, 16>(g, u, hm, qg, sg, qu, su, nchunk, st); break;
-    case 32: launch_k1<BITS, 32>(g, u, hm, qg, sg, qu, su, nchunk, st); break;
-    default: launch_k1<BITS, 64>(g, u, hm, qg, sg, qu, su, nchunk, st); break;
+    case 1: launch_k1<BITS, 1, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, d, og, ou, st); break;
+    case 2: launch_k1<BITS, 2, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, d, og, ou, st); break;
+    case 4: launch_k1<BITS, 4, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, d, og, ou, st); break;
+    case 8: launch_k1<BITS, 8, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, d, og, ou, st); break;
+    case 16: launch_k1<BITS, 16, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, d, og, ou, st); break;
+    case 32: launch_k1<BITS, 32, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, d, og, ou, st); break;
+    default: launch_k1<BITS, 64, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, d, og, ou, st); break;
   }
 }
 
@@ -457,6 +519,102 @@ inline int glu_dispatch(int op, int dt, const void* a, const void* g, const void
   return launch_status();
 }
 
+// ---------------------------------------------------------------------------
+// outlier channel selection: the k columns with the largest L2 norm over all
+// rows (HyC-LoRA's get_statistics_channel_base, compress_function.py:80-88),
+// ties to the lower column index, slots in ascending column order.
+// Deterministic: fp64 sums in a fixed order.
+// ---------------------------------------------------------------------------
+constexpr int kColRows = 256;   // rows per partial sum
+
+// partial[chunk][col] = sum over rows [chunk*kColRows, +kColRows) of t^2 (fp64)
+template <int DT>
+__global__ __launch_bounds__(kBlock) void colsumsq_partial_kernel(
+    const void* __restrict__ t, double* __restrict__ partial, int64_t n, int64_t d) {
+  using E = Elem<DT>;
+  const int64_t col = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.y * kColRows;
+  if (col >= d) return;
+  const typename E::T* p = reinterpret_cast<const typename E::T*>(t);
+  double acc = 0.0;
+  const int64_t r1 = r0 + kColRows < n ? r0 + kColRows : n;
+  for (int64_t r = r0; r < r1; ++r) {
+    const double v = (double)E::ld(p + r * d + col);
+    acc += v * v;
+  }
+  partial[blockIdx.y * d + col] = acc;
+}
+
+__global__ __launch_bounds__(kBlock) void colsumsq_reduce_kernel(
+    const double* __restrict__ partial, double* __restrict__ sumsq, int64_t d, int chunks) {
+  const int64_t col = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (col >= d) return;
+  double acc = 0.0;
+  for (int c = 0; c < chunks; ++c) acc += partial[(int64_t)c * d + col];
+  sumsq[col] = acc;
+}
+
+// flag[col] = 1 iff col ranks among the top k: rank = #{c' : v[c'] > v[col] or
+// (v[c'] == v[col] and c' < col)}.  The values stream through LDS in tiles.
+__global__ __launch_bounds__(kBlock) void outlier_rank_kernel(const double* __restrict__ v,
+                                                              int16_t* __restrict__ flag,
+                                                              int64_t d, int64_t k) {
+  __shared__ double tile[2048];
+  const int64_t col = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const double mine = col < d ? v[col] : 0.0;
+  int64_t rank = 0;
+  for (int64_t base = 0; base < d; base += 2048) {
+    const int64_t len = d - base < 2048 ? d - base : 2048;
+    __syncthreads();
+    for (int64_t i = threadIdx.x; i < len; i += kBlock) tile[i] = v[base + i];
+    __syncthreads();
+    if (col < d) {
+      for (int64_t i = 0; i < len; ++i) {
+        const double o = tile[i];
+        rank += (o > mine) || (o == mine && base + i < col);
+      }
+    }
+  }
+  if (col < d) flag[col] = rank < k ? 1 : 0;
+}
+
+// One block: slot[col] = (selected ? number of selected columns before col : -1),
+// idx[slot] = col.  Each thread scans a contiguous segment, in place.
+__global__ __launch_bounds__(1024) void outlier_slots_kernel(int16_t* __restrict__ slot,
+                                                             int32_t* __restrict__ idx,
+                                                             int64_t d) {
+  __shared__ int32_t counts[1024];
+  const int tid = threadIdx.x;
+  const int64_t seg = (d + 1023) / 1024;
+  const int64_t c0 = tid * seg, c1 = c0 + seg < d ? c0 + seg : d;
+  int32_t cnt = 0;
+  for (int64_t c = c0; c < c1; ++c) cnt += slot[c];
+  counts[tid] = cnt;
+  __syncthreads();
+  if (tid == 0) {
+    int32_t run = 0;
+    for (int i = 0; i < 1024; ++i) {
+      const int32_t x = counts[i];
+      counts[i] = run;
+      run += x;
+    }
+  }
+  __syncthreads();
+  int32_t pos = counts[tid];
+  for (int64_t c = c0; c < c1; ++c) {
+    if (slot[c]) {
+      idx[pos] = (int32_t)c;
+      slot[c] = (int16_t)pos++;
+    } else {
+      slot[c] = -1;
+    }
+  }
+}
+
+inline bool outlier_args_ok(const void* slot, const void* out, int64_t k, int64_t d) {
+  return slot && aligned16(slot) && (d % 8) == 0 && k >= 0 && k < 32768 && (k == 0 || out);
+}
+
 }  // namespace cpt
 
 using namespace cpt;
@@ -479,8 +637,8 @@ int cpt_v3_quantize_group_absmax(const void* t, int dtype, int64_t n, int64_t d,
                     aligned16(t) && ((uintptr_t)payload & 7u) == 0;
   if (fast) {
     const int lpg = (int)(group_size / 8);
-    if (bits == 4) launch_quant_fast_lpg<4>(dtype, lpg, t, q, s, n_el / 8, st);
-    else launch_quant_fast_lpg<8>(dtype, lpg, t, q, s, n_el / 8, st);
+    if (bits == 4) launch_quant_fast_lpg<4, false>(dtype, lpg, t, q, s, n_el / 8, d, Outliers{}, st);
+    else launch_quant_fast_lpg<8, false>(dtype, lpg, t, q, s, n_el / 8, d, Outliers{}, st);
   } else {
     if (bits == 4) launch_quant_generic<4>(dtype, false, t, t, nullptr, q, s, q, s, n_el, group_size, st);
     else launch_quant_generic<8>(dtype, false, t, t, nullptr, q, s, q, s, n_el, group_size, st);
@@ -506,7 +664,7 @@ int cpt_v3_dequantize_group_absmax(const void* payload, const void* scales, int6
     const int64_t nchunk = n_el / 8;
     const int sh = log2_exact(group_size);
     const unsigned grid = grid_for(nchunk);
-#define CPT_DQ(B, O) dequantize_fast_kernel<B, O><<<grid, kBlock, 0, st>>>(q, s, out, nchunk, sh)
+#define CPT_DQ(B, O) dequantize_fast_kernel<B, O, false><<<grid, kBlock, 0, st>>>(q, s, out, nchunk, sh, d, Outliers{})
     if (bits == 4) {
       if (out_dtype == kBF16) CPT_DQ(4, kBF16); else if (out_dtype == kF16) CPT_DQ(4, kF16); else CPT_DQ(4, kF32);
     } else {
@@ -566,8 +724,8 @@ int cpt_silu_mul_quant(const void* h_gate, const void* h_up, int64_t n, int64_t 
                     aligned16(hm) && ((uintptr_t)qg & 7u) == 0 && ((uintptr_t)qu & 7u) == 0;
   if (fast) {
     const int lpg = (int)(group_size / 8);
-    if (bits == 4) launch_k1_lpg<4>(lpg, g, u, hm, qg, sg, qu, su, n_el / 8, st);
-    else launch_k1_lpg<8>(lpg, g, u, hm, qg, sg, qu, su, n_el / 8, st);
+    if (bits == 4) launch_k1_lpg<4, false>(lpg, g, u, hm, qg, sg, qu, su, n_el / 8, d, Outliers{}, Outliers{}, st);
+    else launch_k1_lpg<8, false>(lpg, g, u, hm, qg, sg, qu, su, n_el / 8, d, Outliers{}, Outliers{}, st);
   } else {
     if (bits == 4) launch_quant_generic<4>(kBF16, true, g, u, hm, qg, sg, qu, su, n_el, group_size, st);
     else launch_quant_generic<8>(kBF16, true, g, u, hm, qg, sg, qu, su, n_el, group_size, st);
@@ -601,7 +759,7 @@ int cpt_dequant_swiglu_backward(const void* grad_h_mid, const void* q_gate, cons
     const int64_t nchunk = n_el / 8;
     const unsigned grid = grid_for(nchunk);
     const int sh = log2_exact(group_size);
-#define CPT_K2(B, W) dequant_swiglu_bwd_kernel<B, W><<<grid, kBlock, 0, st>>>(gm, qg, sg, qu, su, og, ou, oh, nchunk, sh)
+#define CPT_K2(B, W) dequant_swiglu_bwd_kernel<B, W, false><<<grid, kBlock, 0, st>>>(gm, qg, sg, qu, su, og, ou, oh, nchunk, sh, d, Outliers{}, Outliers{})
     if (bits == 4) { if (oh) CPT_K2(4, true); else CPT_K2(4, false); }
     else { if (oh) CPT_K2(8, true); else CPT_K2(8, false); }
 #undef CPT_K2
@@ -612,6 +770,133 @@ int cpt_dequant_swiglu_backward(const void* grad_h_mid, const void* q_gate, cons
     else { if (oh) CPT_K2G(8, true); else CPT_K2G(8, false); }
 #undef CPT_K2G
   }
+  return launch_status();
+}
+
+int cpt_outlier_select(const void* t, int dtype, int64_t n, int64_t d, int64_t k,
+                       void* partial, void* sumsq, void* slot, void* idx, void* stream) {
+  if (n < 0 || d < 0 || k < 0 || k > d || k >= 32768) return kErrShape;
+  if (dtype != kF32 && dtype != kF16 && dtype != kBF16) return kErrDType;
+  if (d == 0) return kOk;
+  if (!slot || !sumsq || (n > 0 && (!t || !partial)) || (k > 0 && !idx)) return kErrShape;
+  hipStream_t st = (hipStream_t)stream;
+  const int chunks = (int)((n + kColRows - 1) / kColRows);
+  const unsigned gx = grid_for(d);
+  if (chunks > 0) {
+    dim3 grid(gx, (unsigned)chunks);
+    if (dtype == kBF16) colsumsq_partial_kernel<kBF16><<<grid, kBlock, 0, st>>>(t, (double*)partial, n, d);
+    else if (dtype == kF16) colsumsq_partial_kernel<kF16><<<grid, kBlock, 0, st>>>(t, (double*)partial, n, d);
+    else colsumsq_partial_kernel<kF32><<<grid, kBlock, 0, st>>>(t, (double*)partial, n, d);
+  }
+  colsumsq_reduce_kernel<<<gx, kBlock, 0, st>>>((const double*)partial, (double*)sumsq, d, chunks);
+  outlier_rank_kernel<<<gx, kBlock, 0, st>>>((const double*)sumsq, (int16_t*)slot, d, k);
+  outlier_slots_kernel<<<1, 1024, 0, st>>>((int16_t*)slot, (int32_t*)idx, d);
+  return launch_status();
+}
+
+int cpt_v3_quantize_outlier(const void* t, int dtype, int64_t n, int64_t d, int bits,
+                            int64_t group_size, const void* slot, int64_t k, void* outliers,
+                            void* payload, void* scales, void* stream) {
+  int rc = check_codec(n, d, bits, group_size, true);
+  if (rc) return rc;
+  if (dtype != kF32 && dtype != kF16 && dtype != kBF16) return kErrDType;
+  if (n * d == 0) return kOk;
+  if (!t || !payload || !scales) return kErrShape;
+  if (group_size < 8 || group_size > 512 || !aligned16(t) || ((uintptr_t)payload & 7) ||
+      !outlier_args_ok(slot, outliers, k, d))
+    return kErrAlign;
+  Outliers o{(const int16_t*)slot, (uint16_t*)outliers, k};
+  hipStream_t st = (hipStream_t)stream;
+  const int lpg = (int)(group_size / 8);
+  if (bits == 4) launch_quant_fast_lpg<4, true>(dtype, lpg, t, (uint8_t*)payload, (uint16_t*)scales, n * d / 8, d, o, st);
+  else launch_quant_fast_lpg<8, true>(dtype, lpg, t, (uint8_t*)payload, (uint16_t*)scales, n * d / 8, d, o, st);
+  return launch_status();
+}
+
+int cpt_v3_dequantize_outlier(const void* payload, const void* scales, const void* slot, int64_t k,
+                              const void* outliers, int64_t n, int64_t d, int bits,
+                              int64_t group_size, void* out, void* stream) {
+  int rc = check_codec(n, d, bits, group_size, true);
+  if (rc) return rc;
+  if (n * d == 0) return kOk;
+  if (!payload || !scales || !out) return kErrShape;
+  if (group_size < 8 || !aligned16(out) || ((uintptr_t)payload & 7) ||
+      !outlier_args_ok(slot, outliers, k, d))
+    return kErrAlign;
+  Outliers o{(const int16_t*)slot, (uint16_t*)outliers, k};
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t nchunk = n * d / 8;
+  const int sh = log2_exact(group_size);
+  if (bits == 4)
+    dequantize_fast_kernel<4, kBF16, true><<<grid_for(nchunk), kBlock, 0, st>>>((const uint8_t*)payload, (const uint16_t*)scales, out, nchunk, sh, d, o);
+  else
+    dequantize_fast_kernel<8, kBF16, true><<<grid_for(nchunk), kBlock, 0, st>>>((const uint8_t*)payload, (const uint16_t*)scales, out, nchunk, sh, d, o);
+  return launch_status();
+}
+
+int cpt_silu_mul_quant_outlier(const void* h_gate, const void* h_up, int64_t n, int64_t d,
+                               int bits, int64_t group_size, const void* slot_gate,
+                               const void* slot_up, int64_t k, void* h_mid, void* q_gate,
+                               void* s_gate, void* o_gate, void* q_up, void* s_up, void* o_up,
+                               void* stream) {
+  int rc = check_codec(n, d, bits, group_size, true);
+  if (rc) return rc;
+  if (n * d == 0) return kOk;
+  if (!h_gate || !h_up || !h_mid || !q_gate || !s_gate || !q_up || !s_up) return kErrShape;
+  if (group_size < 8 || group_size > 512 || !aligned16(h_gate) || !aligned16(h_up) ||
+      !aligned16(h_mid) || ((uintptr_t)q_gate & 7) || ((uintptr_t)q_up & 7) ||
+      !outlier_args_ok(slot_gate, o_gate, k, d) || !outlier_args_ok(slot_up, o_up, k, d))
+    return kErrAlign;
+  Outliers og{(const int16_t*)slot_gate, (uint16_t*)o_gate, k};
+  Outliers ou{(const int16_t*)slot_up, (uint16_t*)o_up, k};
+  hipStream_t st = (hipStream_t)stream;
+  const int lpg = (int)(group_size / 8);
+  if (bits == 4)
+    launch_k1_lpg<4, true>(lpg, (const uint16_t*)h_gate, (const uint16_t*)h_up, (uint16_t*)h_mid,
+                           (uint8_t*)q_gate, (uint16_t*)s_gate, (uint8_t*)q_up, (uint16_t*)s_up,
+                           n * d / 8, d, og, ou, st);
+  else
+    launch_k1_lpg<8, true>(lpg, (const uint16_t*)h_gate, (const uint16_t*)h_up, (uint16_t*)h_mid,
+                           (uint8_t*)q_gate, (uint16_t*)s_gate, (uint8_t*)q_up, (uint16_t*)s_up,
+                           n * d / 8, d, og, ou, st);
+  return launch_status();
+}
+
+int cpt_dequant_swiglu_backward_outlier(const void* grad_h_mid, const void* q_gate,
+                                        const void* s_gate, const void* slot_gate,
+                                        const void* o_gate, const void* q_up, const void* s_up,
+                                        const void* slot_up, const void* o_up, int64_t k,
+                                        int64_t n, int64_t d, int bits, int64_t group_size,
+                                        void* grad_h_gate, void* grad_h_up, void* h_mid_hat,
+                                        void* stream) {
+  int rc = check_codec(n, d, bits, group_size, true);
+  if (rc) return rc;
+  if (n * d == 0) return kOk;
+  if (!grad_h_mid || !q_gate || !s_gate || !q_up || !s_up || !grad_h_gate || !grad_h_up)
+    return kErrShape;
+  if (group_size < 8 || !aligned16(grad_h_mid) || !aligned16(grad_h_gate) ||
+      !aligned16(grad_h_up) || (h_mid_hat && !aligned16(h_mid_hat)) ||
+      ((uintptr_t)q_gate & 7) || ((uintptr_t)q_up & 7) ||
+      !outlier_args_ok(slot_gate, o_gate, k, d) || !outlier_args_ok(slot_up, o_up, k, d))
+    return kErrAlign;
+  Outliers og{(const int16_t*)slot_gate, (uint16_t*)o_gate, k};
+  Outliers ou{(const int16_t*)slot_up, (uint16_t*)o_up, k};
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t nchunk = n * d / 8;
+  const unsigned grid = grid_for(nchunk);
+  const int sh = log2_exact(group_size);
+  const uint16_t* gm = (const uint16_t*)grad_h_mid;
+  const uint8_t* qg = (const uint8_t*)q_gate;
+  const uint8_t* qu = (const uint8_t*)q_up;
+  const uint16_t* sg = (const uint16_t*)s_gate;
+  const uint16_t* su = (const uint16_t*)s_up;
+  uint16_t* dg = (uint16_t*)grad_h_gate;
+  uint16_t* du = (uint16_t*)grad_h_up;
+  uint16_t* hm = (uint16_t*)h_mid_hat;
+#define CPT_K2O(B, W) dequant_swiglu_bwd_kernel<B, W, true><<<grid, kBlock, 0, st>>>(gm, qg, sg, qu, su, dg, du, hm, nchunk, sh, d, og, ou)
+  if (bits == 4) { if (hm) CPT_K2O(4, true); else CPT_K2O(4, false); }
+  else { if (hm) CPT_K2O(8, true); else CPT_K2O(8, false); }
+#undef CPT_K2O
   return launch_status();
 }
 

@@ -137,9 +137,13 @@ struct KArgs {
   const uint16_t* b_up;    // dual gate/up GEMM: up weight (layout of b[0])
   int64_t M, N;            // output extent; dual: N = 2 * D (virtual columns)
   int tiles_m, tiles_n;
+  int ksplit;              // >1: split-K, block b works on k-tiles [s*kts, (s+1)*kts)
+  int kt_per_split;
   // plain output
   uint16_t* C;
   int64_t ldc;
+  float alpha;             // EPI_ADD scale
+  float* ws;               // EPI_F32: fp32 partials [ksplit][M][N]
   // FlashFFN epilogues
   int64_t D;               // d_ff (inter)
   uint16_t* h_mid;         // F1 out (may be null)
@@ -154,7 +158,7 @@ struct KArgs {
   uint16_t* h_mid_hat;     // B1 out (may be null)
 };
 
-enum Epi { EPI_STORE = 0, EPI_GLU = 1, EPI_DGLU = 2 };
+enum Epi { EPI_STORE = 0, EPI_GLU = 1, EPI_DGLU = 2, EPI_ADD = 3, EPI_F32 = 4 };
 enum Cache { CACHE_NONE = 0, CACHE_BF16 = 1, CACHE_INT4 = 4, CACHE_INT8 = 8 };
 
 // ---------------------------------------------------------------------------
@@ -355,7 +359,7 @@ __device__ __forceinline__ void sched_interleave_load_read() {
 // ended it, so one barrier per k-tile suffices.
 template <bool AK, bool BKM, bool DUAL>
 __device__ __forceinline__ void mainloop(const KArgs& A, int64_t m0, int64_t n0, uint16_t* lds,
-                                         Acc& acc) {
+                                         Acc& acc, int kt0 = 0, int kt_end = -1) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave & 1, wm = wave >> 1;
@@ -368,8 +372,11 @@ __device__ __forceinline__ void mainloop(const KArgs& A, int64_t m0, int64_t n0,
 
   Loader<AK, BKM, DUAL> L;
   L.init(A, m0, n0, tid);
-  int nk = L.nk0;
-  if (A.npairs > 1) nk += (int)((A.K[1] + BK - 1) / BK);
+  int nk_all = L.nk0;
+  if (A.npairs > 1) nk_all += (int)((A.K[1] + BK - 1) / BK);
+  if (kt_end < 0 || kt_end > nk_all) kt_end = nk_all;
+  const int nk = kt_end - kt0;       // k-tiles of this block
+  if (nk <= 0) return;               // empty split: the accumulators stay zero
 
   uint4 va[8], vb[8];
   auto store = [&](int stage) {
@@ -379,7 +386,7 @@ __device__ __forceinline__ void mainloop(const KArgs& A, int64_t m0, int64_t n0,
     if (BKM || DUAL) sstore_kmajor(sb, tid, vb); else sstore_mnmajor(sb, tid, vb);
   };
 
-  L.issue(0, tid, va, vb);
+  L.issue(kt0, tid, va, vb);
   store(0);
   __syncthreads();
   Frags f0, f1;
@@ -387,7 +394,7 @@ __device__ __forceinline__ void mainloop(const KArgs& A, int64_t m0, int64_t n0,
   for (int kt = 0; kt + 1 < nk; ++kt) {
     const int stage = kt & 1;
     const uint16_t* base = lds + stage * 2 * TILE_ELEMS;
-    L.issue(kt + 1, tid, va, vb);
+    L.issue(kt0 + kt + 1, tid, va, vb);
     read_frags(base, wn, wm, lane, 1, f1);
     mfma_range<0, 16>(f0, acc);
     sched_interleave_load_read<8>();
@@ -449,6 +456,68 @@ __device__ __forceinline__ void epi_store(const KArgs& A, const Acc& acc, int64_
       }
     }
   }
+}
+
+// ---------------------------------------------------------------------------
+// epilogue ADD: C = bf16(C + bf16(alpha * bf16(acc)))   (PEFT's h + s * B(A(x))
+// in bf16: the product, the scaling and the sum are each rounded)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void epi_add(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wn = wave & 1, wm = wave >> 1;
+  static_for<0, 4>([&](auto j) {
+    const int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
+    static_for<0, 4>([&](auto i) {
+      static_for<0, 4>([&](auto g) {
+        const int64_t n = n0 + wn * 128 + i * 32 + g * 8 + (lane >> 5) * 4;
+        if (m >= A.M) return;
+        for (int e = 0; e < 4; ++e) {
+          if (n + e >= A.N) break;
+          uint16_t* cp = A.C + m * A.ldc + n + e;
+          const float t = round_bf16(A.alpha * round_bf16(acc.v[i][j][g * 4 + e]));
+          *cp = (uint16_t)f32_to_bf16_bits(bf16_to_f32(*cp) + t);
+        }
+      });
+    });
+  });
+}
+
+// epilogue F32: fp32 partial of this split into ws[split][M][N]
+__device__ __forceinline__ void epi_f32(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0,
+                                        int split) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wn = wave & 1, wm = wave >> 1;
+  float* base = A.ws + (int64_t)split * A.M * A.N;
+  static_for<0, 4>([&](auto j) {
+    const int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
+    static_for<0, 4>([&](auto i) {
+      static_for<0, 4>([&](auto g) {
+        const int64_t n = n0 + wn * 128 + i * 32 + g * 8 + (lane >> 5) * 4;
+        if (m >= A.M) return;
+        if (n + 3 < A.N && (A.N & 3) == 0) {
+          *reinterpret_cast<float4*>(base + m * A.N + n) =
+              make_float4(acc.v[i][j][g * 4 + 0], acc.v[i][j][g * 4 + 1], acc.v[i][j][g * 4 + 2],
+                          acc.v[i][j][g * 4 + 3]);
+        } else {
+          for (int e = 0; e < 4; ++e)
+            if (n + e < A.N) base[m * A.N + n + e] = acc.v[i][j][g * 4 + e];
+        }
+      });
+    });
+  });
+}
+
+// out[m, n] = bf16(alpha * sum_s ws[s][m][n])  (split-K reduction, fixed order)
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws,
+                                                            uint16_t* __restrict__ out, int64_t M,
+                                                            int64_t N, int64_t ldc, int splits,
+                                                            float alpha) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= M * N) return;
+  float sum = 0.0f;
+  for (int s = 0; s < splits; ++s) sum += ws[(int64_t)s * M * N + e];
+  const int64_t m = e / N, n = e - m * N;
+  out[m * ldc + n] = (uint16_t)f32_to_bf16_bits(alpha * sum);
 }
 
 // ---------------------------------------------------------------------------
@@ -710,14 +779,30 @@ __device__ __forceinline__ void epi_dglu(const KArgs& A, const Acc& acc, int64_t
 template <bool AK, bool BKM, int EPI, int CACHE, int GS>
 __global__ __launch_bounds__(NTHR, 1) void gemm_kernel(KArgs A) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  int tm, tn;
-  tile_coords(A.tiles_m, A.tiles_n, tm, tn);
+  int tm, tn, split = 0;
+  if (A.ksplit > 1) {
+    const int tiles = A.tiles_m * A.tiles_n;
+    const int t = blockIdx.x % tiles;
+    split = blockIdx.x / tiles;
+    tm = t % A.tiles_m;
+    tn = t / A.tiles_m;
+  } else {
+    tile_coords(A.tiles_m, A.tiles_n, tm, tn);
+  }
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   Acc acc;
-  mainloop<AK, BKM, EPI == EPI_GLU>(A, m0, n0, lds, acc);
+  if constexpr (EPI == EPI_F32) {
+    mainloop<AK, BKM, false>(A, m0, n0, lds, acc, split * A.kt_per_split,
+                             (split + 1) * A.kt_per_split);
+    epi_f32(A, acc, m0, n0, split);
+    return;
+  } else {
+    mainloop<AK, BKM, EPI == EPI_GLU>(A, m0, n0, lds, acc);
+  }
   if constexpr (EPI == EPI_STORE) epi_store(A, acc, m0, n0);
+  else if constexpr (EPI == EPI_ADD) epi_add(A, acc, m0, n0);
   else if constexpr (EPI == EPI_GLU) epi_glu<CACHE, GS>(A, acc, m0, n0, lds);
-  else epi_dglu<CACHE, GS>(A, acc, m0, n0);
+  else if constexpr (EPI == EPI_DGLU) epi_dglu<CACHE, GS>(A, acc, m0, n0);
 }
 
 // ---------------------------------------------------------------------------
@@ -735,7 +820,7 @@ int launch(KArgs& A, hipStream_t st) {
       return kErrLaunch;
     attr_set = true;
   }
-  const int64_t tiles = (int64_t)A.tiles_m * A.tiles_n;
+  const int64_t tiles = (int64_t)A.tiles_m * A.tiles_n * (A.ksplit > 1 ? A.ksplit : 1);
   if (tiles <= 0) return kOk;
   if (tiles > 0x7FFFFFFF) return kErrTooLarge;
   hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(NTHR), LDS_BYTES, st, A);
@@ -824,6 +909,61 @@ int cpt_gemm_bf16(const void* a, int64_t lda, int a_kmajor, const void* b, int64
   if (a_kmajor && !b_kmajor) return launch<true, false, EPI_STORE, 0, 0>(A, st);
   if (!a_kmajor && !b_kmajor) return launch<false, false, EPI_STORE, 0, 0>(A, st);
   return launch<false, true, EPI_STORE, 0, 0>(A, st);
+}
+
+int cpt_gemm_bf16_ex(const void* a, int64_t lda, int a_kmajor, const void* b, int64_t ldb,
+                     int b_kmajor, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                     float alpha, int mode, int splits, void* workspace, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return kErrShape;
+  if (mode < 0 || mode > 2) return kErrShape;
+  if (M == 0 || N == 0) return kOk;
+  if (!c || (mode != 1 && (!al16(c) || (ldc & 3))) || ldc < N) return kErrAlign;
+  if (K > 0 && (!operand_ok(a, lda, a_kmajor, M, K) || !operand_ok(b, ldb, b_kmajor, N, K)))
+    return kErrAlign;
+  if (!operand_fits(lda, a_kmajor, M, K) || !operand_fits(ldb, b_kmajor, N, K))
+    return kErrTooLarge;
+  KArgs A{};
+  A.a[0] = {(const uint16_t*)a, lda};
+  A.b[0] = {(const uint16_t*)b, ldb};
+  A.K[0] = K;
+  A.npairs = 1;
+  A.M = M; A.N = N;
+  A.tiles_m = (int)((M + BM - 1) / BM);
+  A.tiles_n = (int)((N + BN - 1) / BN);
+  A.C = (uint16_t*)c;
+  A.ldc = ldc;
+  A.alpha = alpha;
+  hipStream_t st = (hipStream_t)stream;
+  if (mode == 0) {
+    if (a_kmajor && b_kmajor) return launch<true, true, EPI_STORE, 0, 0>(A, st);
+    if (a_kmajor && !b_kmajor) return launch<true, false, EPI_STORE, 0, 0>(A, st);
+    if (!a_kmajor && !b_kmajor) return launch<false, false, EPI_STORE, 0, 0>(A, st);
+    return launch<false, true, EPI_STORE, 0, 0>(A, st);
+  }
+  if (mode == 1) {
+    if (a_kmajor && b_kmajor) return launch<true, true, EPI_ADD, 0, 0>(A, st);
+    if (a_kmajor && !b_kmajor) return launch<true, false, EPI_ADD, 0, 0>(A, st);
+    if (!a_kmajor && !b_kmajor) return launch<false, false, EPI_ADD, 0, 0>(A, st);
+    return launch<false, true, EPI_ADD, 0, 0>(A, st);
+  }
+  // split-K: fp32 partials in the caller's workspace, then a fixed-order reduce
+  const int nk = (int)((K + BK - 1) / BK);
+  if (splits < 1) return kErrShape;
+  if (splits > nk) splits = nk > 0 ? nk : 1;
+  if (!workspace || ((uintptr_t)workspace & 15)) return kErrAlign;
+  A.ws = (float*)workspace;
+  A.ksplit = splits;
+  A.kt_per_split = (nk + splits - 1) / splits;
+  int rc;
+  if (a_kmajor && b_kmajor) rc = launch<true, true, EPI_F32, 0, 0>(A, st);
+  else if (a_kmajor && !b_kmajor) rc = launch<true, false, EPI_F32, 0, 0>(A, st);
+  else if (!a_kmajor && !b_kmajor) rc = launch<false, false, EPI_F32, 0, 0>(A, st);
+  else rc = launch<false, true, EPI_F32, 0, 0>(A, st);
+  if (rc) return rc;
+  const int64_t total = M * N;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     st, (const float*)workspace, (uint16_t*)c, M, N, ldc, splits, alpha);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
 int cpt_ffn_gate_up(const void* x, const void* w_gate, const void* w_up, int64_t n_tok,

@@ -178,3 +178,47 @@ def ffn_down_dgrad(grad_y, w_down, cache: int, group_size: int, c_gate, s_gate, 
                                            _stream(grad_y))
     check(rc, "ffn_down_dgrad")
     return dg, du, hm
+
+
+def addmm_(c: torch.Tensor, a: torch.Tensor, b: torch.Tensor, alpha: float,
+           name: str = "gemm_lora_add") -> torch.Tensor:
+    """In place: c = bf16(c + bf16(alpha * bf16(a @ b))), PEFT's
+    `h + s * B(A(x))` in bf16 (src/flashffn.py:1414,1420,1439,1529)."""
+    _require_device(c, a, b)
+    _check_bf16(c, a, b)
+    M, K = a.shape
+    K_, N = b.shape
+    assert K == K_ and tuple(c.shape) == (M, N) and c.stride(1) == 1
+    a, lda, ak = _layout_a(a)
+    b, ldb, bk = _layout_b(b)
+    with _timed(name):
+        rc = _lib.lib().cpt_gemm_bf16_ex(a.data_ptr(), lda, ak, b.data_ptr(), ldb, bk, c.data_ptr(),
+                                         c.stride(0), M, N, K, float(alpha), 1, 1, None, _stream(a))
+    check(rc, name)
+    return c
+
+
+def mm_splitk(a: torch.Tensor, b: torch.Tensor, alpha: float = 1.0, splits: int | None = None,
+              name: str = "gemm_splitk") -> torch.Tensor:
+    """bf16(alpha * (a @ b)) with the K reduction split across blocks (fp32
+    partials, fixed-order sum): for the thin adapter gradients that reduce
+    over all tokens."""
+    _require_device(a, b)
+    _check_bf16(a, b)
+    M, K = a.shape
+    K_, N = b.shape
+    assert K == K_
+    a, lda, ak = _layout_a(a)
+    b, ldb, bk = _layout_b(b)
+    if splits is None:
+        tiles = ((M + 255) // 256) * ((N + 255) // 256)
+        splits = max(1, min((K + 63) // 64, (512 + tiles - 1) // tiles))
+    ldc = (N + 7) // 8 * 8
+    c = torch.empty((M, ldc), dtype=torch.bfloat16, device=a.device)
+    ws = torch.empty((splits * M * N,), dtype=torch.float32, device=a.device)
+    with _timed(name):
+        rc = _lib.lib().cpt_gemm_bf16_ex(a.data_ptr(), lda, ak, b.data_ptr(), ldb, bk, c.data_ptr(),
+                                         ldc, M, N, K, float(alpha), 2, splits, ws.data_ptr(),
+                                         _stream(a))
+    check(rc, name)
+    return c if ldc == N else c[:, :N]

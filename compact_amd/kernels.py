@@ -298,3 +298,109 @@ def triton_swiglu_backward_glu(grad_h_mid, h_gate, h_up, want_h_mid, inplace, di
 
 triton_silu_mul_quant = silu_mul_quant
 triton_dequant_swiglu_backward = dequant_swiglu_backward
+
+
+# ---------------------------------------------------------------------------
+# outlier channels (config C3; HyC-LoRA zero-and-overwrite on the v3 codec,
+# hyclora/operators/compress_function.py:80-174)
+# ---------------------------------------------------------------------------
+
+def outlier_select(t: torch.Tensor, k: int):
+    """The k columns of t [N, D] with the largest L2 norm over all rows (ties to
+    the lower column).  Returns (slot int16 [D]: -1 or the column's position
+    among the selected in ascending order, idx int32 [k] ascending)."""
+    _require_device(t)
+    t = t.contiguous()
+    n, d = t.shape
+    dev = t.device
+    chunks = max(1, (n + 255) // 256)
+    partial = torch.empty((chunks, d), dtype=torch.float64, device=dev)
+    sumsq = torch.empty((d,), dtype=torch.float64, device=dev)
+    slot = torch.empty((d,), dtype=torch.int16, device=dev)
+    idx = torch.empty((max(k, 1),), dtype=torch.int32, device=dev)
+    check(_lib.lib().cpt_outlier_select(t.data_ptr(), _dtype_code(t), n, d, k, partial.data_ptr(),
+                                        sumsq.data_ptr(), slot.data_ptr(), idx.data_ptr(),
+                                        _stream(t)), "outlier_select")
+    return slot, idx[:k]
+
+
+def _outlier_buf(n, k, dev):
+    return torch.empty((n, k), dtype=torch.bfloat16, device=dev)
+
+
+def v3_quantize_outlier(t, bits, group_size, slot, k):
+    """Codec of t with the slot columns extracted first.  Returns
+    (payload, scales, outliers bf16 [N, k])."""
+    assert bits in (4, 8), f"unsupported bits={bits}"
+    _require_device(t, slot)
+    t = t.contiguous()
+    n, d = t.shape
+    assert d % group_size == 0, f"D={d} not divisible by group_size={group_size}"
+    dev = t.device
+    payload = torch.empty((n, d // 2) if bits == 4 else (n, d),
+                          dtype=torch.uint8 if bits == 4 else torch.int8, device=dev)
+    scales = torch.empty((n, d // group_size), dtype=torch.float16, device=dev)
+    out = _outlier_buf(n, k, dev)
+    check(_lib.lib().cpt_v3_quantize_outlier(t.data_ptr(), _dtype_code(t), n, d, bits, group_size,
+                                             slot.data_ptr(), k, out.data_ptr(), payload.data_ptr(),
+                                             scales.data_ptr(), _stream(t)), "v3_quantize_outlier")
+    return payload, scales, out
+
+
+def v3_dequantize_outlier(payload, scales, outliers, slot, bits, group_size):
+    """Dequantise through bf16 and write the outlier columns back -> bf16 [N, D]."""
+    _require_device(payload, scales, outliers, slot)
+    n = payload.shape[0]
+    d = payload.shape[1] * (2 if bits == 4 else 1)
+    out = torch.empty((n, d), dtype=torch.bfloat16, device=payload.device)
+    k = outliers.shape[1]
+    check(_lib.lib().cpt_v3_dequantize_outlier(payload.data_ptr(), scales.data_ptr(),
+                                               slot.data_ptr(), k, outliers.data_ptr(), n, d, bits,
+                                               group_size, out.data_ptr(), _stream(payload)),
+          "v3_dequantize_outlier")
+    return out
+
+
+def silu_mul_quant_outlier(h_gate, h_up, bits, group_size, slot_gate, slot_up, k):
+    """K1 with outlier channels.  Returns
+    (h_mid, q_gate, s_gate, o_gate, q_up, s_up, o_up)."""
+    _require_device(h_gate, h_up, slot_gate, slot_up)
+    n, d, g = _check_quant_shapes(h_gate, bits, group_size)
+    assert h_up.shape == h_gate.shape and h_up.is_contiguous()
+    dev = h_gate.device
+    h_mid = torch.empty_like(h_gate)
+    shape = (n, d // 2) if bits == 4 else (n, d)
+    qdt = torch.uint8 if bits == 4 else torch.int8
+    qg, qu = torch.empty(shape, dtype=qdt, device=dev), torch.empty(shape, dtype=qdt, device=dev)
+    sg = torch.empty((n, g), dtype=torch.float16, device=dev)
+    su = torch.empty((n, g), dtype=torch.float16, device=dev)
+    og, ou = _outlier_buf(n, k, dev), _outlier_buf(n, k, dev)
+    with _timed("silu_mul_quant_outlier"):
+        rc = _lib.lib().cpt_silu_mul_quant_outlier(
+            h_gate.data_ptr(), h_up.data_ptr(), n, d, bits, group_size, slot_gate.data_ptr(),
+            slot_up.data_ptr(), k, h_mid.data_ptr(), qg.data_ptr(), sg.data_ptr(), og.data_ptr(),
+            qu.data_ptr(), su.data_ptr(), ou.data_ptr(), _stream(h_gate))
+    check(rc, "silu_mul_quant_outlier")
+    _V3_COUNTERS["triton_quant_fwd"] += 1
+    return h_mid, qg, sg, og, qu, su, ou
+
+
+def dequant_swiglu_backward_outlier(grad_h_mid, q_gate, s_gate, o_gate, slot_gate, q_up, s_up,
+                                    o_up, slot_up, bits, group_size, want_h_mid=False):
+    """K2 with the outlier columns restored.  Returns (grad_h_gate, grad_h_up, h_mid^ | None)."""
+    _require_device(grad_h_mid, q_gate, s_gate, o_gate, slot_gate, q_up, s_up, o_up, slot_up)
+    assert grad_h_mid.dtype == torch.bfloat16 and grad_h_mid.is_contiguous()
+    n, d = grad_h_mid.shape
+    dg = torch.empty_like(grad_h_mid)
+    du = torch.empty_like(grad_h_mid)
+    hm = torch.empty_like(grad_h_mid) if want_h_mid else None
+    k = o_gate.shape[1]
+    with _timed("dequant_swiglu_backward_outlier"):
+        rc = _lib.lib().cpt_dequant_swiglu_backward_outlier(
+            grad_h_mid.data_ptr(), q_gate.data_ptr(), s_gate.data_ptr(), slot_gate.data_ptr(),
+            o_gate.data_ptr(), q_up.data_ptr(), s_up.data_ptr(), slot_up.data_ptr(),
+            o_up.data_ptr(), k, n, d, bits, group_size, dg.data_ptr(), du.data_ptr(), _ptr(hm),
+            _stream(grad_h_mid))
+    check(rc, "dequant_swiglu_backward_outlier")
+    _V3_COUNTERS["triton_dequant_bwd"] += 1
+    return dg, du, hm

@@ -87,6 +87,50 @@ int cpt_dequant_swiglu_backward(const void* grad_h_mid, const void* q_gate, cons
                                 int bits, int64_t group_size, void* grad_h_gate,
                                 void* grad_h_up, void* h_mid_hat, void* stream);
 
+/* ---------------- outlier channels (config C3) ---------------- */
+/* The reference has no per-group codec with outlier channels; this is the
+ * build's specification after HyC-LoRA (hyclora/operators/compress_function.py):
+ * the k columns with the largest L2 norm over all rows are kept in bf16
+ * (:80-88), zeroed before quantisation (:111-143) and written back after
+ * dequantisation (:147-174).  slot: int16 [d], -1 or the column's position
+ * among the selected columns in ascending column order; outliers: bf16 [n, k].
+ * The outlier kernels need group_size in 8..512, d % 8 == 0 and 16-byte
+ * aligned rows. */
+
+/* Select the k outlier columns of t [n, d]: fp64 column sums of squares in a
+ * fixed order (partial: fp64 [ceil(n/256), d]; sumsq: fp64 [d]), rank with
+ * ties to the lower column, write slot [d] and idx int32 [k] (ascending). */
+int cpt_outlier_select(const void* t, int dtype, int64_t n, int64_t d, int64_t k,
+                       void* partial, void* sumsq, void* slot, void* idx, void* stream);
+
+/* v3_quantize_group_absmax with the slot columns extracted (copied to
+ * outliers, zeroed) before quantisation. */
+int cpt_v3_quantize_outlier(const void* t, int dtype, int64_t n, int64_t d, int bits,
+                            int64_t group_size, const void* slot, int64_t k, void* outliers,
+                            void* payload, void* scales, void* stream);
+
+/* Dequantise to bf16 [n, d] and write the stored outlier columns back. */
+int cpt_v3_dequantize_outlier(const void* payload, const void* scales, const void* slot, int64_t k,
+                              const void* outliers, int64_t n, int64_t d, int bits,
+                              int64_t group_size, void* out, void* stream);
+
+/* K1 with outlier channels: h_mid from the full g, u; the codes of the
+ * zeroed tensors; outliers of each (slot tables may differ). */
+int cpt_silu_mul_quant_outlier(const void* h_gate, const void* h_up, int64_t n, int64_t d,
+                               int bits, int64_t group_size, const void* slot_gate,
+                               const void* slot_up, int64_t k, void* h_mid, void* q_gate,
+                               void* s_gate, void* o_gate, void* q_up, void* s_up, void* o_up,
+                               void* stream);
+
+/* K2 with the outlier columns restored after the bf16 dequantisation. */
+int cpt_dequant_swiglu_backward_outlier(const void* grad_h_mid, const void* q_gate,
+                                        const void* s_gate, const void* slot_gate,
+                                        const void* o_gate, const void* q_up, const void* s_up,
+                                        const void* slot_up, const void* o_up, int64_t k,
+                                        int64_t n, int64_t d, int bits, int64_t group_size,
+                                        void* grad_h_gate, void* grad_h_up, void* h_mid_hat,
+                                        void* stream);
+
 /* ---------------- MFMA bf16 GEMMs (gfx950) ---------------- */
 
 /* Replaces the cuBLAS GEMMs the reference issues through F.linear / @
@@ -99,6 +143,18 @@ int cpt_dequant_swiglu_backward(const void* grad_h_mid, const void* q_gate, cons
 int cpt_gemm_bf16(const void* a, int64_t lda, int a_kmajor, const void* b, int64_t ldb,
                   int b_kmajor, const void* a2, int64_t lda2, const void* b2, int64_t ldb2,
                   int64_t K2, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream);
+
+/* Extended GEMM for the adapter (LoRA) terms, one operand pair:
+ *   mode 0: C = bf16(A.B)
+ *   mode 1: C = bf16(C + bf16(alpha * bf16(A.B)))   (PEFT's h + s * B(A(x)),
+ *           src/flashffn.py:1414,1420,1439,1529; C read and written in place)
+ *   mode 2: C = bf16(alpha * sum of `splits` fp32 partials of A.B over K
+ *           chunks); `workspace` holds splits * M * N floats (16-byte aligned).
+ *           For the thin adapter gradients that reduce over tokens
+ *           (src/flashffn.py:1538-1545,1575-1582). */
+int cpt_gemm_bf16_ex(const void* a, int64_t lda, int a_kmajor, const void* b, int64_t ldb,
+                     int b_kmajor, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                     float alpha, int mode, int splits, void* workspace, void* stream);
 
 /* Cache kinds of the fused FFN kernels. */
 enum { CPT_CACHE_NONE = 0, CPT_CACHE_BF16 = 1, CPT_CACHE_INT4 = 4, CPT_CACHE_INT8 = 8 };

@@ -11,7 +11,9 @@ Contents
     triton_silu_mul_quant (:1314-1340), triton_dequant_swiglu_backward
     (:1343-1373); all computed by oracle/codec.py.
   OracleFlashFFNv3Function: FlashFFNv3Function.forward/backward
-    (:1395-1602) in the reference's op order, on CPU tensors of any float dtype.
+    (:1395-1602) in the reference's op order, on CPU tensors of any float dtype;
+    with outlier_ratio > 0 (this build's C3 extension, parity unpinned against
+    the reference) the int4/int8 cache keeps HyC-LoRA outlier channels.
   ref_grads_fp32: the fp32 plain-autograd reference of the same factored
     computation (src/verify_flashffn_v3.py:294-327).
   count_saved_bytes / int4_saved_bytes_closed_form: the reference's
@@ -114,6 +116,24 @@ def triton_dequant_swiglu_backward(grad_h_mid, q_gate, s_gate, q_up, s_up, bits,
     return from_f32(dg, dt), from_f32(du, dt), (from_f32(hm, dt) if want_h_mid else None)
 
 
+def outlier_select(h, ratio):
+    """Outlier columns of the bf16 tensor h (codec.outlier_channels spec)."""
+    return codec.outlier_channels(to_f32(h), ratio)
+
+
+def v3_quantize_outlier(h, bits, group_size, idx):
+    v = to_f32(h)
+    q, s, o = codec.outlier_quantize(v, codec.f32_to_bf16_bits(v), idx, bits, group_size)
+    return torch.from_numpy(q), torch.from_numpy(s), torch.from_numpy(o.view(np.int16)).view(torch.bfloat16)
+
+
+def v3_dequantize_outlier(payload, scales, outliers, idx, bits, group_size):
+    ob = outliers.contiguous().view(torch.int16).numpy().view(np.uint16)
+    bits_out = codec.outlier_dequantize_bf16(payload.numpy(), scales.numpy(), ob, idx, bits,
+                                             group_size)
+    return torch.from_numpy(bits_out.view(np.int16)).view(torch.bfloat16)
+
+
 # ---------------------------------------------------------------------------
 # FlashFFNv3Function restated
 # ---------------------------------------------------------------------------
@@ -132,7 +152,7 @@ class OracleFlashFFNv3Function(torch.autograd.Function):
     @staticmethod
     def forward(ctx, x, w_gate, a_gate, b_gate, w_up, a_up, b_up, w_down, a_down, b_down,
                 s_gate=0.0, s_up=0.0, s_down=0.0, cache_mode="int4", group_size=64,
-                use_triton=True):
+                use_triton=True, outlier_ratio=0.0):
         assert cache_mode in ("int4", "int8", "bf16", "recompute"), cache_mode
         orig_shape = x.shape
         hidden_dim = x.shape[-1]
@@ -150,9 +170,19 @@ class OracleFlashFFNv3Function(torch.autograd.Function):
             h_up = h_up + s_up * F.linear(xa_u, b_up)                    # :1420
 
         c_gate = qs_gate = c_up = qs_up = None
+        o_gate = o_up = idx_gate = idx_up = None
         fused_quant = (cache_mode in ("int4", "int8") and use_triton
                        and h_gate.dtype == torch.bfloat16)               # :1424-1426
-        if fused_quant:
+        k_out = (int(h_gate.shape[1] * outlier_ratio)
+                 if cache_mode in ("int4", "int8") and outlier_ratio > 0 else 0)
+        if k_out > 0:
+            # this build's C3 extension: HyC-LoRA outlier channels on the v3 codec
+            bits = 4 if cache_mode == "int4" else 8
+            idx_gate, idx_up = outlier_select(h_gate, outlier_ratio), outlier_select(h_up, outlier_ratio)
+            c_gate, qs_gate, o_gate = v3_quantize_outlier(h_gate, bits, group_size, idx_gate)
+            c_up, qs_up, o_up = v3_quantize_outlier(h_up, bits, group_size, idx_up)
+            h_mid = triton_silu_mul(h_gate, h_up)
+        elif fused_quant:
             bits = 4 if cache_mode == "int4" else 8
             h_mid, c_gate, qs_gate, c_up, qs_up = triton_silu_mul_quant(
                 h_gate, h_up, bits, group_size)                          # :1429
@@ -165,7 +195,7 @@ class OracleFlashFFNv3Function(torch.autograd.Function):
             ha_d = F.linear(h_mid, a_down)                               # :1438
             y = y + s_down * F.linear(ha_d, b_down)                      # :1439
 
-        if not fused_quant:
+        if not fused_quant and k_out == 0:
             if cache_mode in ("int4", "int8"):
                 bits = 4 if cache_mode == "int4" else 8
                 c_gate, qs_gate = v3_quantize_group_absmax(h_gate, bits, group_size)
@@ -175,6 +205,7 @@ class OracleFlashFFNv3Function(torch.autograd.Function):
         ctx.save_for_backward(x, w_gate, a_gate, b_gate, w_up, a_up, b_up,
                               w_down, a_down, b_down, xa_g, xa_u, ha_d,
                               c_gate, qs_gate, c_up, qs_up)              # :1454-1458
+        ctx.outliers = (o_gate, o_up, idx_gate, idx_up)
         ctx.s = (s_gate, s_up, s_down)
         ctx.cache_mode = cache_mode
         ctx.group_size = group_size
@@ -201,7 +232,8 @@ class OracleFlashFFNv3Function(torch.autograd.Function):
                           or need_wu or need_au or need_bu)              # :1488-1489
         need_h_mid = need_wd or (a_down is not None and need_ad)         # :1490
         need_recon = need_gate_path or need_h_mid
-        use_k2 = mode in ("int4", "int8") and ctx.use_triton and need_gate_path
+        use_k2 = (mode in ("int4", "int8") and ctx.use_triton and need_gate_path
+                  and ctx.outliers[0] is None)
 
         hg = hu = None
         if need_recon and not use_k2:                                    # :1500-1516
@@ -214,6 +246,11 @@ class OracleFlashFFNv3Function(torch.autograd.Function):
                     hu = hu + s_up * F.linear(xa_u, b_up)
             elif mode == "bf16":
                 hg, hu = c_gate, c_up
+            elif ctx.outliers[0] is not None:
+                bits = 4 if mode == "int4" else 8
+                o_gate, o_up, idx_gate, idx_up = ctx.outliers
+                hg = v3_dequantize_outlier(c_gate, qs_gate, o_gate, idx_gate, bits, ctx.group_size)
+                hu = v3_dequantize_outlier(c_up, qs_up, o_up, idx_up, bits, ctx.group_size)
             else:
                 bits = 4 if mode == "int4" else 8
                 hg = v3_dequantize_group_absmax(c_gate, qs_gate, bits, ctx.group_size,
@@ -327,7 +364,7 @@ def ref_grads_fp32(ps: dict, x: torch.Tensor, gy: torch.Tensor):
 
 
 def run_function_grads(fn_apply, ps: dict, x, gy, mode: str, group_size: int,
-                       use_triton: bool = True):
+                       use_triton: bool = True, outlier_ratio: float = 0.0):
     """Run an FFN v3 Function (oracle or product) on leaf clones of `ps`.
     Mirrors src/verify_flashffn_v3.py:259-291.  Returns ({name: grad}, y)."""
     def leaf(t, rg):
@@ -343,7 +380,8 @@ def run_function_grads(fn_apply, ps: dict, x, gy, mode: str, group_size: int,
     y = fn_apply(xl, t["w_gate"], t["a_gate"], t["b_gate"],
                  t["w_up"], t["a_up"], t["b_up"],
                  t["w_down"], t["a_down"], t["b_down"],
-                 ps["s_gate"], ps["s_up"], ps["s_down"], mode, group_size, use_triton)
+                 ps["s_gate"], ps["s_up"], ps["s_down"], mode, group_size, use_triton,
+                 outlier_ratio)
     y.backward(gy)
     grads = {"grad_x": xl.grad}
     for k, tt in t.items():

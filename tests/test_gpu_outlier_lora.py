@@ -1,0 +1,182 @@
+"""GPU tests of the C3 pieces: outlier channels (this build's specification
+of HyC-LoRA zero-and-overwrite on the v3 codec -- parity unpinned against the
+reference, which has no such combination, so the oracle's specification is
+the bar) and the LoRA terms on the GEMM engine.
+
+Bars: outlier selection, codes, scales, stored outliers and dequantised values
+bit-exact against the oracle; fused (K1/K2) == standalone bitwise; LoRA GEMM
+paths within the bf16 output rounding of an fp32 reference; the C3-shaped
+Function within rel 2e-2 of the oracle Function and above the reference's V2
+cosine floors against fp32 autograd.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import codec
+from oracle import flashffn_ref as R
+from oracle.flashffn_ref import to_f32
+from tests.inputs import make_pair
+
+pytestmark = pytest.mark.gpu
+
+
+def _cpt():
+    import compact_amd
+    from compact_amd import gemm
+    return compact_amd, gemm
+
+
+def _hot(n, d, seed, hot=(3, 100, 257, 1000)):
+    a, b = make_pair("random", n, d, seed=seed)
+    a, b = a.clone(), b.clone()
+    for j, c in enumerate(hot):
+        if c < d:
+            a[:, c] *= 40 + j
+            b[:, (c * 7) % d] *= 30 + j
+    return a, b
+
+
+@pytest.mark.parametrize("ratio", [0.005, 0.01, 0.05])
+def test_outlier_select_matches_oracle(device, ratio):
+    cpt, _ = _cpt()
+    a, b = _hot(384, 2048, 5)
+    for t in (a, b):
+        k = int(t.shape[1] * ratio)
+        slot, idx = cpt.outlier_select(t.to(device), k)
+        want = codec.outlier_channels(to_f32(t), ratio)
+        assert idx.cpu().numpy().tolist() == want.tolist()
+        s = slot.cpu().numpy()
+        assert (s >= 0).sum() == k
+        assert s[want].tolist() == list(range(k))
+
+
+@pytest.mark.parametrize("bits,group", [(4, 64), (8, 128), (4, 32)])
+def test_outlier_codec_bit_exact(device, bits, group):
+    cpt, _ = _cpt()
+    a, _ = _hot(256, 2048, 7)
+    k = int(2048 * 0.01)
+    slot, idx = cpt.outlier_select(a.to(device), k)
+    q, s, o = cpt.v3_quantize_outlier(a.to(device), bits, group, slot, k)
+    ridx = codec.outlier_channels(to_f32(a), 0.01)
+    bits16 = a.view(torch.int16).numpy().view(np.uint16)
+    rq, rs, ro = codec.outlier_quantize(to_f32(a), bits16, ridx, bits, group)
+    assert np.array_equal(q.cpu().numpy().view(np.uint8), rq.view(np.uint8))
+    assert np.array_equal(s.cpu().numpy().view(np.uint16), rs.view(np.uint16))
+    assert np.array_equal(o.cpu().view(torch.int16).numpy().view(np.uint16), ro)
+    deq = cpt.v3_dequantize_outlier(q, s, o, slot, bits, group)
+    rdeq = codec.outlier_dequantize_bf16(rq, rs, ro, ridx, bits, group)
+    assert np.array_equal(deq.cpu().view(torch.int16).numpy().view(np.uint16), rdeq)
+
+
+@pytest.mark.parametrize("bits,group", [(4, 64), (8, 128)])
+def test_outlier_k1_k2_equal_standalone(device, bits, group):
+    cpt, _ = _cpt()
+    a, b = _hot(256, 1024, 9)
+    ga, gb = a.to(device), b.to(device)
+    k = int(1024 * 0.01)
+    sg_, _ = cpt.outlier_select(ga, k)
+    su_, _ = cpt.outlier_select(gb, k)
+    hm, qg, sg, og, qu, su, ou = cpt.silu_mul_quant_outlier(ga, gb, bits, group, sg_, su_, k)
+    q2, s2, o2 = cpt.v3_quantize_outlier(ga, bits, group, sg_, k)
+    q3, s3, o3 = cpt.v3_quantize_outlier(gb, bits, group, su_, k)
+    assert torch.equal(qg.view(torch.uint8), q2.view(torch.uint8))
+    assert torch.equal(qu.view(torch.uint8), q3.view(torch.uint8))
+    assert torch.equal(sg.view(torch.int16), s2.view(torch.int16))
+    assert torch.equal(og.view(torch.int16), o2.view(torch.int16))
+    assert torch.equal(ou.view(torch.int16), o3.view(torch.int16))
+    assert torch.equal(hm.view(torch.int16), cpt.silu_mul(ga, gb).view(torch.int16))
+    gm = torch.randn(256, 1024, device=device).to(torch.bfloat16)
+    dg, du, h = cpt.dequant_swiglu_backward_outlier(gm, qg, sg, og, sg_, qu, su, ou, su_, bits,
+                                                    group, want_h_mid=True)
+    hg = cpt.v3_dequantize_outlier(qg, sg, og, sg_, bits, group)
+    hu = cpt.v3_dequantize_outlier(qu, su, ou, su_, bits, group)
+    rdg, rdu, rh = cpt.swiglu_backward_glu(gm, hg, hu, True)
+    for x, y in ((dg, rdg), (du, rdu), (h, rh)):
+        assert torch.equal(x.view(torch.int16), y.view(torch.int16))
+
+
+def _close(got, ref):
+    got = got.float().cpu()
+    tol = 1e-2 * ref.abs() + 1e-3 * ref.abs().max()
+    assert not ((got - ref).abs() > tol).any(), float((got - ref).abs().max())
+
+
+def test_lora_addmm_matches_peft_order(device):
+    _, G = _cpt()
+    g = torch.Generator(device=device).manual_seed(3)
+    h = torch.randn(300, 512, device=device, generator=g).to(torch.bfloat16)
+    xa = torch.randn(300, 16, device=device, generator=g).to(torch.bfloat16)
+    bt = (torch.randn(512, 16, device=device, generator=g) * 0.1).to(torch.bfloat16)
+    want = h + 2.0 * (xa @ bt.t())          # torch bf16: same three roundings
+    got = G.addmm_(h.clone(), xa, bt.t(), 2.0)
+    assert (got.float() - want.float()).abs().max() <= 2 * 2 ** -7 * want.float().abs().max()
+    lora = 2.0 * (xa.float().cpu() @ bt.float().cpu().t())
+    ref = h.float().cpu() + lora
+    # the product and its scaling are rounded to bf16 before the sum: the
+    # error is relative to the terms, not to their (possibly cancelling) sum
+    tol = 2 ** -7 * (h.float().cpu().abs() + lora.abs()) + 1e-6
+    assert not ((got.float().cpu() - ref).abs() > tol).any()
+
+
+@pytest.mark.parametrize("mnk", [(16, 4096, 8192), (4096, 16, 8192), (24, 264, 1000)])
+def test_splitk_matches_fp32(device, mnk):
+    _, G = _cpt()
+    m, n, k = mnk
+    g = torch.Generator(device=device).manual_seed(4)
+    a = torch.randn(k, m, device=device, generator=g).to(torch.bfloat16).t()   # token-major
+    b = torch.randn(k, n, device=device, generator=g).to(torch.bfloat16)
+    got = G.mm_splitk(a, b, 0.5)
+    ref = 0.5 * (a.float().cpu() @ b.float().cpu())
+    _close(got, ref)
+
+
+H, D, RANK, S, N = 256, 768, 16, 2.0, 256
+
+
+@pytest.mark.parametrize("ratio", [0.0, 0.01])
+def test_c3_function_vs_oracle(device, ratio):
+    """C3 shape in miniature: LoRA r16 (s=2) on gate/up/down, frozen base,
+    int4 g64 cache, top-1% outlier channels."""
+    cpt, _ = _cpt()
+    ps = R.synthetic_param_set("all", H, D, RANK, S, seed=21, dtype=torch.bfloat16,
+                               peft_init=True, b_std=0.01)
+    gen = torch.Generator().manual_seed(22)
+    x = torch.randn(N, H, generator=gen).to(torch.bfloat16)
+    gy = torch.randn(N, H, generator=gen).to(torch.bfloat16)
+    psd = {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in ps.items()}
+    got, y = R.run_function_grads(cpt.FlashFFNv3Function.apply, psd, x.to(device), gy.to(device),
+                                  "int4", 64, True, ratio)
+    ora, y_o = R.run_function_grads(R.OracleFlashFFNv3Function.apply, ps, x, gy, "int4", 64,
+                                    True, ratio)
+    ref, _ = R.ref_grads_fp32(ps, x, gy)
+    assert R.rel_frob(y.cpu(), y_o) < 1e-2
+    assert set(got) == set(ref)
+    for k in ref:
+        assert R.rel_frob(got[k].cpu(), ora[k]) < 2e-2, k
+        c = R.tensor_cos(got[k].cpu(), ref[k])
+        assert c >= (0.99 if k == "grad_x" else 0.98), (k, c)
+    eager, _ = R.run_function_grads(cpt.FlashFFNv3Function.apply, psd, x.to(device),
+                                    gy.to(device), "int4", 64, False, ratio)
+    for k in got:
+        assert torch.equal(got[k], eager[k]), k
+
+
+def test_c3_saved_bytes(device):
+    cpt, _ = _cpt()
+    ps = {k: (v.to(device) if isinstance(v, torch.Tensor) else v)
+          for k, v in R.synthetic_param_set("all", H, D, RANK, S, seed=23).items()}
+    params = [v for v in ps.values() if isinstance(v, torch.Tensor)]
+    for p in params:
+        p.requires_grad_(True)
+    x = torch.randn(N, H, device=device).to(torch.bfloat16).requires_grad_(True)
+    ptrs = {p.data_ptr() for p in params} | {x.data_ptr()}
+    got, entries = R.count_saved_bytes(
+        lambda: cpt.FlashFFNv3Function.apply(
+            x, ps["w_gate"], ps["a_gate"], ps["b_gate"], ps["w_up"], ps["a_up"], ps["b_up"],
+            ps["w_down"], ps["a_down"], ps["b_down"], S, S, S, "int4", 64, True, 0.01), ptrs)
+    got += x.nbytes
+    k = int(D * 0.01)
+    want = R.saved_bytes_closed_form(N, H, D, 4, 64, n_thin=3, rank=RANK, n_outlier=k)
+    assert got == want + 2 * D * 2, entries     # + the two int16 slot tables

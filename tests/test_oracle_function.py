@@ -121,3 +121,26 @@ def test_saved_bytes_closed_form(mode, bits):
     assert got == want, entries
     if bits == 4:
         assert got == R.int4_saved_bytes_closed_form(n, H, D, RANK, 64)
+
+
+def test_outlier_cache_function_invariants():
+    """C3 extension (parity unpinned against the reference, which has no
+    per-group + outlier combination): with outlier channels the int4 grads are
+    at least as close to the bf16-cache grads as without, and at ratio 0 the
+    path is the plain codec."""
+    ps = R.synthetic_param_set("all", H, D, RANK, S, 11, dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(96, H, generator=g).to(torch.bfloat16)
+    x[:, :4] *= 20                                       # hot input features -> hot h channels
+    gy = torch.randn(96, H, generator=g).to(torch.bfloat16)
+    ref, _ = R.run_function_grads(R.OracleFlashFFNv3Function.apply, ps, x, gy, "bf16", 64)
+    plain, _ = R.run_function_grads(R.OracleFlashFFNv3Function.apply, ps, x, gy, "int4", 64)
+    outl, _ = R.run_function_grads(R.OracleFlashFFNv3Function.apply, ps, x, gy, "int4", 64,
+                                   outlier_ratio=0.05)
+    zero, _ = R.run_function_grads(R.OracleFlashFFNv3Function.apply, ps, x, gy, "int4", 64,
+                                   outlier_ratio=0.001)      # int(256 * 0.001) == 0
+    for k in ref:
+        assert torch.equal(zero[k], plain[k]), k
+    err_plain = sum(R.rel_frob(plain[k], ref[k]) for k in ref)
+    err_outl = sum(R.rel_frob(outl[k], ref[k]) for k in ref)
+    assert err_outl <= err_plain
