@@ -25,9 +25,17 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
-# workload C2
+# workload C2; C3 with --workload c3
 N_TOK, HID, INTER, GROUP, BITS = 8 * 1024, 4096, 11008, 128, 8
 MODE = "int8"
+WORKLOADS = {
+    "c2": dict(group=128, bits=8, mode="int8", lora_rank=0, outlier_ratio=0.0,
+               desc="C2: SwiGLU FFN fwd+bwd, d_model=4096, d_ff=11008, 8x1024 tokens, bf16, "
+                    "int8 per-group(128) cache, full-FT"),
+    "c3": dict(group=64, bits=4, mode="int4", lora_rank=16, outlier_ratio=0.01,
+               desc="C3: C2 + LoRA r16 (alpha 32) on gate/up/down, frozen base, int4 "
+                    "per-group(64) cache with top-1% outlier channels in bf16"),
+}
 
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, published
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
@@ -122,7 +130,11 @@ def main():
     ap.add_argument("--tokens", type=int, default=N_TOK)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=512)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
     args = ap.parse_args()
+    wl = WORKLOADS[args.workload]
+    global GROUP, BITS, MODE
+    GROUP, BITS, MODE = wl["group"], wl["bits"], wl["mode"]
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(multi-GPU sharding is a design note, not a code path)"}))
@@ -137,15 +149,32 @@ def main():
     g = torch.Generator(device=dev).manual_seed(0)
     x = torch.randn(n, h, device=dev, generator=g).to(torch.bfloat16)
     gy = torch.randn(n, h, device=dev, generator=g).to(torch.bfloat16)
-    wg = (torch.randn(d, h, device=dev, generator=g) * 0.02).to(torch.bfloat16).requires_grad_()
-    wu = (torch.randn(d, h, device=dev, generator=g) * 0.02).to(torch.bfloat16).requires_grad_()
-    wd = (torch.randn(h, d, device=dev, generator=g) * 0.02).to(torch.bfloat16).requires_grad_()
+    full_ft = wl["lora_rank"] == 0
+    wg = (torch.randn(d, h, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    wu = (torch.randn(d, h, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    wd = (torch.randn(h, d, device=dev, generator=g) * 0.02).to(torch.bfloat16)
     x.requires_grad_()
-    params = (wg, wu, wd)
+    lora = {}
+    scale = 0.0
+    if full_ft:
+        params = tuple(w.requires_grad_() for w in (wg, wu, wd))
+    else:
+        # LoRA r16, alpha 32: A ~ kaiming-uniform(a=sqrt(5)) (bound 1/sqrt(in)), B ~ N(0, 0.01)
+        r = wl["lora_rank"]
+        scale = 32.0 / r
+        for key, d_in, d_out in (("gate", h, d), ("up", h, d), ("down", d, h)):
+            bound = 1.0 / d_in ** 0.5
+            lora["a_" + key] = ((torch.rand(r, d_in, device=dev, generator=g) * 2 - 1) * bound
+                                ).to(torch.bfloat16).requires_grad_()
+            lora["b_" + key] = (torch.randn(d_out, r, device=dev, generator=g) * 0.01
+                                ).to(torch.bfloat16).requires_grad_()
+        params = tuple(lora.values())
 
     def fwd():
-        return cpt.FlashFFNv3Function.apply(x, wg, None, None, wu, None, None, wd, None, None,
-                                            0.0, 0.0, 0.0, MODE, GROUP, True)
+        return cpt.FlashFFNv3Function.apply(
+            x, wg, lora.get("a_gate"), lora.get("b_gate"), wu, lora.get("a_up"),
+            lora.get("b_up"), wd, lora.get("a_down"), lora.get("b_down"),
+            scale, scale, scale, MODE, GROUP, True, wl["outlier_ratio"])
 
     def step():
         for p in params + (x,):
@@ -172,9 +201,13 @@ def main():
     assert cpt._V3_COUNTERS["triton_dequant_bwd"] == args.steps, "fused dequant (K2) did not run"
     kern = kt.avg_ms()
 
-    sb = saved_bytes(fwd, {p.data_ptr() for p in params} | {x.data_ptr()}) + x.nbytes
+    # parameters (trainable or frozen) and x are excluded, x counted once
+    # (src/verify_flashffn_v3.py:523-543,594-597)
+    all_params = set(params) | {wg, wu, wd}
+    sb = saved_bytes(fwd, {p.data_ptr() for p in all_params} | {x.data_ptr()}) + x.nbytes
 
     algo = algorithmic_work(n, h, d)
+    algo["gemm_fwd_gate"] = algo["gemm_fwd_up"] = algo["gemm_dgrad_down"] = (2 * n * h * d, "mfma")
     kernels = {}
     for name, st in kern.items():
         entry = dict(st)
@@ -189,7 +222,7 @@ def main():
                 entry["frac_mfma_bf16"] = entry["tflops"] / MFMA_BF16_PEAK_TFLOPS
         kernels[name] = entry
     # dominant HIP kernel of this build by total time in the timed steps
-    dom = max(kern, key=lambda k: kern[k]["total_ms"])
+    dom = max((k for k in kern if k in algo), key=lambda k: kern[k]["total_ms"])
     amount, bound = algo[dom]
     rate = amount / (kern[dom]["avg_ms"] * 1e-3)
     if bound == "hbm":
@@ -201,23 +234,24 @@ def main():
                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                     "frac": rate / 1e12 / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
                     "algorithmic_flops": amount}
-    flops = gemm_flops_fwd_bwd(n, h, d)
+    flops = gemm_flops_fwd_bwd(n, h, d, full_ft)
+    if not full_ft:   # thin adapter GEMMs: 18 * N * r * (H + D)
+        flops += 18 * n * wl["lora_rank"] * (h + d)
     out = {
         "metric": "FFN fwd+bwd tokens/sec + saved-activation MB, Llama-7B FFN shape, 1 MI355X",
         "value": n / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seed 0, X~N(0,1), W~N(0,0.02))",
-        "config": {"workload": "C2: SwiGLU FFN fwd+bwd, d_model=4096, d_ff=11008, "
-                               "8x1024 tokens, bf16, int8 per-group(128) cache, full-FT",
-                   "tokens": n, "d_model": h, "d_ff": d, "cache_mode": MODE,
-                   "group_size": GROUP, "parallelism": "none (1 GPU)"},
+        "config": {"workload": wl["desc"], "tokens": n, "d_model": h, "d_ff": d,
+                   "cache_mode": MODE, "group_size": GROUP, "lora_rank": wl["lora_rank"],
+                   "outlier_ratio": wl["outlier_ratio"], "parallelism": "none (1 GPU)"},
         "saved_activation_mb": sb / 1e6,
         "step_tflops": flops / (ms * 1e-3) / 1e12,
         "step_frac_mfma_bf16": flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
         "roofline": roofline,
         "kernels": kernels,
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.workload == "c2":
         out["cpu_baseline"] = cpu_baseline(args.cpu_tokens)
     print(json.dumps(out))
 

@@ -471,11 +471,23 @@ __device__ __forceinline__ void epi_add(const KArgs& A, const Acc& acc, int64_t 
       static_for<0, 4>([&](auto g) {
         const int64_t n = n0 + wn * 128 + i * 32 + g * 8 + (lane >> 5) * 4;
         if (m >= A.M) return;
-        for (int e = 0; e < 4; ++e) {
-          if (n + e >= A.N) break;
-          uint16_t* cp = A.C + m * A.ldc + n + e;
-          const float t = round_bf16(A.alpha * round_bf16(acc.v[i][j][g * 4 + e]));
-          *cp = (uint16_t)f32_to_bf16_bits(bf16_to_f32(*cp) + t);
+        uint16_t* cp = A.C + m * A.ldc + n;
+        if (n + 3 < A.N && ((reinterpret_cast<uintptr_t>(cp) & 7) == 0)) {
+          const uint2 w = *reinterpret_cast<const uint2*>(cp);
+          const float c0 = __uint_as_float(w.x << 16), c1 = __uint_as_float(w.x & 0xFFFF0000u);
+          const float c2 = __uint_as_float(w.y << 16), c3 = __uint_as_float(w.y & 0xFFFF0000u);
+          const f32x16& a = acc.v[i][j];
+          *reinterpret_cast<uint2*>(cp) = make_uint2(
+              pack_bf16x2(c0 + round_bf16(A.alpha * round_bf16(a[g * 4 + 0])),
+                          c1 + round_bf16(A.alpha * round_bf16(a[g * 4 + 1]))),
+              pack_bf16x2(c2 + round_bf16(A.alpha * round_bf16(a[g * 4 + 2])),
+                          c3 + round_bf16(A.alpha * round_bf16(a[g * 4 + 3]))));
+        } else {
+          for (int e = 0; e < 4; ++e) {
+            if (n + e >= A.N) break;
+            const float t = round_bf16(A.alpha * round_bf16(acc.v[i][j][g * 4 + e]));
+            cp[e] = (uint16_t)f32_to_bf16_bits(bf16_to_f32(cp[e]) + t);
+          }
         }
       });
     });

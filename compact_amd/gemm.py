@@ -69,7 +69,14 @@ def _check_bf16(*ts):
 
 
 def mm(a: torch.Tensor, b: torch.Tensor, name: str = "gemm") -> torch.Tensor:
-    """a [M, K] @ b [K, N] -> bf16 [M, N] on the MFMA engine."""
+    """a [M, K] @ b [K, N] -> bf16 [M, N] on the MFMA engine.  Products with
+    too few 256x256 output tiles to fill the chip (the thin adapter products,
+    N or M = rank) split K across blocks instead."""
+    M, K = a.shape
+    N = b.shape[1]
+    tiles = ((M + 255) // 256) * ((N + 255) // 256)
+    if tiles < 128 and K >= 1024:
+        return mm_splitk(a, b, 1.0, name=name)
     return mm2(a, b, None, None, name)
 
 
