@@ -39,6 +39,15 @@ SIGNATURES = {
     "cpt_gemm_bf16_ex": [_P, _L, _I, _P, _L, _I, _P, _L, _L, _L, _L, ctypes.c_float, _I, _I, _P, _P],
     "cpt_ffn_gate_up": [_P, _P, _P, _L, _L, _L, _I, _L, _P, _P, _P, _P, _P, _P, _P, _P],
     "cpt_ffn_down_dgrad": [_P, _P, _L, _L, _L, _I, _L, _P, _P, _P, _P, _P, _P, _P, _P],
+    "cpt_dora_scale": [_P, _P, _P, _L, _L, _I, _P, _P],
+    "cpt_col_dot_div": [_P, _P, _P, _L, _L, _I, _P, _P, _P],
+    "cpt_dora_col_norm": [_P, _P, _P, _L, _L, _L, ctypes.c_double, _I, _P, _P, _I, _P],
+}
+
+# size queries: name -> argument types (restype int64)
+SIZE_QUERIES = {
+    "cpt_col_dot_workspace_bytes": [_L, _L],
+    "cpt_dora_col_norm_workspace_bytes": [_L, _L],
 }
 
 CACHE_NONE, CACHE_BF16, CACHE_INT4, CACHE_INT8 = 0, 1, 4, 8
@@ -64,6 +73,10 @@ def lib():
         fn = getattr(L, name)
         fn.argtypes = argtypes
         fn.restype = ctypes.c_int
+    for name, argtypes in SIZE_QUERIES.items():
+        fn = getattr(L, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int64
     L.cpt_status_string.argtypes = [ctypes.c_int]
     L.cpt_status_string.restype = ctypes.c_char_p
     L.cpt_abi_version.argtypes = []

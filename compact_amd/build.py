@@ -5,7 +5,7 @@ HIP source with hipcc and links them into compact_amd/_build/libcompact_amd.so.
 Cross-compiles without a GPU.  Flags that decide numerics:
   -fhip-fp32-correctly-rounded-divide-sqrt   IEEE division (codec bit-exactness)
   -fno-gpu-flush-denormals-to-zero           keep fp32 denormals
-  -ffp-contract=off                          (codec.hip only) no FMA contraction
+  -ffp-contract=off                          (codec, gemm, adapters) no FMA contraction
   -Xclang -target-feature -Xclang -packed-fp32-ops   no packed-fp32 instructions
 """
 
@@ -31,7 +31,8 @@ COMMON = [
     "-Wall", "-Wno-unused-function",
     f"-I{CSRC}", f"-I{os.path.join(ROOT, 'include')}",
 ]
-PER_FILE = {"codec.hip": ["-ffp-contract=off"], "gemm.hip": ["-ffp-contract=off"]}
+PER_FILE = {"codec.hip": ["-ffp-contract=off"], "gemm.hip": ["-ffp-contract=off"],
+            "adapters.hip": ["-ffp-contract=off"]}
 
 
 def hipcc() -> str:

@@ -22,6 +22,7 @@ Every kernel is a HIP kernel of libcompact_amd.so; there is no CPU path.
 
 from __future__ import annotations
 
+import random
 import warnings
 
 import torch
@@ -395,7 +396,10 @@ def make_v3_forward(mlp: nn.Module, cache_mode: str = "int4", group_size: int = 
     if any(k == "unknown" for k in kinds):
         raise NotImplementedError(f"FlashFFNv3: unsupported projection wrapper(s) on MLP: {kinds}")
     if any(k not in ("plain", "lora") for k in kinds):
-        raise NotImplementedError(f"FlashFFNv3: adapter kinds {kinds} need the adapter Function")
+        # DoRA / AdaLoRA / VeRA / DyLoRA (possibly mixed with plain/LoRA) take
+        # the sibling Function (src/flashffn.py:1660-1661)
+        assert outlier_ratio == 0.0, "outlier channels are not defined for the adapter Function"
+        return make_v3_adapter_forward(mlp, cache_mode, group_size, use_triton)
 
     def v3_forward(x):
         wg, ag, bg, sg = _v3_extract_proj(mlp.gate_proj)
@@ -427,3 +431,347 @@ class FlashFFNv3(nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return self._fwd(x)
+
+
+# ---------------------------------------------------------------------------
+# adapter families: DoRA / AdaLoRA / VeRA / DyLoRA (src/flashffn.py:1697-2230)
+# ---------------------------------------------------------------------------
+
+def _v3_dora_col_norm(w: torch.Tensor, a: torch.Tensor, b: torch.Tensor, s: float,
+                      out_dtype=torch.float32) -> torch.Tensor:
+    """DoRA's column norm ||W + s * B @ A||_2 over dim=1 without forming B @ A
+    (src/flashffn.py:1824-1840): fp32 Gram identity on the device, detached.
+    The reference returns float32; `out_dtype` folds its later `.to(dt)`."""
+    with torch.no_grad():
+        return K.dora_col_norm(w.detach(), a.detach(), b.detach(), s, out_dtype)
+
+
+def _v3_warn_dropout(kind: str, p: float):
+    if p > 0.0:
+        warnings.warn(f"FlashFFNv3 ignores {kind} dropout (p={p}); results differ from the "
+                      "reference forward when training with dropout.")
+
+
+def _v3_extract_proj_adapter(proj: nn.Module, dt: torch.dtype):
+    """(w, a, b, s, m, nu) of one projection, re-extracted per forward
+    (src/flashffn.py:1850-1921).  AdaLoRA's A*E and VeRA's lambda-scaled
+    frozen factors are composed here, in autograd, so their thin chain rules
+    run on [r, in] / [out, r] tensors; DyLoRA passes rank-b slices (b uniform
+    in 1..r in training, r in eval); DoRA adds m [out] and the detached norm
+    nu [out].  Everything is cast to dt through autograd."""
+    kind = _v3_proj_kind(proj)
+
+    def cast(t):
+        return t if (t is None or t.dtype == dt) else t.to(dt)
+
+    if kind == "plain":
+        return cast(proj.weight), None, None, 0.0, None, None
+    if kind == "lora":
+        w, a, b, s = _v3_extract_proj(proj)
+        return cast(w), cast(a), cast(b), s, None, None
+    if kind == "dylora":
+        _v3_warn_dropout("DyLoRA", float(getattr(proj.dropout, "p", 0.0)))
+        b_rank = _rng_randint(1, proj.r) if proj.training else proj.r
+        return (cast(proj.base_layer.weight), cast(proj.lora_A[:b_rank, :]),
+                cast(proj.lora_B[:, :b_rank]), float(proj.scaling), None, None)
+    if kind == "adalora":
+        name = proj.active_adapters[0]
+        _v3_warn_dropout("AdaLoRA", float(getattr(proj.lora_dropout[name], "p", 0.0)))
+        a_eff = proj.lora_A[name] * proj.lora_E[name]
+        s_eff = float(proj.scaling[name]) / (float(proj.ranknum[name]) + 1e-5)
+        return (cast(proj.get_base_layer().weight), cast(a_eff), cast(proj.lora_B[name]),
+                s_eff, None, None)
+    if kind == "vera":
+        name = proj.active_adapters[0]
+        _v3_warn_dropout("VeRA", float(getattr(proj.vera_dropout[name], "p", 0.0)))
+        a_frozen = proj.vera_A[name][:, : proj.in_features]
+        b_frozen = proj.vera_B[name][: proj.out_features, :]
+        a_eff = proj.vera_lambda_d[name].unsqueeze(-1) * a_frozen
+        b_eff = proj.vera_lambda_b[name].unsqueeze(-1) * b_frozen
+        return cast(proj.get_base_layer().weight), cast(a_eff), cast(b_eff), 1.0, None, None
+    if kind == "dora":
+        name = proj.active_adapters[0]
+        _v3_warn_dropout("DoRA", float(getattr(proj.lora_dropout[name], "p", 0.0)))
+        w = cast(proj.get_base_layer().weight)
+        a = cast(proj.lora_A[name].weight)
+        b = cast(proj.lora_B[name].weight)
+        s = float(proj.scaling[name])
+        m = cast(proj.lora_magnitude_vector[name].weight)
+        nu = _v3_dora_col_norm(w, a, b, s, out_dtype=dt)
+        return w, a, b, s, m, nu
+    raise NotImplementedError(
+        f"FlashFFNv3 adapter path: unsupported projection wrapper ({type(proj).__name__}).")
+
+
+def _rng_randint(lo: int, hi: int) -> int:
+    """DyLoRA's per-forward rank draw from Python's global `random` stream,
+    as the reference module draws it (src/dylora.py), so a seeded
+    `random.seed` reproduces the same ranks in both."""
+    return random.randint(lo, hi)
+
+
+def _scaled(t, m, nu, inplace=False):
+    """t * (m / nu) per column, or t when the projection has no magnitude."""
+    if m is None:
+        return t
+    return K.dora_scale(t, m, nu, out=t if inplace else None)
+
+
+class FlashFFNv3AdapterFunction(torch.autograd.Function):
+    """Sibling of FlashFFNv3Function for DoRA / AdaLoRA / VeRA / DyLoRA
+    projections (src/flashffn.py:1924-2208).  AdaLoRA, VeRA and DyLoRA arrive
+    as composed or sliced thin factors (_v3_extract_proj_adapter), so every
+    projection is the LoRA core, optionally with DoRA's magnitude: out =
+    c * (z W^T + s (z A^T) B^T), c = m / nu, nu detached.
+
+      apply(x, w_gate, a_gate, b_gate, m_gate, nu_gate,
+            w_up, a_up, b_up, m_up, nu_up, w_down, a_down, b_down, m_down, nu_down,
+            s_gate=0.0, s_up=0.0, s_down=0.0, cache_mode="int4", group_size=64,
+            use_triton=True)
+
+    The cache layer is FlashFFNv3Function's (h_gate / h_up cached after the
+    scale c).  Backward: dL/draw = g * c feeds the LoRA-core grads; grad_m =
+    sum_n g raw / nu with raw recomputed ('recompute' mode and the down
+    projection, one extra GEMM) or sum_n g h / m from the cache."""
+
+    @staticmethod
+    def forward(ctx, x, w_gate, a_gate, b_gate, m_gate, nu_gate, w_up, a_up, b_up, m_up, nu_up,
+                w_down, a_down, b_down, m_down, nu_down, s_gate=0.0, s_up=0.0, s_down=0.0,
+                cache_mode="int4", group_size=64, use_triton=True):
+        assert cache_mode in ("int4", "int8", "bf16", "recompute"), cache_mode
+        _V3_COUNTERS["forward"] += 1
+        _V3_COUNTERS["adapter_forward"] += 1
+        K._require_device(x)
+        orig_shape = x.shape
+        hidden_dim = x.shape[-1]
+        x_2d = x.reshape(-1, hidden_dim)
+        if not x_2d.is_contiguous():
+            x_2d = x_2d.contiguous()
+        quant = cache_mode in ("int4", "int8")
+        plain_gu = a_gate is None and a_up is None and m_gate is None and m_up is None
+        fusable = plain_gu and _mfma(x_2d, w_gate, w_up) and x_2d.shape[0] > 0
+        fused_quant = quant and use_triton and x.dtype == torch.bfloat16   # :1979-1981
+
+        c_gate = qs_gate = c_up = qs_up = None
+        h_gate = h_up = xa_g = xa_u = None
+        if fusable and fused_quant and group_size in _FUSED_GROUPS:
+            h_mid, _, _, c_gate, qs_gate, c_up, qs_up = G.ffn_gate_up(
+                x_2d, w_gate, w_up, _CACHE_CODE[cache_mode], group_size)
+            _V3_COUNTERS["triton_quant_fwd"] += 1
+        elif fusable and not fused_quant:
+            keep = cache_mode != "recompute"
+            h_mid, h_gate, h_up, *_ = G.ffn_gate_up(
+                x_2d, w_gate, w_up, _lib.CACHE_BF16 if keep else _lib.CACHE_NONE, group_size)
+        else:
+            h_gate, xa_g = _proj(x_2d, w_gate, a_gate, b_gate, s_gate, "gemm_fwd_gate")
+            h_gate = _scaled(h_gate, m_gate, nu_gate, inplace=True)          # :1967
+            h_up, xa_u = _proj(x_2d, w_up, a_up, b_up, s_up, "gemm_fwd_up")
+            h_up = _scaled(h_up, m_up, nu_up, inplace=True)                   # :1975
+            if fused_quant:
+                h_mid, c_gate, qs_gate, c_up, qs_up = K.silu_mul_quant(
+                    h_gate, h_up, _bits(cache_mode), group_size)
+                h_gate = h_up = None
+            else:
+                h_mid = K.silu_mul(h_gate, h_up)
+
+        y, ha_d = _proj(h_mid, w_down, a_down, b_down, s_down, "gemm_fwd_down")   # :1990-1994
+        y = _scaled(y, m_down, nu_down, inplace=True)                              # :1996
+
+        if not fused_quant:                                                         # :1998-2007
+            if quant:
+                c_gate, qs_gate = K.v3_quantize_group_absmax(h_gate, _bits(cache_mode), group_size)
+                c_up, qs_up = K.v3_quantize_group_absmax(h_up, _bits(cache_mode), group_size)
+            elif cache_mode == "bf16":
+                c_gate, c_up = h_gate, h_up
+        del h_gate, h_up, h_mid
+
+        ctx.save_for_backward(x, w_gate, a_gate, b_gate, m_gate, nu_gate,
+                              w_up, a_up, b_up, m_up, nu_up,
+                              w_down, a_down, b_down, m_down, nu_down,
+                              xa_g, xa_u, ha_d, c_gate, qs_gate, c_up, qs_up)
+        ctx.s = (s_gate, s_up, s_down)
+        ctx.cache_mode = cache_mode
+        ctx.group_size = group_size
+        ctx.use_triton = fused_quant
+        ctx.orig_shape = orig_shape
+        ctx.in_dtype = x.dtype
+        if len(orig_shape) == 3:
+            y = y.view(orig_shape[0], orig_shape[1], hidden_dim)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        _V3_COUNTERS["backward"] += 1
+        _V3_COUNTERS["adapter_backward"] += 1
+        (x, w_gate, a_gate, b_gate, m_gate, nu_gate, w_up, a_up, b_up, m_up, nu_up,
+         w_down, a_down, b_down, m_down, nu_down,
+         xa_g, xa_u, ha_d, cq_gate, qs_gate, cq_up, qs_up) = ctx.saved_tensors
+        s_gate, s_up, s_down = ctx.s
+        mode = ctx.cache_mode
+        gs = ctx.group_size
+        hidden_dim = ctx.orig_shape[-1]
+        ng = ctx.needs_input_grad
+        need_x = ng[0]
+        need_wg, need_ag, need_bg, need_mg = ng[1], ng[2], ng[3], ng[4]
+        need_wu, need_au, need_bu, need_mu = ng[6], ng[7], ng[8], ng[9]
+        need_wd, need_ad, need_bd, need_md = ng[11], ng[12], ng[13], ng[14]
+        gy = grad_y.reshape(-1, hidden_dim)
+        if not gy.is_contiguous():
+            gy = gy.contiguous()
+        x_2d = x.reshape(-1, hidden_dim)
+        if not x_2d.is_contiguous():
+            x_2d = x_2d.contiguous()
+
+        need_gate_path = (need_x or need_wg or need_ag or need_bg or need_mg
+                          or need_wu or need_au or need_bu or need_mu)          # :2047-2048
+        need_h_mid = need_wd or need_md or (a_down is not None and need_ad)
+        need_recon = need_gate_path or need_h_mid
+        use_k2 = mode in ("int4", "int8") and ctx.use_triton and need_gate_path
+        plain_gu = a_gate is None and a_up is None and m_gate is None and m_up is None
+        fusable_gu = plain_gu and _mfma(x_2d, w_gate, w_up) and x_2d.shape[0] > 0
+
+        hg = hu = raw_g = raw_u = None
+        if need_recon and not use_k2:                                           # :2055-2078
+            if mode == "recompute":
+                if fusable_gu:
+                    _, hg, hu, *_ = G.ffn_gate_up(x_2d, w_gate, w_up, _lib.CACHE_BF16, gs,
+                                                  want_h_mid=False)
+                else:
+                    raw_g = _linear(x_2d, w_gate, "gemm_recompute_gate")
+                    if a_gate is not None:
+                        raw_g = _addmm(raw_g, xa_g, b_gate.t(), s_gate, "gemm_recompute_gate_lora")
+                    hg = _scaled(raw_g, m_gate, nu_gate)
+                    raw_u = _linear(x_2d, w_up, "gemm_recompute_up")
+                    if a_up is not None:
+                        raw_u = _addmm(raw_u, xa_u, b_up.t(), s_up, "gemm_recompute_up_lora")
+                    hu = _scaled(raw_u, m_up, nu_up)
+            elif mode == "bf16":
+                hg, hu = cq_gate, cq_up
+            else:
+                hg = K.v3_dequantize_group_absmax(cq_gate, qs_gate, _bits(mode), gs, ctx.in_dtype)
+                hu = K.v3_dequantize_group_absmax(cq_up, qs_up, _bits(mode), gs, ctx.in_dtype)
+        elif use_k2 and (need_mg or need_mu):                                   # :2079-2089
+            # grad_m needs h^ itself, which K2 never materialises
+            if need_mg:
+                hg = K.v3_dequantize_group_absmax(cq_gate, qs_gate, _bits(mode), gs, ctx.in_dtype)
+            if need_mu:
+                hu = K.v3_dequantize_group_absmax(cq_up, qs_up, _bits(mode), gs, ctx.in_dtype)
+
+        g_eff_y = _scaled(gy, m_down, nu_down)                                  # :2094
+        gyB_d = None
+        if a_down is not None and (need_gate_path or need_ad):
+            gyB_d = _mm(g_eff_y, b_down, "gemm_gyB_down")
+        fusable_d = a_down is None and _mfma(g_eff_y, w_down) and g_eff_y.shape[0] > 0
+
+        grad_h_gate = grad_h_up = h_mid_hat = None
+        if need_gate_path:
+            if use_k2 and fusable_d and gs in _FUSED_GROUPS:                    # :2101-2110
+                grad_h_gate, grad_h_up, h_mid_hat = G.ffn_down_dgrad(
+                    g_eff_y, w_down, _CACHE_CODE[mode], gs, cq_gate, qs_gate, cq_up, qs_up,
+                    need_h_mid)
+                _V3_COUNTERS["triton_dequant_bwd"] += 1
+            elif (not use_k2) and fusable_d and hg is not None and hu is not None \
+                    and _mfma(hg, hu):
+                grad_h_gate, grad_h_up, h_mid_hat = G.ffn_down_dgrad(
+                    g_eff_y, w_down, _lib.CACHE_BF16, gs, hg, None, hu, None, need_h_mid)
+            else:
+                grad_h_mid = _mm(g_eff_y, w_down, "gemm_dgrad_down")
+                if a_down is not None:
+                    grad_h_mid = _addmm(grad_h_mid, gyB_d, a_down, s_down, "gemm_dgrad_down_lora")
+                if use_k2:
+                    grad_h_gate, grad_h_up, h_mid_hat = K.dequant_swiglu_backward(
+                        grad_h_mid, cq_gate, qs_gate, cq_up, qs_up, _bits(mode), gs,
+                        want_h_mid=need_h_mid)
+                else:
+                    grad_h_gate, grad_h_up, h_mid_hat = K.swiglu_backward_glu(
+                        grad_h_mid, hg, hu, need_h_mid)
+                del grad_h_mid
+
+        grad_w_down = grad_a_down = grad_b_down = grad_m_down = None
+        if need_h_mid:                                                          # :2112-2131
+            if h_mid_hat is None:
+                h_mid_hat = K.silu_mul(hg, hu)
+            if need_wd:
+                grad_w_down = _mm(g_eff_y.t(), h_mid_hat, "gemm_wgrad_down")
+            if need_ad:
+                grad_a_down = _mm_scaled(gyB_d.t(), h_mid_hat, s_down, "gemm_grad_a_down")
+            if need_md:
+                # raw_d is never stored: one extra GEMM recomputes it
+                raw_d, _ = _proj(h_mid_hat, w_down, None, None, 0.0, "gemm_recompute_down")
+                if a_down is not None:
+                    raw_d = _addmm(raw_d, ha_d, b_down.t(), s_down, "gemm_recompute_down_lora")
+                grad_m_down = K.col_dot_div(gy, raw_d, nu_down)
+                del raw_d
+            del h_mid_hat
+        if need_bd:
+            grad_b_down = _mm_scaled(g_eff_y.t(), ha_d, s_down, "gemm_grad_b_down")
+
+        grad_x = None
+        grad_w_gate = grad_a_gate = grad_b_gate = grad_m_gate = None
+        grad_w_up = grad_a_up = grad_b_up = grad_m_up = None
+        if need_gate_path:                                                      # :2134-2191
+            if need_mg:
+                grad_m_gate = (K.col_dot_div(grad_h_gate, raw_g, nu_gate) if raw_g is not None
+                               else K.col_dot_div(grad_h_gate, hg, m_gate))
+            if need_mu:
+                grad_m_up = (K.col_dot_div(grad_h_up, raw_u, nu_up) if raw_u is not None
+                             else K.col_dot_div(grad_h_up, hu, m_up))
+            # h = c * raw  =>  dL/draw = grad_h * c (grad_h is private here)
+            g_eff_g = _scaled(grad_h_gate, m_gate, nu_gate, inplace=True)
+            g_eff_u = _scaled(grad_h_up, m_up, nu_up, inplace=True)
+            ghgB = None
+            if a_gate is not None and (need_x or need_ag):
+                ghgB = _mm(g_eff_g, b_gate, "gemm_ghgB")
+            ghuB = None
+            if a_up is not None and (need_x or need_au):
+                ghuB = _mm(g_eff_u, b_up, "gemm_ghuB")
+            if need_x:
+                if _mfma(g_eff_g, w_gate, g_eff_u, w_up):
+                    grad_x = G.mm2(g_eff_g, w_gate, g_eff_u, w_up, "gemm_dgrad_x")
+                else:
+                    grad_x = g_eff_g @ w_gate + g_eff_u @ w_up
+                if a_gate is not None:
+                    grad_x = _addmm(grad_x, ghgB, a_gate, s_gate, "gemm_dgrad_x_lora_gate")
+                if a_up is not None:
+                    grad_x = _addmm(grad_x, ghuB, a_up, s_up, "gemm_dgrad_x_lora_up")
+            if need_bg:
+                grad_b_gate = _mm_scaled(g_eff_g.t(), xa_g, s_gate, "gemm_grad_b_gate")
+            if need_ag:
+                grad_a_gate = _mm_scaled(ghgB.t(), x_2d, s_gate, "gemm_grad_a_gate")
+            if need_bu:
+                grad_b_up = _mm_scaled(g_eff_u.t(), xa_u, s_up, "gemm_grad_b_up")
+            if need_au:
+                grad_a_up = _mm_scaled(ghuB.t(), x_2d, s_up, "gemm_grad_a_up")
+            if need_wg:
+                grad_w_gate = _mm(g_eff_g.t(), x_2d, "gemm_wgrad_gate")
+            if need_wu:
+                grad_w_up = _mm(g_eff_u.t(), x_2d, "gemm_wgrad_up")
+
+        # frozen weights => no dense [D_out, D_in] gradient was built (:2194-2197)
+        if not (need_wg or need_wu or need_wd):
+            assert grad_w_gate is None and grad_w_up is None and grad_w_down is None, \
+                "FlashFFNv3 invariant violated: dense weight grad with frozen weights"
+        if need_x and len(ctx.orig_shape) == 3:
+            grad_x = grad_x.view(ctx.orig_shape)
+        return (grad_x,
+                grad_w_gate, grad_a_gate, grad_b_gate, grad_m_gate, None,
+                grad_w_up, grad_a_up, grad_b_up, grad_m_up, None,
+                grad_w_down, grad_a_down, grad_b_down, grad_m_down, None,
+                ) + (None,) * (len(ctx.needs_input_grad) - 16)
+
+
+def make_v3_adapter_forward(mlp: nn.Module, cache_mode: str = "int4", group_size: int = 64,
+                            use_triton: bool = True):
+    """Adapter-factored v3 forward for an MLP whose projections may be DoRA /
+    AdaLoRA / VeRA / DyLoRA wrapped, mixed with plain or LoRA ones
+    (src/flashffn.py:2211-2230).  Factors, the DoRA norm and DyLoRA's rank
+    are re-extracted on every call."""
+    def v3_adapter_forward(x):
+        dt = x.dtype
+        wg, ag, bg, sg, mg, nug = _v3_extract_proj_adapter(mlp.gate_proj, dt)
+        wu, au, bu, su, mu, nuu = _v3_extract_proj_adapter(mlp.up_proj, dt)
+        wd, ad, bd, sd, md, nud = _v3_extract_proj_adapter(mlp.down_proj, dt)
+        return FlashFFNv3AdapterFunction.apply(x, wg, ag, bg, mg, nug, wu, au, bu, mu, nuu,
+                                               wd, ad, bd, md, nud, sg, su, sd, cache_mode,
+                                               group_size, use_triton)
+    return v3_adapter_forward

@@ -404,3 +404,71 @@ def dequant_swiglu_backward_outlier(grad_h_mid, q_gate, s_gate, o_gate, slot_gat
     check(rc, "dequant_swiglu_backward_outlier")
     _V3_COUNTERS["triton_dequant_bwd"] += 1
     return dg, du, hm
+
+
+# ---------------------------------------------------------------------------
+# DoRA magnitude (src/flashffn.py:1824-1840, 1967-1975, 2054, 2086-2130)
+# ---------------------------------------------------------------------------
+
+def dora_scale(x: torch.Tensor, m: torch.Tensor, nu: torch.Tensor, out=None) -> torch.Tensor:
+    """x * (m / nu).unsqueeze(0) with the reference's eager rounding: the
+    column scale c = m / nu is rounded to x's dtype, then x * c.  x [N, D],
+    m / nu [D], one dtype.  `out` may be x itself (in place)."""
+    _require_device(x, m, nu)
+    assert x.dim() == 2 and m.shape == nu.shape == (x.shape[1],), \
+        f"dora_scale: x {tuple(x.shape)}, m {tuple(m.shape)}, nu {tuple(nu.shape)}"
+    assert x.dtype == m.dtype == nu.dtype, "dora_scale: x, m and nu share one dtype"
+    x, m, nu = x.contiguous(), m.contiguous(), nu.contiguous()
+    if out is None:
+        out = torch.empty_like(x)
+    assert out.is_contiguous() and out.shape == x.shape and out.dtype == x.dtype
+    n, d = x.shape
+    with _timed("dora_scale"):
+        rc = _lib.lib().cpt_dora_scale(x.data_ptr(), m.data_ptr(), nu.data_ptr(), n, d,
+                                       _dtype_code(x), out.data_ptr(), _stream(x))
+    check(rc, "dora_scale")
+    return out
+
+
+def col_dot_div(a: torch.Tensor, b: torch.Tensor, den: torch.Tensor) -> torch.Tensor:
+    """((a * b).sum(0, dtype=float32) / den.float()).to(den.dtype) for a, b
+    [N, D] and den [D] of one dtype; deterministic fp32 summation."""
+    _require_device(a, b, den)
+    assert a.dim() == 2 and a.shape == b.shape and den.shape == (a.shape[1],)
+    assert a.dtype == b.dtype == den.dtype, "col_dot_div: one dtype expected"
+    a, b, den = a.contiguous(), b.contiguous(), den.contiguous()
+    n, d = a.shape
+    L = _lib.lib()
+    ws = torch.empty((max(1, L.cpt_col_dot_workspace_bytes(n, d)) + 3) // 4,
+                     dtype=torch.float32, device=a.device)
+    out = torch.empty((d,), dtype=a.dtype, device=a.device)
+    with _timed("col_dot_div"):
+        rc = L.cpt_col_dot_div(a.data_ptr(), b.data_ptr(), den.data_ptr(), n, d, _dtype_code(a),
+                               ws.data_ptr(), out.data_ptr(), _stream(a))
+    check(rc, "col_dot_div")
+    return out
+
+
+def dora_col_norm(w: torch.Tensor, a: torch.Tensor, b: torch.Tensor, s: float,
+                  out_dtype=torch.float32) -> torch.Tensor:
+    """||W + s * B @ A||_2 over dim=1 (the DoRA weight norm) without forming
+    B @ A: fp32 Gram identity (src/flashffn.py:1824-1840).  w [out, in],
+    a [r, in], b [out, r], one dtype.  Returns [out] in out_dtype."""
+    _require_device(w, a, b)
+    assert w.dim() == 2 and a.dim() == 2 and b.dim() == 2
+    rows, cols = w.shape
+    r = a.shape[0]
+    assert a.shape == (r, cols) and b.shape == (rows, r), \
+        f"dora_col_norm: w {tuple(w.shape)}, a {tuple(a.shape)}, b {tuple(b.shape)}"
+    assert w.dtype == a.dtype == b.dtype, "dora_col_norm: one dtype expected"
+    w, a, b = w.contiguous(), a.contiguous(), b.contiguous()
+    L = _lib.lib()
+    ws = torch.empty((L.cpt_dora_col_norm_workspace_bytes(rows, r) + 3) // 4 + 1,
+                     dtype=torch.float32, device=w.device)
+    nu = torch.empty((rows,), dtype=out_dtype, device=w.device)
+    with _timed("dora_col_norm"):
+        rc = L.cpt_dora_col_norm(w.data_ptr(), a.data_ptr(), b.data_ptr(), rows, cols, r,
+                                 float(s), _dtype_code(w), ws.data_ptr(), nu.data_ptr(),
+                                 _DT[out_dtype], _stream(w))
+    check(rc, "dora_col_norm")
+    return nu

@@ -183,6 +183,40 @@ int cpt_ffn_down_dgrad(const void* grad_y, const void* w_down, int64_t n_tok, in
                        const void* s_gate, const void* c_up, const void* s_up, void* grad_h_gate,
                        void* grad_h_up, void* h_mid_hat, void* stream);
 
+/* ---------------- adapter families (DoRA magnitude) ---------------- */
+/* VeRA, AdaLoRA and DyLoRA reach the kernels above as composed or sliced thin
+ * factors (src/flashffn.py:1850-1921); DoRA's per-output-channel magnitude
+ * c = m / nu needs the three entry points below.  All tensors of one call
+ * share `dtype`; rd() is round-to-nearest-even to that dtype. */
+
+/* out[i, j] = rd(x[i, j] * rd(m[j] / nu[j])) for x, out [n, d] (out may
+ * alias x).  Replaces `h * (m / nu).unsqueeze(0)` and the chain rule
+ * `g * c` of FlashFFNv3AdapterFunction (src/flashffn.py:1967-1975,2054,
+ * 2128-2130). */
+int cpt_dora_scale(const void* x, const void* m, const void* nu, int64_t n, int64_t d, int dtype,
+                   void* out, void* stream);
+
+/* Bytes of fp32 workspace cpt_col_dot_div needs for [n, d] inputs. */
+int64_t cpt_col_dot_workspace_bytes(int64_t n, int64_t d);
+
+/* out[j] = rd((sum_i rd(a[i, j] * b[i, j])) / den[j]) with the sum in fp32:
+ * the DoRA magnitude gradients `((g * raw).sum(0, dtype=float32) /
+ * den.float()).to(dtype)` (src/flashffn.py:2086-2089,2112-2125).  The
+ * summation order is fixed (128-row chunks, then the chunks in order), so the
+ * result is deterministic. */
+int cpt_col_dot_div(const void* a, const void* b, const void* den, int64_t n, int64_t d,
+                    int dtype, void* workspace, void* out, void* stream);
+
+/* Bytes of fp32 workspace cpt_dora_col_norm needs. */
+int64_t cpt_dora_col_norm_workspace_bytes(int64_t rows, int64_t r);
+
+/* Replaces _v3_dora_col_norm (src/flashffn.py:1824-1840): nu[j] =
+ * ||W_j + s (B A)_j||_2 for W [rows, cols], A [r, cols], B [rows, r] through
+ * the Gram identity, in fp32, without forming B A; nu written in nu_dtype. */
+int cpt_dora_col_norm(const void* w, const void* a, const void* b, int64_t rows, int64_t cols,
+                      int64_t r, double s, int dtype, void* workspace, void* nu, int nu_dtype,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -470,3 +470,374 @@ def saved_bytes_closed_form(n: int, h: int, d: int, bits: int, group: int,
     payload = n * d // 2 if bits == 4 else n * d
     return (n * h * x_bytes_per + 2 * payload + 2 * n * (d // group) * 2
             + n_thin * n * rank * 2 + 2 * n * n_outlier * 2)
+
+
+# ---------------------------------------------------------------------------
+# adapter families (src/flashffn.py:1697-2230)
+# ---------------------------------------------------------------------------
+
+
+@torch.no_grad()
+def dora_col_norm(w, a, b, s):
+    """src/flashffn.py:1824-1840: ||W + s*B@A||_2 over dim=1 through the
+    Gram identity, in float32, without forming B@A."""
+    wf, af, bf = w.float(), a.float(), b.float()
+    w2 = (wf * wf).sum(dim=1)
+    wa = wf @ af.t()
+    cross = (2.0 * s) * (bf * wa).sum(dim=1)
+    gram = af @ af.t()
+    quad = (s * s) * ((bf @ gram) * bf).sum(dim=1)
+    return (w2 + cross + quad).clamp_min_(0.0).sqrt_()
+
+
+def dora_scale(h, m, nu):
+    """src/flashffn.py:1967-1975: h * (m / nu).unsqueeze(0) in h's dtype."""
+    return h * (m / nu).unsqueeze(0)
+
+
+def col_dot_div(a, b, den):
+    """src/flashffn.py:2086-2089: ((a * b).sum(0, fp32) / den.float()).to(den.dtype)."""
+    return ((a * b).sum(0, dtype=torch.float32) / den.float()).to(den.dtype)
+
+
+class OracleFlashFFNv3AdapterFunction(torch.autograd.Function):
+    """CPU restatement of FlashFFNv3AdapterFunction (src/flashffn.py:1924-2208):
+    the LoRA core plus DoRA's per-output-channel magnitude c = m / nu applied
+    after the bypass.  Same argument list:
+      apply(x, w_gate, a_gate, b_gate, m_gate, nu_gate,
+            w_up, a_up, b_up, m_up, nu_up, w_down, a_down, b_down, m_down, nu_down,
+            s_gate, s_up, s_down, cache_mode, group_size, use_triton)"""
+
+    @staticmethod
+    def forward(ctx, x, w_gate, a_gate, b_gate, m_gate, nu_gate, w_up, a_up, b_up, m_up, nu_up,
+                w_down, a_down, b_down, m_down, nu_down, s_gate=0.0, s_up=0.0, s_down=0.0,
+                cache_mode="int4", group_size=64, use_triton=True):
+        assert cache_mode in ("int4", "int8", "bf16", "recompute"), cache_mode
+        # torch's CPU bf16 matrix-vector product ignores the row stride of a
+        # strided [K, 1] right operand (a DyLoRA rank-1 slice B[:, :1]);
+        # contiguous copies of the thin factors keep their values and avoid it
+        a_gate, b_gate, a_up, b_up, a_down, b_down = (
+            None if t is None else t.contiguous()
+            for t in (a_gate, b_gate, a_up, b_up, a_down, b_down))
+        orig_shape = x.shape
+        hidden_dim = x.shape[-1]
+        x_2d = x.reshape(-1, hidden_dim)
+
+        h_gate = F.linear(x_2d, w_gate)                                  # :1962-1967
+        xa_g = None
+        if a_gate is not None:
+            xa_g = F.linear(x_2d, a_gate)
+            h_gate = h_gate + s_gate * F.linear(xa_g, b_gate)
+        if m_gate is not None:
+            h_gate = dora_scale(h_gate, m_gate, nu_gate)
+        h_up = F.linear(x_2d, w_up)                                      # :1969-1975
+        xa_u = None
+        if a_up is not None:
+            xa_u = F.linear(x_2d, a_up)
+            h_up = h_up + s_up * F.linear(xa_u, b_up)
+        if m_up is not None:
+            h_up = dora_scale(h_up, m_up, nu_up)
+
+        c_gate = qs_gate = c_up = qs_up = None
+        fused_quant = (cache_mode in ("int4", "int8") and use_triton
+                       and h_gate.dtype == torch.bfloat16)               # :1979-1981
+        if fused_quant:
+            bits = 4 if cache_mode == "int4" else 8
+            h_mid, c_gate, qs_gate, c_up, qs_up = triton_silu_mul_quant(
+                h_gate, h_up, bits, group_size)
+        else:
+            h_mid = triton_silu_mul(h_gate, h_up)
+
+        y = F.linear(h_mid, w_down)                                      # :1990-1996
+        ha_d = None
+        if a_down is not None:
+            ha_d = F.linear(h_mid, a_down)
+            y = y + s_down * F.linear(ha_d, b_down)
+        if m_down is not None:
+            y = dora_scale(y, m_down, nu_down)
+
+        if not fused_quant:                                              # :1998-2007
+            if cache_mode in ("int4", "int8"):
+                bits = 4 if cache_mode == "int4" else 8
+                c_gate, qs_gate = v3_quantize_group_absmax(h_gate, bits, group_size)
+                c_up, qs_up = v3_quantize_group_absmax(h_up, bits, group_size)
+            elif cache_mode == "bf16":
+                c_gate, c_up = h_gate, h_up
+
+        ctx.save_for_backward(x, w_gate, a_gate, b_gate, m_gate, nu_gate,
+                              w_up, a_up, b_up, m_up, nu_up,
+                              w_down, a_down, b_down, m_down, nu_down,
+                              xa_g, xa_u, ha_d, c_gate, qs_gate, c_up, qs_up)
+        ctx.s = (s_gate, s_up, s_down)
+        ctx.cache_mode = cache_mode
+        ctx.group_size = group_size
+        ctx.use_triton = fused_quant
+        ctx.orig_shape = orig_shape
+        ctx.in_dtype = x.dtype
+        if len(orig_shape) == 3:
+            y = y.view(orig_shape[0], orig_shape[1], hidden_dim)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        (x, w_gate, a_gate, b_gate, m_gate, nu_gate, w_up, a_up, b_up, m_up, nu_up,
+         w_down, a_down, b_down, m_down, nu_down,
+         xa_g, xa_u, ha_d, cq_gate, qs_gate, cq_up, qs_up) = ctx.saved_tensors
+        s_gate, s_up, s_down = ctx.s
+        mode = ctx.cache_mode
+        hidden_dim = ctx.orig_shape[-1]
+        ng = ctx.needs_input_grad
+        need_x = ng[0]
+        need_wg, need_ag, need_bg, need_mg = ng[1], ng[2], ng[3], ng[4]
+        need_wu, need_au, need_bu, need_mu = ng[6], ng[7], ng[8], ng[9]
+        need_wd, need_ad, need_bd, need_md = ng[11], ng[12], ng[13], ng[14]
+        gy = grad_y.reshape(-1, hidden_dim)
+        x_2d = x.reshape(-1, hidden_dim)
+        bits = 4 if mode == "int4" else 8
+
+        need_gate_path = (need_x or need_wg or need_ag or need_bg or need_mg
+                          or need_wu or need_au or need_bu or need_mu)   # :2047-2048
+        need_h_mid = need_wd or need_md or (a_down is not None and need_ad)
+        need_recon = need_gate_path or need_h_mid
+        use_k2 = mode in ("int4", "int8") and ctx.use_triton and need_gate_path
+
+        hg = hu = raw_g = raw_u = None
+        if need_recon and not use_k2:                                    # :2055-2078
+            if mode == "recompute":
+                raw_g = F.linear(x_2d, w_gate)
+                if a_gate is not None:
+                    raw_g = raw_g + s_gate * F.linear(xa_g, b_gate)
+                hg = dora_scale(raw_g, m_gate, nu_gate) if m_gate is not None else raw_g
+                raw_u = F.linear(x_2d, w_up)
+                if a_up is not None:
+                    raw_u = raw_u + s_up * F.linear(xa_u, b_up)
+                hu = dora_scale(raw_u, m_up, nu_up) if m_up is not None else raw_u
+            elif mode == "bf16":
+                hg, hu = cq_gate, cq_up
+            else:
+                hg = v3_dequantize_group_absmax(cq_gate, qs_gate, bits, ctx.group_size,
+                                                ctx.in_dtype)
+                hu = v3_dequantize_group_absmax(cq_up, qs_up, bits, ctx.group_size,
+                                                ctx.in_dtype)
+        elif use_k2 and (need_mg or need_mu):                            # :2079-2089
+            if need_mg:
+                hg = v3_dequantize_group_absmax(cq_gate, qs_gate, bits, ctx.group_size,
+                                                ctx.in_dtype)
+            if need_mu:
+                hu = v3_dequantize_group_absmax(cq_up, qs_up, bits, ctx.group_size,
+                                                ctx.in_dtype)
+
+        g_eff_y = dora_scale(gy, m_down, nu_down) if m_down is not None else gy   # :2094
+        gyB_d = None
+        if a_down is not None and (need_gate_path or need_ad):
+            gyB_d = g_eff_y @ b_down
+
+        grad_h_gate = grad_h_up = h_mid_hat = None
+        if use_k2:                                                       # :2101-2110
+            grad_h_mid = g_eff_y @ w_down
+            if a_down is not None:
+                grad_h_mid = grad_h_mid + s_down * (gyB_d @ a_down)
+            grad_h_gate, grad_h_up, h_mid_hat = triton_dequant_swiglu_backward(
+                grad_h_mid, cq_gate, qs_gate, cq_up, qs_up, bits, ctx.group_size,
+                want_h_mid=need_h_mid)
+
+        grad_w_down = grad_a_down = grad_b_down = grad_m_down = None
+        if need_h_mid:                                                   # :2112-2131
+            if h_mid_hat is None:
+                h_mid_hat = triton_silu_mul(hg, hu)
+            if need_wd:
+                grad_w_down = g_eff_y.t() @ h_mid_hat
+            if need_ad:
+                grad_a_down = s_down * (gyB_d.t() @ h_mid_hat)
+            if need_md:
+                raw_d = F.linear(h_mid_hat, w_down)
+                if a_down is not None:
+                    raw_d = raw_d + s_down * F.linear(ha_d, b_down)
+                grad_m_down = col_dot_div(gy, raw_d, nu_down)
+        if need_bd:
+            grad_b_down = s_down * (g_eff_y.t() @ ha_d)
+
+        grad_x = None
+        grad_w_gate = grad_a_gate = grad_b_gate = grad_m_gate = None
+        grad_w_up = grad_a_up = grad_b_up = grad_m_up = None
+        if need_gate_path:                                               # :2134-2191
+            if grad_h_gate is None:
+                grad_h_mid = g_eff_y @ w_down
+                if a_down is not None:
+                    grad_h_mid = grad_h_mid + s_down * (gyB_d @ a_down)
+                grad_h_gate, grad_h_up = triton_swiglu_backward(grad_h_mid, hg, hu)
+            if need_mg:
+                grad_m_gate = (col_dot_div(grad_h_gate, raw_g, nu_gate) if raw_g is not None
+                               else col_dot_div(grad_h_gate, hg, m_gate))
+            if need_mu:
+                grad_m_up = (col_dot_div(grad_h_up, raw_u, nu_up) if raw_u is not None
+                             else col_dot_div(grad_h_up, hu, m_up))
+            g_eff_g = dora_scale(grad_h_gate, m_gate, nu_gate) if m_gate is not None else grad_h_gate
+            g_eff_u = dora_scale(grad_h_up, m_up, nu_up) if m_up is not None else grad_h_up
+            ghgB = g_eff_g @ b_gate if a_gate is not None and (need_x or need_ag) else None
+            ghuB = g_eff_u @ b_up if a_up is not None and (need_x or need_au) else None
+            if need_x:
+                grad_x = g_eff_g @ w_gate
+                if a_gate is not None:
+                    grad_x = grad_x + s_gate * (ghgB @ a_gate)
+                grad_x = grad_x + g_eff_u @ w_up
+                if a_up is not None:
+                    grad_x = grad_x + s_up * (ghuB @ a_up)
+            if need_bg:
+                grad_b_gate = s_gate * (g_eff_g.t() @ xa_g)
+            if need_ag:
+                grad_a_gate = s_gate * (ghgB.t() @ x_2d)
+            if need_bu:
+                grad_b_up = s_up * (g_eff_u.t() @ xa_u)
+            if need_au:
+                grad_a_up = s_up * (ghuB.t() @ x_2d)
+            if need_wg:
+                grad_w_gate = g_eff_g.t() @ x_2d
+            if need_wu:
+                grad_w_up = g_eff_u.t() @ x_2d
+
+        if need_x and len(ctx.orig_shape) == 3:
+            grad_x = grad_x.view(ctx.orig_shape)
+        return (grad_x,
+                grad_w_gate, grad_a_gate, grad_b_gate, grad_m_gate, None,
+                grad_w_up, grad_a_up, grad_b_up, grad_m_up, None,
+                grad_w_down, grad_a_down, grad_b_down, grad_m_down, None,
+                ) + (None,) * (len(ctx.needs_input_grad) - 16)
+
+
+ADAPTER_KINDS = ("dora", "adalora", "vera", "dylora")
+
+
+def synthetic_adapter_set(kind: str, h: int, d: int, rank: int, alpha: float, seed: int,
+                          dtype=torch.bfloat16):
+    """Seeded raw parameters of one adapter family on gate/up/down, after the
+    reference's non-degenerate initialisation (src/verify_v3_adapters.py:101-149):
+    W ~ N(0, 0.02); B ~ N(0, 0.02); DoRA m = ||W_j|| * (1 + 0.2 N(0, 1));
+    AdaLoRA E ~ N(0, 0.5), ranknum = rank; VeRA lambda_d = 0.1 + 0.05 N,
+    lambda_b ~ N(0, 0.05) with shared frozen A, B; DyLoRA ranks b per projection."""
+    g = torch.Generator().manual_seed(seed)
+    ps = {"kind": kind}
+    dims = {"gate": (h, d), "up": (h, d), "down": (d, h)}
+    for key, (d_in, d_out) in dims.items():
+        w = torch.randn(d_out, d_in, generator=g) * 0.02
+        p = {"w": w.to(dtype)}
+        bound = 1.0 / np.sqrt(d_in)
+        a = (torch.rand(rank, d_in, generator=g) * 2 - 1) * bound
+        b = torch.randn(d_out, rank, generator=g) * 0.02
+        if kind == "dora":
+            p["a"], p["b"], p["s"] = a.to(dtype), b.to(dtype), alpha / rank
+            m = w.to(dtype).float().norm(dim=1) * (1.0 + 0.2 * torch.randn(d_out, generator=g))
+            p["m"] = m.to(dtype)
+        elif kind == "adalora":
+            p["a"], p["b"] = a.to(dtype), b.to(dtype)
+            p["e"] = (torch.randn(rank, 1, generator=g) * 0.5).to(dtype)
+            p["s_eff"] = (alpha / rank) / (float(rank) + 1e-5)
+        elif kind == "vera":
+            p["a_frozen"], p["b_frozen"] = a.to(dtype), b.to(dtype)
+            p["lam_d"] = (0.1 + 0.05 * torch.randn(rank, generator=g)).to(dtype)
+            p["lam_b"] = (torch.randn(d_out, generator=g) * 0.05).to(dtype)
+        elif kind == "dylora":
+            p["a"], p["b"], p["s"] = a.to(dtype), b.to(dtype), alpha / rank
+            p["b_rank"] = int(torch.randint(1, rank + 1, (1,), generator=g))
+        else:
+            raise ValueError(kind)
+        ps[key] = p
+    return ps
+
+
+def adapter_trainables(ps):
+    """name -> tensor of every trainable adapter parameter (reference
+    src/verify_v3_adapters.py:153-176)."""
+    names = {"dora": ("a", "b", "m"), "adalora": ("a", "e", "b"), "vera": ("lam_d", "lam_b"),
+             "dylora": ("a", "b")}[ps["kind"]]
+    return {f"{key}.{n}": ps[key][n] for key in PROJ for n in names}
+
+
+def adapter_factors(p, kind, leaves):
+    """The Function's factored arguments (w, a, b, s, m, nu) of one
+    projection from leaf tensors, composed in autograd like
+    _v3_extract_proj_adapter (src/flashffn.py:1850-1921).  `leaves` maps the
+    raw names of `p` to (possibly grad-tracking) tensors."""
+    w = p["w"]
+    if kind == "dora":
+        a, b, s, m = leaves["a"], leaves["b"], p["s"], leaves["m"]
+        nu = dora_col_norm(w, a.detach(), b.detach(), s).to(w.dtype)
+        return w, a, b, s, m, nu
+    if kind == "adalora":
+        return w, leaves["a"] * leaves["e"], leaves["b"], p["s_eff"], None, None
+    if kind == "vera":
+        a_eff = leaves["lam_d"].unsqueeze(-1) * p["a_frozen"]
+        b_eff = leaves["lam_b"].unsqueeze(-1) * p["b_frozen"]
+        return w, a_eff, b_eff, 1.0, None, None
+    if kind == "dylora":
+        r = p["b_rank"]
+        return w, leaves["a"][:r, :], leaves["b"][:, :r], p["s"], None, None
+    raise ValueError(kind)
+
+
+def run_adapter_grads(fn_apply, ps, x, gy, mode: str, group_size: int, use_triton: bool = True):
+    """Run an adapter Function (oracle or product) on leaf clones of the
+    trainables of `ps` (their device is x's).  Returns ({name: grad}, y)."""
+    kind = ps["kind"]
+    xl = x.detach().clone().requires_grad_(True)
+    leaves, args = {}, []
+    for key in PROJ:
+        p = {k: (v.to(x.device) if isinstance(v, torch.Tensor) else v) for k, v in ps[key].items()}
+        lv = {n: p[n].detach().clone().requires_grad_(True)
+              for n in ("a", "b", "m", "e", "lam_d", "lam_b") if n in p
+              and not (kind == "vera" and n in ("a", "b"))}
+        for n, t in lv.items():
+            leaves[f"{key}.{n}"] = t
+        w, a, b, s, m, nu = adapter_factors(p, kind, lv)
+        args.append((w, a, b, m, nu, s))
+    (wg, ag, bg, mg, nug, sg), (wu, au, bu, mu, nuu, su), (wd, ad, bd, md, nud, sd) = args
+    y = fn_apply(xl, wg, ag, bg, mg, nug, wu, au, bu, mu, nuu, wd, ad, bd, md, nud,
+                 sg, su, sd, mode, group_size, use_triton)
+    y.backward(gy)
+    grads = {"grad_x": xl.grad}
+    for k, t in leaves.items():
+        grads[k] = t.grad
+    return grads, y.detach()
+
+
+def ref_adapter_grads_fp32(ps, x, gy):
+    """fp32 plain autograd of the adapter families' own forward
+    (src/verify_v3_adapters.py:204-258): DoRA c = m / ||W + s B A||.detach()
+    (PEFT DoraLinearLayer), AdaLoRA (A*E) with s / (ranknum + 1e-5), VeRA
+    lambda_b * ((x A^T) * lambda_d) B^T, DyLoRA rank-b slices."""
+    kind = ps["kind"]
+    xl = x.detach().float().requires_grad_(True)
+    leaves = {}
+
+    def leaf(key, n):
+        t = ps[key][n].detach().float().requires_grad_(True)
+        leaves[f"{key}.{n}"] = t
+        return t
+
+    def proj(z, key):
+        p = ps[key]
+        w = p["w"].float()
+        if kind == "dora":
+            a, b, m = leaf(key, "a"), leaf(key, "b"), leaf(key, "m")
+            nu = (w + p["s"] * (b @ a)).detach().norm(p=2, dim=1)
+            raw = F.linear(z, w) + p["s"] * F.linear(F.linear(z, a), b)
+            return raw * (m / nu).unsqueeze(0)
+        if kind == "adalora":
+            a, e, b = leaf(key, "a"), leaf(key, "e"), leaf(key, "b")
+            return F.linear(z, w) + p["s_eff"] * F.linear(F.linear(z, a * e), b)
+        if kind == "vera":
+            ld, lb = leaf(key, "lam_d"), leaf(key, "lam_b")
+            u = F.linear(z, p["a_frozen"].float()) * ld
+            return F.linear(z, w) + F.linear(u, p["b_frozen"].float()) * lb
+        if kind == "dylora":
+            a, b = leaf(key, "a"), leaf(key, "b")
+            r = p["b_rank"]
+            return F.linear(z, w) + p["s"] * F.linear(F.linear(z, a[:r, :]), b[:, :r])
+        raise ValueError(kind)
+
+    h_mid = F.silu(proj(xl, "gate")) * proj(xl, "up")
+    y = proj(h_mid, "down")
+    y.backward(gy.detach().float())
+    grads = {"grad_x": xl.grad}
+    grads.update({k: t.grad for k, t in leaves.items()})
+    return grads, y.detach()

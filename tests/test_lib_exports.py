@@ -43,7 +43,8 @@ def test_python_binding_covers_header(lib):
     for name in declared_symbols():
         if name in ("cpt_status_string", "cpt_abi_version"):
             continue
-        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+        assert name in _lib.SIGNATURES or name in _lib.SIZE_QUERIES, \
+            f"{name} has no ctypes signature"
 
 
 def test_status_strings_and_version(lib):
@@ -64,6 +65,20 @@ def test_argument_errors_need_no_gpu(lib):
     assert rc == _lib.ERR_BITS
     with pytest.raises(AssertionError):
         _lib.check(rc, "probe")
+    assert lib.cpt_dora_scale(None, None, None, 4, 8, 9, None, None) == _lib.ERR_DTYPE
+    assert lib.cpt_dora_scale(None, None, None, -1, 8, 2, None, None) == _lib.ERR_SHAPE
+    assert lib.cpt_col_dot_div(None, None, None, 4, 8, 2, None, None, None) == _lib.ERR_SHAPE
+    assert lib.cpt_dora_col_norm(None, None, None, 4, 8, 2, 1.0, 2, None, None, 2,
+                                 None) == _lib.ERR_SHAPE
+
+
+def test_workspace_size_queries(lib):
+    """Workspaces: fp32 partials per 128-row chunk for the column dot; ||W||^2,
+    W A^T and A A^T for the DoRA norm."""
+    assert lib.cpt_col_dot_workspace_bytes(1000, 24) == 8 * 24 * 4
+    assert lib.cpt_col_dot_workspace_bytes(0, 24) == 24 * 4
+    assert lib.cpt_dora_col_norm_workspace_bytes(100, 8) == (100 + 800 + 64) * 4
+    assert lib.cpt_dora_col_norm_workspace_bytes(-1, 8) == -1
 
 
 def test_product_refuses_cpu_tensors():
