@@ -14,9 +14,10 @@ from .kernels import (  # noqa: F401
     triton_silu_mul_quant, triton_dequant_swiglu_backward,
     outlier_select, v3_quantize_outlier, v3_dequantize_outlier, silu_mul_quant_outlier,
     dequant_swiglu_backward_outlier, dora_scale, col_dot_div, dora_col_norm,
+    topk_abs, topk_scatter,
 )
 from .flashffn import (  # noqa: F401
     FlashFFNv3Function, FlashFFNv3, make_v3_forward, _v3_extract_proj, _v3_proj_kind,
     FlashFFNv3AdapterFunction, make_v3_adapter_forward, _v3_extract_proj_adapter,
-    _v3_dora_col_norm,
+    _v3_dora_col_norm, FlashFFNFunction, FlashFFN, StandardFFN,
 )

@@ -42,6 +42,8 @@ SIGNATURES = {
     "cpt_dora_scale": [_P, _P, _P, _L, _L, _I, _P, _P],
     "cpt_col_dot_div": [_P, _P, _P, _L, _L, _I, _P, _P, _P],
     "cpt_dora_col_norm": [_P, _P, _P, _L, _L, _L, ctypes.c_double, _I, _P, _P, _I, _P],
+    "cpt_topk_abs": [_P, _I, _L, _L, _L, _P, _P, _P],
+    "cpt_topk_scatter": [_P, _P, _I, _L, _L, _L, _P, _P],
 }
 
 # size queries: name -> argument types (restype int64)

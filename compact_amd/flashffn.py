@@ -775,3 +775,154 @@ def make_v3_adapter_forward(mlp: nn.Module, cache_mode: str = "int4", group_size
                                                wd, ad, bd, md, nud, sg, su, sd, cache_mode,
                                                group_size, use_triton)
     return v3_adapter_forward
+
+
+# ---------------------------------------------------------------------------
+# v1/v2 API: FlashFFNFunction with top-K compression, FlashFFN, StandardFFN
+# (src/flashffn.py:300-519)
+# ---------------------------------------------------------------------------
+
+def _gate_up(x_2d, w_gate, w_up, keep: bool):
+    """(h_mid, h_gate | None, h_up | None): the fused dual GEMM + GLU on the
+    engine for bf16, the library GEMMs + the GLU kernel otherwise."""
+    if _mfma(x_2d, w_gate, w_up) and x_2d.shape[0] > 0:
+        h_mid, hg, hu, *_ = G.ffn_gate_up(x_2d, w_gate, w_up,
+                                          _lib.CACHE_BF16 if keep else _lib.CACHE_NONE, 64)
+        return h_mid, hg, hu
+    hg = _linear(x_2d, w_gate, "gemm_fwd_gate")
+    hu = _linear(x_2d, w_up, "gemm_fwd_up")
+    return K.silu_mul(hg, hu), (hg if keep else None), (hu if keep else None)
+
+
+def _glu_backward(gy, w_down, hg, hu):
+    """(grad_h_gate, grad_h_up) of h_mid = SiLU(hg) * hu through y = h_mid W_d^T."""
+    if _mfma(gy, w_down, hg, hu) and gy.shape[0] > 0:
+        dg, du, _ = G.ffn_down_dgrad(gy, w_down, _lib.CACHE_BF16, 64, hg, None, hu, None, False)
+        return dg, du
+    return K.swiglu_backward(_mm(gy, w_down, "gemm_dgrad_down"), hg, hu)
+
+
+def _dgrad_x(dg, w_gate, du, w_up):
+    if _mfma(dg, w_gate, du, w_up):
+        return G.mm2(dg, w_gate, du, w_up, "gemm_dgrad_x")
+    return dg @ w_gate + du @ w_up
+
+
+class FlashFFNFunction(torch.autograd.Function):
+    """SwiGLU FFN with top-K activation compression (src/flashffn.py:300-449).
+
+    The mode follows the weights' requires_grad, as in the reference:
+      'recompute' (some weight trains): saves x and, per token, the
+          k = max(1, int(D * k_fraction)) entries of h_mid with the largest
+          magnitude (values + int16 columns).  Backward: grad_w_down from the
+          sparse h_mid (approximate by design), every other grad exact from
+          recomputed h_gate / h_up;
+      'activations' (all weights frozen): saves h_gate and h_up; backward
+          returns grad_x only.
+    Device path: the fused dual GEMM + GLU forward and the fused dgrad GEMM +
+    SwiGLU backward on the MFMA engine (bf16), the top-K select and scatter
+    kernels; library GEMMs + the GLU kernels for other dtypes."""
+
+    @staticmethod
+    def forward(ctx, x, w_gate, w_up, w_down, k_fraction=0.3):
+        K._require_device(x)
+        orig_shape = x.shape
+        hidden_dim = x.shape[-1]
+        inter = w_gate.shape[0]
+        x_2d = x.reshape(-1, hidden_dim)
+        if not x_2d.is_contiguous():
+            x_2d = x_2d.contiguous()
+        weights_need_grad = w_gate.requires_grad or w_up.requires_grad or w_down.requires_grad
+        h_mid, h_gate, h_up = _gate_up(x_2d, w_gate, w_up, keep=not weights_need_grad)
+        y = _linear(h_mid, w_down, "gemm_fwd_down")
+        if weights_need_grad:                                              # :349-361
+            k = max(1, int(inter * k_fraction))
+            values, indices = K.topk_abs(h_mid, k)
+            ctx.save_for_backward(x, w_gate, w_up, w_down, values, indices)
+            ctx.save_mode = "recompute"
+            ctx.k = k
+            ctx.intermediate_dim = inter
+        else:                                                              # :362-366
+            ctx.save_for_backward(h_gate, h_up, w_gate, w_up, w_down)
+            ctx.save_mode = "activations"
+        del h_mid
+        ctx.orig_shape = orig_shape
+        if len(orig_shape) == 3:
+            y = y.view(orig_shape[0], orig_shape[1], hidden_dim)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        orig_shape = ctx.orig_shape
+        hidden_dim = orig_shape[-1]
+        gy = grad_output.reshape(-1, hidden_dim)
+        if not gy.is_contiguous():
+            gy = gy.contiguous()
+        if ctx.save_mode == "activations":                                 # :386-405
+            h_gate, h_up, w_gate, w_up, w_down = ctx.saved_tensors
+            dg, du = _glu_backward(gy, w_down, h_gate, h_up)
+            grad_x = _dgrad_x(dg, w_gate, du, w_up)
+            if len(orig_shape) == 3:
+                grad_x = grad_x.view(orig_shape)
+            return grad_x, None, None, None, None
+
+        x, w_gate, w_up, w_down, values, indices = ctx.saved_tensors      # :407-449
+        x_2d = x.reshape(-1, hidden_dim)
+        if not x_2d.is_contiguous():
+            x_2d = x_2d.contiguous()
+        need_x, need_wg, need_wu, need_wd = ctx.needs_input_grad[:4]
+        grad_w_down = None
+        if need_wd:
+            h_mid_sparse = K.topk_scatter(values, indices, ctx.intermediate_dim)
+            grad_w_down = _mm(gy.t(), h_mid_sparse, "gemm_wgrad_down")
+            del h_mid_sparse
+        grad_x = grad_w_gate = grad_w_up = None
+        if need_x or need_wg or need_wu:
+            _, hg, hu = _gate_up(x_2d, w_gate, w_up, keep=True)
+            dg, du = _glu_backward(gy, w_down, hg, hu)
+            del hg, hu
+            if need_wg:
+                grad_w_gate = _mm(dg.t(), x_2d, "gemm_wgrad_gate")
+            if need_wu:
+                grad_w_up = _mm(du.t(), x_2d, "gemm_wgrad_up")
+            if need_x:
+                grad_x = _dgrad_x(dg, w_gate, du, w_up)
+        if need_x and len(orig_shape) == 3:
+            grad_x = grad_x.view(orig_shape)
+        return grad_x, grad_w_gate, grad_w_up, grad_w_down, None
+
+
+class FlashFFN(nn.Module):
+    """SwiGLU FFN module over FlashFFNFunction (src/flashffn.py:456-496).
+    As in the reference, `bias` creates bias parameters that the compressed
+    forward does not use."""
+
+    def __init__(self, hidden_dim: int, intermediate_dim: int, k_fraction: float = 0.3,
+                 bias: bool = False):
+        super().__init__()
+        self.hidden_dim = hidden_dim
+        self.intermediate_dim = intermediate_dim
+        self.k_fraction = k_fraction
+        self.gate_proj = nn.Linear(hidden_dim, intermediate_dim, bias=bias)
+        self.up_proj = nn.Linear(hidden_dim, intermediate_dim, bias=bias)
+        self.down_proj = nn.Linear(intermediate_dim, hidden_dim, bias=bias)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return FlashFFNFunction.apply(x, self.gate_proj.weight, self.up_proj.weight,
+                                      self.down_proj.weight, self.k_fraction)
+
+
+class StandardFFN(nn.Module):
+    """The unfused SwiGLU FFN the reference compares against
+    (src/flashffn.py:499-519): torch modules and autograd, no compression."""
+
+    def __init__(self, hidden_dim: int, intermediate_dim: int, bias: bool = False):
+        super().__init__()
+        self.gate_proj = nn.Linear(hidden_dim, intermediate_dim, bias=bias)
+        self.up_proj = nn.Linear(hidden_dim, intermediate_dim, bias=bias)
+        self.down_proj = nn.Linear(intermediate_dim, hidden_dim, bias=bias)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        h_gate = self.gate_proj(x)
+        h_up = self.up_proj(x)
+        return self.down_proj(F.silu(h_gate) * h_up)

@@ -472,3 +472,42 @@ def dora_col_norm(w: torch.Tensor, a: torch.Tensor, b: torch.Tensor, s: float,
                                  _DT[out_dtype], _stream(w))
     check(rc, "dora_col_norm")
     return nu
+
+
+# ---------------------------------------------------------------------------
+# top-K activation compression (FlashFFN v1/v2, src/flashffn.py:349-356,410-415)
+# ---------------------------------------------------------------------------
+
+def topk_abs(t: torch.Tensor, k: int):
+    """Per row of t [N, D]: the k entries of largest |t| -> (values [N, k] in
+    t's dtype, indices int16 [N, k]) in ascending column order, ties at the
+    k-th magnitude resolved to the lowest columns (torch.topk's sorted=False
+    order and tie choice are unspecified; this fixes both)."""
+    _require_device(t)
+    assert t.dim() == 2, "topk_abs expects [N, D]"
+    t = t.contiguous()
+    n, d = t.shape
+    assert 0 <= k <= d, f"k={k} out of range for D={d}"
+    values = torch.empty((n, k), dtype=t.dtype, device=t.device)
+    indices = torch.empty((n, k), dtype=torch.int16, device=t.device)
+    with _timed("topk_abs"):
+        rc = _lib.lib().cpt_topk_abs(t.data_ptr(), _dtype_code(t), n, d, k, values.data_ptr(),
+                                     indices.data_ptr(), _stream(t))
+    check(rc, "topk_abs")
+    return values, indices
+
+
+def topk_scatter(values: torch.Tensor, indices: torch.Tensor, d: int) -> torch.Tensor:
+    """Dense [N, d] rows with `values` at `indices` and zeros elsewhere
+    (`zeros(...).scatter_(-1, indices.long(), values)`)."""
+    _require_device(values, indices)
+    assert values.shape == indices.shape and indices.dtype == torch.int16
+    values, indices = values.contiguous(), indices.contiguous()
+    n, k = values.shape
+    out = torch.empty((n, d), dtype=values.dtype, device=values.device)
+    with _timed("topk_scatter"):
+        rc = _lib.lib().cpt_topk_scatter(values.data_ptr(), indices.data_ptr(),
+                                         _dtype_code(values), n, d, k, out.data_ptr(),
+                                         _stream(values))
+    check(rc, "topk_scatter")
+    return out

@@ -217,6 +217,22 @@ int cpt_dora_col_norm(const void* w, const void* a, const void* b, int64_t rows,
                       int64_t r, double s, int dtype, void* workspace, void* nu, int nu_dtype,
                       void* stream);
 
+/* ---------------- top-K activation compression (FlashFFN v1/v2 API) ---------------- */
+
+/* Replaces `torch.topk(h_mid.abs(), k, dim=-1, sorted=False)` + gather + the
+ * int16 index cast of FlashFFNFunction (src/flashffn.py:349-356): per row of
+ * t [n, d], the k entries of largest magnitude -> values [n, k] (t's dtype)
+ * and columns indices [n, k] int16, in ascending column order; of entries
+ * tied at the k-th magnitude the lowest columns are kept.  d <= 32767. */
+int cpt_topk_abs(const void* t, int dtype, int64_t n, int64_t d, int64_t k, void* values,
+                 void* indices, void* stream);
+
+/* Replaces `zeros(n, d).scatter_(-1, indices, values)` (src/flashffn.py:
+ * 410-415): out [n, d] = values at their columns, zero elsewhere.
+ * d <= 32767 and d * sizeof(dtype) <= 64 KiB (one row is assembled in LDS). */
+int cpt_topk_scatter(const void* values, const void* indices, int dtype, int64_t n, int64_t d,
+                     int64_t k, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

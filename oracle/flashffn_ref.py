@@ -841,3 +841,96 @@ def ref_adapter_grads_fp32(ps, x, gy):
     grads = {"grad_x": xl.grad}
     grads.update({k: t.grad for k, t in leaves.items()})
     return grads, y.detach()
+
+
+# ---------------------------------------------------------------------------
+# v1/v2 API with top-K compression (src/flashffn.py:300-519)
+# ---------------------------------------------------------------------------
+
+
+def topk_abs(t: torch.Tensor, k: int):
+    """Per row: the k entries of largest |t| in ascending column order, ties
+    at the k-th magnitude to the lowest columns (a fixed choice of
+    `torch.topk(t.abs(), k, sorted=False)`, src/flashffn.py:353-356).
+    Returns (values in t's dtype, indices int16)."""
+    a = to_f32(t)
+    n, d = a.shape
+    mag = np.abs(a)
+    cols = np.broadcast_to(np.arange(d), (n, d))
+    # descending magnitude, then ascending column (lexsort: last key is primary)
+    order = np.lexsort((cols, -mag), axis=1)[:, :k]
+    order.sort(axis=1)
+    vals = np.take_along_axis(t.detach().cpu().contiguous().view(-1, d).numpy()
+                              if t.dtype == torch.float32 else
+                              t.detach().cpu().contiguous().view(torch.int16).numpy(),
+                              order, axis=1)
+    values = torch.from_numpy(np.ascontiguousarray(vals))
+    if t.dtype != torch.float32:
+        values = values.view(t.dtype)
+    return values, torch.from_numpy(order.astype(np.int16))
+
+
+def topk_scatter(values: torch.Tensor, indices: torch.Tensor, d: int):
+    """src/flashffn.py:410-415: zeros [N, d] with values scattered at indices."""
+    out = torch.zeros(values.shape[0], d, dtype=values.dtype)
+    out.scatter_(-1, indices.long(), values)
+    return out
+
+
+class OracleFlashFFNFunction(torch.autograd.Function):
+    """CPU restatement of FlashFFNFunction (src/flashffn.py:300-449): mode by
+    the weights' requires_grad; 'recompute' keeps the top-K of h_mid and
+    recomputes h_gate / h_up, 'activations' keeps h_gate / h_up."""
+
+    @staticmethod
+    def forward(ctx, x, w_gate, w_up, w_down, k_fraction=0.3):
+        orig_shape = x.shape
+        hidden_dim = x.shape[-1]
+        inter = w_gate.shape[0]
+        x_2d = x.reshape(-1, hidden_dim)
+        h_gate = F.linear(x_2d, w_gate)
+        h_up = F.linear(x_2d, w_up)
+        h_mid = triton_silu_mul(h_gate, h_up)
+        y = F.linear(h_mid, w_down)
+        if w_gate.requires_grad or w_up.requires_grad or w_down.requires_grad:
+            k = max(1, int(inter * k_fraction))
+            values, indices = topk_abs(h_mid, k)
+            ctx.save_for_backward(x, w_gate, w_up, w_down, values, indices)
+            ctx.save_mode = "recompute"
+            ctx.intermediate_dim = inter
+        else:
+            ctx.save_for_backward(h_gate, h_up, w_gate, w_up, w_down)
+            ctx.save_mode = "activations"
+        ctx.orig_shape = orig_shape
+        if len(orig_shape) == 3:
+            y = y.view(orig_shape[0], orig_shape[1], hidden_dim)
+        return y
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        orig_shape = ctx.orig_shape
+        hidden_dim = orig_shape[-1]
+        gy = grad_output.reshape(-1, hidden_dim)
+        if ctx.save_mode == "activations":
+            h_gate, h_up, w_gate, w_up, w_down = ctx.saved_tensors
+            dg, du = triton_swiglu_backward(gy @ w_down, h_gate, h_up)
+            grad_x = dg @ w_gate + du @ w_up
+            if len(orig_shape) == 3:
+                grad_x = grad_x.view(orig_shape)
+            return grad_x, None, None, None, None
+        x, w_gate, w_up, w_down, values, indices = ctx.saved_tensors
+        x_2d = x.reshape(-1, hidden_dim)
+        need_x, need_wg, need_wu, need_wd = ctx.needs_input_grad[:4]
+        grad_w_down = None
+        if need_wd:
+            grad_w_down = gy.t() @ topk_scatter(values, indices, ctx.intermediate_dim)
+        grad_x = grad_w_gate = grad_w_up = None
+        if need_x or need_wg or need_wu:
+            dg, du = triton_swiglu_backward(gy @ w_down, F.linear(x_2d, w_gate),
+                                            F.linear(x_2d, w_up))
+            grad_w_gate = dg.t() @ x_2d if need_wg else None
+            grad_w_up = du.t() @ x_2d if need_wu else None
+            grad_x = dg @ w_gate + du @ w_up if need_x else None
+        if need_x and len(orig_shape) == 3:
+            grad_x = grad_x.view(orig_shape)
+        return grad_x, grad_w_gate, grad_w_up, grad_w_down, None
