@@ -697,92 +697,120 @@ __device__ __forceinline__ void epi_glu(const KArgs& A, const Acc& acc, int64_t 
 // n-side = d: d = n0 + 128 wn + 32 i + 8 q + 4 (lane/32) + e.
 // ---------------------------------------------------------------------------
 template <int CACHE, int GS>
-__device__ __forceinline__ void epi_dglu(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0) {
+__device__ __forceinline__ void epi_dglu(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0,
+                                         uint16_t* lds) {
+  // B1: grad_h_mid = bf16(acc) is staged through LDS as a row-major
+  // 256 x 256 bf16 tile, then each row is processed by 32 consecutive threads
+  // owning 8 columns each, so every cache load and output store is a
+  // contiguous, coalesced row segment (the MFMA layout would scatter them
+  // over 32 rows per instruction).
   constexpr int BITS = CACHE == CACHE_INT4 ? 4 : 8;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int LD = 264;   // LDS row stride in bf16 (528 bytes)
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave & 1, wm = wave >> 1;
-  const int64_t D = A.D;
-  const int64_t G = D / GS;
-  const uint8_t* __restrict__ qg = A.q_gate;
-  const uint8_t* __restrict__ qu = A.q_up;
-  const uint16_t* __restrict__ sgp = A.s_gate;
-  const uint16_t* __restrict__ sup = A.s_up;
-  const uint16_t* __restrict__ hgp = A.h_gate;
-  const uint16_t* __restrict__ hup = A.h_up;
-  uint16_t* __restrict__ og_p = A.grad_gate;
-  uint16_t* __restrict__ ou_p = A.grad_up;
-  uint16_t* __restrict__ oh_p = A.h_mid_hat;
   static_for<0, 4>([&](auto j) {
-    const int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
-    const bool mok = m < A.M;
-    // 1) gather this row's cache words for all 16 runs (independent loads)
-    uint2 cw[4][4];     // [i][q]: .x gate, .y up (codes) or packed bf16 pairs
-    uint2 cw2[4][4];    // bf16 cache: second half of the 4 values
-    float sc[4][4][2];  // scales
+    const int ml = wm * 128 + j * 32 + (lane & 31);
     static_for<0, 4>([&](auto i) {
-      static_for<0, 4>([&](auto q) {
-        const int64_t d = n0 + wn * 128 + i * 32 + q * 8 + (lane >> 5) * 4;
-        const bool ok = mok && d < D;
-        if constexpr (CACHE == CACHE_BF16) {
-          const uint2 wg = ok ? *reinterpret_cast<const uint2*>(hgp + m * D + d) : make_uint2(0, 0);
-          const uint2 wu = ok ? *reinterpret_cast<const uint2*>(hup + m * D + d) : make_uint2(0, 0);
-          cw[i][q] = wg;
-          cw2[i][q] = wu;
-        } else {
-          sc[i][q][0] = ok ? f16_bits_to_f32(sgp[m * G + d / GS]) : 0.0f;
-          sc[i][q][1] = ok ? f16_bits_to_f32(sup[m * G + d / GS]) : 0.0f;
-          if constexpr (BITS == 8) {
-            cw[i][q].x = ok ? *reinterpret_cast<const uint32_t*>(qg + m * D + d) : 0u;
-            cw[i][q].y = ok ? *reinterpret_cast<const uint32_t*>(qu + m * D + d) : 0u;
-          } else {
-            cw[i][q].x = ok ? *reinterpret_cast<const uint16_t*>(qg + m * (D >> 1) + (d >> 1)) : 0u;
-            cw[i][q].y = ok ? *reinterpret_cast<const uint16_t*>(qu + m * (D >> 1) + (d >> 1)) : 0u;
-          }
-        }
-      });
-    });
-    // 2) dequantise, SwiGLU backward, store
-    static_for<0, 4>([&](auto i) {
-      static_for<0, 4>([&](auto q) {
-        const int64_t d = n0 + wn * 128 + i * 32 + q * 8 + (lane >> 5) * 4;
-        if (!mok || d >= D) return;
-        float hg[4], hu[4];
-        if constexpr (CACHE == CACHE_BF16) {
-          const uint2 wg = cw[i][q], wu = cw2[i][q];
-          hg[0] = __uint_as_float(wg.x << 16); hg[1] = __uint_as_float(wg.x & 0xFFFF0000u);
-          hg[2] = __uint_as_float(wg.y << 16); hg[3] = __uint_as_float(wg.y & 0xFFFF0000u);
-          hu[0] = __uint_as_float(wu.x << 16); hu[1] = __uint_as_float(wu.x & 0xFFFF0000u);
-          hu[2] = __uint_as_float(wu.y << 16); hu[3] = __uint_as_float(wu.y & 0xFFFF0000u);
-        } else if constexpr (BITS == 8) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            hg[e] = round_bf16((float)(int8_t)((cw[i][q].x >> (8 * e)) & 0xFFu) * sc[i][q][0]);
-            hu[e] = round_bf16((float)(int8_t)((cw[i][q].y >> (8 * e)) & 0xFFu) * sc[i][q][1]);
-          }
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            hg[e] = round_bf16(((float)((cw[i][q].x >> (4 * e)) & 0xFu) - 8.0f) * sc[i][q][0]);
-            hu[e] = round_bf16(((float)((cw[i][q].y >> (4 * e)) & 0xFu) - 8.0f) * sc[i][q][1]);
-          }
-        }
-        float og[4], ou[4], oh[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float hact;
-          swiglu_bwd1(round_bf16(acc.v[i][j][q * 4 + e]), hg[e], hu[e], og[e], ou[e], hact);
-          oh[e] = hact * hu[e];
-        }
-        *reinterpret_cast<uint2*>(og_p + m * D + d) =
-            make_uint2(pack_bf16x2(og[0], og[1]), pack_bf16x2(og[2], og[3]));
-        *reinterpret_cast<uint2*>(ou_p + m * D + d) =
-            make_uint2(pack_bf16x2(ou[0], ou[1]), pack_bf16x2(ou[2], ou[3]));
-        if (oh_p)
-          *reinterpret_cast<uint2*>(oh_p + m * D + d) =
-              make_uint2(pack_bf16x2(oh[0], oh[1]), pack_bf16x2(oh[2], oh[3]));
+      const f32x16& a = acc.v[i][j];
+      static_for<0, 4>([&](auto g) {
+        const int nl = wn * 128 + i * 32 + g * 8 + (lane >> 5) * 4;
+        *reinterpret_cast<uint2*>(lds + ml * LD + nl) =
+            make_uint2(pack_bf16x2(a[g * 4 + 0], a[g * 4 + 1]), pack_bf16x2(a[g * 4 + 2], a[g * 4 + 3]));
       });
     });
   });
+  __syncthreads();
+  const int64_t D = A.D;
+  const int64_t G = D / GS;
+  const int cl = (tid & 31) * 8;
+  const int64_t d = n0 + cl;           // D % 8 == 0: the 8 columns are all in or all out
+  const bool dok = d < D;
+  constexpr int UNROLL = 4;
+#pragma unroll 1
+  for (int p0 = 0; p0 < 32; p0 += UNROLL) {
+    uint4 dh[UNROLL];
+    uint4 cg[UNROLL], cu[UNROLL];    // codes (low bytes used) or bf16 cache
+    float sgv[UNROLL], suv[UNROLL];
+    bool ok[UNROLL];
+    int64_t mrow[UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      const int r = (p0 + u) * 8 + (tid >> 5);
+      const int64_t m = m0 + r;
+      mrow[u] = m;
+      ok[u] = dok && m < A.M;
+      dh[u] = *reinterpret_cast<const uint4*>(lds + r * LD + cl);
+      cg[u] = cu[u] = make_uint4(0, 0, 0, 0);
+      sgv[u] = suv[u] = 0.0f;
+      if (ok[u]) {
+        if constexpr (CACHE == CACHE_BF16) {
+          cg[u] = *reinterpret_cast<const uint4*>(A.h_gate + m * D + d);
+          cu[u] = *reinterpret_cast<const uint4*>(A.h_up + m * D + d);
+        } else {
+          sgv[u] = f16_bits_to_f32(A.s_gate[m * G + d / GS]);
+          suv[u] = f16_bits_to_f32(A.s_up[m * G + d / GS]);
+          if constexpr (BITS == 8) {
+            const uint2 wg = *reinterpret_cast<const uint2*>(A.q_gate + m * D + d);
+            const uint2 wu = *reinterpret_cast<const uint2*>(A.q_up + m * D + d);
+            cg[u] = make_uint4(wg.x, wg.y, 0, 0);
+            cu[u] = make_uint4(wu.x, wu.y, 0, 0);
+          } else {
+            cg[u].x = *reinterpret_cast<const uint32_t*>(A.q_gate + m * (D >> 1) + (d >> 1));
+            cu[u].x = *reinterpret_cast<const uint32_t*>(A.q_up + m * (D >> 1) + (d >> 1));
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      if (!ok[u]) continue;
+      float hg[8], hu[8], dhf[8];
+      const uint32_t dw[4] = {dh[u].x, dh[u].y, dh[u].z, dh[u].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dhf[e] = __uint_as_float(e & 1 ? dw[e >> 1] & 0xFFFF0000u : dw[e >> 1] << 16);
+      if constexpr (CACHE == CACHE_BF16) {
+        const uint32_t wg[4] = {cg[u].x, cg[u].y, cg[u].z, cg[u].w};
+        const uint32_t wu[4] = {cu[u].x, cu[u].y, cu[u].z, cu[u].w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          hg[e] = __uint_as_float(e & 1 ? wg[e >> 1] & 0xFFFF0000u : wg[e >> 1] << 16);
+          hu[e] = __uint_as_float(e & 1 ? wu[e >> 1] & 0xFFFF0000u : wu[e >> 1] << 16);
+        }
+      } else if constexpr (BITS == 8) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t wg = e < 4 ? cg[u].x : cg[u].y, wu = e < 4 ? cu[u].x : cu[u].y;
+          hg[e] = round_bf16((float)(int8_t)((wg >> (8 * (e & 3))) & 0xFFu) * sgv[u]);
+          hu[e] = round_bf16((float)(int8_t)((wu >> (8 * (e & 3))) & 0xFFu) * suv[u]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          hg[e] = round_bf16(((float)((cg[u].x >> (4 * e)) & 0xFu) - 8.0f) * sgv[u]);
+          hu[e] = round_bf16(((float)((cu[u].x >> (4 * e)) & 0xFu) - 8.0f) * suv[u]);
+        }
+      }
+      float og[8], ou[8], oh[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float hact;
+        swiglu_bwd1(dhf[e], hg[e], hu[e], og[e], ou[e], hact);
+        oh[e] = hact * hu[e];
+      }
+      const int64_t off = mrow[u] * D + d;
+      *reinterpret_cast<uint4*>(A.grad_gate + off) =
+          make_uint4(pack_bf16x2(og[0], og[1]), pack_bf16x2(og[2], og[3]),
+                     pack_bf16x2(og[4], og[5]), pack_bf16x2(og[6], og[7]));
+      *reinterpret_cast<uint4*>(A.grad_up + off) =
+          make_uint4(pack_bf16x2(ou[0], ou[1]), pack_bf16x2(ou[2], ou[3]),
+                     pack_bf16x2(ou[4], ou[5]), pack_bf16x2(ou[6], ou[7]));
+      if (A.h_mid_hat)
+        *reinterpret_cast<uint4*>(A.h_mid_hat + off) =
+            make_uint4(pack_bf16x2(oh[0], oh[1]), pack_bf16x2(oh[2], oh[3]),
+                       pack_bf16x2(oh[4], oh[5]), pack_bf16x2(oh[6], oh[7]));
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -814,7 +842,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_kernel(KArgs A) {
   if constexpr (EPI == EPI_STORE) epi_store(A, acc, m0, n0);
   else if constexpr (EPI == EPI_ADD) epi_add(A, acc, m0, n0);
   else if constexpr (EPI == EPI_GLU) epi_glu<CACHE, GS>(A, acc, m0, n0, lds);
-  else if constexpr (EPI == EPI_DGLU) epi_dglu<CACHE, GS>(A, acc, m0, n0);
+  else if constexpr (EPI == EPI_DGLU) epi_dglu<CACHE, GS>(A, acc, m0, n0, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -1048,6 +1076,10 @@ int cpt_ffn_down_dgrad(const void* grad_y, const void* w_down, int64_t n_tok, in
       !operand_ok(w_down, inter, false, inter, hidden) || !al16(grad_h_gate) ||
       !al16(grad_h_up) || (h_mid_hat && !al16(h_mid_hat)))
     return kErrAlign;
+  // the epilogue reads 8 columns per access: 16 B of bf16 cache, 8 B of int8
+  // codes or 4 B of int4 codes
+  const uintptr_t cmask = cache == CACHE_BF16 ? 15u : (cache == CACHE_INT8 ? 7u : 3u);
+  if (((uintptr_t)c_gate & cmask) || ((uintptr_t)c_up & cmask)) return kErrAlign;
   if (!operand_fits(hidden, true, n_tok, hidden) || !operand_fits(inter, false, inter, hidden))
     return kErrTooLarge;
   KArgs A{};
