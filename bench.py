@@ -38,6 +38,7 @@ WORKLOADS = {
 }
 
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E, published
+PROBE_COPY_BYTES = 1 << 30      # calibration copy of the --probe mode
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
 
 
@@ -122,6 +123,26 @@ def cpu_baseline(budget_tokens=512):
             "median_s": med}
 
 
+def measured_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of `kernel` at `workload`, measured with
+    rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over `bench.py --probe` and
+    calibrated by the probe's copy kernel.  Read from the committed profile
+    summaries (a line `traffic_bytes_per_launch <kernel> <workload> <bytes>`);
+    None if no summary covers the pair."""
+    pdir = os.path.join(ROOT, "profiles")
+    if not os.path.isdir(pdir):
+        return None
+    for fn in sorted(os.listdir(pdir)):
+        if not fn.endswith(".md"):
+            continue
+        for line in open(os.path.join(pdir, fn)):
+            parts = line.strip().strip("`").split()
+            if len(parts) == 4 and parts[0] == "traffic_bytes_per_launch" \
+                    and parts[1] == kernel and parts[2] == workload:
+                return float(parts[3])
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -131,6 +152,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=512)
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
+    ap.add_argument("--probe", action="store_true",
+                    help="HBM-counter probe (run under rocprofv3 --pmc): a 1 GiB calibration "
+                         "copy, then --steps untimed steps; prints one status line")
     args = ap.parse_args()
     wl = WORKLOADS[args.workload]
     global GROUP, BITS, MODE
@@ -182,6 +206,20 @@ def main():
         y = fwd()
         y.backward(gy)
 
+    if args.probe:
+        # calibration: torch's copy kernel reads and writes exactly PROBE_COPY_BYTES
+        src = torch.ones(PROBE_COPY_BYTES // 2, device=dev, dtype=torch.bfloat16)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        del src, dst
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        print(json.dumps({"probe": args.workload, "steps": args.steps,
+                          "copy_bytes": PROBE_COPY_BYTES}))
+        return
+
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -227,12 +265,14 @@ def main():
     rate = amount / (kern[dom]["avg_ms"] * 1e-3)
     if bound == "hbm":
         roofline = {"kernel": dom, "bound": "hbm", "achieved": rate / 1e9, "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": rate / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                    "unit": "GB/s", "frac": rate / 1e9 / HBM_PEAK_GBS,
+                    "traffic": measured_traffic(dom, args.workload),
                     "algorithmic_bytes": amount}
     else:
         roofline = {"kernel": dom, "bound": "mfma", "achieved": rate / 1e12,
                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                    "frac": rate / 1e12 / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
+                    "frac": rate / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+                    "traffic": measured_traffic(dom, args.workload),
                     "algorithmic_flops": amount}
     flops = gemm_flops_fwd_bwd(n, h, d, full_ft)
     if not full_ft:   # thin adapter GEMMs: 18 * N * r * (H + D)
