@@ -541,150 +541,101 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 template <int CACHE, int GS>
 __device__ __forceinline__ void epi_glu(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0,
                                         uint16_t* lds) {
+  // F1: h_gate = bf16(acc gate half), h_up = bf16(acc up half) are staged
+  // through LDS as two row-major 256 x 128 bf16 tiles; then 16 consecutive
+  // threads own one row (8 columns each): h_mid, the bf16 cache or the codes
+  // go out as contiguous row segments, and a quantisation group is GS / 8
+  // consecutive lanes (shuffle-xor max).
+  static_assert(GS >= 8 && GS <= 128 && 128 % GS == 0, "group must divide the 128-column tile");
   constexpr int BITS = CACHE == CACHE_INT4 ? 4 : 8;
   constexpr bool QUANT = CACHE == CACHE_INT4 || CACHE == CACHE_INT8;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int LD = 136;                  // LDS row stride in bf16 (272 bytes)
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave & 1, wm = wave >> 1;
   const int half = lane >> 5;
+  uint16_t* sg = lds;
+  uint16_t* su = lds + 256 * LD;
+  // acc[i][j] (i = 0, 1 gate; i = 2, 3 up) -> d = 64 wn + 32 (i & 1) + 8 q + 4 half + e
+  static_for<0, 4>([&](auto j) {
+    const int ml = wm * 128 + j * 32 + (lane & 31);
+    static_for<0, 2>([&](auto i) {
+      const f32x16& ag = acc.v[i][j];
+      const f32x16& au = acc.v[i + 2][j];
+      static_for<0, 4>([&](auto q) {
+        const int dl = wn * 64 + i * 32 + q * 8 + half * 4;
+        *reinterpret_cast<uint2*>(sg + ml * LD + dl) =
+            make_uint2(pack_bf16x2(ag[q * 4 + 0], ag[q * 4 + 1]), pack_bf16x2(ag[q * 4 + 2], ag[q * 4 + 3]));
+        *reinterpret_cast<uint2*>(su + ml * LD + dl) =
+            make_uint2(pack_bf16x2(au[q * 4 + 0], au[q * 4 + 1]), pack_bf16x2(au[q * 4 + 2], au[q * 4 + 3]));
+      });
+    });
+  });
+  __syncthreads();
   const int64_t D = A.D;
-  const int64_t dw0 = (n0 >> 1) + wn * 64;   // first d of this wave
   const int64_t G = D / GS;
-
-  // per-run absmax (bits of |bf16(acc)|), [t = gate/up][j][i][q]
-  uint32_t am[2][4][2][4];
-  if (QUANT) {
+  const int cl = (tid & 15) * 8;
+  const int64_t d = (n0 >> 1) + cl;        // D % 8 == 0: 8 columns all in or all out
+  const bool dok = d < D;
+#pragma unroll 2
+  for (int p = 0; p < 16; ++p) {
+    const int r = p * 16 + (tid >> 4);
+    const int64_t m = m0 + r;
+    const bool ok = dok && m < A.M;
+    const uint4 wg = *reinterpret_cast<const uint4*>(sg + r * LD + cl);
+    const uint4 wu = *reinterpret_cast<const uint4*>(su + r * LD + cl);
+    const uint32_t gw[4] = {wg.x, wg.y, wg.z, wg.w};
+    const uint32_t uw[4] = {wu.x, wu.y, wu.z, wu.w};
+    float g[8], u[8];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int e = 0; e < 8; ++e) {
+      g[e] = __uint_as_float(e & 1 ? gw[e >> 1] & 0xFFFF0000u : gw[e >> 1] << 16);
+      u[e] = __uint_as_float(e & 1 ? uw[e >> 1] & 0xFFFF0000u : uw[e >> 1] << 16);
+    }
+    const int64_t off = m * D + d;
+    if (A.h_mid && ok) {
+      float h[8];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const f32x16& a = acc.v[i + 2 * t][j];
-            uint32_t v = 0;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v = max(v, absbits(round_bf16(a[q * 4 + e])));
-            am[t][j][i][q] = v;
-          }
-    // combine runs of one group inside the lane
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if (GS >= 16) {
-#pragma unroll
-          for (int i = 0; i < 2; ++i) {
-            am[t][j][i][0] = am[t][j][i][1] = max(am[t][j][i][0], am[t][j][i][1]);
-            am[t][j][i][2] = am[t][j][i][3] = max(am[t][j][i][2], am[t][j][i][3]);
-          }
-        }
-        if (GS >= 32) {
-#pragma unroll
-          for (int i = 0; i < 2; ++i) {
-            const uint32_t v = max(am[t][j][i][0], am[t][j][i][2]);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) am[t][j][i][q] = v;
-          }
-        }
-        if (GS >= 64) {
-          const uint32_t v = max(am[t][j][0][0], am[t][j][1][0]);
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) am[t][j][i][q] = v;
-        }
+      for (int e = 0; e < 8; ++e) h[e] = silu_mul1(g[e], u[e]);
+      *reinterpret_cast<uint4*>(A.h_mid + off) =
+          make_uint4(pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]),
+                     pack_bf16x2(h[4], h[5]), pack_bf16x2(h[6], h[7]));
+    }
+    if constexpr (CACHE == CACHE_BF16) {
+      if (ok) {
+        *reinterpret_cast<uint4*>(A.h_gate + off) = wg;
+        *reinterpret_cast<uint4*>(A.h_up + off) = wu;
       }
-    // the other half of each run-pair lives in lane ^ 32
-    if (GS >= 8) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-              am[t][j][i][q] = max(am[t][j][i][q], (uint32_t)__shfl_xor((int)am[t][j][i][q], 32));
     }
-    if (GS == 128) {
-      // a group spans both waves of a wave-row: exchange through LDS
-      uint32_t* sm = reinterpret_cast<uint32_t*>(lds);
+    if constexpr (QUANT) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t) {
+        const float* v = t ? u : g;
+        uint32_t am = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int ml = wm * 128 + j * 32 + (lane & 31);
-          if (half == 0) sm[((t * 256 + ml) << 1) + wn] = am[t][j][0][0];
-        }
-      __syncthreads();
+        for (int e = 0; e < 8; ++e) am = max(am, absbits(v[e]));
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+        for (int off_l = 1; off_l < GS / 8; off_l <<= 1)
+          am = max(am, (uint32_t)__shfl_xor((int)am, off_l));
+        const uint16_t sh = scale_bits<BITS>(am);
+        const float safe = safe_scale(sh);
+        const float rs = __builtin_amdgcn_rcpf(safe);
+        if (!ok) continue;
+        if ((tid & (GS / 8 - 1)) == 0) (t ? A.s_up : A.s_gate)[m * G + d / GS] = sh;
+        uint8_t* qp = t ? A.q_up : A.q_gate;
+        if constexpr (BITS == 8) {
+          uint32_t w0 = 0, w1 = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int ml = wm * 128 + j * 32 + (lane & 31);
-          const uint32_t v = max(am[t][j][0][0], sm[((t * 256 + ml) << 1) + (wn ^ 1)]);
-#pragma unroll
-          for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) am[t][j][i][q] = v;
-        }
-    }
-  }
-
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int64_t d = dw0 + i * 32 + q * 8 + half * 4;
-        if (m >= A.M || d >= D) continue;
-        const f32x16& ag = acc.v[i][j];
-        const f32x16& au = acc.v[i + 2][j];
-        float g[4], u[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          g[e] = round_bf16(ag[q * 4 + e]);
-          u[e] = round_bf16(au[q * 4 + e]);
-        }
-        if (A.h_mid) {
-          float h[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) h[e] = silu_mul1(g[e], u[e]);
-          *reinterpret_cast<uint2*>(A.h_mid + m * D + d) =
-              make_uint2(pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]));
-        }
-        if (CACHE == CACHE_BF16) {
-          *reinterpret_cast<uint2*>(A.h_gate + m * D + d) =
-              make_uint2(pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3]));
-          *reinterpret_cast<uint2*>(A.h_up + m * D + d) =
-              make_uint2(pack_bf16x2(u[0], u[1]), pack_bf16x2(u[2], u[3]));
-        }
-        if (QUANT) {
-#pragma unroll
-          for (int t = 0; t < 2; ++t) {
-            const float* v = t ? u : g;
-            const uint16_t sh = scale_bits<BITS>(am[t][j][i][q]);
-            const float safe = safe_scale(sh);
-            const float rs = __builtin_amdgcn_rcpf(safe);
-            uint16_t* sp = t ? A.s_up : A.s_gate;
-            uint8_t* qp = t ? A.q_up : A.q_gate;
-            const bool first_of_group = GS <= 4 ? true : (half == 0 && ((d & (GS - 1)) == 0));
-            if (first_of_group) sp[m * G + d / GS] = sh;
-            if (BITS == 8) {
-              uint32_t w = 0;
-#pragma unroll
-              for (int e = 0; e < 4; ++e) w |= ((uint32_t)quant_code<8>(v[e], safe, rs) & 0xFFu) << (8 * e);
-              *reinterpret_cast<uint32_t*>(qp + m * D + d) = w;
-            } else {
-              uint32_t w = 0;
-#pragma unroll
-              for (int e = 0; e < 4; ++e) w |= (uint32_t)(quant_code<4>(v[e], safe, rs) + 8) << (4 * e);
-              *reinterpret_cast<uint16_t*>(qp + m * (D >> 1) + (d >> 1)) = (uint16_t)w;
-            }
+          for (int e = 0; e < 4; ++e) {
+            w0 |= ((uint32_t)quant_code<8>(v[e], safe, rs) & 0xFFu) << (8 * e);
+            w1 |= ((uint32_t)quant_code<8>(v[e + 4], safe, rs) & 0xFFu) << (8 * e);
           }
+          *reinterpret_cast<uint2*>(qp + off) = make_uint2(w0, w1);
+        } else {
+          uint32_t w = 0;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) w |= (uint32_t)(quant_code<4>(v[e], safe, rs) + 8) << (4 * e);
+          *reinterpret_cast<uint32_t*>(qp + m * (D >> 1) + (d >> 1)) = w;
         }
       }
     }
@@ -1027,7 +978,9 @@ int cpt_ffn_gate_up(const void* x, const void* w_gate, const void* w_up, int64_t
       !operand_ok(w_gate, hidden, true, inter, hidden) ||
       !operand_ok(w_up, hidden, true, inter, hidden) || (h_mid && !al16(h_mid)))
     return kErrAlign;
-  if (quant && ((uintptr_t)q_gate & 3 || (uintptr_t)q_up & 3)) return kErrAlign;
+  // the epilogue stores 8 codes per access: 8 bytes (int8) or 4 bytes (int4)
+  const uintptr_t qmask = cache == CACHE_INT8 ? 7u : 3u;
+  if (quant && (((uintptr_t)q_gate & qmask) || ((uintptr_t)q_up & qmask))) return kErrAlign;
   if (!operand_fits(hidden, true, n_tok, hidden) || !operand_fits(hidden, true, inter, hidden))
     return kErrTooLarge;
   KArgs A{};
