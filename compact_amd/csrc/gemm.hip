@@ -17,8 +17,8 @@
 //   acc[i][j][r] -> n = nw + 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4
 //                   m = mw + 32 j + lane % 32
 // LDS: two stages x two operands x 256 rows x 64 bf16 in padded rows
-// (146 KiB; see lds_row), conflict-free for the fragment reads (32
-// consecutive rows, one chunk) and for the transposed stores (rows 8 apart).
+// (146 KiB; see lds_row), conflict-free on gfx950's 64 banks for the fragment
+// reads and for the stores of either operand layout.
 // Grid: one block per output tile, block ids remapped so each XCD works on a
 // contiguous range of tiles, grouped 8 tile-rows deep for L2 reuse.
 
@@ -54,9 +54,19 @@ constexpr int GROUP_ROWS = 8;                  // tile-rows per L2 group
 // bank groups (36-dword stride), and so do 8 rows spaced 8 apart (292-dword
 // stride), which keeps fragment reads and transposed stores conflict-free
 // while the address stays affine in the chunk.
-constexpr int ROW_ELEMS = 72;
-__device__ __forceinline__ int lds_row(int row) { return row * ROW_ELEMS + ((row >> 3) << 3); }
-__device__ __forceinline__ int lds_off(int row, int chunk) { return lds_row(row) + (chunk << 3); }
+// LDS is 64 banks of 4 bytes on gfx950, and a 128-bit access is served 16
+// lanes at a time, so 16 lanes must cover 64 distinct banks.  Fragment reads
+// take 16 consecutive rows at one 16-byte chunk; K-major stores take 2 rows x 8
+// chunks; transposed (MN-major) stores take 16 rows spaced 8 apart, one chunk.
+//   K-major tiles:  row r at r * 64 + (r / 2) * 8 elements   (reads, stores 1-way)
+//   MN-major tiles: row r at r * 72 + (r / 16) * 8 elements  (reads, stores 1-way)
+// Both stay affine in the chunk, so fragment addresses are immediate offsets.
+template <bool KM>
+__device__ __forceinline__ int lds_row(int row) {
+  return KM ? row * 64 + ((row >> 1) << 3) : row * 72 + ((row >> 4) << 3);
+}
+template <bool KM>
+__device__ __forceinline__ int lds_off(int row, int chunk) { return lds_row<KM>(row) + (chunk << 3); }
 
 // ---------------------------------------------------------------------------
 // global -> registers -> LDS
@@ -82,7 +92,7 @@ __device__ __forceinline__ void sstore_kmajor(uint16_t* lds, int tid, const uint
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
     const int q = tid + NTHR * it;
-    *reinterpret_cast<uint4*>(lds + lds_off(q >> 3, q & 7)) = reg[it];
+    *reinterpret_cast<uint4*>(lds + lds_off<true>(q >> 3, q & 7)) = reg[it];
   }
 }
 
@@ -117,7 +127,7 @@ __device__ __forceinline__ void sstore_mnmajor(uint16_t* lds, int tid, const uin
       const uint32_t lo = dword_of(reg[2 * w], i >> 1), hi = dword_of(reg[2 * w + 1], i >> 1);
       o[w] = (i & 1) ? ((lo >> 16) | (hi & 0xFFFF0000u)) : ((lo & 0xFFFFu) | (hi << 16));
     }
-    *reinterpret_cast<uint4*>(lds + lds_off(mb * 8 + i, kb)) = make_uint4(o[0], o[1], o[2], o[3]);
+    *reinterpret_cast<uint4*>(lds + lds_off<false>(mb * 8 + i, kb)) = make_uint4(o[0], o[1], o[2], o[3]);
   }
 }
 
@@ -303,6 +313,7 @@ struct Frags {
   bf16x8 m[4];   // m-side fragments (MFMA B slot)
 };
 
+template <bool AKM, bool BKM>
 __device__ __forceinline__ void read_frags(const uint16_t* stage_base, int wn, int wm, int lane,
                                            int s, Frags& f) {
   const uint16_t* sa = stage_base;
@@ -310,10 +321,10 @@ __device__ __forceinline__ void read_frags(const uint16_t* stage_base, int wn, i
   const int chunk = s * 2 + (lane >> 5);
 #pragma unroll
   for (int i = 0; i < 4; ++i)
-    f.n[i] = *reinterpret_cast<const bf16x8*>(sb + lds_off(wn * 128 + i * 32 + (lane & 31), chunk));
+    f.n[i] = *reinterpret_cast<const bf16x8*>(sb + lds_off<BKM>(wn * 128 + i * 32 + (lane & 31), chunk));
 #pragma unroll
   for (int j = 0; j < 4; ++j)
-    f.m[j] = *reinterpret_cast<const bf16x8*>(sa + lds_off(wm * 128 + j * 32 + (lane & 31), chunk));
+    f.m[j] = *reinterpret_cast<const bf16x8*>(sa + lds_off<AKM>(wm * 128 + j * 32 + (lane & 31), chunk));
 }
 
 template <int I0, int I1>
@@ -390,37 +401,37 @@ __device__ __forceinline__ void mainloop(const KArgs& A, int64_t m0, int64_t n0,
   store(0);
   __syncthreads();
   Frags f0, f1;
-  read_frags(lds, wn, wm, lane, 0, f0);
+  read_frags<AK, BKM || DUAL>(lds, wn, wm, lane, 0, f0);
   for (int kt = 0; kt + 1 < nk; ++kt) {
     const int stage = kt & 1;
     const uint16_t* base = lds + stage * 2 * TILE_ELEMS;
     L.issue(kt0 + kt + 1, tid, va, vb);
-    read_frags(base, wn, wm, lane, 1, f1);
+    read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 1, f1);
     mfma_range<0, 16>(f0, acc);
     sched_interleave_load_read<8>();
     sched_interleave<8, SG_VMEM_R>();
-    read_frags(base, wn, wm, lane, 2, f0);
+    read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 2, f0);
     mfma_range<0, 16>(f1, acc);
     sched_interleave<8, SG_DS_R>();
-    read_frags(base, wn, wm, lane, 3, f1);
+    read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 3, f1);
     mfma_range<0, 16>(f0, acc);
     sched_interleave<8, SG_DS_R>();
     store(stage ^ 1);
     mfma_range<0, 8>(f1, acc);
     sched_interleave<8, SG_DS_W, 2>();
     __syncthreads();
-    read_frags(lds + (stage ^ 1) * 2 * TILE_ELEMS, wn, wm, lane, 0, f0);
+    read_frags<AK, BKM || DUAL>(lds + (stage ^ 1) * 2 * TILE_ELEMS, wn, wm, lane, 0, f0);
     mfma_range<8, 16>(f1, acc);
     sched_interleave<8, SG_DS_R>();
   }
   {
     // last k-tile: no loads, no stores
     const uint16_t* base = lds + ((nk - 1) & 1) * 2 * TILE_ELEMS;
-    read_frags(base, wn, wm, lane, 1, f1);
+    read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 1, f1);
     mfma_range<0, 16>(f0, acc);
-    read_frags(base, wn, wm, lane, 2, f0);
+    read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 2, f0);
     mfma_range<0, 16>(f1, acc);
-    read_frags(base, wn, wm, lane, 3, f1);
+    read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 3, f1);
     mfma_range<0, 16>(f0, acc);
     mfma_range<0, 16>(f1, acc);
   }
