@@ -276,6 +276,43 @@ struct Loader {
     }
   }
 
+  // the A and B halves of issue(), for schedules that spread them apart
+  __device__ __forceinline__ void issue_a(int kt, int tid, uint4 (&va)[8]) const {
+    const int p = kt >= nk0 ? 1 : 0;
+    const int64_t k0 = (int64_t)(kt - p * nk0) * BK;
+    const int64_t Kp = p ? K[1] : K[0];
+    const __amdgpu_buffer_rsrc_t rA = p ? ra[1] : ra[0];
+    const bool kok = k0 + (tid & 7) * 8 < Kp;
+    if (AK) {
+      const uint32_t adv = (uint32_t)(k0 * 2);
+#pragma unroll
+      for (int it = 0; it < 8; ++it) va[it] = bload(rA, kok ? oa[it] + adv : kOOB);
+    } else {
+      const uint32_t adv = (uint32_t)(k0 * lda * 2);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) va[r] = bload(rA, oa[r] == kOOB ? kOOB : oa[r] + adv);
+    }
+  }
+  __device__ __forceinline__ void issue_b(int kt, int tid, uint4 (&vb)[8]) const {
+    const int p = kt >= nk0 ? 1 : 0;
+    const int64_t k0 = (int64_t)(kt - p * nk0) * BK;
+    const int64_t Kp = p ? K[1] : K[0];
+    const __amdgpu_buffer_rsrc_t rB = p ? rb[1] : rb[0];
+    const bool kok = k0 + (tid & 7) * 8 < Kp;
+    if (DUAL || BKM) {
+      const uint32_t adv = (uint32_t)(k0 * 2);
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const __amdgpu_buffer_rsrc_t r = (DUAL && ((it >> 1) & 1)) ? rup : rB;
+        vb[it] = bload(r, kok ? ob[it] + adv : kOOB);
+      }
+    } else {
+      const uint32_t adv = (uint32_t)(k0 * ldb * 2);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) vb[r] = bload(rB, ob[r] == kOOB ? kOOB : ob[r] + adv);
+    }
+  }
+
   // global loads of k-tile kt into registers (16 x 128-bit, no branches)
   __device__ __forceinline__ void issue(int kt, int tid, uint4 (&va)[8], uint4 (&vb)[8]) const {
     const int p = kt >= nk0 ? 1 : 0;
@@ -405,14 +442,29 @@ __device__ __forceinline__ void mainloop(const KArgs& A, int64_t m0, int64_t n0,
   for (int kt = 0; kt + 1 < nk; ++kt) {
     const int stage = kt & 1;
     const uint16_t* base = lds + stage * 2 * TILE_ELEMS;
-    L.issue(kt0 + kt + 1, tid, va, vb);
-    read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 1, f1);
-    mfma_range<0, 16>(f0, acc);
-    sched_interleave_load_read<8>();
-    sched_interleave<8, SG_VMEM_R>();
-    read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 2, f0);
-    mfma_range<0, 16>(f1, acc);
-    sched_interleave<8, SG_DS_R>();
+    if constexpr (AK && !BKM && !DUAL) {
+      // K-major A, MN-major B (the NN products): A's loads in s0, B's in s1
+      // (measured +5% over issuing all 16 in s0)
+      L.issue_a(kt0 + kt + 1, tid, va);
+      read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 1, f1);
+      mfma_range<0, 16>(f0, acc);
+      sched_interleave_load_read<8>();
+      sched_interleave<8, SG_MFMA>();
+      L.issue_b(kt0 + kt + 1, tid, vb);
+      read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 2, f0);
+      mfma_range<0, 16>(f1, acc);
+      sched_interleave_load_read<8>();
+      sched_interleave<8, SG_MFMA>();
+    } else {
+      L.issue(kt0 + kt + 1, tid, va, vb);
+      read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 1, f1);
+      mfma_range<0, 16>(f0, acc);
+      sched_interleave_load_read<8>();
+      sched_interleave<8, SG_VMEM_R>();
+      read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 2, f0);
+      mfma_range<0, 16>(f1, acc);
+      sched_interleave<8, SG_DS_R>();
+    }
     read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 3, f1);
     mfma_range<0, 16>(f0, acc);
     sched_interleave<8, SG_DS_R>();
