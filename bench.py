@@ -143,6 +143,97 @@ def measured_traffic(kernel: str, workload: str):
     return None
 
 
+def model_step_bench(args):
+    """Whole-model training step (BASELINE configs C4 / C5): tokens/s of the
+    step (forward, backward, AdamW) with every MLP on FlashFFN v3, the per-step
+    saved-for-backward bytes of the MLPs, and the dominant FFN kernel's
+    roofline.  Random-initialised weights, uniform-random token IDs."""
+    import torch
+    import compact_amd as cpt
+    from compact_amd import e2e
+    from compact_amd.kernels import KernelTimer
+
+    cfg = e2e.CONFIGS[args.workload]
+    dev = torch.device("cuda:0")
+    model, opt = e2e.prepare(cfg, dev, flash=True)
+    ids = e2e.random_batch(cfg, dev)
+    n_tok = cfg["batch"] * cfg["seq"]
+
+    # saved-for-backward bytes of the MLPs only: count while inside an MLP forward
+    mlps = [layer.mlp for layer in model.model.layers]
+    inside = [False]
+    seen, total = set(), [0]
+    exclude = {p.data_ptr() for p in model.parameters()}
+
+    def pack(t):
+        if inside[0]:
+            key = (t.data_ptr(), t.nbytes)
+            if t.data_ptr() not in exclude and key not in seen:
+                seen.add(key)
+                total[0] += t.nbytes
+        return t
+    hooks = []
+    for m in mlps:
+        hooks.append(m.register_forward_pre_hook(lambda mod, a: inside.__setitem__(0, True)))
+        hooks.append(m.register_forward_hook(lambda mod, a, o: inside.__setitem__(0, False)))
+    with torch.autograd.graph.saved_tensors_hooks(pack, lambda t: t), e2e.fused_attention_only():
+        loss = model(input_ids=ids, labels=ids).loss
+    del loss
+    for h in hooks:
+        h.remove()
+    ffn_saved = total[0]
+
+    for _ in range(args.warmup):
+        e2e.train_step(model, opt, ids)
+    torch.cuda.synchronize()
+    cpt.v3_reset_counters()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with KernelTimer() as kt:
+        e0.record(stream)
+        for _ in range(args.steps):
+            loss = e2e.train_step(model, opt, ids)
+        e1.record(stream)
+        torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    assert cpt._V3_COUNTERS["forward"] == args.steps * cfg["layers"], cpt._V3_COUNTERS
+    kern = kt.avg_ms()
+    h, d = cfg["hidden"], cfg["inter"]
+    global GROUP, BITS
+    GROUP, BITS = cfg["group"], 4 if cfg["cache_mode"] == "int4" else 8
+    work = algorithmic_work(n_tok, h, d)
+    work["gemm_fwd_gate"] = work["gemm_fwd_up"] = work["gemm_dgrad_down"] = \
+        (2 * n_tok * h * d, "mfma")
+    dom_name = max((k for k in kern if k in work), key=lambda k: kern[k]["total_ms"])
+    amount, bound = work[dom_name]
+    rate = amount / (kern[dom_name]["avg_ms"] * 1e-3)
+    roofline = {"kernel": dom_name, "bound": "mfma", "achieved": rate / 1e12,
+                "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                "frac": rate / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+                "traffic": measured_traffic(dom_name, args.workload),
+                "algorithmic_flops": amount}
+    if bound == "hbm":
+        roofline.update(bound="hbm", achieved=rate / 1e9, peak=HBM_PEAK_GBS, unit="GB/s",
+                        frac=rate / 1e9 / HBM_PEAK_GBS)
+    out = {
+        "metric": "whole-model training step tokens/sec (every MLP on FlashFFN v3), 1 MI355X",
+        "value": n_tok / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random-init weights, uniform-random token IDs, seed 0)",
+        "config": {"workload": cfg["desc"], "tokens": n_tok, "layers": cfg["layers"],
+                   "d_model": h, "d_ff": d, "cache_mode": cfg["cache_mode"],
+                   "group_size": cfg["group"], "outlier_ratio": cfg["outlier_ratio"],
+                   "parallelism": "none (1 GPU)"},
+        "loss": float(loss),
+        "ffn_saved_activation_mb": ffn_saved / 1e6,
+        "ffn_saved_activation_mb_per_layer": ffn_saved / 1e6 / cfg["layers"],
+        "roofline": roofline,
+        "kernels": kern,
+    }
+    print(json.dumps(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -151,18 +242,23 @@ def main():
     ap.add_argument("--tokens", type=int, default=N_TOK)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=512)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["c4", "c5"], default="c2",
+                    help="c2 (default) / c3: the FFN block; c4 / c5: a whole-model training "
+                         "step (TinyLlama full-FT / Llama-7B LoRA) with every MLP on FlashFFN v3")
     ap.add_argument("--probe", action="store_true",
                     help="HBM-counter probe (run under rocprofv3 --pmc): a 1 GiB calibration "
                          "copy, then --steps untimed steps; prints one status line")
     args = ap.parse_args()
-    wl = WORKLOADS[args.workload]
-    global GROUP, BITS, MODE
-    GROUP, BITS, MODE = wl["group"], wl["bits"], wl["mode"]
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
                                    "(multi-GPU sharding is a design note, not a code path)"}))
         sys.exit(2)
+    if args.workload in ("c4", "c5"):
+        model_step_bench(args)
+        return
+    wl = WORKLOADS[args.workload]
+    global GROUP, BITS, MODE
+    GROUP, BITS, MODE = wl["group"], wl["bits"], wl["mode"]
 
     import torch
     import compact_amd as cpt

@@ -1,0 +1,71 @@
+"""Model-level patch (reference src/train_glue.py:810-876) on CPU: which MLPs
+are patched, which wrappers are refused, and the PEFT-shaped LoRA injection.
+The patched forward itself runs on the GPU (tests/test_gpu_model.py)."""
+
+import pytest
+import torch
+import torch.nn as nn
+
+from compact_amd import model_patch as MP
+from tests.peft_like import SwiGLUMLP, adapter_wrap
+
+
+def tiny_llama(layers=2):
+    from transformers import LlamaConfig, LlamaForCausalLM
+    cfg = LlamaConfig(hidden_size=64, intermediate_size=192, num_hidden_layers=layers,
+                      num_attention_heads=4, num_key_value_heads=2, vocab_size=128,
+                      max_position_embeddings=64)
+    torch.manual_seed(0)
+    return LlamaForCausalLM(cfg)
+
+
+def test_apply_patches_every_mlp():
+    model = tiny_llama(3)
+    assert MP.apply_flash_ffn_v3(model, "int8", 64) == 3
+    for layer in model.model.layers:
+        # the instance attribute shadows the class forward
+        assert "forward" in layer.mlp.__dict__
+
+
+def test_lora_injection_and_patch():
+    model = tiny_llama(2)
+    n = MP.inject_lora(model, ("q_proj", "v_proj", "gate_proj", "up_proj", "down_proj"), 8, 16.0)
+    assert n == 2 * 5
+    trainable = {k for k, p in model.named_parameters() if p.requires_grad}
+    assert trainable and all("lora_" in k for k in trainable)
+    assert MP.apply_flash_ffn_v3(model, "int4", 64, outlier_ratio=0.01) == 2
+    from compact_amd import _v3_proj_kind
+    assert _v3_proj_kind(model.model.layers[0].mlp.gate_proj) == "lora"
+
+
+def test_adapter_families_patch():
+    mlp = adapter_wrap(SwiGLUMLP(64, 192), "dora", 8, 16.0, which=("gate",))
+    holder = nn.Module()
+    holder.mlp = mlp
+    assert MP.apply_flash_ffn_v3(holder, "int4") == 1
+
+
+def test_unknown_wrapper_raises_value_error():
+    mlp = SwiGLUMLP(64, 192)
+
+    class Weird(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.base_layer = nn.Linear(64, 192)
+
+    mlp.up_proj = Weird()
+    holder = nn.Module()
+    holder.mlp = mlp
+    with pytest.raises(ValueError):
+        MP.apply_flash_ffn_v3(holder, "int8")
+
+
+def test_bamboo_mlp_refused():
+    mlp = SwiGLUMLP(64, 192)
+    mlp.predictor = nn.Module()
+    mlp.predictor.fc1 = nn.Linear(64, 8)
+    mlp.predictor.fc2 = nn.Linear(8, 192)
+    holder = nn.Module()
+    holder.mlp = mlp
+    with pytest.raises(ValueError):
+        MP.apply_flash_ffn_v3(holder, "int8")
