@@ -525,89 +525,193 @@ inline int glu_dispatch(int op, int dt, const void* a, const void* g, const void
 // ties to the lower column index, slots in ascending column order.
 // Deterministic: fp64 sums in a fixed order.
 // ---------------------------------------------------------------------------
-constexpr int kColRows = 256;   // rows per partial sum
+constexpr int kColRows = 64;    // rows per partial sum
 
 // partial[chunk][col] = sum over rows [chunk*kColRows, +kColRows) of t^2 (fp64)
 template <int DT>
-__global__ __launch_bounds__(kBlock) void colsumsq_partial_kernel(
+__global__ __launch_bounds__(64) void colsumsq_partial_kernel(
     const void* __restrict__ t, double* __restrict__ partial, int64_t n, int64_t d) {
+  // one wavefront per 512-column strip and kColRows rows; 8 columns per lane
+  // (one 128-bit load of bf16/fp16), fp64 accumulation in row order
   using E = Elem<DT>;
-  const int64_t col = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int64_t col = ((int64_t)blockIdx.x * 64 + threadIdx.x) * 8;
   const int64_t r0 = (int64_t)blockIdx.y * kColRows;
   if (col >= d) return;
-  const typename E::T* p = reinterpret_cast<const typename E::T*>(t);
-  double acc = 0.0;
   const int64_t r1 = r0 + kColRows < n ? r0 + kColRows : n;
+  double acc[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0;
   for (int64_t r = r0; r < r1; ++r) {
-    const double v = (double)E::ld(p + r * d + col);
-    acc += v * v;
+    float v[8];
+    if constexpr (DT == kF32) {
+      const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(t) + r * d + col);
+      const float4 a = p[0], b = p[1];
+      v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+      Vec8<DT>::ld(reinterpret_cast<const typename E::T*>(t) + r * d + col, 0, v);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += (double)v[e] * (double)v[e];
   }
-  partial[blockIdx.y * d + col] = acc;
+  double* out = partial + blockIdx.y * d + col;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) out[e] = acc[e];
 }
 
 __global__ __launch_bounds__(kBlock) void colsumsq_reduce_kernel(
     const double* __restrict__ partial, double* __restrict__ sumsq, int64_t d, int chunks) {
-  const int64_t col = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (col >= d) return;
+  // 64 columns per block; wave w sums chunks w, w + 4, ...; the four wave
+  // sums are added in wave order (fixed order, deterministic)
+  __shared__ double part[kBlock / 64][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t col = (int64_t)blockIdx.x * 64 + lane;
   double acc = 0.0;
-  for (int c = 0; c < chunks; ++c) acc += partial[(int64_t)c * d + col];
-  sumsq[col] = acc;
+  if (col < d)
+    for (int c = wave; c < chunks; c += kBlock / 64) acc += partial[(int64_t)c * d + col];
+  part[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0 && col < d) sumsq[col] = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
 }
 
-// flag[col] = 1 iff col ranks among the top k: rank = #{c' : v[c'] > v[col] or
-// (v[c'] == v[col] and c' < col)}.  The values stream through LDS in tiles.
-__global__ __launch_bounds__(kBlock) void outlier_rank_kernel(const double* __restrict__ v,
-                                                              int16_t* __restrict__ flag,
-                                                              int64_t d, int64_t k) {
-  __shared__ double tile[2048];
-  const int64_t col = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  const double mine = col < d ? v[col] : 0.0;
-  int64_t rank = 0;
-  for (int64_t base = 0; base < d; base += 2048) {
-    const int64_t len = d - base < 2048 ? d - base : 2048;
+// One block picks the k columns with the largest sum of squares (ties to the
+// lower column): slot[c] = the column's position among the picked ones in
+// ascending column order, or -1; idx[pos] = c.  The k-th largest is found by
+// radix select over the fp64 bit patterns (sums of squares are >= 0, so
+// their unsigned bit order is their numeric order), 8 bits per pass, each
+// pass a 256-bin LDS histogram; wave 0 picks the digit.  A final pass in
+// column order keeps the values above the threshold and the lowest-column
+// ties (ballot prefix counts).
+constexpr int kPickThreads = 1024;
+constexpr int64_t kPickStagedMax = 16384;  // 128 KiB of fp64 sums staged in LDS
+constexpr int kPickWaves = kPickThreads / 64;
+
+template <bool STAGED>
+__global__ __launch_bounds__(kPickThreads) void outlier_pick_kernel(const double* __restrict__ vg,
+                                                                    int64_t d, int64_t k,
+                                                                    int16_t* __restrict__ slot,
+                                                                    int32_t* __restrict__ idx) {
+  // STAGED: the d sums are copied to LDS once and every pass reads them there
+  extern __shared__ __align__(16) unsigned char pick_smem[];
+  const double* v = vg;
+  if constexpr (STAGED) {
+    double* sv = reinterpret_cast<double*>(pick_smem);
+    for (int64_t i = threadIdx.x; i < d; i += kPickThreads) sv[i] = vg[i];
     __syncthreads();
-    for (int64_t i = threadIdx.x; i < len; i += kBlock) tile[i] = v[base + i];
+    v = sv;
+  }
+  __shared__ int hist[256];
+  __shared__ unsigned long long sh_prefix;
+  __shared__ int sh_rem;
+  __shared__ int sh_cnt[kPickWaves][2];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  unsigned long long prefix = 0, mask = 0;
+  int remaining = (int)k;
+  if (k > 0) {
+    for (int pass = 7; pass >= 0; --pass) {
+      const int shift = pass * 8;
+      if (tid < 256) hist[tid] = 0;
+      __syncthreads();
+      for (int64_t i0 = 0; i0 < d; i0 += kPickThreads) {
+        // the two top bytes (sign, exponent) are shared by nearly all sums:
+        // there, one LDS atomic per distinct digit in the wavefront instead
+        // of 64 atomics on one bin
+        const int64_t i = i0 + tid;
+        int digit = -1;
+        if (i < d) {
+          const unsigned long long key = (unsigned long long)__double_as_longlong(v[i]);
+          if ((key & mask) == prefix) digit = (int)((key >> shift) & 0xFF);
+        }
+        if (pass < 6) {                 // mantissa bytes: spread digits, plain atomics
+          if (digit >= 0) atomicAdd(&hist[digit], 1);
+          continue;
+        }
+        uint64_t pending = __ballot(digit >= 0);
+        while (pending) {
+          const int leader = __ffsll((unsigned long long)pending) - 1;
+          const int dl = __shfl(digit, leader);
+          const uint64_t same = __ballot(digit == dl);
+          if (lane == leader) atomicAdd(&hist[dl], (int)__popcll(same));
+          pending &= ~same;
+        }
+      }
+      __syncthreads();
+      if (wave == 0) {
+        // lane l owns digits 255-4l .. 252-4l (descending)
+        int c[4], local = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          c[q] = hist[255 - 4 * lane - q];
+          local += c[q];
+        }
+        int cum = local;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const int u = __shfl_up(cum, off);
+          if (lane >= off) cum += u;
+        }
+        int before = cum - local;   // counts of all larger digits
+        if (before < remaining && cum >= remaining) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if (before + c[q] >= remaining) {
+              sh_prefix = prefix | ((unsigned long long)(255 - 4 * lane - q) << shift);
+              sh_rem = remaining - before;
+              break;
+            }
+            before += c[q];
+          }
+        }
+      }
+      __syncthreads();
+      prefix = sh_prefix;
+      remaining = sh_rem;
+      mask |= 0xFFull << shift;
+      __syncthreads();
+    }
+  }
+  const unsigned long long thr = prefix;
+  const int need_eq = remaining;
+  const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+  int run_eq = 0, run_sel = 0;
+  for (int64_t c0 = 0; c0 < d; c0 += kPickThreads) {
+    const int64_t c = c0 + tid;
+    bool gt = false, eq = false;
+    if (c < d && k > 0) {
+      const unsigned long long key = (unsigned long long)__double_as_longlong(v[c]);
+      gt = key > thr;
+      eq = key == thr;
+    }
+    const uint64_t m_eq = __ballot(eq);
+    if (lane == 0) sh_cnt[wave][0] = __popcll(m_eq);
     __syncthreads();
-    if (col < d) {
-      for (int64_t i = 0; i < len; ++i) {
-        const double o = tile[i];
-        rank += (o > mine) || (o == mine && base + i < col);
+    int eq_before = run_eq + __popcll(m_eq & below), eq_tot = 0;
+#pragma unroll
+    for (int w = 0; w < kPickWaves; ++w) {
+      eq_before += w < wave ? sh_cnt[w][0] : 0;
+      eq_tot += sh_cnt[w][0];
+    }
+    const bool sel = gt || (eq && eq_before < need_eq);
+    const uint64_t m_sel = __ballot(sel);
+    if (lane == 0) sh_cnt[wave][1] = __popcll(m_sel);
+    __syncthreads();
+    int pos = run_sel + __popcll(m_sel & below), sel_tot = 0;
+#pragma unroll
+    for (int w = 0; w < kPickWaves; ++w) {
+      pos += w < wave ? sh_cnt[w][1] : 0;
+      sel_tot += sh_cnt[w][1];
+    }
+    if (c < d) {
+      if (sel && pos < k) {
+        slot[c] = (int16_t)pos;
+        idx[pos] = (int32_t)c;
+      } else {
+        slot[c] = -1;
       }
     }
-  }
-  if (col < d) flag[col] = rank < k ? 1 : 0;
-}
-
-// One block: slot[col] = (selected ? number of selected columns before col : -1),
-// idx[slot] = col.  Each thread scans a contiguous segment, in place.
-__global__ __launch_bounds__(1024) void outlier_slots_kernel(int16_t* __restrict__ slot,
-                                                             int32_t* __restrict__ idx,
-                                                             int64_t d) {
-  __shared__ int32_t counts[1024];
-  const int tid = threadIdx.x;
-  const int64_t seg = (d + 1023) / 1024;
-  const int64_t c0 = tid * seg, c1 = c0 + seg < d ? c0 + seg : d;
-  int32_t cnt = 0;
-  for (int64_t c = c0; c < c1; ++c) cnt += slot[c];
-  counts[tid] = cnt;
-  __syncthreads();
-  if (tid == 0) {
-    int32_t run = 0;
-    for (int i = 0; i < 1024; ++i) {
-      const int32_t x = counts[i];
-      counts[i] = run;
-      run += x;
-    }
-  }
-  __syncthreads();
-  int32_t pos = counts[tid];
-  for (int64_t c = c0; c < c1; ++c) {
-    if (slot[c]) {
-      idx[pos] = (int32_t)c;
-      slot[c] = (int16_t)pos++;
-    } else {
-      slot[c] = -1;
-    }
+    run_eq += eq_tot;
+    run_sel += sel_tot;
+    __syncthreads();
   }
 }
 
@@ -779,18 +883,30 @@ int cpt_outlier_select(const void* t, int dtype, int64_t n, int64_t d, int64_t k
   if (dtype != kF32 && dtype != kF16 && dtype != kBF16) return kErrDType;
   if (d == 0) return kOk;
   if (!slot || !sumsq || (n > 0 && (!t || !partial)) || (k > 0 && !idx)) return kErrShape;
+  if (n > 0 && ((d % 8) || !aligned16(t))) return kErrAlign;   // 8-column vector loads
   hipStream_t st = (hipStream_t)stream;
   const int chunks = (int)((n + kColRows - 1) / kColRows);
   const unsigned gx = grid_for(d);
   if (chunks > 0) {
-    dim3 grid(gx, (unsigned)chunks);
-    if (dtype == kBF16) colsumsq_partial_kernel<kBF16><<<grid, kBlock, 0, st>>>(t, (double*)partial, n, d);
-    else if (dtype == kF16) colsumsq_partial_kernel<kF16><<<grid, kBlock, 0, st>>>(t, (double*)partial, n, d);
-    else colsumsq_partial_kernel<kF32><<<grid, kBlock, 0, st>>>(t, (double*)partial, n, d);
+    dim3 grid((unsigned)((d + 511) / 512), (unsigned)chunks);
+    if (dtype == kBF16) colsumsq_partial_kernel<kBF16><<<grid, 64, 0, st>>>(t, (double*)partial, n, d);
+    else if (dtype == kF16) colsumsq_partial_kernel<kF16><<<grid, 64, 0, st>>>(t, (double*)partial, n, d);
+    else colsumsq_partial_kernel<kF32><<<grid, 64, 0, st>>>(t, (double*)partial, n, d);
   }
-  colsumsq_reduce_kernel<<<gx, kBlock, 0, st>>>((const double*)partial, (double*)sumsq, d, chunks);
-  outlier_rank_kernel<<<gx, kBlock, 0, st>>>((const double*)sumsq, (int16_t*)slot, d, k);
-  outlier_slots_kernel<<<1, 1024, 0, st>>>((int16_t*)slot, (int32_t*)idx, d);
+  colsumsq_reduce_kernel<<<(unsigned)((d + 63) / 64), kBlock, 0, st>>>((const double*)partial,
+                                                                        (double*)sumsq, d, chunks);
+  static bool staged_attr = false;
+  if (!staged_attr) {
+    staged_attr = hipFuncSetAttribute((const void*)outlier_pick_kernel<true>,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize,
+                                      (int)(kPickStagedMax * sizeof(double))) == hipSuccess;
+  }
+  if (staged_attr && d <= kPickStagedMax)
+    outlier_pick_kernel<true><<<1, kPickThreads, (size_t)d * sizeof(double), st>>>(
+        (const double*)sumsq, d, k, (int16_t*)slot, (int32_t*)idx);
+  else
+    outlier_pick_kernel<false><<<1, kPickThreads, 0, st>>>((const double*)sumsq, d, k,
+                                                           (int16_t*)slot, (int32_t*)idx);
   return launch_status();
 }
 

@@ -313,7 +313,7 @@ def outlier_select(t: torch.Tensor, k: int):
     t = t.contiguous()
     n, d = t.shape
     dev = t.device
-    chunks = max(1, (n + 255) // 256)
+    chunks = max(1, (n + 63) // 64)            # 64-row fp64 partial sums
     partial = torch.empty((chunks, d), dtype=torch.float64, device=dev)
     sumsq = torch.empty((d,), dtype=torch.float64, device=dev)
     slot = torch.empty((d,), dtype=torch.int16, device=dev)
