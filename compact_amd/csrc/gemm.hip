@@ -525,36 +525,58 @@ __device__ __forceinline__ void epi_store(const KArgs& A, const Acc& acc, int64_
 // epilogue ADD: C = bf16(C + bf16(alpha * bf16(acc)))   (PEFT's h + s * B(A(x))
 // in bf16: the product, the scaling and the sum are each rounded)
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ void epi_add(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+__device__ __forceinline__ void epi_add(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0,
+                                        uint16_t* lds) {
+  // bf16(acc) is staged through LDS as a row-major tile; 32 consecutive
+  // threads then own one row (8 columns each), so C is read and written back
+  // in contiguous row segments
+  constexpr int LD = 264;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave & 1, wm = wave >> 1;
   static_for<0, 4>([&](auto j) {
-    const int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
+    const int ml = wm * 128 + j * 32 + (lane & 31);
     static_for<0, 4>([&](auto i) {
+      const f32x16& a = acc.v[i][j];
       static_for<0, 4>([&](auto g) {
-        const int64_t n = n0 + wn * 128 + i * 32 + g * 8 + (lane >> 5) * 4;
-        if (m >= A.M) return;
-        uint16_t* cp = A.C + m * A.ldc + n;
-        if (n + 3 < A.N && ((reinterpret_cast<uintptr_t>(cp) & 7) == 0)) {
-          const uint2 w = *reinterpret_cast<const uint2*>(cp);
-          const float c0 = __uint_as_float(w.x << 16), c1 = __uint_as_float(w.x & 0xFFFF0000u);
-          const float c2 = __uint_as_float(w.y << 16), c3 = __uint_as_float(w.y & 0xFFFF0000u);
-          const f32x16& a = acc.v[i][j];
-          *reinterpret_cast<uint2*>(cp) = make_uint2(
-              pack_bf16x2(c0 + round_bf16(A.alpha * round_bf16(a[g * 4 + 0])),
-                          c1 + round_bf16(A.alpha * round_bf16(a[g * 4 + 1]))),
-              pack_bf16x2(c2 + round_bf16(A.alpha * round_bf16(a[g * 4 + 2])),
-                          c3 + round_bf16(A.alpha * round_bf16(a[g * 4 + 3]))));
-        } else {
-          for (int e = 0; e < 4; ++e) {
-            if (n + e >= A.N) break;
-            const float t = round_bf16(A.alpha * round_bf16(acc.v[i][j][g * 4 + e]));
-            cp[e] = (uint16_t)f32_to_bf16_bits(bf16_to_f32(cp[e]) + t);
-          }
-        }
+        const int nl = wn * 128 + i * 32 + g * 8 + (lane >> 5) * 4;
+        *reinterpret_cast<uint2*>(lds + ml * LD + nl) =
+            make_uint2(pack_bf16x2(a[g * 4 + 0], a[g * 4 + 1]), pack_bf16x2(a[g * 4 + 2], a[g * 4 + 3]));
       });
     });
   });
+  __syncthreads();
+  const int cl = (tid & 31) * 8;
+  const int64_t n = n0 + cl;
+  const bool vec = ((A.ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(A.C) & 15) == 0);
+#pragma unroll 4
+  for (int p = 0; p < 32; ++p) {
+    const int r = p * 8 + (tid >> 5);
+    const int64_t m = m0 + r;
+    if (m >= A.M || n >= A.N) continue;
+    const uint4 w = *reinterpret_cast<const uint4*>(lds + r * LD + cl);
+    const uint32_t aw[4] = {w.x, w.y, w.z, w.w};
+    float t[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      t[e] = round_bf16(A.alpha * __uint_as_float(e & 1 ? aw[e >> 1] & 0xFFFF0000u : aw[e >> 1] << 16));
+    uint16_t* cp = A.C + m * A.ldc + n;
+    if (vec && n + 7 < A.N) {
+      const uint4 c = *reinterpret_cast<const uint4*>(cp);
+      const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        o[e] = __uint_as_float(e & 1 ? cw[e >> 1] & 0xFFFF0000u : cw[e >> 1] << 16) + t[e];
+      *reinterpret_cast<uint4*>(cp) = make_uint4(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]),
+                                                 pack_bf16x2(o[4], o[5]), pack_bf16x2(o[6], o[7]));
+    } else {
+      for (int e = 0; e < 8; ++e) {
+        if (n + e >= A.N) break;
+        cp[e] = (uint16_t)f32_to_bf16_bits(bf16_to_f32(cp[e]) + t[e]);
+      }
+    }
+  }
 }
 
 // epilogue F32: fp32 partial of this split into ws[split][M][N]
@@ -854,9 +876,120 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_kernel(KArgs A) {
     mainloop<AK, BKM, EPI == EPI_GLU>(A, m0, n0, lds, acc);
   }
   if constexpr (EPI == EPI_STORE) epi_store(A, acc, m0, n0);
-  else if constexpr (EPI == EPI_ADD) epi_add(A, acc, m0, n0);
+  else if constexpr (EPI == EPI_ADD) epi_add(A, acc, m0, n0, lds);
   else if constexpr (EPI == EPI_GLU) epi_glu<CACHE, GS>(A, acc, m0, n0, lds);
   else if constexpr (EPI == EPI_DGLU) epi_dglu<CACHE, GS>(A, acc, m0, n0, lds);
+}
+
+// ---------------------------------------------------------------------------
+// thin LoRA add: C = bf16(C + bf16(alpha * bf16(A . B))) for K <= 16 (the
+// rank).  The product is K multiply-adds per output, so the op is the
+// read-modify-write of C: one thread owns 8 columns of a 256-column strip,
+// keeps B's 8 x K values in registers and walks 32 rows, reading and writing
+// C in 16-byte row segments.  Products of bf16 values are exact in fp32, so
+// the fp32 sum matches an MFMA's up to summation order.
+// ---------------------------------------------------------------------------
+constexpr int kThinK = 16;
+constexpr int kThinRows = 256;
+
+template <bool AVEC, int BVEC>
+__global__ __launch_bounds__(256) void thin_add_kernel(const uint16_t* __restrict__ a, int64_t sam,
+                                                       int64_t sak, const uint16_t* __restrict__ b,
+                                                       int64_t sbk, int64_t sbn, uint16_t* c,
+                                                       int64_t ldc, int64_t M, int64_t N, int K,
+                                                       float alpha, bool cvec) {
+  constexpr int RU = 4;   // rows in flight per thread
+  const int tid = threadIdx.x;
+  const int64_t n = (int64_t)blockIdx.x * 256 + (tid & 31) * 8;
+  if (n >= N) return;
+  float bw[8][kThinK];
+  if constexpr (BVEC == 2) {   // MN-major B: one 16-byte load of the 8 columns per k
+#pragma unroll
+    for (int k = 0; k < kThinK; ++k) {
+      const uint4 w4 = (k < K && n + 7 < N) ? *reinterpret_cast<const uint4*>(b + k * sbk + n)
+                                           : make_uint4(0, 0, 0, 0);
+      const uint32_t w[4] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        bw[e][k] = __uint_as_float(e & 1 ? w[e >> 1] & 0xFFFF0000u : w[e >> 1] << 16);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    if constexpr (BVEC == 2) {
+      // loaded above
+    } else if constexpr (BVEC == 1) {   // K-major B with K == 16: two 16-byte loads per column
+      const bool ok = n + e < N;
+      const uint4* bp = reinterpret_cast<const uint4*>(b + (n + e) * sbn);
+      const uint4 w0 = ok ? bp[0] : make_uint4(0, 0, 0, 0), w1 = ok ? bp[1] : make_uint4(0, 0, 0, 0);
+      const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+      for (int k = 0; k < kThinK; ++k)
+        bw[e][k] = __uint_as_float(k & 1 ? w[k >> 1] & 0xFFFF0000u : w[k >> 1] << 16);
+    } else {
+#pragma unroll
+      for (int k = 0; k < kThinK; ++k)
+        bw[e][k] = (k < K && n + e < N) ? bf16_to_f32(b[k * sbk + (n + e) * sbn]) : 0.0f;
+    }
+  }
+  const int64_t m0 = (int64_t)blockIdx.y * kThinRows;
+  const int64_t m1 = m0 + kThinRows < M ? m0 + kThinRows : M;
+  for (int64_t mb = m0 + (tid >> 5); mb < m1; mb += 8 * RU) {
+    uint4 aw[RU][2], cw[RU];
+    bool ok[RU];
+#pragma unroll
+    for (int q = 0; q < RU; ++q) {
+      const int64_t m = mb + 8 * q;
+      ok[q] = m < m1;
+      aw[q][0] = aw[q][1] = cw[q] = make_uint4(0, 0, 0, 0);
+      if (!ok[q]) continue;
+      if constexpr (AVEC) {
+        const uint4* ap = reinterpret_cast<const uint4*>(a + m * sam);
+        aw[q][0] = ap[0];
+        aw[q][1] = ap[1];
+      }
+      if (cvec && n + 7 < N) cw[q] = *reinterpret_cast<const uint4*>(c + m * ldc + n);
+    }
+#pragma unroll
+    for (int q = 0; q < RU; ++q) {
+      if (!ok[q]) continue;
+      const int64_t m = mb + 8 * q;
+      float av[kThinK];
+      if constexpr (AVEC) {
+        const uint32_t w[8] = {aw[q][0].x, aw[q][0].y, aw[q][0].z, aw[q][0].w,
+                               aw[q][1].x, aw[q][1].y, aw[q][1].z, aw[q][1].w};
+#pragma unroll
+        for (int k = 0; k < kThinK; ++k)
+          av[k] = __uint_as_float(k & 1 ? w[k >> 1] & 0xFFFF0000u : w[k >> 1] << 16);
+      } else {
+#pragma unroll
+        for (int k = 0; k < kThinK; ++k) av[k] = k < K ? bf16_to_f32(a[m * sam + k * sak]) : 0.0f;
+      }
+      float t[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kThinK; ++k) acc += av[k] * bw[e][k];
+        t[e] = round_bf16(alpha * round_bf16(acc));
+      }
+      uint16_t* cp = c + m * ldc + n;
+      if (cvec && n + 7 < N) {
+        const uint32_t w[4] = {cw[q].x, cw[q].y, cw[q].z, cw[q].w};
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          o[e] = __uint_as_float(e & 1 ? w[e >> 1] & 0xFFFF0000u : w[e >> 1] << 16) + t[e];
+        *reinterpret_cast<uint4*>(cp) = make_uint4(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]),
+                                                   pack_bf16x2(o[4], o[5]), pack_bf16x2(o[6], o[7]));
+      } else {
+        for (int e = 0; e < 8; ++e) {
+          if (n + e >= N) break;
+          cp[e] = (uint16_t)f32_to_bf16_bits(bf16_to_f32(cp[e]) + t[e]);
+        }
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -993,6 +1126,29 @@ int cpt_gemm_bf16_ex(const void* a, int64_t lda, int a_kmajor, const void* b, in
     if (a_kmajor && !b_kmajor) return launch<true, false, EPI_STORE, 0, 0>(A, st);
     if (!a_kmajor && !b_kmajor) return launch<false, false, EPI_STORE, 0, 0>(A, st);
     return launch<false, true, EPI_STORE, 0, 0>(A, st);
+  }
+  if (mode == 1 && K > 0 && K <= kThinK) {
+    const int64_t sam = a_kmajor ? lda : 1, sak = a_kmajor ? 1 : lda;
+    const int64_t sbk = b_kmajor ? 1 : ldb, sbn = b_kmajor ? ldb : 1;
+    const bool avec = a_kmajor && K == kThinK && (lda & 7) == 0 && al16(a);
+    // 1: K-major B, K == 16, rows 16-byte aligned; 2: MN-major B whose 8-column
+    // runs are 16-byte aligned and complete (N % 8 == 0)
+    const int bvec = (b_kmajor && K == kThinK && (ldb & 7) == 0 && al16(b)) ? 1
+                     : (!b_kmajor && (ldb & 7) == 0 && (N & 7) == 0 && al16(b)) ? 2 : 0;
+    const bool cvec = (ldc & 7) == 0 && al16(c);
+    const dim3 grid((unsigned)((N + 255) / 256), (unsigned)((M + kThinRows - 1) / kThinRows));
+    if (grid.y > 65535) return kErrTooLarge;
+#define CPT_THIN(AV, BV)                                                                         \
+  hipLaunchKernelGGL((thin_add_kernel<AV, BV>), grid, dim3(256), 0, st, (const uint16_t*)a, sam, \
+                     sak, (const uint16_t*)b, sbk, sbn, (uint16_t*)c, ldc, M, N, (int)K, alpha,  \
+                     cvec)
+    if (avec) {
+      if (bvec == 1) CPT_THIN(true, 1); else if (bvec == 2) CPT_THIN(true, 2); else CPT_THIN(true, 0);
+    } else {
+      if (bvec == 1) CPT_THIN(false, 1); else if (bvec == 2) CPT_THIN(false, 2); else CPT_THIN(false, 0);
+    }
+#undef CPT_THIN
+    return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
   }
   if (mode == 1) {
     if (a_kmajor && b_kmajor) return launch<true, true, EPI_ADD, 0, 0>(A, st);
