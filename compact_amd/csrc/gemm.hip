@@ -490,6 +490,135 @@ __device__ __forceinline__ void mainloop(const KArgs& A, int64_t m0, int64_t n0,
   __syncthreads();   // the epilogue may reuse LDS
 }
 
+
+// Continuous-pipeline main loop: during k-tile kt the registers hold tile kt+1,
+// which is written to the other LDS stage group by group across the four
+// sub-steps, each group reloaded with tile kt+2 right after its write.  Loads
+// and LDS writes are spread evenly (no burst), and each load has a whole
+// k-tile to land.  K-major operands go 2 registers per group; an MN-major
+// operand's 8 registers form one transpose group (A in sub-step 0, B in 2).
+template <bool AK, bool BKM, bool DUAL>
+__device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t n0, uint16_t* lds,
+                                            Acc& acc) {
+  constexpr bool BK_ = BKM || DUAL;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wn = wave & 1, wm = wave >> 1;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc.v[i][j][r] = 0.0f;
+  Loader<AK, BKM, DUAL> L;
+  L.init(A, m0, n0, tid);
+  int nk = L.nk0;
+  if (A.npairs > 1) nk += (int)((A.K[1] + BK - 1) / BK);
+  if (nk <= 0) return;
+  uint4 va[8], vb[8];
+  auto ldA = [&](int kt, int it) -> uint4 {
+    const int p = kt >= L.nk0 ? 1 : 0;
+    const int64_t k0 = (int64_t)(kt - p * L.nk0) * BK;
+    const int64_t Kp = p ? L.K[1] : L.K[0];
+    const __amdgpu_buffer_rsrc_t rA = p ? L.ra[1] : L.ra[0];
+    if (AK) {
+      const bool kok = k0 + (tid & 7) * 8 < Kp;
+      return bload(rA, kok ? L.oa[it] + (uint32_t)(k0 * 2) : kOOB);
+    }
+    return bload(rA, L.oa[it] == kOOB ? kOOB : L.oa[it] + (uint32_t)(k0 * L.lda * 2));
+  };
+  auto ldB = [&](int kt, int it) -> uint4 {
+    const int p = kt >= L.nk0 ? 1 : 0;
+    const int64_t k0 = (int64_t)(kt - p * L.nk0) * BK;
+    const int64_t Kp = p ? L.K[1] : L.K[0];
+    const __amdgpu_buffer_rsrc_t rB = p ? L.rb[1] : L.rb[0];
+    if (BK_) {
+      const bool kok = k0 + (tid & 7) * 8 < Kp;
+      const __amdgpu_buffer_rsrc_t r = (DUAL && ((it >> 1) & 1)) ? L.rup : rB;
+      return bload(r, kok ? L.ob[it] + (uint32_t)(k0 * 2) : kOOB);
+    }
+    return bload(rB, L.ob[it] == kOOB ? kOOB : L.ob[it] + (uint32_t)(k0 * L.ldb * 2));
+  };
+  // group g of tile kt: store the held registers into `stage`, reload them with tile kt_load
+  auto group = [&](int g, int stage, int kt_load) {
+    uint16_t* sa = lds + stage * 2 * TILE_ELEMS;
+    uint16_t* sb = sa + TILE_ELEMS;
+    if (AK) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int it = 2 * g + h, q = tid + NTHR * it;
+        *reinterpret_cast<uint4*>(sa + lds_off<true>(q >> 3, q & 7)) = va[it];
+        va[it] = ldA(kt_load, it);
+      }
+    } else if (g == 0) {
+      sstore_mnmajor(sa, tid, va);
+#pragma unroll
+      for (int it = 0; it < 8; ++it) va[it] = ldA(kt_load, it);
+    }
+    if (BK_) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int it = 2 * g + h, q = tid + NTHR * it;
+        *reinterpret_cast<uint4*>(sb + lds_off<true>(q >> 3, q & 7)) = vb[it];
+        vb[it] = ldB(kt_load, it);
+      }
+    } else if (g == 2) {
+      sstore_mnmajor(sb, tid, vb);
+#pragma unroll
+      for (int it = 0; it < 8; ++it) vb[it] = ldB(kt_load, it);
+    }
+  };
+  // prologue: tile 0 into stage 0, tile 1 into registers
+#pragma unroll
+  for (int it = 0; it < 8; ++it) { va[it] = ldA(0, it); vb[it] = ldB(0, it); }
+  {
+    uint16_t* sa = lds;
+    uint16_t* sb = sa + TILE_ELEMS;
+    if (AK) sstore_kmajor(sa, tid, va); else sstore_mnmajor(sa, tid, va);
+    if (BK_) sstore_kmajor(sb, tid, vb); else sstore_mnmajor(sb, tid, vb);
+  }
+#pragma unroll
+  for (int it = 0; it < 8; ++it) { va[it] = ldA(1, it); vb[it] = ldB(1, it); }
+  __syncthreads();
+  Frags f0, f1;
+  read_frags<AK, BK_>(lds, wn, wm, lane, 0, f0);
+  constexpr int MASK = SG_DS_R | SG_DS_W | SG_VMEM_R;
+  for (int kt = 0; kt + 1 < nk; ++kt) {
+    const int stage = kt & 1;
+    const uint16_t* base = lds + stage * 2 * TILE_ELEMS;
+    read_frags<AK, BK_>(base, wn, wm, lane, 1, f1);
+    mfma_range<0, 16>(f0, acc);
+    group(0, stage ^ 1, kt + 2);
+    sched_interleave<16, MASK, 2>();
+    read_frags<AK, BK_>(base, wn, wm, lane, 2, f0);
+    mfma_range<0, 16>(f1, acc);
+    group(1, stage ^ 1, kt + 2);
+    sched_interleave<16, MASK, 1>();
+    read_frags<AK, BK_>(base, wn, wm, lane, 3, f1);
+    mfma_range<0, 16>(f0, acc);
+    group(2, stage ^ 1, kt + 2);
+    sched_interleave<16, MASK, 2>();
+    mfma_range<0, 8>(f1, acc);
+    group(3, stage ^ 1, kt + 2);
+    sched_interleave<8, MASK, 1>();
+    __syncthreads();
+    read_frags<AK, BK_>(lds + (stage ^ 1) * 2 * TILE_ELEMS, wn, wm, lane, 0, f0);
+    mfma_range<8, 16>(f1, acc);
+    sched_interleave<8, SG_DS_R>();
+  }
+  {
+    const uint16_t* base = lds + ((nk - 1) & 1) * 2 * TILE_ELEMS;
+    read_frags<AK, BK_>(base, wn, wm, lane, 1, f1);
+    mfma_range<0, 16>(f0, acc);
+    read_frags<AK, BK_>(base, wn, wm, lane, 2, f0);
+    mfma_range<0, 16>(f1, acc);
+    read_frags<AK, BK_>(base, wn, wm, lane, 3, f1);
+    mfma_range<0, 16>(f0, acc);
+    mfma_range<0, 16>(f1, acc);
+  }
+  __syncthreads();
+}
+
 __device__ __forceinline__ uint32_t absbits(float x) { return __float_as_uint(x) & 0x7FFFFFFFu; }
 
 // ---------------------------------------------------------------------------
@@ -873,7 +1002,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_kernel(KArgs A) {
     epi_f32(A, acc, m0, n0, split);
     return;
   } else {
-    mainloop<AK, BKM, EPI == EPI_GLU>(A, m0, n0, lds, acc);
+    mainloop_pp<AK, BKM, EPI == EPI_GLU>(A, m0, n0, lds, acc);
   }
   if constexpr (EPI == EPI_STORE) epi_store(A, acc, m0, n0);
   else if constexpr (EPI == EPI_ADD) epi_add(A, acc, m0, n0, lds);
