@@ -1001,6 +1001,8 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_kernel(KArgs A) {
                              (split + 1) * A.kt_per_split);
     epi_f32(A, acc, m0, n0, split);
     return;
+  } else if constexpr (!AK && !BKM) {
+    mainloop<AK, BKM, false>(A, m0, n0, lds, acc);   // TN: the burst schedule measures faster
   } else {
     mainloop_pp<AK, BKM, EPI == EPI_GLU>(A, m0, n0, lds, acc);
   }
