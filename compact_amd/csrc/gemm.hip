@@ -589,7 +589,7 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
     read_frags<AK, BK_>(base, wn, wm, lane, 1, f1);
     mfma_range<0, 16>(f0, acc);
     group(0, stage ^ 1, kt + 2);
-    sched_interleave<16, MASK, 2>();
+    sched_interleave<16, MASK, AK ? 1 : 2>();
     read_frags<AK, BK_>(base, wn, wm, lane, 2, f0);
     mfma_range<0, 16>(f1, acc);
     group(1, stage ^ 1, kt + 2);
@@ -597,7 +597,7 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
     read_frags<AK, BK_>(base, wn, wm, lane, 3, f1);
     mfma_range<0, 16>(f0, acc);
     group(2, stage ^ 1, kt + 2);
-    sched_interleave<16, MASK, 2>();
+    sched_interleave<16, MASK, BK_ ? 1 : 2>();
     mfma_range<0, 8>(f1, acc);
     group(3, stage ^ 1, kt + 2);
     sched_interleave<8, MASK, 1>();
