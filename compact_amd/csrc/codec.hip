@@ -93,13 +93,23 @@ struct Outliers {
   const int16_t* slot;   // [D], -1 for ordinary columns
   uint16_t* out;         // [N, k] bf16
   int64_t k;
+  FastDivU32 rows;       // divides a chunk index by the chunks per row (D / 8)
 };
+
+// (row, first column) of 8-element chunk c of a row-major [N, D] tensor;
+// chunk indices fit 32 bits (checked on the host)
+__device__ __forceinline__ void chunk_rc(int64_t c, int64_t d, const Outliers& o, int64_t& row,
+                                         int64_t& col) {
+  const uint32_t r = o.rows.div((uint32_t)c);
+  row = r;
+  col = ((int64_t)((uint32_t)c - r * o.rows.d)) * 8;
+}
 
 __device__ __forceinline__ void extract_outliers8(float v[8], int64_t c, int64_t d,
                                                   const Outliers& o, bool valid) {
   if (!valid) return;
-  const int64_t e0 = c * 8;
-  const int64_t row = e0 / d, col = e0 - row * d;
+  int64_t row, col;
+  chunk_rc(c, d, o, row, col);
   const uint4 w = *reinterpret_cast<const uint4*>(o.slot + col);   // 8 x int16
   const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -116,8 +126,8 @@ __device__ __forceinline__ void extract_outliers8(float v[8], int64_t c, int64_t
 // (compress_function.py:147-174).
 __device__ __forceinline__ void restore_outliers8(float v[8], int64_t c, int64_t d,
                                                   const Outliers& o) {
-  const int64_t e0 = c * 8;
-  const int64_t row = e0 / d, col = e0 - row * d;
+  int64_t row, col;
+  chunk_rc(c, d, o, row, col);
   const uint4 w = *reinterpret_cast<const uint4*>(o.slot + col);
   const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -130,16 +140,28 @@ __device__ __forceinline__ void restore_outliers8(float v[8], int64_t c, int64_t
 // ---------------------------------------------------------------------------
 // standalone quantise, fast path (input dtype DT, group size 8*LPG)
 // ---------------------------------------------------------------------------
+constexpr int kQuantCPT = 2;   // chunks per thread: both loads in flight before either codes
+
 template <int DT, int BITS, int LPG, bool OUTL>
 __global__ __launch_bounds__(kBlock) void quantize_fast_kernel(
     const void* __restrict__ t, uint8_t* __restrict__ q, uint16_t* __restrict__ s,
     int64_t nchunk, int64_t d, Outliers o) {
-  const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  const bool valid = c < nchunk;
-  float v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  if (valid) Vec8<DT>::ld(t, c, v);
-  if (OUTL) extract_outliers8(v, c, d, o, valid);
-  quant_chunk<BITS, LPG>(v, valid, c, q, s);
+  const int64_t base = (int64_t)blockIdx.x * kBlock * kQuantCPT + threadIdx.x;
+  float v[kQuantCPT][8];
+#pragma unroll
+  for (int i = 0; i < kQuantCPT; ++i) {
+    const int64_t c = base + i * kBlock;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[i][j] = 0.0f;
+    if (c < nchunk) Vec8<DT>::ld(t, c, v[i]);
+  }
+#pragma unroll
+  for (int i = 0; i < kQuantCPT; ++i) {
+    const int64_t c = base + i * kBlock;
+    const bool valid = c < nchunk;
+    if (OUTL) extract_outliers8(v[i], c, d, o, valid);
+    quant_chunk<BITS, LPG>(v[i], valid, c, q, s);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -418,7 +440,7 @@ inline int check_codec(int64_t n, int64_t d, int bits, int64_t gs, bool need_pow
 template <int BITS, int LPG, bool OUTL>
 void launch_quant_fast(int dt, const void* t, uint8_t* q, uint16_t* s, int64_t nchunk, int64_t d,
                        Outliers o, hipStream_t st) {
-  const unsigned grid = grid_for(nchunk);
+  const unsigned grid = grid_for((nchunk + kQuantCPT - 1) / kQuantCPT);
   if (dt == kBF16)
     quantize_fast_kernel<kBF16, BITS, LPG, OUTL><<<grid, kBlock, 0, st>>>(t, q, s, nchunk, d, o);
   else if (dt == kF16)
@@ -921,7 +943,8 @@ int cpt_v3_quantize_outlier(const void* t, int dtype, int64_t n, int64_t d, int 
   if (group_size < 8 || group_size > 512 || !aligned16(t) || ((uintptr_t)payload & 7) ||
       !outlier_args_ok(slot, outliers, k, d))
     return kErrAlign;
-  Outliers o{(const int16_t*)slot, (uint16_t*)outliers, k};
+  if (n * d / 8 > 0xFFFFFFFFll) return kErrTooLarge;   // 32-bit chunk indices
+  Outliers o{(const int16_t*)slot, (uint16_t*)outliers, k, FastDivU32::make((uint32_t)(d / 8))};
   hipStream_t st = (hipStream_t)stream;
   const int lpg = (int)(group_size / 8);
   if (bits == 4) launch_quant_fast_lpg<4, true>(dtype, lpg, t, (uint8_t*)payload, (uint16_t*)scales, n * d / 8, d, o, st);
@@ -939,7 +962,8 @@ int cpt_v3_dequantize_outlier(const void* payload, const void* scales, const voi
   if (group_size < 8 || !aligned16(out) || ((uintptr_t)payload & 7) ||
       !outlier_args_ok(slot, outliers, k, d))
     return kErrAlign;
-  Outliers o{(const int16_t*)slot, (uint16_t*)outliers, k};
+  if (n * d / 8 > 0xFFFFFFFFll) return kErrTooLarge;   // 32-bit chunk indices
+  Outliers o{(const int16_t*)slot, (uint16_t*)outliers, k, FastDivU32::make((uint32_t)(d / 8))};
   hipStream_t st = (hipStream_t)stream;
   const int64_t nchunk = n * d / 8;
   const int sh = log2_exact(group_size);
@@ -963,8 +987,9 @@ int cpt_silu_mul_quant_outlier(const void* h_gate, const void* h_up, int64_t n, 
       !aligned16(h_mid) || ((uintptr_t)q_gate & 7) || ((uintptr_t)q_up & 7) ||
       !outlier_args_ok(slot_gate, o_gate, k, d) || !outlier_args_ok(slot_up, o_up, k, d))
     return kErrAlign;
-  Outliers og{(const int16_t*)slot_gate, (uint16_t*)o_gate, k};
-  Outliers ou{(const int16_t*)slot_up, (uint16_t*)o_up, k};
+  if (n * d / 8 > 0xFFFFFFFFll) return kErrTooLarge;   // 32-bit chunk indices
+  Outliers og{(const int16_t*)slot_gate, (uint16_t*)o_gate, k, FastDivU32::make((uint32_t)(d / 8))};
+  Outliers ou{(const int16_t*)slot_up, (uint16_t*)o_up, k, FastDivU32::make((uint32_t)(d / 8))};
   hipStream_t st = (hipStream_t)stream;
   const int lpg = (int)(group_size / 8);
   if (bits == 4)
@@ -995,8 +1020,9 @@ int cpt_dequant_swiglu_backward_outlier(const void* grad_h_mid, const void* q_ga
       ((uintptr_t)q_gate & 7) || ((uintptr_t)q_up & 7) ||
       !outlier_args_ok(slot_gate, o_gate, k, d) || !outlier_args_ok(slot_up, o_up, k, d))
     return kErrAlign;
-  Outliers og{(const int16_t*)slot_gate, (uint16_t*)o_gate, k};
-  Outliers ou{(const int16_t*)slot_up, (uint16_t*)o_up, k};
+  if (n * d / 8 > 0xFFFFFFFFll) return kErrTooLarge;   // 32-bit chunk indices
+  Outliers og{(const int16_t*)slot_gate, (uint16_t*)o_gate, k, FastDivU32::make((uint32_t)(d / 8))};
+  Outliers ou{(const int16_t*)slot_up, (uint16_t*)o_up, k, FastDivU32::make((uint32_t)(d / 8))};
   hipStream_t st = (hipStream_t)stream;
   const int64_t nchunk = n * d / 8;
   const unsigned grid = grid_for(nchunk);

@@ -123,6 +123,30 @@ template <> struct Vec8<kBF16> : Vec8Half<kBF16> {};
 
 __host__ __device__ __forceinline__ bool is_pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
 
+// Unsigned 32-bit division by a run-time invariant divisor with one multiply-high
+// (Granlund & Montgomery, "Division by Invariant Integers using Multiplication",
+// PLDI 1994, section 4): l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1,
+// n / d = (t + ((n - t) >> 1)) >> (l - 1) with t = mulhi(m, n); exact for all
+// 32-bit n and d >= 1.
+struct FastDivU32 {
+  uint32_t d = 1, m = 1;
+  int l = 0;
+  __host__ static FastDivU32 make(uint32_t divisor) {
+    FastDivU32 f;
+    f.d = divisor;
+    int l = 0;
+    while ((1ull << l) < divisor) ++l;
+    f.l = l;
+    f.m = (uint32_t)((((1ull << 32) * ((1ull << l) - divisor)) / divisor) + 1);
+    return f;
+  }
+  __device__ __forceinline__ uint32_t div(uint32_t n) const {
+    if (d == 1) return n;
+    const uint32_t t = __umulhi(m, n);
+    return (t + ((n - t) >> 1)) >> (l - 1);
+  }
+};
+
 __host__ __forceinline__ bool aligned16(const void* p) {
   return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
 }
