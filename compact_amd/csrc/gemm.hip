@@ -4,9 +4,10 @@
 //
 // Operands are bf16.  Each operand is either K-major (K contiguous: A stored
 // [M][lda], B stored [N][ldb] -- the nn.Linear weight layout) or MN-major
-// (A stored [K][lda], B stored [K][ldb]).  Tiles are staged in LDS K-major
-// so every MFMA fragment is one 128-bit LDS read; MN-major operands are
-// transposed 8x8 in registers on their way into LDS.
+// (A stored [K][lda], B stored [K][ldb]).  Tiles go to LDS in their memory
+// layout: a K-major fragment is one 128-bit LDS read, an MN-major fragment two
+// LDS transpose reads (ds_read_b64_tr_b16), so no operand is transposed in
+// registers.
 //
 // Block tile 256 (m) x 256 (n) x 64 (k), 256 threads = 4 wavefronts in a
 // 2 x 2 arrangement, each owning 128 x 128 outputs as 4 x 4 tiles of
@@ -16,8 +17,8 @@
 // epilogues want (a quantisation group is a run of columns of one row).
 //   acc[i][j][r] -> n = nw + 32 i + 8 (r / 4) + 4 (lane / 32) + r % 4
 //                   m = mw + 32 j + lane % 32
-// LDS: two stages x two operands x 256 rows x 64 bf16 in padded rows
-// (146 KiB; see lds_row), conflict-free on gfx950's 64 banks for the fragment
+// LDS: two stages x two operands x 256 x 64 bf16 in padded rows (146 KiB; see
+// lds_off and lds_mn), conflict-free on gfx950's 64 banks for the fragment
 // reads and for the stores of either operand layout.
 // Grid: one block per output tile, block ids remapped so each XCD works on a
 // contiguous range of tiles, grouped 8 tile-rows deep for L2 reuse.
@@ -49,24 +50,35 @@ constexpr int TILE_ELEMS = 256 * 72 + 32 * 8;  // one operand stage in LDS (padd
 constexpr int LDS_BYTES = 4 * TILE_ELEMS * 2;   // 2 stages x 2 operands (146 KiB)
 constexpr int GROUP_ROWS = 8;                  // tile-rows per L2 group
 
-// Padded rows: row r starts at r * 72 + (r / 8) * 8 elements (144 bytes per
-// row plus 16 bytes per 8 rows).  8 consecutive rows fall on distinct 16-byte
-// bank groups (36-dword stride), and so do 8 rows spaced 8 apart (292-dword
-// stride), which keeps fragment reads and transposed stores conflict-free
-// while the address stays affine in the chunk.
-// LDS is 64 banks of 4 bytes on gfx950, and a 128-bit access is served 16
-// lanes at a time, so 16 lanes must cover 64 distinct banks.  Fragment reads
-// take 16 consecutive rows at one 16-byte chunk; K-major stores take 2 rows x 8
-// chunks; transposed (MN-major) stores take 16 rows spaced 8 apart, one chunk.
-//   K-major tiles:  row r at r * 64 + (r / 2) * 8 elements   (reads, stores 1-way)
-//   MN-major tiles: row r at r * 72 + (r / 16) * 8 elements  (reads, stores 1-way)
-// Both stay affine in the chunk, so fragment addresses are immediate offsets.
-template <bool KM>
-__device__ __forceinline__ int lds_row(int row) {
-  return KM ? row * 64 + ((row >> 1) << 3) : row * 72 + ((row >> 4) << 3);
+// K-major tiles: row r (m or n) at r * 64 + (r / 2) * 8 elements, 8-element
+// (16-byte) k chunks.  LDS is 64 banks of 4 bytes on gfx950 and a 128-bit
+// access is served 16 lanes at a time, so 16 lanes must cover 64 distinct
+// banks: fragment reads take 16 consecutive rows at one chunk, stores take 2
+// rows x 8 chunks, both 1-way.  The address stays affine in the chunk, so
+// fragment addresses are immediate offsets.
+__device__ __forceinline__ int lds_off(int row, int chunk) {
+  return row * 64 + ((row >> 1) << 3) + (chunk << 3);
 }
-template <bool KM>
-__device__ __forceinline__ int lds_off(int row, int chunk) { return lds_row<KM>(row) + (chunk << 3); }
+
+// MN-major tiles are kept as they lie in memory: 64 k-rows of 256 mn, rows
+// LDM = 288 elements apart (576 bytes, 64 mod 256).  Stores are plain 16-byte
+// row segments (16 lanes = 256 contiguous bytes).  Fragments (8 consecutive k
+// of one mn per lane) come out of the gfx950 transpose read ds_read_b64_tr_b16:
+// within each 16-lane group, lane s addresses the 4 elements at k-row s / 4,
+// mn 4 (s % 4) of a 4 x 16 block and lane j receives column j of it, element e
+// from row e.  One read yields 4 k of the fragment, two reads make the 8.  A
+// 32-lane pass reads 4 rows x 64 bytes, which the 64-byte row skew spreads over
+// all 64 banks.
+constexpr int LDM = 288;
+__device__ __forceinline__ int lds_mn(int k, int mn) { return k * LDM + mn; }
+static_assert(64 * LDM <= TILE_ELEMS, "MN-major stage must fit the stage size");
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+__device__ __forceinline__ i16x4 lds_read_tr(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+}
 
 // ---------------------------------------------------------------------------
 // global -> registers -> LDS
@@ -92,7 +104,7 @@ __device__ __forceinline__ void sstore_kmajor(uint16_t* lds, int tid, const uint
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
     const int q = tid + NTHR * it;
-    *reinterpret_cast<uint4*>(lds + lds_off<true>(q >> 3, q & 7)) = reg[it];
+    *reinterpret_cast<uint4*>(lds + lds_off(q >> 3, q & 7)) = reg[it];
   }
 }
 
@@ -112,23 +124,14 @@ __device__ __forceinline__ void gload_mnmajor(const uint16_t* p, int64_t ld, int
   }
 }
 
-__device__ __forceinline__ uint32_t dword_of(const uint4& v, int i) {
-  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+// MN-major tile: the thread's row r (k = 8 (tid / 32) + r) into its 16-byte
+// mn segment, untransposed.
+__device__ __forceinline__ void sstore_mn_row(uint16_t* lds, int tid, int r, const uint4& v) {
+  *reinterpret_cast<uint4*>(lds + lds_mn((tid >> 5) * 8 + r, (tid & 31) * 8)) = v;
 }
-
-// 8x8 transpose of 16-bit elements: LDS row (mn) i gets element i of reg[0..7] (k).
 __device__ __forceinline__ void sstore_mnmajor(uint16_t* lds, int tid, const uint4 (&reg)[8]) {
-  const int mb = tid & 31, kb = tid >> 5;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    uint32_t o[4];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const uint32_t lo = dword_of(reg[2 * w], i >> 1), hi = dword_of(reg[2 * w + 1], i >> 1);
-      o[w] = (i & 1) ? ((lo >> 16) | (hi & 0xFFFF0000u)) : ((lo & 0xFFFFu) | (hi << 16));
-    }
-    *reinterpret_cast<uint4*>(lds + lds_off<false>(mb * 8 + i, kb)) = make_uint4(o[0], o[1], o[2], o[3]);
-  }
+  for (int r = 0; r < 8; ++r) sstore_mn_row(lds, tid, r, reg[r]);
 }
 
 // ---------------------------------------------------------------------------
@@ -350,6 +353,16 @@ struct Frags {
   bf16x8 m[4];   // m-side fragments (MFMA B slot)
 };
 
+// MFMA fragment of an MN-major tile: 8 consecutive k (sub-step s, lane half)
+// of mn row rowbase + lane % 32, as two transpose reads of 4 k each.
+__device__ __forceinline__ bf16x8 frag_mn(const uint16_t* t, int rowbase, int s, int lane) {
+  const int k = s * 16 + 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int mn = rowbase + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const i16x4 lo = lds_read_tr(t + lds_mn(k, mn));
+  const i16x4 hi = lds_read_tr(t + lds_mn(k + 4, mn));
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 template <bool AKM, bool BKM>
 __device__ __forceinline__ void read_frags(const uint16_t* stage_base, int wn, int wm, int lane,
                                            int s, Frags& f) {
@@ -357,11 +370,19 @@ __device__ __forceinline__ void read_frags(const uint16_t* stage_base, int wn, i
   const uint16_t* sb = stage_base + TILE_ELEMS;
   const int chunk = s * 2 + (lane >> 5);
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    f.n[i] = *reinterpret_cast<const bf16x8*>(sb + lds_off<BKM>(wn * 128 + i * 32 + (lane & 31), chunk));
+  for (int i = 0; i < 4; ++i) {
+    if (BKM)
+      f.n[i] = *reinterpret_cast<const bf16x8*>(sb + lds_off(wn * 128 + i * 32 + (lane & 31), chunk));
+    else
+      f.n[i] = frag_mn(sb, wn * 128 + i * 32, s, lane);
+  }
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
-    f.m[j] = *reinterpret_cast<const bf16x8*>(sa + lds_off<AKM>(wm * 128 + j * 32 + (lane & 31), chunk));
+  for (int j = 0; j < 4; ++j) {
+    if (AKM)
+      f.m[j] = *reinterpret_cast<const bf16x8*>(sa + lds_off(wm * 128 + j * 32 + (lane & 31), chunk));
+    else
+      f.m[j] = frag_mn(sa, wm * 128 + j * 32, s, lane);
+  }
 }
 
 template <int I0, int I1>
@@ -495,8 +516,7 @@ __device__ __forceinline__ void mainloop(const KArgs& A, int64_t m0, int64_t n0,
 // which is written to the other LDS stage group by group across the four
 // sub-steps, each group reloaded with tile kt+2 right after its write.  Loads
 // and LDS writes are spread evenly (no burst), and each load has a whole
-// k-tile to land.  K-major operands go 2 registers per group; an MN-major
-// operand's 8 registers form one transpose group (A in sub-step 0, B in 2).
+// k-tile to land.  Each operand goes 2 registers per group.
 template <bool AK, bool BKM, bool DUAL>
 __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t n0, uint16_t* lds,
                                             Acc& acc) {
@@ -543,29 +563,19 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
   auto group = [&](int g, int stage, int kt_load) {
     uint16_t* sa = lds + stage * 2 * TILE_ELEMS;
     uint16_t* sb = sa + TILE_ELEMS;
-    if (AK) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int it = 2 * g + h, q = tid + NTHR * it;
-        *reinterpret_cast<uint4*>(sa + lds_off<true>(q >> 3, q & 7)) = va[it];
-        va[it] = ldA(kt_load, it);
-      }
-    } else if (g == 0) {
-      sstore_mnmajor(sa, tid, va);
-#pragma unroll
-      for (int it = 0; it < 8; ++it) va[it] = ldA(kt_load, it);
+    for (int h = 0; h < 2; ++h) {
+      const int it = 2 * g + h, q = tid + NTHR * it;
+      if (AK) *reinterpret_cast<uint4*>(sa + lds_off(q >> 3, q & 7)) = va[it];
+      else sstore_mn_row(sa, tid, it, va[it]);
+      va[it] = ldA(kt_load, it);
     }
-    if (BK_) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int it = 2 * g + h, q = tid + NTHR * it;
-        *reinterpret_cast<uint4*>(sb + lds_off<true>(q >> 3, q & 7)) = vb[it];
-        vb[it] = ldB(kt_load, it);
-      }
-    } else if (g == 2) {
-      sstore_mnmajor(sb, tid, vb);
-#pragma unroll
-      for (int it = 0; it < 8; ++it) vb[it] = ldB(kt_load, it);
+    for (int h = 0; h < 2; ++h) {
+      const int it = 2 * g + h, q = tid + NTHR * it;
+      if (BK_) *reinterpret_cast<uint4*>(sb + lds_off(q >> 3, q & 7)) = vb[it];
+      else sstore_mn_row(sb, tid, it, vb[it]);
+      vb[it] = ldB(kt_load, it);
     }
   };
   // prologue: tile 0 into stage 0, tile 1 into registers
@@ -583,28 +593,31 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
   Frags f0, f1;
   read_frags<AK, BK_>(lds, wn, wm, lane, 0, f0);
   constexpr int MASK = SG_DS_R | SG_DS_W | SG_VMEM_R;
+  // memory instructions per MFMA: an MN-major operand's fragments take two
+  // transpose reads each
+  constexpr int PER = (AK && BK_) ? 1 : 2;
   for (int kt = 0; kt + 1 < nk; ++kt) {
     const int stage = kt & 1;
     const uint16_t* base = lds + stage * 2 * TILE_ELEMS;
     read_frags<AK, BK_>(base, wn, wm, lane, 1, f1);
     mfma_range<0, 16>(f0, acc);
     group(0, stage ^ 1, kt + 2);
-    sched_interleave<16, MASK, AK ? 1 : 2>();
+    sched_interleave<16, MASK, PER>();
     read_frags<AK, BK_>(base, wn, wm, lane, 2, f0);
     mfma_range<0, 16>(f1, acc);
     group(1, stage ^ 1, kt + 2);
-    sched_interleave<16, MASK, 1>();
+    sched_interleave<16, MASK, PER>();
     read_frags<AK, BK_>(base, wn, wm, lane, 3, f1);
     mfma_range<0, 16>(f0, acc);
     group(2, stage ^ 1, kt + 2);
-    sched_interleave<16, MASK, BK_ ? 1 : 2>();
+    sched_interleave<16, MASK, PER>();
     mfma_range<0, 8>(f1, acc);
     group(3, stage ^ 1, kt + 2);
     sched_interleave<8, MASK, 1>();
     __syncthreads();
     read_frags<AK, BK_>(lds + (stage ^ 1) * 2 * TILE_ELEMS, wn, wm, lane, 0, f0);
     mfma_range<8, 16>(f1, acc);
-    sched_interleave<8, SG_DS_R>();
+    sched_interleave<8, SG_DS_R, PER>();
   }
   {
     const uint16_t* base = lds + ((nk - 1) & 1) * 2 * TILE_ELEMS;
@@ -1001,8 +1014,6 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_kernel(KArgs A) {
                              (split + 1) * A.kt_per_split);
     epi_f32(A, acc, m0, n0, split);
     return;
-  } else if constexpr (!AK && !BKM) {
-    mainloop<AK, BKM, false>(A, m0, n0, lds, acc);   // TN: the burst schedule measures faster
   } else {
     mainloop_pp<AK, BKM, EPI == EPI_GLU>(A, m0, n0, lds, acc);
   }
