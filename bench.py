@@ -123,6 +123,47 @@ def cpu_baseline(budget_tokens=512):
             "median_s": med}
 
 
+def library_arm(x, gy, wg, wu, wd, steps, warmup):
+    """The same C2 step in the reference's structure (src/flashffn.py:1409-1587)
+    with every GEMM through torch.matmul (hipBLASLt on ROCm) and the codec as the
+    standalone K1 / K2 kernels of this build: what the reference's composition
+    of library GEMMs and separate codec kernels gives on this GPU.  Returns
+    ms per step (HIP events around `steps` steps, mean)."""
+    import torch
+    from compact_amd import kernels as K
+
+    def lib_step():
+        hg = x @ wg.t()
+        hu = x @ wu.t()
+        h_mid, cg, sg, cu, su = K.silu_mul_quant(hg, hu, BITS, GROUP)
+        del hg, hu
+        y = h_mid @ wd.t()
+        del h_mid, y
+        ghm = gy @ wd
+        dg, du, hmh = K.dequant_swiglu_backward(ghm, cg, sg, cu, su, BITS, GROUP,
+                                                want_h_mid=True)
+        del ghm
+        gwd = gy.t() @ hmh
+        gx = dg @ wg
+        gx = gx + du @ wu
+        gwg = dg.t() @ x
+        gwu = du.t() @ x
+        return gx, gwg, gwu, gwd
+
+    with torch.no_grad():
+        for _ in range(warmup):
+            lib_step()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            lib_step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
 def measured_traffic(kernel: str, workload: str):
     """HBM bytes per launch of `kernel` at `workload`, measured with
     rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE over `bench.py --probe` and
@@ -242,6 +283,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=N_TOK)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-tokens", type=int, default=512)
+    ap.add_argument("--no-library-arm", action="store_true",
+                    help="skip timing the hipBLASLt composition of the same step")
     ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["c4", "c5"], default="c2",
                     help="c2 (default) / c3: the FFN block; c4 / c5: a whole-model training "
                          "step (TinyLlama full-FT / Llama-7B LoRA) with every MLP on FlashFFN v3")
@@ -387,6 +430,14 @@ def main():
         "roofline": roofline,
         "kernels": kernels,
     }
+    if full_ft and not args.no_library_arm:
+        lib_ms = library_arm(x.detach(), gy, wg.detach(), wu.detach(), wd.detach(),
+                             args.steps, args.warmup)
+        out["library_arm"] = {
+            "ms_per_step": lib_ms, "tokens_per_s": n / (lib_ms * 1e-3),
+            "speedup_of_this_build": lib_ms / ms,
+            "what": "same step in the reference's structure: GEMMs through torch.matmul "
+                    "(hipBLASLt), K1/K2 codec as standalone kernels, same inputs and box"}
     if not args.no_cpu_baseline and args.workload == "c2":
         out["cpu_baseline"] = cpu_baseline(args.cpu_tokens)
     print(json.dumps(out))

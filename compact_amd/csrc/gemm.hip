@@ -169,6 +169,14 @@ struct KArgs {
   uint16_t* grad_gate;     // B1 out
   uint16_t* grad_up;
   uint16_t* h_mid_hat;     // B1 out (may be null)
+  // low-rank adapter terms applied as the epilogue reads the accumulators
+  // (acc_block); lrank == 0: none
+  const uint16_t* lp[2];   // P_t [M, lrank], rows lldp apart (tokens x rank)
+  const uint16_t* lq[2];   // Q_t: [N, lrank] rows lrank apart (lq_km) or [lrank, N] rows lldq apart
+  float lalpha[2];
+  int64_t lldp, lldq;
+  int lrank;
+  int lq_km;
 };
 
 enum Epi { EPI_STORE = 0, EPI_GLU = 1, EPI_DGLU = 2, EPI_ADD = 3, EPI_F32 = 4 };
@@ -635,20 +643,124 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
 __device__ __forceinline__ uint32_t absbits(float x) { return __float_as_uint(x) & 0x7FFFFFFFu; }
 
 // ---------------------------------------------------------------------------
+// Low-rank adapter terms in PEFT's op order (h + s * B(A(x)),
+// src/flashffn.py:1414,1420,1439,1529,1558-1566), applied to each accumulator
+// block as the epilogue reads it out (acc_block):
+//   acc = bf16(bf16(acc) + bf16(alpha_t * bf16(P_t . Q_t)))   term 0, then 1
+// The rank is at most 16, so each 32 x 32 block of a term is one
+// v_mfma_f32_32x32x16_bf16 with k past the rank read as zero; the fragments
+// come straight from global memory (P and Q are a few hundred KB and stay in
+// L2).  The epilogues round acc to bf16 again, which leaves these values as
+// they are.  In the dual gate/up GEMM term 0 belongs to the gate columns and
+// term 1 to the up columns.  The accumulators themselves are never rewritten:
+// they live in AGPRs, and a pass that modified them through VALU would force
+// copies of all 256.
+// ---------------------------------------------------------------------------
+// Fragments come through buffer loads whose records end at the operand's last
+// byte, so rows past the edge (and an absent term's null P, zero records) read
+// as zero without a branch; k past the rank is pushed out of range.
+__device__ __forceinline__ bf16x8 lora_frag_km(__amdgpu_buffer_rsrc_t rs, int64_t ld, int64_t row,
+                                               int r, int lane) {
+  const int k0 = (lane >> 5) * 8;
+  const uint32_t off = k0 < r ? (uint32_t)((row * ld + k0) * 2) : kOOB;
+  return __builtin_bit_cast(bf16x8, bload(rs, off));
+}
+
+// Q stored [r][ld] (n contiguous): 8 k of column n, one 2-byte load each
+__device__ __forceinline__ bf16x8 lora_frag_mn(__amdgpu_buffer_rsrc_t rs, int64_t ld, int64_t n,
+                                               int r, int lane) {
+  const int k0 = (lane >> 5) * 8;
+  uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t off = k0 + e < r ? (uint32_t)(((int64_t)(k0 + e) * ld + n) * 2) : kOOB;
+    w[e >> 1] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0) << ((e & 1) * 16);
+  }
+  return __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
+}
+
+// The adapter fragments of one wave, loaded once per tile ahead of the
+// epilogue: p[t][j] the m-side rows of P_t (block j), q[t][i] the n-side rows
+// of Q_t (block i; in the dual GEMM only the blocks of term t's columns).
+struct LoraFr {
+  bf16x8 p[2][4];
+  bf16x8 q[2][4];
+};
+
+template <bool DUAL, int LT>
+__device__ __forceinline__ void lora_load(const KArgs& A, int64_t m0, int64_t n0, LoraFr& F) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wn = wave & 1, wm = wave >> 1;
+  const int r = A.lrank;
+#pragma unroll
+  for (int t = 0; t < LT; ++t) {
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(A.lp[t], A.lp[t] ? A.M * A.lldp * 2 : 0);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      F.p[t][j] = lora_frag_km(rp, A.lldp, m0 + wm * 128 + j * 32 + (lane & 31), r, lane);
+    if constexpr (DUAL) {
+      // virtual columns: blocks 0, 1 are gate d0 + 64 wn + 32 i, blocks 2, 3 the same d of up
+      const __amdgpu_buffer_rsrc_t rq = make_rsrc(A.lq[t], A.lq[t] ? A.D * r * 2 : 0);
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii)
+        F.q[t][2 * t + ii] = lora_frag_km(rq, r, (n0 >> 1) + wn * 64 + ii * 32 + (lane & 31), r, lane);
+    } else {
+      const int64_t qbytes = A.lq_km ? A.N * r * 2 : (int64_t)r * A.lldq * 2;
+      const __amdgpu_buffer_rsrc_t rq = make_rsrc(A.lq[t], qbytes);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t n = n0 + wn * 128 + i * 32 + (lane & 31);
+        F.q[t][i] = A.lq_km ? lora_frag_km(rq, r, n, r, lane) : lora_frag_mn(rq, A.lldq, n, r, lane);
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ f32x16 lora_term(const f32x16& a, const bf16x8& qf, const bf16x8& pf,
+                                            float alpha) {
+  const f32x16 zero = {};
+  const f32x16 l = __builtin_amdgcn_mfma_f32_32x32x16_bf16(qf, pf, zero, 0, 0, 0);
+  f32x16 o;
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    o[r] = round_bf16(round_bf16(a[r]) + round_bf16(alpha * round_bf16(l[r])));
+  return o;
+}
+
+// Accumulator block (i, j) as the epilogue should see it: with the kernel's
+// LT adapter terms applied.  An absent term has a null P (zero fragments) and
+// alpha = -0.0, so its bf16(alpha * 0) is -0.0 and x + (-0.0) == x for every x,
+// signed zeros included: no branch is needed.
+template <bool DUAL, int LT>
+__device__ __forceinline__ f32x16 acc_block(const KArgs& A, const Acc& acc, const LoraFr& F,
+                                            int i, int j) {
+  f32x16 v = acc.v[i][j];
+#pragma unroll
+  for (int t = 0; t < LT; ++t) {
+    if (DUAL && (i >> 1) != t) continue;
+    v = lora_term(v, F.q[t][i], F.p[t][j], A.lalpha[t]);
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------------------
 // epilogue: plain bf16 store
 // ---------------------------------------------------------------------------
+template <int LT>
 __device__ __forceinline__ void epi_store(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wn = wave & 1, wm = wave >> 1;
+  LoraFr F;
+  if constexpr (LT > 0) lora_load<false, LT>(A, m0, n0, F);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
+      const f32x16 a = acc_block<false, LT>(A, acc, F, i, j);
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int64_t n = n0 + wn * 128 + i * 32 + g * 8 + (lane >> 5) * 4;
-        const f32x16& a = acc.v[i][j];
         if (m >= A.M) continue;
         if (n + 3 < A.N) {
           *reinterpret_cast<uint2*>(A.C + m * A.ldc + n) =
@@ -765,7 +877,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
 // Wave (wn, wm) holds gate in acc[0..1][j] and up in acc[2..3][j] for
 // d = d0 + 64 wn + 32 i + 8 q + 4 (lane/32) + e, m = m0 + 128 wm + 32 j + lane%32.
 // ---------------------------------------------------------------------------
-template <int CACHE, int GS>
+template <int CACHE, int GS, int LT>
 __device__ __forceinline__ void epi_glu(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0,
                                         uint16_t* lds) {
   // F1: h_gate = bf16(acc gate half), h_up = bf16(acc up half) are staged
@@ -783,12 +895,14 @@ __device__ __forceinline__ void epi_glu(const KArgs& A, const Acc& acc, int64_t 
   const int half = lane >> 5;
   uint16_t* sg = lds;
   uint16_t* su = lds + 256 * LD;
+  LoraFr F;
+  if constexpr (LT > 0) lora_load<true, LT>(A, m0, n0, F);
   // acc[i][j] (i = 0, 1 gate; i = 2, 3 up) -> d = 64 wn + 32 (i & 1) + 8 q + 4 half + e
   static_for<0, 4>([&](auto j) {
     const int ml = wm * 128 + j * 32 + (lane & 31);
     static_for<0, 2>([&](auto i) {
-      const f32x16& ag = acc.v[i][j];
-      const f32x16& au = acc.v[i + 2][j];
+      const f32x16 ag = acc_block<true, LT>(A, acc, F, i, j);
+      const f32x16 au = acc_block<true, LT>(A, acc, F, i + 2, j);
       static_for<0, 4>([&](auto q) {
         const int dl = wn * 64 + i * 32 + q * 8 + half * 4;
         *reinterpret_cast<uint2*>(sg + ml * LD + dl) =
@@ -874,7 +988,7 @@ __device__ __forceinline__ void epi_glu(const KArgs& A, const Acc& acc, int64_t 
 // read the bf16 cache); SwiGLU backward -> grad_h_gate, grad_h_up, h_mid^.
 // n-side = d: d = n0 + 128 wn + 32 i + 8 q + 4 (lane/32) + e.
 // ---------------------------------------------------------------------------
-template <int CACHE, int GS>
+template <int CACHE, int GS, int LT>
 __device__ __forceinline__ void epi_dglu(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0,
                                          uint16_t* lds) {
   // B1: grad_h_mid = bf16(acc) is staged through LDS as a row-major
@@ -887,10 +1001,12 @@ __device__ __forceinline__ void epi_dglu(const KArgs& A, const Acc& acc, int64_t
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave & 1, wm = wave >> 1;
+  LoraFr F;
+  if constexpr (LT > 0) lora_load<false, LT>(A, m0, n0, F);
   static_for<0, 4>([&](auto j) {
     const int ml = wm * 128 + j * 32 + (lane & 31);
     static_for<0, 4>([&](auto i) {
-      const f32x16& a = acc.v[i][j];
+      const f32x16 a = acc_block<false, LT>(A, acc, F, i, j);
       static_for<0, 4>([&](auto g) {
         const int nl = wn * 128 + i * 32 + g * 8 + (lane >> 5) * 4;
         *reinterpret_cast<uint2*>(lds + ml * LD + nl) =
@@ -994,7 +1110,7 @@ __device__ __forceinline__ void epi_dglu(const KArgs& A, const Acc& acc, int64_t
 // ---------------------------------------------------------------------------
 // kernel
 // ---------------------------------------------------------------------------
-template <bool AK, bool BKM, int EPI, int CACHE, int GS>
+template <bool AK, bool BKM, int EPI, int CACHE, int GS, int LT = 0>
 __global__ __launch_bounds__(NTHR, 1) void gemm_kernel(KArgs A) {
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   int tm, tn, split = 0;
@@ -1017,10 +1133,10 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_kernel(KArgs A) {
   } else {
     mainloop_pp<AK, BKM, EPI == EPI_GLU>(A, m0, n0, lds, acc);
   }
-  if constexpr (EPI == EPI_STORE) epi_store(A, acc, m0, n0);
+  if constexpr (EPI == EPI_STORE) epi_store<LT>(A, acc, m0, n0);
   else if constexpr (EPI == EPI_ADD) epi_add(A, acc, m0, n0, lds);
-  else if constexpr (EPI == EPI_GLU) epi_glu<CACHE, GS>(A, acc, m0, n0, lds);
-  else if constexpr (EPI == EPI_DGLU) epi_dglu<CACHE, GS>(A, acc, m0, n0, lds);
+  else if constexpr (EPI == EPI_GLU) epi_glu<CACHE, GS, LT>(A, acc, m0, n0, lds);
+  else if constexpr (EPI == EPI_DGLU) epi_dglu<CACHE, GS, LT>(A, acc, m0, n0, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -1139,9 +1255,9 @@ __global__ __launch_bounds__(256) void thin_add_kernel(const uint16_t* __restric
 // ---------------------------------------------------------------------------
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-template <bool AK, bool BKM, int EPI, int CACHE, int GS>
+template <bool AK, bool BKM, int EPI, int CACHE, int GS, int LT = 0>
 int launch(KArgs& A, hipStream_t st) {
-  auto kern = gemm_kernel<AK, BKM, EPI, CACHE, GS>;
+  auto kern = gemm_kernel<AK, BKM, EPI, CACHE, GS, LT>;
   static bool attr_set = false;   // per instantiation
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -1170,39 +1286,65 @@ inline bool operand_fits(int64_t ld, bool kmajor, int64_t mn, int64_t K) {
   return rows * ld * 2 < ((int64_t)1 << 31);
 }
 
-template <int EPI, int CACHE>
-int dispatch_gs(int64_t gs, KArgs& A, hipStream_t st, bool ak, bool bk) {
-  // fused epilogues exist for a/b layouts used by the FFN: F1 (k, k), B1 (k, mn)
-  (void)ak; (void)bk;
-  if constexpr (EPI == EPI_GLU) {
-    switch (gs) {
-      case 32: return launch<true, true, EPI, CACHE, 32>(A, st);
-      case 64: return launch<true, true, EPI, CACHE, 64>(A, st);
-      case 128: return launch<true, true, EPI, CACHE, 128>(A, st);
-      default: return kErrGroupPow2;
-    }
-  } else {
-    switch (gs) {
-      case 32: return launch<true, false, EPI, CACHE, 32>(A, st);
-      case 64: return launch<true, false, EPI, CACHE, 64>(A, st);
-      case 128: return launch<true, false, EPI, CACHE, 128>(A, st);
-      default: return kErrGroupPow2;
-    }
+template <int EPI, int CACHE, int LT>
+int dispatch_gs(int64_t gs, KArgs& A, hipStream_t st) {
+  // fused epilogues exist for the operand layouts of the FFN: F1 (k, k), B1 (k, mn)
+  constexpr bool BKM = EPI == EPI_GLU;
+  switch (gs) {
+    case 32: return launch<true, BKM, EPI, CACHE, 32, LT>(A, st);
+    case 64: return launch<true, BKM, EPI, CACHE, 64, LT>(A, st);
+    case 128: return launch<true, BKM, EPI, CACHE, 128, LT>(A, st);
+    default: return kErrGroupPow2;
   }
 }
 
-}  // namespace gemm
-}  // namespace cpt
+// Adapter terms of one call (see acc_block).  P_t [M, rank] with rows ldp
+// apart; Q_t [n_q, rank] contiguous (q_kmajor) or [rank, n_q] with rows ldq
+// apart.  rank 0: no terms.
+struct LoraTerms {
+  int rank = 0;
+  int q_kmajor = 1;
+  int64_t ldp = 0, ldq = 0;
+  const void* p[2] = {nullptr, nullptr};
+  const void* q[2] = {nullptr, nullptr};
+  float alpha[2] = {0.0f, 0.0f};
+};
 
-using namespace cpt;
-using namespace cpt::gemm;
+// n_q: the extent of Q's n side (N, or inter for the fused FFN kernels);
+// m_p: P's rows.  An absent term keeps a null P and alpha = -0.0 (a no-op,
+// see acc_block).  Returns the number of terms the kernel must carry.
+inline int set_lora(KArgs& A, const LoraTerms& L, int64_t m_p, int64_t n_q, int& terms) {
+  terms = 0;
+  A.lalpha[0] = A.lalpha[1] = -0.0f;
+  if (L.rank == 0) return kOk;
+  if (L.rank != 8 && L.rank != 16) return kErrShape;
+  if (L.ldp < L.rank || (L.ldp & 7)) return kErrAlign;
+  if (!L.q_kmajor && L.ldq < n_q) return kErrShape;
+  if (!L.p[0] && !L.p[1]) return kErrShape;
+  // 32-bit buffer offsets, with one tile of overhang past the last row
+  if ((m_p + 256) * L.ldp * 2 >= ((int64_t)1 << 31)) return kErrTooLarge;
+  if ((L.q_kmajor ? (n_q + 256) * L.rank : L.rank * L.ldq) * 2 >= ((int64_t)1 << 31))
+    return kErrTooLarge;
+  for (int t = 0; t < 2; ++t) {
+    if (!L.p[t]) continue;
+    if (!L.q[t]) return kErrShape;
+    if (!al16(L.p[t]) || (L.q_kmajor && !al16(L.q[t]))) return kErrAlign;
+    A.lp[t] = (const uint16_t*)L.p[t];
+    A.lq[t] = (const uint16_t*)L.q[t];
+    A.lalpha[t] = L.alpha[t];
+    terms = t + 1;
+  }
+  A.lrank = L.rank;
+  A.lq_km = L.q_kmajor;
+  A.lldp = L.ldp;
+  A.lldq = L.ldq;
+  return kOk;
+}
 
-extern "C" {
-
-int cpt_gemm_bf16(const void* a, int64_t lda, int a_kmajor, const void* b, int64_t ldb,
-                  int b_kmajor, const void* a2, int64_t lda2, const void* b2, int64_t ldb2,
-                  int64_t K2, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K,
-                  void* stream) {
+int gemm_bf16_impl(const void* a, int64_t lda, int a_kmajor, const void* b, int64_t ldb,
+                   int b_kmajor, const void* a2, int64_t lda2, const void* b2, int64_t ldb2,
+                   int64_t K2, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                   const LoraTerms& L, void* stream) {
   if (M < 0 || N < 0 || K < 0 || K2 < 0) return kErrShape;
   if (M == 0 || N == 0) return kOk;
   if (!c || !al16(c) || (ldc & 3) || ldc < N) return kErrAlign;
@@ -1233,12 +1375,184 @@ int cpt_gemm_bf16(const void* a, int64_t lda, int a_kmajor, const void* b, int64
   A.tiles_n = (int)((N + BN - 1) / BN);
   A.C = (uint16_t*)c;
   A.ldc = ldc;
+  int terms = 0;
+  if (const int rc = set_lora(A, L, M, N, terms)) return rc;
   hipStream_t st = (hipStream_t)stream;
+  if (terms) {
+    // adapter terms are carried by the layouts that need them: K-major A
+    if (!a_kmajor) return kErrShape;
+    if (terms == 1)
+      return b_kmajor ? launch<true, true, EPI_STORE, 0, 0, 1>(A, st)
+                      : launch<true, false, EPI_STORE, 0, 0, 1>(A, st);
+    return b_kmajor ? launch<true, true, EPI_STORE, 0, 0, 2>(A, st)
+                    : launch<true, false, EPI_STORE, 0, 0, 2>(A, st);
+  }
   if (a_kmajor && b_kmajor) return launch<true, true, EPI_STORE, 0, 0>(A, st);
   if (a_kmajor && !b_kmajor) return launch<true, false, EPI_STORE, 0, 0>(A, st);
   if (!a_kmajor && !b_kmajor) return launch<false, false, EPI_STORE, 0, 0>(A, st);
   return launch<false, true, EPI_STORE, 0, 0>(A, st);
 }
+
+int ffn_gate_up_impl(const void* x, const void* w_gate, const void* w_up, int64_t n_tok,
+                     int64_t hidden, int64_t inter, int cache, int64_t group_size, void* h_mid,
+                     void* h_gate, void* h_up, void* q_gate, void* s_gate, void* q_up,
+                     void* s_up, const LoraTerms& L, void* stream) {
+  if (n_tok < 0 || hidden < 0 || inter < 0) return kErrShape;
+  if (cache != CACHE_NONE && cache != CACHE_BF16 && cache != CACHE_INT4 && cache != CACHE_INT8)
+    return kErrBits;
+  const bool quant = cache == CACHE_INT4 || cache == CACHE_INT8;
+  if (quant) {
+    if (group_size <= 0 || inter % group_size) return kErrRagged;
+    if (!is_pow2(group_size)) return kErrGroupPow2;
+    if (group_size != 32 && group_size != 64 && group_size != 128) return kErrGroupPow2;
+    if (!q_gate || !s_gate || !q_up || !s_up) return kErrShape;
+  }
+  if (cache == CACHE_BF16 && (!h_gate || !h_up || !al16(h_gate) || !al16(h_up))) return kErrShape;
+  if (!quant && cache != CACHE_BF16 && !h_mid) return kErrShape;
+  if (n_tok == 0 || inter == 0) return kOk;
+  if ((inter & 7) || !operand_ok(x, hidden, true, n_tok, hidden) ||
+      !operand_ok(w_gate, hidden, true, inter, hidden) ||
+      !operand_ok(w_up, hidden, true, inter, hidden) || (h_mid && !al16(h_mid)))
+    return kErrAlign;
+  // the epilogue stores 8 codes per access: 8 bytes (int8) or 4 bytes (int4)
+  const uintptr_t qmask = cache == CACHE_INT8 ? 7u : 3u;
+  if (quant && (((uintptr_t)q_gate & qmask) || ((uintptr_t)q_up & qmask))) return kErrAlign;
+  if (!operand_fits(hidden, true, n_tok, hidden) || !operand_fits(hidden, true, inter, hidden))
+    return kErrTooLarge;
+  KArgs A{};
+  A.a[0] = {(const uint16_t*)x, hidden};
+  A.b[0] = {(const uint16_t*)w_gate, hidden};
+  A.K[0] = hidden;
+  A.npairs = 1;
+  A.b_up = (const uint16_t*)w_up;
+  A.M = n_tok;
+  A.N = 2 * inter;
+  A.D = inter;
+  A.tiles_m = (int)((n_tok + BM - 1) / BM);
+  A.tiles_n = (int)((inter + 127) / 128);
+  A.h_mid = (uint16_t*)h_mid;
+  A.h_gate = (uint16_t*)h_gate;
+  A.h_up = (uint16_t*)h_up;
+  A.q_gate = (uint8_t*)q_gate;
+  A.s_gate = (uint16_t*)s_gate;
+  A.q_up = (uint8_t*)q_up;
+  A.s_up = (uint16_t*)s_up;
+  int terms = 0;
+  if (const int rc = set_lora(A, L, n_tok, inter, terms)) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  // the dual kernel carries both terms (gate, up); an absent one is a no-op
+  switch (cache) {
+    case CACHE_NONE:
+      return terms ? launch<true, true, EPI_GLU, CACHE_NONE, 64, 2>(A, st)
+                   : launch<true, true, EPI_GLU, CACHE_NONE, 64>(A, st);
+    case CACHE_BF16:
+      return terms ? launch<true, true, EPI_GLU, CACHE_BF16, 64, 2>(A, st)
+                   : launch<true, true, EPI_GLU, CACHE_BF16, 64>(A, st);
+    case CACHE_INT4:
+      return terms ? dispatch_gs<EPI_GLU, CACHE_INT4, 2>(group_size, A, st)
+                   : dispatch_gs<EPI_GLU, CACHE_INT4, 0>(group_size, A, st);
+    default:
+      return terms ? dispatch_gs<EPI_GLU, CACHE_INT8, 2>(group_size, A, st)
+                   : dispatch_gs<EPI_GLU, CACHE_INT8, 0>(group_size, A, st);
+  }
+}
+
+int ffn_down_dgrad_impl(const void* grad_y, const void* w_down, int64_t n_tok, int64_t hidden,
+                        int64_t inter, int cache, int64_t group_size, const void* c_gate,
+                        const void* s_gate, const void* c_up, const void* s_up,
+                        void* grad_h_gate, void* grad_h_up, void* h_mid_hat,
+                        const LoraTerms& L, void* stream) {
+  if (n_tok < 0 || hidden < 0 || inter < 0) return kErrShape;
+  if (cache != CACHE_BF16 && cache != CACHE_INT4 && cache != CACHE_INT8) return kErrBits;
+  const bool quant = cache != CACHE_BF16;
+  if (quant) {
+    if (group_size <= 0 || inter % group_size) return kErrRagged;
+    if (!is_pow2(group_size)) return kErrGroupPow2;
+    if (group_size != 32 && group_size != 64 && group_size != 128) return kErrGroupPow2;
+    if (!s_gate || !s_up) return kErrShape;
+  }
+  if (!c_gate || !c_up || !grad_h_gate || !grad_h_up) return kErrShape;
+  if (n_tok == 0 || inter == 0) return kOk;
+  if ((inter & 7) || !operand_ok(grad_y, hidden, true, n_tok, hidden) ||
+      !operand_ok(w_down, inter, false, inter, hidden) || !al16(grad_h_gate) ||
+      !al16(grad_h_up) || (h_mid_hat && !al16(h_mid_hat)))
+    return kErrAlign;
+  // the epilogue reads 8 columns per access: 16 B of bf16 cache, 8 B of int8
+  // codes or 4 B of int4 codes
+  const uintptr_t cmask = cache == CACHE_BF16 ? 15u : (cache == CACHE_INT8 ? 7u : 3u);
+  if (((uintptr_t)c_gate & cmask) || ((uintptr_t)c_up & cmask)) return kErrAlign;
+  if (!operand_fits(hidden, true, n_tok, hidden) || !operand_fits(inter, false, inter, hidden))
+    return kErrTooLarge;
+  KArgs A{};
+  A.a[0] = {(const uint16_t*)grad_y, hidden};
+  A.b[0] = {(const uint16_t*)w_down, inter};   // W_d [H, D]: n-side d, k = h, MN-major
+  A.K[0] = hidden;
+  A.npairs = 1;
+  A.M = n_tok;
+  A.N = inter;
+  A.D = inter;
+  A.tiles_m = (int)((n_tok + BM - 1) / BM);
+  A.tiles_n = (int)((inter + BN - 1) / BN);
+  if (quant) {
+    A.q_gate = (uint8_t*)c_gate;
+    A.q_up = (uint8_t*)c_up;
+    A.s_gate = (uint16_t*)s_gate;
+    A.s_up = (uint16_t*)s_up;
+  } else {
+    A.h_gate = (uint16_t*)c_gate;
+    A.h_up = (uint16_t*)c_up;
+  }
+  A.grad_gate = (uint16_t*)grad_h_gate;
+  A.grad_up = (uint16_t*)grad_h_up;
+  A.h_mid_hat = (uint16_t*)h_mid_hat;
+  int terms = 0;
+  if (const int rc = set_lora(A, L, n_tok, inter, terms)) return rc;
+  if (terms > 1) return kErrShape;
+  hipStream_t st = (hipStream_t)stream;
+  switch (cache) {
+    case CACHE_BF16:
+      return terms ? launch<true, false, EPI_DGLU, CACHE_BF16, 64, 1>(A, st)
+                   : launch<true, false, EPI_DGLU, CACHE_BF16, 64>(A, st);
+    case CACHE_INT4:
+      return terms ? dispatch_gs<EPI_DGLU, CACHE_INT4, 1>(group_size, A, st)
+                   : dispatch_gs<EPI_DGLU, CACHE_INT4, 0>(group_size, A, st);
+    default:
+      return terms ? dispatch_gs<EPI_DGLU, CACHE_INT8, 1>(group_size, A, st)
+                   : dispatch_gs<EPI_DGLU, CACHE_INT8, 0>(group_size, A, st);
+  }
+}
+
+}  // namespace gemm
+}  // namespace cpt
+
+using namespace cpt;
+using namespace cpt::gemm;
+
+extern "C" {
+
+int cpt_gemm_bf16(const void* a, int64_t lda, int a_kmajor, const void* b, int64_t ldb,
+                  int b_kmajor, const void* a2, int64_t lda2, const void* b2, int64_t ldb2,
+                  int64_t K2, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                  void* stream) {
+  return gemm_bf16_impl(a, lda, a_kmajor, b, ldb, b_kmajor, a2, lda2, b2, ldb2, K2, c, ldc, M, N,
+                        K, LoraTerms{}, stream);
+}
+
+int cpt_gemm_bf16_lora(const void* a, int64_t lda, int a_kmajor, const void* b, int64_t ldb,
+                       int b_kmajor, const void* a2, int64_t lda2, const void* b2, int64_t ldb2,
+                       int64_t K2, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                       int64_t rank, int64_t ldp, int q_kmajor, int64_t ldq, const void* p0,
+                       const void* q0, float alpha0, const void* p1, const void* q1,
+                       float alpha1, void* stream) {
+  if (rank <= 0) return kErrShape;
+  LoraTerms L;
+  L.rank = (int)rank; L.ldp = ldp; L.q_kmajor = q_kmajor ? 1 : 0; L.ldq = ldq;
+  L.p[0] = p0; L.q[0] = q0; L.alpha[0] = alpha0;
+  L.p[1] = p1; L.q[1] = q1; L.alpha[1] = alpha1;
+  return gemm_bf16_impl(a, lda, a_kmajor, b, ldb, b_kmajor, a2, lda2, b2, ldb2, K2, c, ldc, M, N,
+                        K, L, stream);
+}
+
 
 int cpt_gemm_bf16_ex(const void* a, int64_t lda, int a_kmajor, const void* b, int64_t ldb,
                      int b_kmajor, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K,
@@ -1318,112 +1632,52 @@ int cpt_gemm_bf16_ex(const void* a, int64_t lda, int a_kmajor, const void* b, in
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
+
+
 int cpt_ffn_gate_up(const void* x, const void* w_gate, const void* w_up, int64_t n_tok,
                     int64_t hidden, int64_t inter, int cache, int64_t group_size, void* h_mid,
                     void* h_gate, void* h_up, void* q_gate, void* s_gate, void* q_up,
                     void* s_up, void* stream) {
-  if (n_tok < 0 || hidden < 0 || inter < 0) return kErrShape;
-  if (cache != CACHE_NONE && cache != CACHE_BF16 && cache != CACHE_INT4 && cache != CACHE_INT8)
-    return kErrBits;
-  const bool quant = cache == CACHE_INT4 || cache == CACHE_INT8;
-  if (quant) {
-    if (group_size <= 0 || inter % group_size) return kErrRagged;
-    if (!is_pow2(group_size)) return kErrGroupPow2;
-    if (group_size != 32 && group_size != 64 && group_size != 128) return kErrGroupPow2;
-    if (!q_gate || !s_gate || !q_up || !s_up) return kErrShape;
-  }
-  if (cache == CACHE_BF16 && (!h_gate || !h_up || !al16(h_gate) || !al16(h_up))) return kErrShape;
-  if (!quant && cache != CACHE_BF16 && !h_mid) return kErrShape;
-  if (n_tok == 0 || inter == 0) return kOk;
-  if ((inter & 7) || !operand_ok(x, hidden, true, n_tok, hidden) ||
-      !operand_ok(w_gate, hidden, true, inter, hidden) ||
-      !operand_ok(w_up, hidden, true, inter, hidden) || (h_mid && !al16(h_mid)))
-    return kErrAlign;
-  // the epilogue stores 8 codes per access: 8 bytes (int8) or 4 bytes (int4)
-  const uintptr_t qmask = cache == CACHE_INT8 ? 7u : 3u;
-  if (quant && (((uintptr_t)q_gate & qmask) || ((uintptr_t)q_up & qmask))) return kErrAlign;
-  if (!operand_fits(hidden, true, n_tok, hidden) || !operand_fits(hidden, true, inter, hidden))
-    return kErrTooLarge;
-  KArgs A{};
-  A.a[0] = {(const uint16_t*)x, hidden};
-  A.b[0] = {(const uint16_t*)w_gate, hidden};
-  A.K[0] = hidden;
-  A.npairs = 1;
-  A.b_up = (const uint16_t*)w_up;
-  A.M = n_tok;
-  A.N = 2 * inter;
-  A.D = inter;
-  A.tiles_m = (int)((n_tok + BM - 1) / BM);
-  A.tiles_n = (int)((inter + 127) / 128);
-  A.h_mid = (uint16_t*)h_mid;
-  A.h_gate = (uint16_t*)h_gate;
-  A.h_up = (uint16_t*)h_up;
-  A.q_gate = (uint8_t*)q_gate;
-  A.s_gate = (uint16_t*)s_gate;
-  A.q_up = (uint8_t*)q_up;
-  A.s_up = (uint16_t*)s_up;
-  hipStream_t st = (hipStream_t)stream;
-  switch (cache) {
-    case CACHE_NONE: return launch<true, true, EPI_GLU, CACHE_NONE, 64>(A, st);
-    case CACHE_BF16: return launch<true, true, EPI_GLU, CACHE_BF16, 64>(A, st);
-    case CACHE_INT4: return dispatch_gs<EPI_GLU, CACHE_INT4>(group_size, A, st, true, true);
-    default: return dispatch_gs<EPI_GLU, CACHE_INT8>(group_size, A, st, true, true);
-  }
+  return ffn_gate_up_impl(x, w_gate, w_up, n_tok, hidden, inter, cache, group_size, h_mid, h_gate,
+                          h_up, q_gate, s_gate, q_up, s_up, LoraTerms{}, stream);
+}
+
+int cpt_ffn_gate_up_lora(const void* x, const void* w_gate, const void* w_up, int64_t n_tok,
+                         int64_t hidden, int64_t inter, int cache, int64_t group_size,
+                         void* h_mid, void* h_gate, void* h_up, void* q_gate, void* s_gate,
+                         void* q_up, void* s_up, int64_t rank, int64_t ldp, const void* p_gate,
+                         const void* b_gate, float alpha_gate, const void* p_up,
+                         const void* b_up, float alpha_up, void* stream) {
+  if (rank <= 0) return kErrShape;
+  LoraTerms L;
+  L.rank = (int)rank; L.ldp = ldp; L.q_kmajor = 1;
+  L.p[0] = p_gate; L.q[0] = b_gate; L.alpha[0] = alpha_gate;
+  L.p[1] = p_up; L.q[1] = b_up; L.alpha[1] = alpha_up;
+  return ffn_gate_up_impl(x, w_gate, w_up, n_tok, hidden, inter, cache, group_size, h_mid, h_gate,
+                          h_up, q_gate, s_gate, q_up, s_up, L, stream);
 }
 
 int cpt_ffn_down_dgrad(const void* grad_y, const void* w_down, int64_t n_tok, int64_t hidden,
                        int64_t inter, int cache, int64_t group_size, const void* c_gate,
                        const void* s_gate, const void* c_up, const void* s_up, void* grad_h_gate,
                        void* grad_h_up, void* h_mid_hat, void* stream) {
-  if (n_tok < 0 || hidden < 0 || inter < 0) return kErrShape;
-  if (cache != CACHE_BF16 && cache != CACHE_INT4 && cache != CACHE_INT8) return kErrBits;
-  const bool quant = cache != CACHE_BF16;
-  if (quant) {
-    if (group_size <= 0 || inter % group_size) return kErrRagged;
-    if (!is_pow2(group_size)) return kErrGroupPow2;
-    if (group_size != 32 && group_size != 64 && group_size != 128) return kErrGroupPow2;
-    if (!s_gate || !s_up) return kErrShape;
-  }
-  if (!c_gate || !c_up || !grad_h_gate || !grad_h_up) return kErrShape;
-  if (n_tok == 0 || inter == 0) return kOk;
-  if ((inter & 7) || !operand_ok(grad_y, hidden, true, n_tok, hidden) ||
-      !operand_ok(w_down, inter, false, inter, hidden) || !al16(grad_h_gate) ||
-      !al16(grad_h_up) || (h_mid_hat && !al16(h_mid_hat)))
-    return kErrAlign;
-  // the epilogue reads 8 columns per access: 16 B of bf16 cache, 8 B of int8
-  // codes or 4 B of int4 codes
-  const uintptr_t cmask = cache == CACHE_BF16 ? 15u : (cache == CACHE_INT8 ? 7u : 3u);
-  if (((uintptr_t)c_gate & cmask) || ((uintptr_t)c_up & cmask)) return kErrAlign;
-  if (!operand_fits(hidden, true, n_tok, hidden) || !operand_fits(inter, false, inter, hidden))
-    return kErrTooLarge;
-  KArgs A{};
-  A.a[0] = {(const uint16_t*)grad_y, hidden};
-  A.b[0] = {(const uint16_t*)w_down, inter};   // W_d [H, D]: n-side d, k = h, MN-major
-  A.K[0] = hidden;
-  A.npairs = 1;
-  A.M = n_tok;
-  A.N = inter;
-  A.D = inter;
-  A.tiles_m = (int)((n_tok + BM - 1) / BM);
-  A.tiles_n = (int)((inter + BN - 1) / BN);
-  if (quant) {
-    A.q_gate = (uint8_t*)c_gate;
-    A.q_up = (uint8_t*)c_up;
-    A.s_gate = (uint16_t*)s_gate;
-    A.s_up = (uint16_t*)s_up;
-  } else {
-    A.h_gate = (uint16_t*)c_gate;
-    A.h_up = (uint16_t*)c_up;
-  }
-  A.grad_gate = (uint16_t*)grad_h_gate;
-  A.grad_up = (uint16_t*)grad_h_up;
-  A.h_mid_hat = (uint16_t*)h_mid_hat;
-  hipStream_t st = (hipStream_t)stream;
-  switch (cache) {
-    case CACHE_BF16: return launch<true, false, EPI_DGLU, CACHE_BF16, 64>(A, st);
-    case CACHE_INT4: return dispatch_gs<EPI_DGLU, CACHE_INT4>(group_size, A, st, true, false);
-    default: return dispatch_gs<EPI_DGLU, CACHE_INT8>(group_size, A, st, true, false);
-  }
+  return ffn_down_dgrad_impl(grad_y, w_down, n_tok, hidden, inter, cache, group_size, c_gate,
+                             s_gate, c_up, s_up, grad_h_gate, grad_h_up, h_mid_hat, LoraTerms{},
+                             stream);
+}
+
+int cpt_ffn_down_dgrad_lora(const void* grad_y, const void* w_down, int64_t n_tok,
+                            int64_t hidden, int64_t inter, int cache, int64_t group_size,
+                            const void* c_gate, const void* s_gate, const void* c_up,
+                            const void* s_up, void* grad_h_gate, void* grad_h_up,
+                            void* h_mid_hat, int64_t rank, int64_t ldp, const void* p,
+                            const void* a_down, float alpha, void* stream) {
+  if (rank <= 0) return kErrShape;
+  LoraTerms L;
+  L.rank = (int)rank; L.ldp = ldp; L.q_kmajor = 0; L.ldq = inter;
+  L.p[0] = p; L.q[0] = a_down; L.alpha[0] = alpha;
+  return ffn_down_dgrad_impl(grad_y, w_down, n_tok, hidden, inter, cache, group_size, c_gate,
+                             s_gate, c_up, s_up, grad_h_gate, grad_h_up, h_mid_hat, L, stream);
 }
 
 }  // extern "C"

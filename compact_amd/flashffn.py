@@ -83,15 +83,36 @@ def _mm_scaled(a, b, s, name):
     return s * (a @ b)
 
 
+def _lora_ok(*pairs) -> bool:
+    """The adapter terms (a, b) present ride in the GEMM epilogues: bf16 on the
+    engine, one shared rank of 8 or 16."""
+    ranks = {a.shape[0] for a, b in pairs if a is not None}
+    return (len(ranks) <= 1 and all(G.lora_fusable(r) for r in ranks)
+            and all(_mfma(a, b) for a, b in pairs if a is not None))
+
+
 def _proj(x_2d, w, a, b, s, name):
     """out = x W^T (+ s * (x A^T) B^T) in PEFT op order (src/flashffn.py:1410-1420).
     Returns (out, xA | None)."""
+    if a is not None and _mfma(x_2d, w) and _lora_ok((a, b)) and x_2d.shape[0] > 0:
+        xa = _mm(x_2d, a.t(), name + "_xa")
+        return G.linear_lora(x_2d, w, xa, b, s, name), xa
     h = _linear(x_2d, w, name)
     xa = None
     if a is not None:
         xa = _mm(x_2d, a.t(), name + "_xa")
         h = _addmm(h, xa, b.t(), s, name + "_lora")
     return h, xa
+
+
+def _gate_up_lora(x_2d, a_gate, b_gate, s_gate, a_up, b_up, s_up):
+    """(xa_g | None, xa_u | None, ffn_gate_up keyword terms) for the fused
+    gate/up GEMM."""
+    xa_g = _mm(x_2d, a_gate.t(), "gemm_fwd_gate_xa") if a_gate is not None else None
+    xa_u = _mm(x_2d, a_up.t(), "gemm_fwd_up_xa") if a_up is not None else None
+    kw = dict(lora_gate=None if a_gate is None else (xa_g, b_gate, s_gate),
+              lora_up=None if a_up is None else (xa_u, b_up, s_up))
+    return xa_g, xa_u, kw
 
 
 class FlashFFNv3Function(torch.autograd.Function):
@@ -125,28 +146,33 @@ class FlashFFNv3Function(torch.autograd.Function):
         inter = w_gate.shape[0]
         k_out = int(inter * outlier_ratio) if (quant and outlier_ratio > 0) else 0
         assert k_out == 0 or x.dtype == torch.bfloat16, "outlier channels need bf16 activations"
-        fusable = (a_gate is None and a_up is None and _mfma(x_2d, w_gate, w_up)
+        # the dual gate/up kernel, with the gate/up LoRA terms in its epilogue
+        fusable = (_mfma(x_2d, w_gate, w_up) and _lora_ok((a_gate, b_gate), (a_up, b_up))
                    and x_2d.shape[0] > 0)
 
         c_gate = qs_gate = c_up = qs_up = None
         o_gate = o_up = slot_gate = slot_up = None
         h_gate = h_up = None
         xa_g = xa_u = None
+        lkw = {}
+        if fusable:
+            xa_g, xa_u, lkw = _gate_up_lora(x_2d, a_gate, b_gate, s_gate, a_up, b_up, s_up)
         fused_quant = (quant and use_triton and x.dtype == torch.bfloat16)   # :1424-1426
         if fusable and fused_quant and k_out == 0 and group_size in _FUSED_GROUPS:
             # dual GEMM + GLU + codec in one kernel (K1 fused into the epilogue)
             h_mid, _, _, c_gate, qs_gate, c_up, qs_up = G.ffn_gate_up(
-                x_2d, w_gate, w_up, _CACHE_CODE[cache_mode], group_size)
+                x_2d, w_gate, w_up, _CACHE_CODE[cache_mode], group_size, **lkw)
             _V3_COUNTERS["triton_quant_fwd"] += 1
         elif fusable and not fused_quant and k_out == 0:
             # h_gate/h_up are needed (bf16 cache, eager codec) or not (recompute)
             keep = cache_mode != "recompute"
             h_mid, h_gate, h_up, *_ = G.ffn_gate_up(
-                x_2d, w_gate, w_up, _lib.CACHE_BF16 if keep else _lib.CACHE_NONE, group_size)
+                x_2d, w_gate, w_up, _lib.CACHE_BF16 if keep else _lib.CACHE_NONE, group_size,
+                **lkw)
         else:
             if fusable:
                 _, h_gate, h_up, *_ = G.ffn_gate_up(x_2d, w_gate, w_up, _lib.CACHE_BF16,
-                                                    group_size, want_h_mid=False)
+                                                    group_size, want_h_mid=False, **lkw)
             else:
                 h_gate, xa_g = _proj(x_2d, w_gate, a_gate, b_gate, s_gate, "gemm_fwd_gate")
                 h_up, xa_u = _proj(x_2d, w_up, a_up, b_up, s_up, "gemm_fwd_up")
@@ -218,16 +244,20 @@ class FlashFFNv3Function(torch.autograd.Function):
         need_h_mid = need_wd or (a_down is not None and need_ad)          # :1490
         need_recon = need_gate_path or need_h_mid
         use_k2 = mode in ("int4", "int8") and ctx.use_triton and need_gate_path
-        fusable = (a_down is None and _mfma(gy, w_down) and gy.shape[0] > 0 and not outl)
-        fusable_gu = (a_gate is None and a_up is None and _mfma(x_2d, w_gate, w_up)
+        lora_d = _lora_ok((a_down, b_down))
+        fusable = _mfma(gy, w_down) and lora_d and gy.shape[0] > 0 and not outl
+        fusable_gu = (_mfma(x_2d, w_gate, w_up) and _lora_ok((a_gate, b_gate), (a_up, b_up))
                       and x_2d.shape[0] > 0)
 
         hg = hu = None
         if need_recon and not use_k2:                                     # :1500-1516
             if mode == "recompute":
                 if fusable_gu:
+                    # the forward's kernel and terms on the same inputs: bitwise equal
+                    lkw = dict(lora_gate=None if a_gate is None else (xa_g, b_gate, s_gate),
+                               lora_up=None if a_up is None else (xa_u, b_up, s_up))
                     _, hg, hu, *_ = G.ffn_gate_up(x_2d, w_gate, w_up, _lib.CACHE_BF16, gs,
-                                                  want_h_mid=False)
+                                                  want_h_mid=False, **lkw)
                 else:
                     hg = _linear(x_2d, w_gate, "gemm_recompute_gate")
                     if a_gate is not None:
@@ -249,21 +279,30 @@ class FlashFFNv3Function(torch.autograd.Function):
         if a_down is not None and (need_gate_path or need_ad):
             gyB_d = _mm(gy, b_down, "gemm_gyB_down")                      # :1521
 
+        # the down projection's LoRA term of grad_h_mid (:1527-1529) rides in
+        # the dgrad GEMM's epilogue
+        dlora = (gyB_d, a_down, s_down) if (a_down is not None and lora_d) else None
         grad_h_gate = grad_h_up = h_mid_hat = None
         if need_gate_path:
             if use_k2 and fusable and gs in _FUSED_GROUPS:                # :1525-1533
                 # dgrad GEMM with dequantise + SwiGLU backward in its epilogue
                 grad_h_gate, grad_h_up, h_mid_hat = G.ffn_down_dgrad(
                     gy, w_down, _CACHE_CODE[mode], gs, c_gate, qs_gate, c_up, qs_up,
-                    need_h_mid)
+                    need_h_mid, lora=dlora)
                 _V3_COUNTERS["triton_dequant_bwd"] += 1
             elif (not use_k2) and fusable and hg is not None and _mfma(hg, hu):
                 grad_h_gate, grad_h_up, h_mid_hat = G.ffn_down_dgrad(
-                    gy, w_down, _lib.CACHE_BF16, gs, hg, None, hu, None, need_h_mid)
+                    gy, w_down, _lib.CACHE_BF16, gs, hg, None, hu, None, need_h_mid,
+                    lora=dlora)
             else:
-                grad_h_mid = _mm(gy, w_down, "gemm_dgrad_down")
-                if a_down is not None:
-                    grad_h_mid = _addmm(grad_h_mid, gyB_d, a_down, s_down, "gemm_dgrad_down_lora")
+                if dlora is not None and _mfma(gy, w_down) and gy.shape[0] > 0:
+                    grad_h_mid = G.mm2(gy, w_down, name="gemm_dgrad_down", lora=[
+                        (gyB_d, a_down, s_down)])
+                else:
+                    grad_h_mid = _mm(gy, w_down, "gemm_dgrad_down")
+                    if a_down is not None:
+                        grad_h_mid = _addmm(grad_h_mid, gyB_d, a_down, s_down,
+                                            "gemm_dgrad_down_lora")
                 if use_k2 and outl:
                     grad_h_gate, grad_h_up, h_mid_hat = K.dequant_swiglu_backward_outlier(
                         grad_h_mid, c_gate, qs_gate, o_gate, slot_gate, c_up, qs_up, o_up,
@@ -299,15 +338,22 @@ class FlashFFNv3Function(torch.autograd.Function):
             if a_up is not None and (need_x or need_au):
                 ghuB = _mm(grad_h_up, b_up, "gemm_ghuB")
             if need_x:
-                if _mfma(grad_h_gate, w_gate, grad_h_up, w_up):
-                    # dg @ W_g + du @ W_u as one K-concatenated GEMM
-                    grad_x = G.mm2(grad_h_gate, w_gate, grad_h_up, w_up, "gemm_dgrad_x")
+                xl = [(ghgB, a_gate, s_gate) if a_gate is not None else None,
+                      (ghuB, a_up, s_up) if a_up is not None else None]
+                if _mfma(grad_h_gate, w_gate, grad_h_up, w_up) and fusable_gu:
+                    # dg @ W_g + du @ W_u as one K-concatenated GEMM, the gate and up
+                    # LoRA terms (:1561-1566) in its epilogue
+                    grad_x = G.mm2(grad_h_gate, w_gate, grad_h_up, w_up, "gemm_dgrad_x",
+                                   lora=[t for t in xl if t is not None] or None)
                 else:
-                    grad_x = grad_h_gate @ w_gate + grad_h_up @ w_up
-                if a_gate is not None:
-                    grad_x = _addmm(grad_x, ghgB, a_gate, s_gate, "gemm_dgrad_x_lora_gate")
-                if a_up is not None:
-                    grad_x = _addmm(grad_x, ghuB, a_up, s_up, "gemm_dgrad_x_lora_up")
+                    if _mfma(grad_h_gate, w_gate, grad_h_up, w_up):
+                        grad_x = G.mm2(grad_h_gate, w_gate, grad_h_up, w_up, "gemm_dgrad_x")
+                    else:
+                        grad_x = grad_h_gate @ w_gate + grad_h_up @ w_up
+                    if a_gate is not None:
+                        grad_x = _addmm(grad_x, ghgB, a_gate, s_gate, "gemm_dgrad_x_lora_gate")
+                    if a_up is not None:
+                        grad_x = _addmm(grad_x, ghuB, a_up, s_up, "gemm_dgrad_x_lora_up")
             if need_bg:
                 grad_b_gate = _mm_scaled(grad_h_gate.t(), xa_g, s_gate, "gemm_grad_b_gate")
             if need_ag:
@@ -634,8 +680,11 @@ class FlashFFNv3AdapterFunction(torch.autograd.Function):
         if need_recon and not use_k2:                                           # :2055-2078
             if mode == "recompute":
                 if fusable_gu:
+                    # the forward's kernel and terms on the same inputs: bitwise equal
+                    lkw = dict(lora_gate=None if a_gate is None else (xa_g, b_gate, s_gate),
+                               lora_up=None if a_up is None else (xa_u, b_up, s_up))
                     _, hg, hu, *_ = G.ffn_gate_up(x_2d, w_gate, w_up, _lib.CACHE_BF16, gs,
-                                                  want_h_mid=False)
+                                                  want_h_mid=False, **lkw)
                 else:
                     raw_g = _linear(x_2d, w_gate, "gemm_recompute_gate")
                     if a_gate is not None:

@@ -7,6 +7,11 @@ linear(x, w)    x @ w.T (F.linear without bias).
 ffn_gate_up     fused dual GEMM + GLU + codec (forward of gate/up + K1).
 ffn_down_dgrad  fused grad_y @ w_down + dequantise + SwiGLU backward (+ K2).
 
+LoRA adapter terms (`lora=` / `lora_gate=`, `lora_up=`): PEFT's
+`h + s * B(A(x))` applied in the GEMM epilogue, each step rounded to bf16 as
+the reference does (src/flashffn.py:1414,1420,1439,1529,1558-1566), for ranks
+8 and 16.
+
 These replace the cuBLAS GEMMs the reference issues through F.linear / @
 (src/flashffn.py:1410-1439,1503-1587).  bf16 only: the MFMA path.
 """
@@ -68,6 +73,49 @@ def _check_bf16(*ts):
         assert t.dim() == 2
 
 
+LORA_RANKS = (8, 16)
+
+
+def lora_fusable(rank: int) -> bool:
+    """Adapter terms of this rank ride in the GEMM epilogues."""
+    return rank in LORA_RANKS
+
+
+def _lora_args(terms, n_q):
+    """(rank, ldp, q_kmajor, ldq, [(p, q, alpha) x 2], keep) for up to two
+    terms (p [M, r], q the logical [r, N] factor, alpha); `keep` holds any
+    re-laid copies alive until the launch."""
+    terms = [t for t in terms if t is not None]
+    assert 1 <= len(terms) <= 2
+    r = terms[0][0].shape[1]
+    assert lora_fusable(r), f"adapter rank {r} not in {LORA_RANKS}"
+    keep, ps, qs = [], [], []
+    for pm, q, _ in terms:
+        _check_bf16(pm, q)
+        assert pm.shape[1] == r and q.shape[0] == r and q.shape[1] == n_q
+        if pm.stride(1) != 1 or pm.stride(0) % 8 or pm.data_ptr() % 16:
+            pm = pm.contiguous()
+        ps.append(pm)
+        qs.append(q)
+    ldp = ps[0].stride(0)
+    if any(x.stride(0) != ldp for x in ps):
+        ps = [x.contiguous() for x in ps]
+        ldp = r
+    # Q: K-major when the [N, r] storage is contiguous, else MN-major rows
+    if all(q.stride(0) == 1 and q.stride(1) == r and q.data_ptr() % 16 == 0 for q in qs):
+        q_kmajor, ldq = 1, r
+    elif all(q.stride(1) == 1 for q in qs) and len({q.stride(0) for q in qs}) == 1:
+        q_kmajor, ldq = 0, qs[0].stride(0)
+    else:
+        qs = [q.t().contiguous().t() for q in qs]
+        q_kmajor, ldq = 1, r
+    keep += ps + qs
+    out = [(ps[i].data_ptr(), qs[i].data_ptr(), float(terms[i][2])) for i in range(len(terms))]
+    while len(out) < 2:
+        out.append((None, None, 0.0))
+    return r, ldp, q_kmajor, ldq, out, keep
+
+
 def mm(a: torch.Tensor, b: torch.Tensor, name: str = "gemm") -> torch.Tensor:
     """a [M, K] @ b [K, N] -> bf16 [M, N] on the MFMA engine.  Products with
     too few 256x256 output tiles to fill the chip (the thin adapter products,
@@ -80,8 +128,10 @@ def mm(a: torch.Tensor, b: torch.Tensor, name: str = "gemm") -> torch.Tensor:
     return mm2(a, b, None, None, name)
 
 
-def mm2(a, b, a2=None, b2=None, name: str = "gemm") -> torch.Tensor:
-    """a @ b (+ a2 @ b2) in one fp32 accumulation -> bf16 [M, N]."""
+def mm2(a, b, a2=None, b2=None, name: str = "gemm", lora=None) -> torch.Tensor:
+    """a @ b (+ a2 @ b2) in one fp32 accumulation -> bf16 [M, N], then the
+    adapter terms `lora` = [(p [M, r], q [r, N], alpha), ...] (at most two),
+    each `out = bf16(out + bf16(alpha * bf16(p @ q)))`."""
     _require_device(a, b)
     _check_bf16(a, b)
     M, K = a.shape
@@ -113,9 +163,23 @@ def mm2(a, b, a2=None, b2=None, name: str = "gemm") -> torch.Tensor:
         p_a2, p_b2 = a2.data_ptr(), b2.data_ptr()
     ldc = (N + 7) // 8 * 8
     c = torch.empty((M, ldc), dtype=torch.bfloat16, device=a.device)
-    with _timed(name):
-        rc = _lib.lib().cpt_gemm_bf16(a.data_ptr(), lda, ak, b.data_ptr(), ldb, bk, p_a2, lda2,
-                                      p_b2, ldb2, K2, c.data_ptr(), ldc, M, N, K, _stream(a))
+    if lora:
+        if ak != 1:
+            a = a.contiguous()
+            a, lda, ak = _layout_a(a)
+            assert a2 is None, "adapter terms with a K-concatenated MN-major A"
+        r, ldp, qk, ldq, t, keep = _lora_args(lora, N)
+        with _timed(name):
+            rc = _lib.lib().cpt_gemm_bf16_lora(
+                a.data_ptr(), lda, ak, b.data_ptr(), ldb, bk, p_a2, lda2, p_b2, ldb2, K2,
+                c.data_ptr(), ldc, M, N, K, r, ldp, qk, ldq, t[0][0], t[0][1], t[0][2],
+                t[1][0], t[1][1], t[1][2], _stream(a))
+        del keep
+    else:
+        with _timed(name):
+            rc = _lib.lib().cpt_gemm_bf16(a.data_ptr(), lda, ak, b.data_ptr(), ldb, bk, p_a2,
+                                          lda2, p_b2, ldb2, K2, c.data_ptr(), ldc, M, N, K,
+                                          _stream(a))
     check(rc, name)
     return c if ldc == N else c[:, :N]
 
@@ -125,9 +189,19 @@ def linear(x: torch.Tensor, w: torch.Tensor, name: str = "gemm") -> torch.Tensor
     return mm(x, w.t(), name)
 
 
-def ffn_gate_up(x, w_gate, w_up, cache: int, group_size: int, want_h_mid: bool = True):
+def linear_lora(x: torch.Tensor, w: torch.Tensor, xa: torch.Tensor, b: torch.Tensor,
+                alpha: float, name: str = "gemm") -> torch.Tensor:
+    """PEFT's LoRA Linear without dropout: bf16(bf16(x W^T) + bf16(alpha *
+    bf16(xa B^T))) with xa = x A^T [M, r] and B [N, r]."""
+    return mm2(x, w.t(), None, None, name, lora=[(xa, b.t(), alpha)])
+
+
+def ffn_gate_up(x, w_gate, w_up, cache: int, group_size: int, want_h_mid: bool = True,
+                lora_gate=None, lora_up=None):
     """Fused dual GEMM + GLU + codec.  Returns (h_mid | None, h_gate | None,
-    h_up | None, q_gate | None, s_gate | None, q_up | None, s_up | None)."""
+    h_up | None, q_gate | None, s_gate | None, q_up | None, s_up | None).
+    lora_gate / lora_up = (xa [n, r], B [inter, r], s): the projection's LoRA
+    term, added to h_gate / h_up before the GLU and the codec."""
     _require_device(x, w_gate, w_up)
     _check_bf16(x, w_gate, w_up)
     n, hdim = x.shape
@@ -152,18 +226,33 @@ def ffn_gate_up(x, w_gate, w_up, cache: int, group_size: int, want_h_mid: bool =
     def p(t):
         return None if t is None else t.data_ptr()
 
-    with _timed("ffn_gate_up"):
-        rc = _lib.lib().cpt_ffn_gate_up(x.data_ptr(), w_gate.data_ptr(), w_up.data_ptr(), n,
-                                        hdim, d, cache, group_size, p(h_mid), p(hg), p(hu),
-                                        p(qg), p(sg), p(qu), p(su), _stream(x))
+    if lora_gate is not None or lora_up is not None:
+        # term 0 on the gate columns, term 1 on the up columns (absent: no-op)
+        present = [t for t in (lora_gate, lora_up) if t is not None]
+        r, ldp, _, _, t, keep = _lora_args([(xa, bw.t(), s) for xa, bw, s in present], d)
+        if lora_gate is None:
+            t = [(None, None, 0.0), t[0]]
+        with _timed("ffn_gate_up"):
+            rc = _lib.lib().cpt_ffn_gate_up_lora(
+                x.data_ptr(), w_gate.data_ptr(), w_up.data_ptr(), n, hdim, d, cache, group_size,
+                p(h_mid), p(hg), p(hu), p(qg), p(sg), p(qu), p(su), r, ldp, t[0][0], t[0][1],
+                t[0][2], t[1][0], t[1][1], t[1][2], _stream(x))
+        del keep
+    else:
+        with _timed("ffn_gate_up"):
+            rc = _lib.lib().cpt_ffn_gate_up(x.data_ptr(), w_gate.data_ptr(), w_up.data_ptr(), n,
+                                            hdim, d, cache, group_size, p(h_mid), p(hg), p(hu),
+                                            p(qg), p(sg), p(qu), p(su), _stream(x))
     check(rc, "ffn_gate_up")
     return h_mid, hg, hu, qg, sg, qu, su
 
 
 def ffn_down_dgrad(grad_y, w_down, cache: int, group_size: int, c_gate, s_gate, c_up, s_up,
-                   want_h_mid: bool):
+                   want_h_mid: bool, lora=None):
     """Fused grad_y @ w_down + dequantise + SwiGLU backward.
-    Returns (grad_h_gate, grad_h_up, h_mid_hat | None)."""
+    Returns (grad_h_gate, grad_h_up, h_mid_hat | None).  lora = (gy B_d
+    [n, r], A_d [r, inter], s): the down projection's LoRA term of
+    grad_h_mid."""
     _require_device(grad_y, w_down)
     _check_bf16(grad_y, w_down)
     n, hdim = grad_y.shape
@@ -178,11 +267,23 @@ def ffn_down_dgrad(grad_y, w_down, cache: int, group_size: int, c_gate, s_gate, 
     def p(t):
         return None if t is None else t.contiguous().data_ptr()
 
-    with _timed("ffn_down_dgrad"):
-        rc = _lib.lib().cpt_ffn_down_dgrad(grad_y.data_ptr(), w_down.data_ptr(), n, hdim, d,
-                                           cache, group_size, p(c_gate), p(s_gate), p(c_up),
-                                           p(s_up), dg.data_ptr(), du.data_ptr(), p(hm),
-                                           _stream(grad_y))
+    if lora is not None:
+        gyb, a_down, s = lora
+        a_down = a_down.contiguous()          # [r, inter] rows: the MN-major factor
+        r, ldp, qk, ldq, t, keep = _lora_args([(gyb, a_down, s)], d)
+        assert qk == 0 and ldq == d
+        with _timed("ffn_down_dgrad"):
+            rc = _lib.lib().cpt_ffn_down_dgrad_lora(
+                grad_y.data_ptr(), w_down.data_ptr(), n, hdim, d, cache, group_size, p(c_gate),
+                p(s_gate), p(c_up), p(s_up), dg.data_ptr(), du.data_ptr(), p(hm), r, ldp,
+                t[0][0], t[0][1], t[0][2], _stream(grad_y))
+        del keep
+    else:
+        with _timed("ffn_down_dgrad"):
+            rc = _lib.lib().cpt_ffn_down_dgrad(grad_y.data_ptr(), w_down.data_ptr(), n, hdim, d,
+                                               cache, group_size, p(c_gate), p(s_gate), p(c_up),
+                                               p(s_up), dg.data_ptr(), du.data_ptr(), p(hm),
+                                               _stream(grad_y))
     check(rc, "ffn_down_dgrad")
     return dg, du, hm
 

@@ -156,6 +156,25 @@ int cpt_gemm_bf16_ex(const void* a, int64_t lda, int a_kmajor, const void* b, in
                      int b_kmajor, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K,
                      float alpha, int mode, int splits, void* workspace, void* stream);
 
+/* Low-rank adapter terms folded into a GEMM's output ahead of its epilogue,
+ * in PEFT's op order `h + s * B(A(x))` (src/flashffn.py:1414,1420,1439,1529,
+ * 1558-1566):
+ *   out = bf16(bf16(out) + bf16(alpha_t * bf16(P_t . Q_t)))   t = 0, then 1
+ * rank in {8, 16}; P_t [M, rank] (tokens x rank, e.g. x A^T or grad_y B) with
+ * rows ldp apart (ldp % 8 == 0, 16-byte aligned); Q_t the [rank, N] factor,
+ * given as [N, rank] contiguous (q_kmajor = 1: an nn.Linear B weight) or as
+ * [rank, N] with rows ldq apart (q_kmajor = 0: an A weight).  A term whose P
+ * is NULL is skipped.  Replaces the separate `F.linear(xa, b)`, scale and add
+ * of the reference; the result equals cpt_gemm_bf16 followed by
+ * cpt_gemm_bf16_ex mode 1 up to the fp32 summation order of the rank-sized
+ * dot products. */
+int cpt_gemm_bf16_lora(const void* a, int64_t lda, int a_kmajor, const void* b, int64_t ldb,
+                       int b_kmajor, const void* a2, int64_t lda2, const void* b2, int64_t ldb2,
+                       int64_t K2, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K,
+                       int64_t rank, int64_t ldp, int q_kmajor, int64_t ldq, const void* p0,
+                       const void* q0, float alpha0, const void* p1, const void* q1,
+                       float alpha1, void* stream);
+
 /* Cache kinds of the fused FFN kernels. */
 enum { CPT_CACHE_NONE = 0, CPT_CACHE_BF16 = 1, CPT_CACHE_INT4 = 4, CPT_CACHE_INT8 = 8 };
 
@@ -171,6 +190,18 @@ int cpt_ffn_gate_up(const void* x, const void* w_gate, const void* w_up, int64_t
                     void* h_gate, void* h_up, void* q_gate, void* s_gate, void* q_up,
                     void* s_up, void* stream);
 
+/* cpt_ffn_gate_up with LoRA adapters on the gate and/or up projection
+ * (src/flashffn.py:1410-1420): h_gate = bf16(bf16(x W_g^T) + bf16(alpha_gate
+ * * bf16(p_gate . b_gate^T))) with p_gate = x A_g^T [n_tok, rank] (rows ldp
+ * apart) and b_gate the B weight [inter, rank]; likewise h_up.  The GLU and
+ * the codec then see these h.  Either term may be absent (NULL p). */
+int cpt_ffn_gate_up_lora(const void* x, const void* w_gate, const void* w_up, int64_t n_tok,
+                         int64_t hidden, int64_t inter, int cache, int64_t group_size,
+                         void* h_mid, void* h_gate, void* h_up, void* q_gate, void* s_gate,
+                         void* q_up, void* s_up, int64_t rank, int64_t ldp, const void* p_gate,
+                         const void* b_gate, float alpha_gate, const void* p_up,
+                         const void* b_up, float alpha_up, void* stream);
+
 /* Fused backward of the down projection into the GLU (replaces gy @ w_down
  * and K2, src/flashffn.py:1525-1533): grad_h_mid = bf16(grad_y @ w_down)
  * with grad_y [n_tok, hidden], w_down [hidden, inter]; the epilogue reads the
@@ -182,6 +213,17 @@ int cpt_ffn_down_dgrad(const void* grad_y, const void* w_down, int64_t n_tok, in
                        int64_t inter, int cache, int64_t group_size, const void* c_gate,
                        const void* s_gate, const void* c_up, const void* s_up, void* grad_h_gate,
                        void* grad_h_up, void* h_mid_hat, void* stream);
+
+/* cpt_ffn_down_dgrad with a LoRA adapter on the down projection
+ * (src/flashffn.py:1527-1529): grad_h_mid = bf16(bf16(grad_y W_d) +
+ * bf16(alpha * bf16(p . a_down))) with p = grad_y B_d [n_tok, rank] (rows ldp
+ * apart) and a_down the A weight [rank, inter]. */
+int cpt_ffn_down_dgrad_lora(const void* grad_y, const void* w_down, int64_t n_tok,
+                            int64_t hidden, int64_t inter, int cache, int64_t group_size,
+                            const void* c_gate, const void* s_gate, const void* c_up,
+                            const void* s_up, void* grad_h_gate, void* grad_h_up,
+                            void* h_mid_hat, int64_t rank, int64_t ldp, const void* p,
+                            const void* a_down, float alpha, void* stream);
 
 /* ---------------- adapter families (DoRA magnitude) ---------------- */
 /* VeRA, AdaLoRA and DyLoRA reach the kernels above as composed or sliced thin

@@ -1,0 +1,153 @@
+"""GPU tests of the LoRA adapter terms carried by the GEMM epilogues
+(PEFT's `h + s * B(A(x))`, src/flashffn.py:1414,1420,1439,1529,1558-1566):
+
+  * a plain GEMM with one or two terms against the fp32 reference of the
+    same bf16 inputs, with PEFT's rounding (the product and its scaling are
+    rounded to bf16 before the sum, so the bar is relative to the terms), and
+    against the composition GEMM + thin adapter add (equal up to the fp32
+    summation order of the rank-sized dot products: at most a few elements,
+    each within one bf16 step);
+  * the fused gate/up and down-dgrad kernels with their terms against the
+    plain GEMM with the same terms followed by the standalone K1 / K2 kernels:
+    bitwise, since both apply the terms with the same instructions;
+  * an absent term (adapter on gate only, or up only) leaves its columns
+    bitwise equal to the adapter-free kernel.
+"""
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _cpt():
+    import compact_amd
+    from compact_amd import _lib, gemm
+    return compact_amd, gemm, _lib
+
+
+def rnd(shape, seed, device, scale=1.0):
+    g = torch.Generator(device=device).manual_seed(seed)
+    return (torch.randn(*shape, device=device, generator=g) * scale).to(torch.bfloat16)
+
+
+def peft_ref(h_f32, terms):
+    """fp32 value of out = h + sum_t s_t * (p_t @ q_t) and the size of the terms
+    the bf16 roundings are relative to."""
+    out, mag = h_f32.clone(), h_f32.abs().clone()
+    for p, q, s in terms:
+        l = s * (p.float().cpu() @ q.float().cpu())
+        out += l
+        mag += l.abs()
+    return out, mag
+
+
+def bits16(t):
+    return t.contiguous().view(torch.int16)
+
+
+@pytest.mark.parametrize("rank", [8, 16])
+@pytest.mark.parametrize("bk", [True, False])
+@pytest.mark.parametrize("q_kmajor", [True, False])
+@pytest.mark.parametrize("nterms", [1, 2])
+def test_mm2_lora_terms(device, rank, bk, q_kmajor, nterms):
+    _, G, _ = _cpt()
+    m, n, k = 300, 264, 136
+    a = rnd((m, k), 1, device)
+    b = rnd((n, k), 2, device).t() if bk else rnd((k, n), 2, device)
+    terms = []
+    for t in range(nterms):
+        p = rnd((m, rank), 10 + t, device)
+        q = rnd((n, rank), 20 + t, device, 0.1).t() if q_kmajor else rnd((rank, n), 20 + t, device, 0.1)
+        terms.append((p, q, 2.0 if t == 0 else -0.5))
+    got = G.mm2(a, b, lora=terms)
+    # fp32 reference with PEFT's roundings
+    base = G.mm(a, b)
+    ref, mag = peft_ref(base.float().cpu(), terms)
+    tol = nterms * 2 ** -7 * mag + 1e-6
+    assert not ((got.float().cpu() - ref).abs() > tol).any()
+    # the composition through the thin adapter add
+    comp = base.clone()
+    for p, q, s in terms:
+        comp = G.addmm_(comp, p, q, s)
+    diff = bits16(got) != bits16(comp)
+    assert diff.float().mean().item() < 1e-3, int(diff.sum())
+
+
+@pytest.mark.parametrize("cache,bits,group", [("int4", 4, 64), ("int8", 8, 128), ("bf16", 0, 64),
+                                              ("none", 0, 64)])
+@pytest.mark.parametrize("which", ["both", "gate", "up"])
+@pytest.mark.parametrize("rank", [8, 16])
+def test_gate_up_lora_fused_equals_composed(device, cache, bits, group, which, rank):
+    cpt, G, _lib = _cpt()
+    code = {"int4": _lib.CACHE_INT4, "int8": _lib.CACHE_INT8, "bf16": _lib.CACHE_BF16,
+            "none": _lib.CACHE_NONE}[cache]
+    n_tok, hid, inter = 300, 128, 384
+    x = rnd((n_tok, hid), 30, device)
+    wg, wu = rnd((inter, hid), 31, device, 0.05), rnd((inter, hid), 32, device, 0.05)
+    xa_g, xa_u = rnd((n_tok, rank), 33, device), rnd((n_tok, rank), 34, device)
+    bg, bu = rnd((inter, rank), 35, device, 0.05), rnd((inter, rank), 36, device, 0.05)
+    lg = (xa_g, bg, 2.0) if which in ("both", "gate") else None
+    lu = (xa_u, bu, 2.0) if which in ("both", "up") else None
+    hm, hg, hu, qg, sg, qu, su = G.ffn_gate_up(x, wg, wu, code, group, lora_gate=lg, lora_up=lu)
+    hg_ref = G.mm2(x, wg.t(), lora=[(xa_g, bg.t(), 2.0)]) if lg else G.linear(x, wg)
+    hu_ref = G.mm2(x, wu.t(), lora=[(xa_u, bu.t(), 2.0)]) if lu else G.linear(x, wu)
+    assert torch.equal(bits16(hm), bits16(cpt.silu_mul(hg_ref, hu_ref)))
+    if cache == "bf16":
+        assert torch.equal(bits16(hg), bits16(hg_ref))
+        assert torch.equal(bits16(hu), bits16(hu_ref))
+    if bits:
+        _, rqg, rsg, rqu, rsu = cpt.silu_mul_quant(hg_ref, hu_ref, bits, group)
+        assert torch.equal(qg.view(torch.uint8), rqg.view(torch.uint8))
+        assert torch.equal(qu.view(torch.uint8), rqu.view(torch.uint8))
+        assert torch.equal(bits16(sg), bits16(rsg))
+        assert torch.equal(bits16(su), bits16(rsu))
+
+
+def test_absent_term_is_a_no_op(device):
+    """Adapter on gate only: h_up must equal the adapter-free kernel's bit for
+    bit (zero rows of x included)."""
+    _, G, _lib = _cpt()
+    n_tok, hid, inter, rank = 64, 64, 256, 16
+    x = rnd((n_tok, hid), 40, device)
+    x[::3] = -0.0
+    wg, wu = rnd((inter, hid), 41, device, 0.05), rnd((inter, hid), 42, device, 0.05)
+    xa_g, bg = rnd((n_tok, rank), 43, device), rnd((inter, rank), 44, device, 0.05)
+    _, hg, hu, *_ = G.ffn_gate_up(x, wg, wu, _lib.CACHE_BF16, 64, lora_gate=(xa_g, bg, 2.0))
+    _, hg0, hu0, *_ = G.ffn_gate_up(x, wg, wu, _lib.CACHE_BF16, 64)
+    assert torch.equal(bits16(hu), bits16(hu0))
+
+
+@pytest.mark.parametrize("cache,bits,group", [("int4", 4, 64), ("int8", 8, 128), ("bf16", 0, 64)])
+@pytest.mark.parametrize("want_h_mid", [True, False])
+@pytest.mark.parametrize("rank", [8, 16])
+def test_down_dgrad_lora_fused_equals_composed(device, cache, bits, group, want_h_mid, rank):
+    cpt, G, _lib = _cpt()
+    code = {"int4": _lib.CACHE_INT4, "int8": _lib.CACHE_INT8, "bf16": _lib.CACHE_BF16}[cache]
+    n_tok, hid, inter = 300, 128, 384
+    hg, hu = rnd((n_tok, inter), 50, device, 3.0), rnd((n_tok, inter), 51, device, 2.0)
+    gy, wd = rnd((n_tok, hid), 52, device), rnd((hid, inter), 53, device, 0.05)
+    gyb, ad = rnd((n_tok, rank), 54, device), rnd((rank, inter), 55, device, 0.05)
+    lora = (gyb, ad, 2.0)
+    gmid = G.mm2(gy, wd, lora=[lora])
+    if bits:
+        _, qg, sg, qu, su = cpt.silu_mul_quant(hg, hu, bits, group)
+        dg, du, hm = G.ffn_down_dgrad(gy, wd, code, group, qg, sg, qu, su, want_h_mid, lora=lora)
+        rdg, rdu, rhm = cpt.dequant_swiglu_backward(gmid, qg, sg, qu, su, bits, group,
+                                                    want_h_mid=want_h_mid)
+    else:
+        dg, du, hm = G.ffn_down_dgrad(gy, wd, code, group, hg, None, hu, None, want_h_mid,
+                                      lora=lora)
+        rdg, rdu, rhm = cpt.swiglu_backward_glu(gmid, hg, hu, want_h_mid)
+    assert torch.equal(bits16(dg), bits16(rdg))
+    assert torch.equal(bits16(du), bits16(rdu))
+    if want_h_mid:
+        assert torch.equal(bits16(hm), bits16(rhm))
+
+
+def test_rank_outside_epilogue_set_raises(device):
+    _, G, _ = _cpt()
+    a, b = rnd((64, 64), 60, device), rnd((64, 64), 61, device)
+    p, q = rnd((64, 4), 62, device), rnd((4, 64), 63, device)
+    with pytest.raises(AssertionError):
+        G.mm2(a, b, lora=[(p, q, 1.0)])
