@@ -544,31 +544,35 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
   if (A.npairs > 1) nk += (int)((A.K[1] + BK - 1) / BK);
   if (nk <= 0) return;
   uint4 va[8], vb[8];
-  auto ldA = [&](int kt, int it) -> uint4 {
+  // Per-tile load state, computed once per k-tile: the pair's buffer and a
+  // per-lane byte delta added to every fixed per-thread offset.  An offset at
+  // or past kOOB reads zero (records < 2^31 and offsets + delta < 2^32), so
+  // MN-major lanes outside the tile keep reading zero with no select, and a
+  // K-major lane whose chunk lies past K gets delta kOOB (one select per
+  // operand per tile, not per load).
+  struct TileLd {
+    __amdgpu_buffer_rsrc_t ra, rb;
+    uint32_t da, db;
+  };
+  auto tile = [&](int kt) -> TileLd {
+    TileLd T;
     const int p = kt >= L.nk0 ? 1 : 0;
     const int64_t k0 = (int64_t)(kt - p * L.nk0) * BK;
     const int64_t Kp = p ? L.K[1] : L.K[0];
-    const __amdgpu_buffer_rsrc_t rA = p ? L.ra[1] : L.ra[0];
-    if (AK) {
-      const bool kok = k0 + (tid & 7) * 8 < Kp;
-      return bload(rA, kok ? L.oa[it] + (uint32_t)(k0 * 2) : kOOB);
-    }
-    return bload(rA, L.oa[it] == kOOB ? kOOB : L.oa[it] + (uint32_t)(k0 * L.lda * 2));
+    T.ra = p ? L.ra[1] : L.ra[0];
+    T.rb = p ? L.rb[1] : L.rb[0];
+    const bool kok = k0 + (tid & 7) * 8 < Kp;
+    T.da = AK ? (kok ? (uint32_t)(k0 * 2) : kOOB) : (uint32_t)(k0 * L.lda * 2);
+    T.db = BK_ ? (kok ? (uint32_t)(k0 * 2) : kOOB) : (uint32_t)(k0 * L.ldb * 2);
+    return T;
   };
-  auto ldB = [&](int kt, int it) -> uint4 {
-    const int p = kt >= L.nk0 ? 1 : 0;
-    const int64_t k0 = (int64_t)(kt - p * L.nk0) * BK;
-    const int64_t Kp = p ? L.K[1] : L.K[0];
-    const __amdgpu_buffer_rsrc_t rB = p ? L.rb[1] : L.rb[0];
-    if (BK_) {
-      const bool kok = k0 + (tid & 7) * 8 < Kp;
-      const __amdgpu_buffer_rsrc_t r = (DUAL && ((it >> 1) & 1)) ? L.rup : rB;
-      return bload(r, kok ? L.ob[it] + (uint32_t)(k0 * 2) : kOOB);
-    }
-    return bload(rB, L.ob[it] == kOOB ? kOOB : L.ob[it] + (uint32_t)(k0 * L.ldb * 2));
+  auto ldA = [&](const TileLd& T, int it) -> uint4 { return bload(T.ra, L.oa[it] + T.da); };
+  auto ldB = [&](const TileLd& T, int it) -> uint4 {
+    const __amdgpu_buffer_rsrc_t r = (DUAL && ((it >> 1) & 1)) ? L.rup : T.rb;
+    return bload(r, L.ob[it] + T.db);
   };
-  // group g of tile kt: store the held registers into `stage`, reload them with tile kt_load
-  auto group = [&](int g, int stage, int kt_load) {
+  // group g of tile kt: store the held registers into `stage`, reload them with tile T
+  auto group = [&](int g, int stage, const TileLd& T) {
     uint16_t* sa = lds + stage * 2 * TILE_ELEMS;
     uint16_t* sb = sa + TILE_ELEMS;
 #pragma unroll
@@ -576,27 +580,33 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
       const int it = 2 * g + h, q = tid + NTHR * it;
       if (AK) *reinterpret_cast<uint4*>(sa + lds_off(q >> 3, q & 7)) = va[it];
       else sstore_mn_row(sa, tid, it, va[it]);
-      va[it] = ldA(kt_load, it);
+      va[it] = ldA(T, it);
     }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int it = 2 * g + h, q = tid + NTHR * it;
       if (BK_) *reinterpret_cast<uint4*>(sb + lds_off(q >> 3, q & 7)) = vb[it];
       else sstore_mn_row(sb, tid, it, vb[it]);
-      vb[it] = ldB(kt_load, it);
+      vb[it] = ldB(T, it);
     }
   };
   // prologue: tile 0 into stage 0, tile 1 into registers
+  {
+    const TileLd T0 = tile(0);
 #pragma unroll
-  for (int it = 0; it < 8; ++it) { va[it] = ldA(0, it); vb[it] = ldB(0, it); }
+    for (int it = 0; it < 8; ++it) { va[it] = ldA(T0, it); vb[it] = ldB(T0, it); }
+  }
   {
     uint16_t* sa = lds;
     uint16_t* sb = sa + TILE_ELEMS;
     if (AK) sstore_kmajor(sa, tid, va); else sstore_mnmajor(sa, tid, va);
     if (BK_) sstore_kmajor(sb, tid, vb); else sstore_mnmajor(sb, tid, vb);
   }
+  {
+    const TileLd T1 = tile(1);
 #pragma unroll
-  for (int it = 0; it < 8; ++it) { va[it] = ldA(1, it); vb[it] = ldB(1, it); }
+    for (int it = 0; it < 8; ++it) { va[it] = ldA(T1, it); vb[it] = ldB(T1, it); }
+  }
   __syncthreads();
   Frags f0, f1;
   read_frags<AK, BK_>(lds, wn, wm, lane, 0, f0);
@@ -607,20 +617,21 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
   for (int kt = 0; kt + 1 < nk; ++kt) {
     const int stage = kt & 1;
     const uint16_t* base = lds + stage * 2 * TILE_ELEMS;
+    const TileLd T2 = tile(kt + 2);
     read_frags<AK, BK_>(base, wn, wm, lane, 1, f1);
     mfma_range<0, 16>(f0, acc);
-    group(0, stage ^ 1, kt + 2);
+    group(0, stage ^ 1, T2);
     sched_interleave<16, MASK, PER>();
     read_frags<AK, BK_>(base, wn, wm, lane, 2, f0);
     mfma_range<0, 16>(f1, acc);
-    group(1, stage ^ 1, kt + 2);
+    group(1, stage ^ 1, T2);
     sched_interleave<16, MASK, PER>();
     read_frags<AK, BK_>(base, wn, wm, lane, 3, f1);
     mfma_range<0, 16>(f0, acc);
-    group(2, stage ^ 1, kt + 2);
+    group(2, stage ^ 1, T2);
     sched_interleave<16, MASK, PER>();
     mfma_range<0, 8>(f1, acc);
-    group(3, stage ^ 1, kt + 2);
+    group(3, stage ^ 1, T2);
     sched_interleave<8, MASK, 1>();
     __syncthreads();
     read_frags<AK, BK_>(lds + (stage ^ 1) * 2 * TILE_ELEMS, wn, wm, lane, 0, f0);
