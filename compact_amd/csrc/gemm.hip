@@ -81,25 +81,11 @@ __device__ __forceinline__ i16x4 lds_read_tr(const uint16_t* p) {
 }
 
 // ---------------------------------------------------------------------------
-// global -> registers -> LDS
+// registers -> LDS (the tile's global loads are in Loader / mainloop_pp)
 // ---------------------------------------------------------------------------
 
-// K-major tile: rows r0..r0+255, k0..k0+63 of p[row * ld + k]; thread owns 8
-// 16-byte chunks, 8 consecutive threads cover one 128-byte row slice.
-__device__ __forceinline__ void gload_kmajor(const uint16_t* p, int64_t ld, int64_t rows, int64_t K,
-                                             int64_t r0, int64_t k0, int tid, uint4 (&reg)[8]) {
-#pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    const int q = tid + NTHR * it;
-    const int row = q >> 3, c = q & 7;
-    const int64_t gr = r0 + row, gk = k0 + c * 8;
-    if (gr < rows && gk < K)
-      reg[it] = *reinterpret_cast<const uint4*>(p + gr * ld + gk);
-    else
-      reg[it] = make_uint4(0, 0, 0, 0);
-  }
-}
-
+// K-major tile: the thread holds 8 16-byte chunks q = tid + 256 it, chunk
+// q % 8 (8 k) of row q / 8; 8 consecutive threads cover one 128-byte row slice.
 __device__ __forceinline__ void sstore_kmajor(uint16_t* lds, int tid, const uint4 (&reg)[8]) {
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
@@ -108,24 +94,9 @@ __device__ __forceinline__ void sstore_kmajor(uint16_t* lds, int tid, const uint
   }
 }
 
-// MN-major tile: thread owns an 8 (k) x 8 (mn) block: k = k0 + 8 (tid / 32) + r,
-// mn = r0 + 8 (tid % 32) + 0..7 of p[k * ld + mn].  Requires rows % 8 == 0.
-__device__ __forceinline__ void gload_mnmajor(const uint16_t* p, int64_t ld, int64_t rows, int64_t K,
-                                              int64_t r0, int64_t k0, int tid, uint4 (&reg)[8]) {
-  const int mb = tid & 31, kb = tid >> 5;
-  const int64_t gmn = r0 + mb * 8;
-#pragma unroll
-  for (int r = 0; r < 8; ++r) {
-    const int64_t gk = k0 + kb * 8 + r;
-    if (gmn < rows && gk < K)
-      reg[r] = *reinterpret_cast<const uint4*>(p + gk * ld + gmn);
-    else
-      reg[r] = make_uint4(0, 0, 0, 0);
-  }
-}
-
-// MN-major tile: the thread's row r (k = 8 (tid / 32) + r) into its 16-byte
-// mn segment, untransposed.
+// MN-major tile: the thread holds an 8 (k) x 8 (mn) block, k = 8 (tid / 32)
+// + r, mn = 8 (tid % 32) + 0..7; its row r goes into its 16-byte mn segment,
+// untransposed.
 __device__ __forceinline__ void sstore_mn_row(uint16_t* lds, int tid, int r, const uint4& v) {
   *reinterpret_cast<uint4*>(lds + lds_mn((tid >> 5) * 8 + r, (tid & 31) * 8)) = v;
 }
@@ -237,7 +208,6 @@ struct Loader {
   int64_t K[2];
   int nk0;
   int64_t lda, ldb;
-  uint32_t ka_ok_shift;    // unused placeholder for alignment of the struct
 
   __device__ __forceinline__ void init(const KArgs& A, int64_t m0, int64_t n0, int tid) {
     lda = A.a[0].ld;
@@ -284,74 +254,6 @@ struct Loader {
 #pragma unroll
       for (int r = 0; r < 8; ++r)
         ob[r] = mn < A.N ? (uint32_t)((((tid >> 5) * 8 + r) * ldb + mn) * 2) : kOOB;
-    }
-  }
-
-  // the A and B halves of issue(), for schedules that spread them apart
-  __device__ __forceinline__ void issue_a(int kt, int tid, uint4 (&va)[8]) const {
-    const int p = kt >= nk0 ? 1 : 0;
-    const int64_t k0 = (int64_t)(kt - p * nk0) * BK;
-    const int64_t Kp = p ? K[1] : K[0];
-    const __amdgpu_buffer_rsrc_t rA = p ? ra[1] : ra[0];
-    const bool kok = k0 + (tid & 7) * 8 < Kp;
-    if (AK) {
-      const uint32_t adv = (uint32_t)(k0 * 2);
-#pragma unroll
-      for (int it = 0; it < 8; ++it) va[it] = bload(rA, kok ? oa[it] + adv : kOOB);
-    } else {
-      const uint32_t adv = (uint32_t)(k0 * lda * 2);
-#pragma unroll
-      for (int r = 0; r < 8; ++r) va[r] = bload(rA, oa[r] == kOOB ? kOOB : oa[r] + adv);
-    }
-  }
-  __device__ __forceinline__ void issue_b(int kt, int tid, uint4 (&vb)[8]) const {
-    const int p = kt >= nk0 ? 1 : 0;
-    const int64_t k0 = (int64_t)(kt - p * nk0) * BK;
-    const int64_t Kp = p ? K[1] : K[0];
-    const __amdgpu_buffer_rsrc_t rB = p ? rb[1] : rb[0];
-    const bool kok = k0 + (tid & 7) * 8 < Kp;
-    if (DUAL || BKM) {
-      const uint32_t adv = (uint32_t)(k0 * 2);
-#pragma unroll
-      for (int it = 0; it < 8; ++it) {
-        const __amdgpu_buffer_rsrc_t r = (DUAL && ((it >> 1) & 1)) ? rup : rB;
-        vb[it] = bload(r, kok ? ob[it] + adv : kOOB);
-      }
-    } else {
-      const uint32_t adv = (uint32_t)(k0 * ldb * 2);
-#pragma unroll
-      for (int r = 0; r < 8; ++r) vb[r] = bload(rB, ob[r] == kOOB ? kOOB : ob[r] + adv);
-    }
-  }
-
-  // global loads of k-tile kt into registers (16 x 128-bit, no branches)
-  __device__ __forceinline__ void issue(int kt, int tid, uint4 (&va)[8], uint4 (&vb)[8]) const {
-    const int p = kt >= nk0 ? 1 : 0;
-    const int64_t k0 = (int64_t)(kt - p * nk0) * BK;
-    const int64_t Kp = p ? K[1] : K[0];
-    const __amdgpu_buffer_rsrc_t rA = p ? ra[1] : ra[0];
-    const __amdgpu_buffer_rsrc_t rB = p ? rb[1] : rb[0];
-    const bool kok = k0 + (tid & 7) * 8 < Kp;   // K-major chunk inside K
-    if (AK) {
-      const uint32_t adv = (uint32_t)(k0 * 2);
-#pragma unroll
-      for (int it = 0; it < 8; ++it) va[it] = bload(rA, kok ? oa[it] + adv : kOOB);
-    } else {
-      const uint32_t adv = (uint32_t)(k0 * lda * 2);
-#pragma unroll
-      for (int r = 0; r < 8; ++r) va[r] = bload(rA, oa[r] == kOOB ? kOOB : oa[r] + adv);
-    }
-    if (DUAL || BKM) {
-      const uint32_t adv = (uint32_t)(k0 * 2);
-#pragma unroll
-      for (int it = 0; it < 8; ++it) {
-        const __amdgpu_buffer_rsrc_t r = (DUAL && ((it >> 1) & 1)) ? rup : rB;
-        vb[it] = bload(r, kok ? ob[it] + adv : kOOB);
-      }
-    } else {
-      const uint32_t adv = (uint32_t)(k0 * ldb * 2);
-#pragma unroll
-      for (int r = 0; r < 8; ++r) vb[r] = bload(rB, ob[r] == kOOB ? kOOB : ob[r] + adv);
     }
   }
 };
@@ -415,111 +317,6 @@ __device__ __forceinline__ void sched_interleave() {
   }
 }
 
-template <int N>
-__device__ __forceinline__ void sched_interleave_load_read() {
-  // N times: one MFMA, one global load, one LDS read
-#pragma unroll
-  for (int t = 0; t < N; ++t) {
-    __builtin_amdgcn_sched_group_barrier(SG_MFMA, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(SG_VMEM_R, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(SG_DS_R, 1, 0);
-  }
-}
-
-// Software-pipelined main loop.  Per k-tile (4 sub-steps of k16, fragment
-// register sets f0/f1 alternating):
-//   s0: 16 MFMAs interleaved with the 16 global loads of tile kt+1 and the
-//       8 LDS reads of s1;  s1, s2: 16 MFMAs with the 8 LDS reads of s+1;
-//   s3: 8 MFMAs interleaved with the 16 LDS writes of tile kt+1 (other
-//       stage), one barrier, then 8 MFMAs with the 8 LDS reads of (kt+1, s0).
-// The other stage was last read during tile kt-1, before the barrier that
-// ended it, so one barrier per k-tile suffices.
-template <bool AK, bool BKM, bool DUAL>
-__device__ __forceinline__ void mainloop(const KArgs& A, int64_t m0, int64_t n0, uint16_t* lds,
-                                         Acc& acc, int kt0 = 0, int kt_end = -1) {
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wn = wave & 1, wm = wave >> 1;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc.v[i][j][r] = 0.0f;
-
-  Loader<AK, BKM, DUAL> L;
-  L.init(A, m0, n0, tid);
-  int nk_all = L.nk0;
-  if (A.npairs > 1) nk_all += (int)((A.K[1] + BK - 1) / BK);
-  if (kt_end < 0 || kt_end > nk_all) kt_end = nk_all;
-  const int nk = kt_end - kt0;       // k-tiles of this block
-  if (nk <= 0) return;               // empty split: the accumulators stay zero
-
-  uint4 va[8], vb[8];
-  auto store = [&](int stage) {
-    uint16_t* sa = lds + stage * 2 * TILE_ELEMS;
-    uint16_t* sb = sa + TILE_ELEMS;
-    if (AK) sstore_kmajor(sa, tid, va); else sstore_mnmajor(sa, tid, va);
-    if (BKM || DUAL) sstore_kmajor(sb, tid, vb); else sstore_mnmajor(sb, tid, vb);
-  };
-
-  L.issue(kt0, tid, va, vb);
-  store(0);
-  __syncthreads();
-  Frags f0, f1;
-  read_frags<AK, BKM || DUAL>(lds, wn, wm, lane, 0, f0);
-  for (int kt = 0; kt + 1 < nk; ++kt) {
-    const int stage = kt & 1;
-    const uint16_t* base = lds + stage * 2 * TILE_ELEMS;
-    if constexpr (AK && !BKM && !DUAL) {
-      // K-major A, MN-major B (the NN products): A's loads in s0, B's in s1
-      // (measured +5% over issuing all 16 in s0)
-      L.issue_a(kt0 + kt + 1, tid, va);
-      read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 1, f1);
-      mfma_range<0, 16>(f0, acc);
-      sched_interleave_load_read<8>();
-      sched_interleave<8, SG_MFMA>();
-      L.issue_b(kt0 + kt + 1, tid, vb);
-      read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 2, f0);
-      mfma_range<0, 16>(f1, acc);
-      sched_interleave_load_read<8>();
-      sched_interleave<8, SG_MFMA>();
-    } else {
-      L.issue(kt0 + kt + 1, tid, va, vb);
-      read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 1, f1);
-      mfma_range<0, 16>(f0, acc);
-      sched_interleave_load_read<8>();
-      sched_interleave<8, SG_VMEM_R>();
-      read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 2, f0);
-      mfma_range<0, 16>(f1, acc);
-      sched_interleave<8, SG_DS_R>();
-    }
-    read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 3, f1);
-    mfma_range<0, 16>(f0, acc);
-    sched_interleave<8, SG_DS_R>();
-    store(stage ^ 1);
-    mfma_range<0, 8>(f1, acc);
-    sched_interleave<8, SG_DS_W, 2>();
-    __syncthreads();
-    read_frags<AK, BKM || DUAL>(lds + (stage ^ 1) * 2 * TILE_ELEMS, wn, wm, lane, 0, f0);
-    mfma_range<8, 16>(f1, acc);
-    sched_interleave<8, SG_DS_R>();
-  }
-  {
-    // last k-tile: no loads, no stores
-    const uint16_t* base = lds + ((nk - 1) & 1) * 2 * TILE_ELEMS;
-    read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 1, f1);
-    mfma_range<0, 16>(f0, acc);
-    read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 2, f0);
-    mfma_range<0, 16>(f1, acc);
-    read_frags<AK, BKM || DUAL>(base, wn, wm, lane, 3, f1);
-    mfma_range<0, 16>(f0, acc);
-    mfma_range<0, 16>(f1, acc);
-  }
-  __syncthreads();   // the epilogue may reuse LDS
-}
-
-
 // Continuous-pipeline main loop: during k-tile kt the registers hold tile kt+1,
 // which is written to the other LDS stage group by group across the four
 // sub-steps, each group reloaded with tile kt+2 right after its write.  Loads
@@ -527,7 +324,7 @@ __device__ __forceinline__ void mainloop(const KArgs& A, int64_t m0, int64_t n0,
 // k-tile to land.  Each operand goes 2 registers per group.
 template <bool AK, bool BKM, bool DUAL>
 __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t n0, uint16_t* lds,
-                                            Acc& acc) {
+                                            Acc& acc, int kt0 = 0, int kt_end = -1) {
   constexpr bool BK_ = BKM || DUAL;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -540,9 +337,13 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
       for (int r = 0; r < 16; ++r) acc.v[i][j][r] = 0.0f;
   Loader<AK, BKM, DUAL> L;
   L.init(A, m0, n0, tid);
-  int nk = L.nk0;
-  if (A.npairs > 1) nk += (int)((A.K[1] + BK - 1) / BK);
-  if (nk <= 0) return;
+  int nk_all = L.nk0;
+  if (A.npairs > 1) nk_all += (int)((A.K[1] + BK - 1) / BK);
+  if (kt_end < 0 || kt_end > nk_all) kt_end = nk_all;
+  // k-tiles [kt0, kt_end); the prefetch past kt_end stays inside the operands
+  // or reads zero past K
+  const int nk = kt_end - kt0;
+  if (nk <= 0) return;   // empty range: the accumulators stay zero
   uint4 va[8], vb[8];
   // Per-tile load state, computed once per k-tile: the pair's buffer and a
   // per-lane byte delta added to every fixed per-thread offset.  An offset at
@@ -592,7 +393,7 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
   };
   // prologue: tile 0 into stage 0, tile 1 into registers
   {
-    const TileLd T0 = tile(0);
+    const TileLd T0 = tile(kt0);
 #pragma unroll
     for (int it = 0; it < 8; ++it) { va[it] = ldA(T0, it); vb[it] = ldB(T0, it); }
   }
@@ -603,7 +404,7 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
     if (BK_) sstore_kmajor(sb, tid, vb); else sstore_mnmajor(sb, tid, vb);
   }
   {
-    const TileLd T1 = tile(1);
+    const TileLd T1 = tile(kt0 + 1);
 #pragma unroll
     for (int it = 0; it < 8; ++it) { va[it] = ldA(T1, it); vb[it] = ldB(T1, it); }
   }
@@ -617,7 +418,7 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
   for (int kt = 0; kt + 1 < nk; ++kt) {
     const int stage = kt & 1;
     const uint16_t* base = lds + stage * 2 * TILE_ELEMS;
-    const TileLd T2 = tile(kt + 2);
+    const TileLd T2 = tile(kt0 + kt + 2);
     read_frags<AK, BK_>(base, wn, wm, lane, 1, f1);
     mfma_range<0, 16>(f0, acc);
     group(0, stage ^ 1, T2);
@@ -1137,8 +938,8 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_kernel(KArgs A) {
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   Acc acc;
   if constexpr (EPI == EPI_F32) {
-    mainloop<AK, BKM, false>(A, m0, n0, lds, acc, split * A.kt_per_split,
-                             (split + 1) * A.kt_per_split);
+    mainloop_pp<AK, BKM, false>(A, m0, n0, lds, acc, split * A.kt_per_split,
+                                (split + 1) * A.kt_per_split);
     epi_f32(A, acc, m0, n0, split);
     return;
   } else {
