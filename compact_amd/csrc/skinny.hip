@@ -1,0 +1,359 @@
+// Skinny products of the low-rank adapters: C[M, R] = alpha * A[M, K] . Q^T
+// with Q [R, K] and R <= 32 (the rank).  These are the thin GEMMs of the LoRA
+// terms that the reference issues through F.linear / @ (src/flashffn.py:1414,
+// 1420,1439 forward: x A^T and h_mid A_d^T; :1521,1556-1557 backward: grad_y
+// B_d, grad_h_gate B_g, grad_h_up B_u).
+//
+// They read a tall token-major operand once (x, h_mid, grad_y, grad_h_*: up
+// to 180 MB) and produce a [tokens, rank] result, so they are HBM-bound: a
+// 256 x 256 MFMA tile would waste 15/16 of its work and, with only M/256
+// tiles, leave most CUs idle.  Here each wavefront owns 32 rows and one K
+// range and streams A straight from global memory into the A slot of
+// v_mfma_f32_16x16x32_bf16 (a lane's 16-byte load is the 8 consecutive k of
+// one row the instruction wants), with Q's fragments (a few hundred KB, L2
+// resident) in the B slot.  K is split across blocks so the grid has enough
+// waves in flight to cover HBM latency; the fp32 partials [splits][M][R] are
+// then summed in split order (deterministic) and rounded to bf16 once.
+//
+// 16x16x32 bf16 MFMA operand layout: lane l holds A[l % 16][8 (l / 16) + e]
+// and B[8 (l / 16) + e][l % 16], e = 0..7; the result lane l holds
+// D[4 (l / 16) + i][l % 16], i = 0..3.
+
+#include "common.h"
+#include "compact_amd.h"
+
+namespace cpt {
+namespace skinny {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t kOOB = 0x80000000u;   // offsets >= 2^31 read zero (records < 2^31)
+constexpr int kRsrcWord3 = 0x00020000;
+#ifndef CPT_SKINNY_RB
+#define CPT_SKINNY_RB 2
+#endif
+#ifndef CPT_SKINNY_UNROLL
+#define CPT_SKINNY_UNROLL 4
+#endif
+constexpr int kRowBlocks = CPT_SKINNY_RB;      // 16-row blocks per wavefront (share Q's fragments)
+constexpr int kRowsPerBlock = 4 * 16 * kRowBlocks;   // 4 wavefronts per block
+constexpr int kUnroll = CPT_SKINNY_UNROLL;     // k32 steps in flight per wavefront
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcWord3);
+}
+
+__device__ __forceinline__ bf16x8 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// NB column blocks of 16 (R <= 16 NB); each wavefront owns kRowBlocks blocks
+// of 16 rows, so one Q fragment serves kRowBlocks MFMAs.  Grid:
+// (ceil(M / kRowsPerBlock), splits); split s covers k in
+// [s * kchunk, min(K, (s + 1) * kchunk)), kchunk % 32 == 0.
+// ws != null: fp32 partials ws[(s * M + m) * R + r]; else C = bf16(alpha * acc).
+template <int NB>
+__global__ __launch_bounds__(256) void skinny_proj_kernel(
+    const uint16_t* __restrict__ a, int64_t lda, const uint16_t* __restrict__ q, int64_t ldq,
+    int64_t M, int R, int64_t K, int64_t kchunk, float* __restrict__ ws, uint16_t* __restrict__ c,
+    int64_t ldc, float alpha) {
+  constexpr int RB = kRowBlocks;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t m0 = ((int64_t)blockIdx.x * 4 + wave) * 16 * RB;
+  if (m0 >= M) return;   // whole wavefront
+  const int s = blockIdx.y;
+  const int64_t k_begin = (int64_t)s * kchunk;
+  const int64_t k_end = min(K, k_begin + kchunk);
+  // rows of A past M and rows of Q past R read zero through the records
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(a, M * lda * 2);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(q, (int64_t)R * ldq * 2);
+  const int kq = 8 * (lane >> 4);
+  uint32_t oa[RB];
+#pragma unroll
+  for (int b = 0; b < RB; ++b) oa[b] = (uint32_t)(((m0 + 16 * b + (lane & 15)) * lda + kq) * 2);
+  uint32_t oq[NB];
+#pragma unroll
+  for (int t = 0; t < NB; ++t) oq[t] = (uint32_t)(((int64_t)(t * 16 + (lane & 15)) * ldq + kq) * 2);
+  f32x4 acc[RB][NB];
+#pragma unroll
+  for (int b = 0; b < RB; ++b)
+#pragma unroll
+    for (int t = 0; t < NB; ++t) acc[b][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  int64_t k = k_begin;
+  for (; k + 32 * kUnroll <= k_end; k += 32 * kUnroll) {
+    bf16x8 av[kUnroll][RB], qv[kUnroll][NB];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const uint32_t dk = (uint32_t)((k + 32 * u) * 2);
+#pragma unroll
+      for (int b = 0; b < RB; ++b) av[u][b] = bload(ra, oa[b] + dk);
+#pragma unroll
+      for (int t = 0; t < NB; ++t) qv[u][t] = bload(rq, oq[t] + dk);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+      for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int t = 0; t < NB; ++t)
+          acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av[u][b], qv[u][t], acc[b][t], 0, 0, 0);
+  }
+  for (; k < k_end; k += 32) {
+    // K % 8 == 0 and kchunk % 32 == 0: a lane's 8-wide chunk is wholly in or out
+    const bool ok = k + kq < k_end;
+    const uint32_t dk = (uint32_t)(k * 2);
+    bf16x8 qv[NB];
+#pragma unroll
+    for (int t = 0; t < NB; ++t) qv[t] = bload(rq, ok ? oq[t] + dk : kOOB);
+#pragma unroll
+    for (int b = 0; b < RB; ++b) {
+      const bf16x8 av = bload(ra, ok ? oa[b] + dk : kOOB);
+#pragma unroll
+      for (int t = 0; t < NB; ++t)
+        acc[b][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, qv[t], acc[b][t], 0, 0, 0);
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < RB; ++b)
+#pragma unroll
+    for (int t = 0; t < NB; ++t) {
+      const int col = t * 16 + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t row = m0 + 16 * b + 4 * (lane >> 4) + i;
+        if (row >= M || col >= R) continue;
+        if (ws)
+          ws[((int64_t)s * M + row) * R + col] = acc[b][t][i];
+        else
+          c[row * ldc + col] = (uint16_t)f32_to_bf16_bits(alpha * acc[b][t][i]);
+      }
+    }
+}
+
+// C[m, r] = bf16(alpha * sum_s ws[s][m][r]), splits summed in order
+__global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restrict__ ws,
+                                                            uint16_t* __restrict__ c, int64_t M,
+                                                            int R, int64_t ldc, int splits,
+                                                            float alpha) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= M * R) return;
+  float sum = 0.0f;
+  for (int s = 0; s < splits; ++s) sum += ws[(int64_t)s * M * R + e];
+  const int64_t m = e / R, r = e - m * R;
+  c[m * ldc + r] = (uint16_t)f32_to_bf16_bits(alpha * sum);
+}
+
+// ---------------------------------------------------------------------------
+// Token reductions of the adapter gradients: Z[N, R] = alpha * X^T . P with
+// X [T, N] and P [T, R] token-major (rows t), R <= 32: grad_B = s * grad_y^T
+// (x A^T) and grad_A^T = s * x^T (grad B) (src/flashffn.py:1538-1545,
+// 1575-1582).  The reduction runs over the tokens, which are X's strided
+// dimension, so a block stages a [64 tokens x 64 columns] piece of X (and the
+// matching [64 x R] piece of P) in LDS with coalesced 128-byte row loads and
+// the MFMA fragments (8 consecutive tokens of one column) come out of
+// ds_read_b64_tr_b16.  Each wavefront owns 16 of the 64 columns; blocks split
+// the tokens, and the fp32 partials [splits][N][R] are summed in split order.
+// ---------------------------------------------------------------------------
+constexpr int kRedCols = 64;    // X columns per block (16 per wavefront)
+constexpr int kRedTok = 64;     // tokens per step
+constexpr int kRedLdX = 72;     // LDS row stride of the X piece (elements)
+constexpr int kRedLdP = 40;     // LDS row stride of the P piece (elements)
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+__device__ __forceinline__ i16x4 lds_read_tr(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+}
+
+// fragment of 8 consecutive tokens (k) of column `col` from a [tokens][ld]
+// LDS piece: ds_read_b64_tr_b16 gives, within each 16-lane group, lane j the
+// 4 tokens of column j of a 4 x 16 block whose rows the lanes address
+// (lane s: token row s / 4, columns 4 (s % 4)); two reads make the 8
+template <int LD>
+__device__ __forceinline__ bf16x8 red_frag(const uint16_t* piece, int k0, int col0, int lane) {
+  const int k = k0 + 8 * (lane >> 4) + ((lane & 15) >> 2);
+  const int c = col0 + 4 * (lane & 3);
+  const i16x4 lo = lds_read_tr(piece + k * LD + c);
+  const i16x4 hi = lds_read_tr(piece + (k + 4) * LD + c);
+  return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// Grid: (ceil(N / 64), splits); split s covers tokens [s * tchunk,
+// min(T, (s + 1) * tchunk)), tchunk % 64 == 0.  N % 8 == 0, R % 8 == 0.
+template <int NB>
+__global__ __launch_bounds__(256) void skinny_red_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ p, int64_t ldp,
+    int64_t T, int64_t N, int R, int64_t tchunk, float* __restrict__ ws) {
+  __shared__ __attribute__((aligned(16))) uint16_t xs[2][kRedTok * kRedLdX];
+  __shared__ __attribute__((aligned(16))) uint16_t ps[2][kRedTok * kRedLdP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t n0 = (int64_t)blockIdx.x * kRedCols;
+  const int s = blockIdx.y;
+  const int64_t t_begin = (int64_t)s * tchunk;
+  const int64_t t_end = min(T, t_begin + tchunk);
+  // tokens past T read zero through the records; columns past N / R are
+  // masked per 8-wide chunk (N % 8 == 0, R % 8 == 0)
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, T * ldx * 2);
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(p, T * ldp * 2);
+  // X piece: thread loads rows tid / 8 and tid / 8 + 32, columns 8 (tid % 8)
+  const int xr = tid >> 3, xc = (tid & 7) * 8;
+  const bool xok = n0 + xc < N;
+  // P piece: 64 tokens x R (<= 32) columns, 8 columns per thread
+  const int pcpr = (R + 7) / 8;                 // 8-wide chunks per token row
+  const int pr = tid / 4, pc = (tid % 4) * 8;   // 4 chunks per row slot (R <= 32)
+  const bool pok = pc < R;
+  f32x4 acc[NB];
+#pragma unroll
+  for (int t = 0; t < NB; ++t) acc[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  (void)pcpr;
+  uint4 vx0, vx1, vp;
+  auto load = [&](int64_t t0) {
+    const bool in = t0 < t_end;
+    const uint32_t ox0 = (uint32_t)(((t0 + xr) * ldx + n0 + xc) * 2);
+    const uint32_t ox1 = (uint32_t)(((t0 + xr + 32) * ldx + n0 + xc) * 2);
+    const uint32_t op = (uint32_t)(((t0 + pr) * ldp + pc) * 2);
+    auto v0 = __builtin_amdgcn_raw_buffer_load_b128(rx, (in && xok && t0 + xr < t_end) ? ox0 : kOOB, 0, 0);
+    auto v1 = __builtin_amdgcn_raw_buffer_load_b128(rx, (in && xok && t0 + xr + 32 < t_end) ? ox1 : kOOB, 0, 0);
+    auto v2 = __builtin_amdgcn_raw_buffer_load_b128(rp, (in && pok && t0 + pr < t_end) ? op : kOOB, 0, 0);
+    vx0 = __builtin_bit_cast(uint4, v0);
+    vx1 = __builtin_bit_cast(uint4, v1);
+    vp = __builtin_bit_cast(uint4, v2);
+  };
+  auto store = [&](int buf) {
+    *reinterpret_cast<uint4*>(&xs[buf][xr * kRedLdX + xc]) = vx0;
+    *reinterpret_cast<uint4*>(&xs[buf][(xr + 32) * kRedLdX + xc]) = vx1;
+    *reinterpret_cast<uint4*>(&ps[buf][pr * kRedLdP + pc]) = vp;
+  };
+  int buf = 0;
+  load(t_begin);
+  store(0);
+  __syncthreads();
+  for (int64_t t0 = t_begin; t0 < t_end; t0 += kRedTok) {
+    load(t0 + kRedTok);   // next piece in flight while this one is used
+#pragma unroll
+    for (int kk = 0; kk < kRedTok; kk += 32) {
+      const bf16x8 a = red_frag<kRedLdX>(xs[buf], kk, wave * 16, lane);
+#pragma unroll
+      for (int t = 0; t < NB; ++t) {
+        const bf16x8 b = red_frag<kRedLdP>(ps[buf], kk, t * 16, lane);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[t], 0, 0, 0);
+      }
+    }
+    buf ^= 1;
+    store(buf);           // the other buffer was last read before the previous barrier
+    __syncthreads();
+  }
+  float* w = ws + (int64_t)s * N * R;
+#pragma unroll
+  for (int t = 0; t < NB; ++t) {
+    const int col = t * 16 + (lane & 15);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t n = n0 + wave * 16 + 4 * (lane >> 4) + i;
+      if (n < N && col < R) w[n * R + col] = acc[t][i];
+    }
+  }
+}
+
+// out = bf16(alpha * sum_s ws[s][n][r]) at out[n * ldo + r] or, transposed,
+// out[r * ldo + n]; splits summed in order
+__global__ __launch_bounds__(256) void skinny_red_reduce_kernel(const float* __restrict__ ws,
+                                                                uint16_t* __restrict__ out,
+                                                                int64_t N, int R, int64_t ldo,
+                                                                int trans, int splits,
+                                                                float alpha) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= N * R) return;
+  // transposed output: consecutive threads take consecutive n of one r
+  const int64_t n = trans ? e % N : e / R;
+  const int64_t r = trans ? e / N : e % R;
+  float sum = 0.0f;
+  for (int sp = 0; sp < splits; ++sp) sum += ws[(int64_t)sp * N * R + n * R + r];
+  out[trans ? r * ldo + n : n * ldo + r] = (uint16_t)f32_to_bf16_bits(alpha * sum);
+}
+
+inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace skinny
+}  // namespace cpt
+
+using namespace cpt;
+using namespace cpt::skinny;
+
+extern "C" {
+
+int cpt_gemm_bf16_skinny(const void* a, int64_t lda, const void* q, int64_t ldq, void* c,
+                         int64_t ldc, int64_t M, int64_t R, int64_t K, float alpha, int splits,
+                         void* workspace, void* stream) {
+  if (M < 0 || R < 0 || K < 0 || splits < 1) return kErrShape;
+  if (R > 32) return kErrShape;
+  if (M == 0 || R == 0) return kOk;
+  if (!a || !q || !c || !al16(a) || !al16(q) || (lda & 7) || (ldq & 7) || (K & 7) || lda < K ||
+      ldq < K || ldc < R)
+    return kErrAlign;
+  // 32-bit buffer offsets: A spans M rows (plus a wavefront's overhang), Q 32
+  if ((M + kRowsPerBlock) * lda * 2 >= ((int64_t)1 << 31) || 32 * ldq * 2 >= ((int64_t)1 << 31))
+    return kErrTooLarge;
+  const int64_t kchunk = ((K + splits - 1) / splits + 31) / 32 * 32;
+  splits = (int)(kchunk > 0 ? (K + kchunk - 1) / kchunk : 1);
+  if (splits < 1) splits = 1;
+  if (splits > 1 && (!workspace || ((uintptr_t)workspace & 3))) return kErrAlign;
+  const int64_t blocks = (M + kRowsPerBlock - 1) / kRowsPerBlock;
+  if (blocks > 0x7FFFFFFF || splits > 65535) return kErrTooLarge;
+  hipStream_t st = (hipStream_t)stream;
+  float* ws = splits > 1 ? (float*)workspace : nullptr;
+  const dim3 grid((unsigned)blocks, (unsigned)splits);
+  if (R <= 16)
+    hipLaunchKernelGGL(skinny_proj_kernel<1>, grid, dim3(256), 0, st, (const uint16_t*)a, lda,
+                       (const uint16_t*)q, ldq, M, (int)R, K, kchunk, ws, (uint16_t*)c, ldc, alpha);
+  else
+    hipLaunchKernelGGL(skinny_proj_kernel<2>, grid, dim3(256), 0, st, (const uint16_t*)a, lda,
+                       (const uint16_t*)q, ldq, M, (int)R, K, kchunk, ws, (uint16_t*)c, ldc, alpha);
+  if (hipGetLastError() != hipSuccess) return kErrLaunch;
+  if (splits > 1) {
+    const int64_t total = M * R;
+    hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                       st, (const float*)ws, (uint16_t*)c, M, (int)R, ldc, splits, alpha);
+    if (hipGetLastError() != hipSuccess) return kErrLaunch;
+  }
+  return kOk;
+}
+
+int cpt_gemm_bf16_skinny_t(const void* x, int64_t ldx, const void* p, int64_t ldp, void* out,
+                           int64_t ldo, int out_trans, int64_t T, int64_t N, int64_t R,
+                           float alpha, int splits, void* workspace, void* stream) {
+  if (T < 0 || N < 0 || R < 0 || splits < 1) return kErrShape;
+  if (R > 32) return kErrShape;
+  if (N == 0 || R == 0) return kOk;
+  if (!x || !p || !out || !workspace || !al16(x) || !al16(p) || (ldx & 7) || (ldp & 7) ||
+      (N & 7) || (R & 7) || ldx < N || ldp < R || ldo < (out_trans ? N : R) ||
+      ((uintptr_t)workspace & 3))
+    return kErrAlign;
+  if ((T + kRedTok) * ldx * 2 >= ((int64_t)1 << 31) || (T + kRedTok) * ldp * 2 >= ((int64_t)1 << 31))
+    return kErrTooLarge;
+  const int64_t tchunk = ((T + splits - 1) / splits + kRedTok - 1) / kRedTok * kRedTok;
+  splits = (int)(tchunk > 0 ? (T + tchunk - 1) / tchunk : 1);
+  if (splits < 1) splits = 1;
+  const int64_t blocks = (N + kRedCols - 1) / kRedCols;
+  if (blocks > 0x7FFFFFFF || splits > 65535) return kErrTooLarge;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)blocks, (unsigned)splits);
+  if (R <= 16)
+    hipLaunchKernelGGL(skinny_red_kernel<1>, grid, dim3(256), 0, st, (const uint16_t*)x, ldx,
+                       (const uint16_t*)p, ldp, T, N, (int)R, tchunk, (float*)workspace);
+  else
+    hipLaunchKernelGGL(skinny_red_kernel<2>, grid, dim3(256), 0, st, (const uint16_t*)x, ldx,
+                       (const uint16_t*)p, ldp, T, N, (int)R, tchunk, (float*)workspace);
+  if (hipGetLastError() != hipSuccess) return kErrLaunch;
+  const int64_t total = N * R;
+  hipLaunchKernelGGL(skinny_red_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
+                     0, st, (const float*)workspace, (uint16_t*)out, N, (int)R, ldo,
+                     out_trans ? 1 : 0, splits, alpha);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+}  // extern "C"

@@ -116,12 +116,81 @@ def _lora_args(terms, n_q):
     return r, ldp, q_kmajor, ldq, out, keep
 
 
+SKINNY_MAX_RANK = 32
+
+
+def skinny(a: torch.Tensor, q: torch.Tensor, alpha: float = 1.0,
+           name: str = "gemm_skinny") -> torch.Tensor:
+    """bf16(alpha * a [M, K] @ q[R, K].T) for a rank R <= 32: the tall-skinny
+    adapter products (x A^T, grad_y B, ...), streamed once through HBM with K
+    split across blocks (fp32 partials summed in a fixed order)."""
+    _require_device(a, q)
+    _check_bf16(a, q)
+    M, K = a.shape
+    R = q.shape[0]
+    assert q.shape[1] == K and R <= SKINNY_MAX_RANK
+    if a.stride(1) != 1 or a.stride(0) % 8 or a.stride(0) < K or a.data_ptr() % 16:
+        a = a.contiguous()
+    if q.stride(1) != 1 or q.stride(0) % 8 or q.stride(0) < K or q.data_ptr() % 16:
+        q = q.contiguous()
+    # K ranges for ~512 blocks of 128 rows (each range >= 256 of K): more
+    # ranges cost more partials than they gain in parallelism (measured at
+    # M = 8192, K = 4096 / 11008: 3.6 / 4.9 TB/s)
+    blocks = (M + 127) // 128
+    splits = max(1, min(K // 256, (512 + blocks - 1) // blocks))
+    c = torch.empty((M, R), dtype=torch.bfloat16, device=a.device)
+    ws = (torch.empty((splits * M * R,), dtype=torch.float32, device=a.device)
+          if splits > 1 else None)
+    with _timed(name):
+        rc = _lib.lib().cpt_gemm_bf16_skinny(a.data_ptr(), a.stride(0), q.data_ptr(),
+                                             q.stride(0), c.data_ptr(), R, M, R, K, float(alpha),
+                                             splits, None if ws is None else ws.data_ptr(),
+                                             _stream(a))
+    check(rc, name)
+    return c
+
+
+def _row_major(t: torch.Tensor) -> bool:
+    return t.stride(1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0
+
+
+def skinny_t(x: torch.Tensor, p: torch.Tensor, alpha: float = 1.0, trans: bool = False,
+             name: str = "gemm_skinny_t") -> torch.Tensor:
+    """bf16(alpha * x[T, N].T @ p[T, R]) -> [N, R] (or its transpose [R, N]
+    with trans) for R <= 32: the adapter-factor gradients that reduce over
+    the tokens, x and p token-major."""
+    _require_device(x, p)
+    _check_bf16(x, p)
+    T, N = x.shape
+    R = p.shape[1]
+    assert p.shape[0] == T and R <= SKINNY_MAX_RANK
+    if not _row_major(x) or x.stride(0) < N:
+        x = x.contiguous()
+    if not _row_major(p) or p.stride(0) < R:
+        p = p.contiguous()
+    blocks = (N + 63) // 64
+    splits = max(1, min(max(T // 256, 1), (768 + blocks - 1) // blocks))
+    out = torch.empty((R, N) if trans else (N, R), dtype=torch.bfloat16, device=x.device)
+    ws = torch.empty((splits * N * R,), dtype=torch.float32, device=x.device)
+    with _timed(name):
+        rc = _lib.lib().cpt_gemm_bf16_skinny_t(x.data_ptr(), x.stride(0), p.data_ptr(),
+                                               p.stride(0), out.data_ptr(), out.stride(0),
+                                               1 if trans else 0, T, N, R, float(alpha), splits,
+                                               ws.data_ptr(), _stream(x))
+    check(rc, name)
+    return out
+
+
 def mm(a: torch.Tensor, b: torch.Tensor, name: str = "gemm") -> torch.Tensor:
-    """a [M, K] @ b [K, N] -> bf16 [M, N] on the MFMA engine.  Products with
-    too few 256x256 output tiles to fill the chip (the thin adapter products,
-    N or M = rank) split K across blocks instead."""
+    """a [M, K] @ b [K, N] -> bf16 [M, N] on the MFMA engine.  Tall products
+    with N <= 32 (the adapter terms' x A^T, grad_y B, ...) go to the skinny
+    kernel; other products with too few 256x256 output tiles to fill the chip
+    (N or M = rank) split K across blocks instead."""
     M, K = a.shape
     N = b.shape[1]
+    if (N <= SKINNY_MAX_RANK and K >= 256 and K % 8 == 0 and M >= 256
+            and a.stride(1) == 1):
+        return skinny(a, b.t(), 1.0, name)
     tiles = ((M + 255) // 256) * ((N + 255) // 256)
     if tiles < 128 and K >= 1024:
         return mm_splitk(a, b, 1.0, name=name)
@@ -310,12 +379,20 @@ def mm_splitk(a: torch.Tensor, b: torch.Tensor, alpha: float = 1.0, splits: int 
               name: str = "gemm_splitk") -> torch.Tensor:
     """bf16(alpha * (a @ b)) with the K reduction split across blocks (fp32
     partials, fixed-order sum): for the thin adapter gradients that reduce
-    over all tokens."""
+    over all tokens.  With a token-major operand on each side and M or N <=
+    32 (the rank: grad_A = s (grad B)^T x, grad_B = s grad_y^T (x A^T)) the
+    token-reduction kernel runs instead of 256 x 256 tiles."""
     _require_device(a, b)
     _check_bf16(a, b)
     M, K = a.shape
     K_, N = b.shape
     assert K == K_
+    at = a.t()
+    if splits is None and _row_major(at) and _row_major(b) and K >= 256:
+        if M <= SKINNY_MAX_RANK and M % 8 == 0 and N % 8 == 0:
+            return skinny_t(b, at, alpha, trans=True, name=name)
+        if N <= SKINNY_MAX_RANK and N % 8 == 0 and M % 8 == 0:
+            return skinny_t(at, b, alpha, trans=False, name=name)
     a, lda, ak = _layout_a(a)
     b, ldb, bk = _layout_b(b)
     if splits is None:

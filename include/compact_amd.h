@@ -144,6 +144,30 @@ int cpt_gemm_bf16(const void* a, int64_t lda, int a_kmajor, const void* b, int64
                   int b_kmajor, const void* a2, int64_t lda2, const void* b2, int64_t ldb2,
                   int64_t K2, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* Skinny product of the adapter terms: C[M, R] = bf16(alpha * A[M, K] . Q^T)
+ * with A [M][lda] and Q [R][ldq] both K-contiguous, R <= 32 (the rank), bf16
+ * in and out, fp32 accumulate.  Replaces the thin F.linear / @ of the LoRA
+ * terms (src/flashffn.py:1414,1420,1439: x A^T, h_mid A_d^T; :1521,1556-1557:
+ * grad_y B_d, grad_h_gate B_g, grad_h_up B_u).  HBM-bound: A is streamed once.
+ * K is split `splits` ways; with splits > 1 `workspace` holds splits * M * R
+ * floats and the partials are summed in split order (deterministic).
+ * Pointers 16-byte aligned, lda, ldq and K multiples of 8. */
+int cpt_gemm_bf16_skinny(const void* a, int64_t lda, const void* q, int64_t ldq, void* c,
+                         int64_t ldc, int64_t M, int64_t R, int64_t K, float alpha, int splits,
+                         void* workspace, void* stream);
+
+/* Token reduction of the adapter gradients: Z[N, R] = bf16(alpha * X^T . P)
+ * with X [T][ldx] and P [T][ldp] token-major, R <= 32, written to
+ * out[n * ldo + r] or, with out_trans, out[r * ldo + n] (Z^T).  Replaces the
+ * thin gradient GEMMs of the LoRA factors (src/flashffn.py:1538-1545,
+ * 1575-1582: grad_B = s grad_y^T (x A^T), grad_A = s (grad B)^T x).  The
+ * tokens are split `splits` ways; `workspace` holds splits * N * R floats and
+ * the partials are summed in split order (deterministic).  Pointers 16-byte
+ * aligned, ldx, ldp, N and R multiples of 8. */
+int cpt_gemm_bf16_skinny_t(const void* x, int64_t ldx, const void* p, int64_t ldp, void* out,
+                           int64_t ldo, int out_trans, int64_t T, int64_t N, int64_t R,
+                           float alpha, int splits, void* workspace, void* stream);
+
 /* Extended GEMM for the adapter (LoRA) terms, one operand pair:
  *   mode 0: C = bf16(A.B)
  *   mode 1: C = bf16(C + bf16(alpha * bf16(A.B)))   (PEFT's h + s * B(A(x)),

@@ -143,3 +143,65 @@ def test_c2_shapes_gemm_numerics(device):
     cols = torch.arange(0, d, 1009, device=device)
     ref2 = gy.float().t() @ y[:, cols].float()
     assert_gemm_close(dw[:, cols], ref2.cpu())
+
+
+@pytest.mark.parametrize("m,r,k", [(8192, 16, 4096), (8192, 16, 11008), (300, 8, 264),
+                                   (1000, 32, 1032), (257, 20, 4104), (64, 16, 256)])
+def test_skinny_matches_reference(device, m, r, k):
+    """The skinny adapter product (K split across blocks, fp32 partials in a
+    fixed order) against an fp32 product of the same bf16 operands; repeated
+    calls are bit-identical."""
+    _, G = _cpt()
+    a = rnd((m, k), 70, device)
+    q = rnd((r, k), 71, device, 0.05)
+    got = G.skinny(a, q, 2.0)
+    assert got.shape == (m, r)
+    rows = torch.arange(0, m, max(1, m // 64), device=device)
+    assert_gemm_close(got[rows], 2.0 * (a[rows].float().cpu() @ q.float().cpu().t()))
+    assert torch.equal(got.view(torch.int16), G.skinny(a, q, 2.0).view(torch.int16))
+
+
+def test_mm_routes_thin_products_to_skinny(device):
+    """mm() with N <= 32 on a row-major A gives the skinny kernel's result,
+    including a transposed [K, r] weight view (B = W^T of an [r, K] weight)
+    and a [K, r] B factor."""
+    _, G = _cpt()
+    x = rnd((2048, 4096), 72, device)
+    a_w = rnd((16, 4096), 73, device, 0.02)       # LoRA A [r, in]
+    b_w = rnd((4096, 16), 74, device, 0.02)       # LoRA B [out, r]
+    assert torch.equal(G.mm(x, a_w.t()).view(torch.int16), G.skinny(x, a_w).view(torch.int16))
+    got = G.mm(x, b_w)
+    assert torch.equal(got.view(torch.int16), G.skinny(x, b_w.t().contiguous()).view(torch.int16))
+    assert_gemm_close(got, ref_mm(x, b_w))
+
+
+@pytest.mark.parametrize("t,n,r", [(8192, 11008, 16), (8192, 4096, 16), (1000, 264, 8),
+                                   (300, 136, 32), (4097, 1024, 24)])
+@pytest.mark.parametrize("trans", [False, True])
+def test_skinny_t_matches_reference(device, t, n, r, trans):
+    """The token reduction of the adapter gradients, alpha * x^T p (or its
+    transpose), against an fp32 product of the same bf16 operands; repeated
+    calls are bit-identical."""
+    _, G = _cpt()
+    x = rnd((t, n), 80, device)
+    p = rnd((t, r), 81, device, 0.05)
+    got = G.skinny_t(x, p, 2.0, trans=trans)
+    assert got.shape == ((r, n) if trans else (n, r))
+    cols = torch.arange(0, n, max(1, n // 48), device=device)
+    ref = 2.0 * (x[:, cols].float().cpu().t() @ p.float().cpu())
+    sub = got[:, cols].t() if trans else got[cols]
+    assert_gemm_close(sub, ref)
+    assert torch.equal(got.view(torch.int16), G.skinny_t(x, p, 2.0, trans=trans).view(torch.int16))
+
+
+def test_mm_splitk_routes_adapter_gradients(device):
+    """mm_splitk on the two adapter-gradient patterns (s (gB)^T x and
+    s gy^T (xA)) gives the token-reduction kernel's result."""
+    _, G = _cpt()
+    x = rnd((2048, 1024), 82, device)
+    gb = rnd((2048, 16), 83, device, 0.1)
+    got = G.mm_splitk(gb.t(), x, 0.5)
+    assert torch.equal(got.view(torch.int16), G.skinny_t(x, gb, 0.5, trans=True).view(torch.int16))
+    got2 = G.mm_splitk(x.t(), gb, 0.5)
+    assert torch.equal(got2.view(torch.int16), G.skinny_t(x, gb, 0.5).view(torch.int16))
+    assert_gemm_close(got2, 0.5 * ref_mm(x.t(), gb))
