@@ -63,6 +63,7 @@ def algorithmic_work(n, h, d):
         "ffn_gate_up": (2 * gemm, "mfma"),          # x @ [Wg; Wu]^T (+ GLU + codec)
         "gemm_fwd_down": (gemm, "mfma"),            # h_mid @ Wd^T
         "ffn_down_dgrad": (gemm, "mfma"),           # gy @ Wd (+ dequant + SwiGLU bwd)
+        "gemm_dgrad_down": (gemm, "mfma"),          # gy @ Wd (K2 runs after it)
         "gemm_wgrad_down": (gemm, "mfma"),          # gy^T @ h_mid^
         "gemm_dgrad_x": (2 * gemm, "mfma"),         # dg @ Wg + du @ Wu
         "gemm_wgrad_gate": (gemm, "mfma"),          # dg^T @ x

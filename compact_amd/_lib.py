@@ -48,6 +48,8 @@ SIGNATURES = {
     "cpt_gemm_bf16_skinny": [_P, _L, _P, _L, _P, _L, _L, _L, _L, ctypes.c_float, _I, _P, _P],
     "cpt_gemm_bf16_skinny_t": [_P, _L, _P, _L, _P, _L, _I, _L, _L, _L, ctypes.c_float, _I, _P,
                                _P],
+    "cpt_ffn_down_dgrad_outlier": [_P, _P, _L, _L, _L, _I, _L, _P, _P, _P, _P, _P, _P, _P, _P,
+                                   _L, _P, _P, _P, _L, _L, _P, _P, ctypes.c_float, _P],
     "cpt_dora_scale": [_P, _P, _P, _L, _L, _I, _P, _P],
     "cpt_col_dot_div": [_P, _P, _P, _L, _L, _I, _P, _P, _P],
     "cpt_dora_col_norm": [_P, _P, _P, _L, _L, _L, ctypes.c_double, _I, _P, _P, _I, _P],

@@ -140,6 +140,13 @@ struct KArgs {
   uint16_t* grad_gate;     // B1 out
   uint16_t* grad_up;
   uint16_t* h_mid_hat;     // B1 out (may be null)
+  // B1 outlier channels (C3): columns with slot[d] >= 0 take the stored bf16
+  // value o[m * k_out + slot] after the dequantisation (slot_g null: none)
+  const int16_t* slot_g;
+  const int16_t* slot_u;
+  const uint16_t* o_g;
+  const uint16_t* o_u;
+  int64_t k_out;
   // low-rank adapter terms applied as the epilogue reads the accumulators
   // (acc_block); lrank == 0: none
   const uint16_t* lp[2];   // P_t [M, lrank], rows lldp apart (tokens x rank)
@@ -832,6 +839,22 @@ __device__ __forceinline__ void epi_dglu(const KArgs& A, const Acc& acc, int64_t
   const int cl = (tid & 31) * 8;
   const int64_t d = n0 + cl;           // D % 8 == 0: the 8 columns are all in or all out
   const bool dok = d < D;
+  // outlier channels among this thread's 8 columns (the same for every row)
+  int sg8[8], su8[8];
+  bool any_out = false;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) sg8[e] = su8[e] = -1;
+  if (CACHE != CACHE_BF16 && A.slot_g && dok) {
+    const uint4 wg = *reinterpret_cast<const uint4*>(A.slot_g + d);
+    const uint4 wu = *reinterpret_cast<const uint4*>(A.slot_u + d);
+    const uint32_t ag[4] = {wg.x, wg.y, wg.z, wg.w}, au[4] = {wu.x, wu.y, wu.z, wu.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sg8[e] = (int16_t)((ag[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+      su8[e] = (int16_t)((au[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+      any_out |= sg8[e] >= 0 || su8[e] >= 0;
+    }
+  }
   constexpr int UNROLL = 4;
 #pragma unroll 1
   for (int p0 = 0; p0 < 32; p0 += UNROLL) {
@@ -895,6 +918,15 @@ __device__ __forceinline__ void epi_dglu(const KArgs& A, const Acc& acc, int64_t
         for (int e = 0; e < 8; ++e) {
           hg[e] = round_bf16(((float)((cg[u].x >> (4 * e)) & 0xFu) - 8.0f) * sgv[u]);
           hu[e] = round_bf16(((float)((cu[u].x >> (4 * e)) & 0xFu) - 8.0f) * suv[u]);
+        }
+      }
+      if (CACHE != CACHE_BF16 && any_out) {
+        // outlier columns: the stored bf16 value replaces the dequantised one
+        // (HyC-LoRA's zero-and-overwrite, restored after the bf16 round trip)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (sg8[e] >= 0) hg[e] = bf16_to_f32(A.o_g[mrow[u] * A.k_out + sg8[e]]);
+          if (su8[e] >= 0) hu[e] = bf16_to_f32(A.o_u[mrow[u] * A.k_out + su8[e]]);
         }
       }
       float og[8], ou[8], oh[8];
@@ -1269,10 +1301,20 @@ int ffn_gate_up_impl(const void* x, const void* w_gate, const void* w_up, int64_
   }
 }
 
+// outlier channels of the B1 epilogue (k == 0: none)
+struct OutlierArgs {
+  const void* slot_gate = nullptr;
+  const void* o_gate = nullptr;
+  const void* slot_up = nullptr;
+  const void* o_up = nullptr;
+  int64_t k = 0;
+};
+
 int ffn_down_dgrad_impl(const void* grad_y, const void* w_down, int64_t n_tok, int64_t hidden,
                         int64_t inter, int cache, int64_t group_size, const void* c_gate,
                         const void* s_gate, const void* c_up, const void* s_up,
                         void* grad_h_gate, void* grad_h_up, void* h_mid_hat,
+                        const OutlierArgs& O,
                         const LoraTerms& L, void* stream) {
   if (n_tok < 0 || hidden < 0 || inter < 0) return kErrShape;
   if (cache != CACHE_BF16 && cache != CACHE_INT4 && cache != CACHE_INT8) return kErrBits;
@@ -1317,6 +1359,18 @@ int ffn_down_dgrad_impl(const void* grad_y, const void* w_down, int64_t n_tok, i
   A.grad_gate = (uint16_t*)grad_h_gate;
   A.grad_up = (uint16_t*)grad_h_up;
   A.h_mid_hat = (uint16_t*)h_mid_hat;
+  if (O.k > 0) {
+    if (!quant) return kErrShape;
+    if (!O.slot_gate || !O.slot_up || !O.o_gate || !O.o_up || !al16(O.slot_gate) ||
+        !al16(O.slot_up) || O.k >= 32768)
+      return kErrAlign;
+    if (n_tok * O.k >= ((int64_t)1 << 31)) return kErrTooLarge;
+    A.slot_g = (const int16_t*)O.slot_gate;
+    A.slot_u = (const int16_t*)O.slot_up;
+    A.o_g = (const uint16_t*)O.o_gate;
+    A.o_u = (const uint16_t*)O.o_up;
+    A.k_out = O.k;
+  }
   int terms = 0;
   if (const int rc = set_lora(A, L, n_tok, inter, terms)) return rc;
   if (terms > 1) return kErrShape;
@@ -1474,8 +1528,8 @@ int cpt_ffn_down_dgrad(const void* grad_y, const void* w_down, int64_t n_tok, in
                        const void* s_gate, const void* c_up, const void* s_up, void* grad_h_gate,
                        void* grad_h_up, void* h_mid_hat, void* stream) {
   return ffn_down_dgrad_impl(grad_y, w_down, n_tok, hidden, inter, cache, group_size, c_gate,
-                             s_gate, c_up, s_up, grad_h_gate, grad_h_up, h_mid_hat, LoraTerms{},
-                             stream);
+                             s_gate, c_up, s_up, grad_h_gate, grad_h_up, h_mid_hat, OutlierArgs{},
+                             LoraTerms{}, stream);
 }
 
 int cpt_ffn_down_dgrad_lora(const void* grad_y, const void* w_down, int64_t n_tok,
@@ -1489,7 +1543,28 @@ int cpt_ffn_down_dgrad_lora(const void* grad_y, const void* w_down, int64_t n_to
   L.rank = (int)rank; L.ldp = ldp; L.q_kmajor = 0; L.ldq = inter;
   L.p[0] = p; L.q[0] = a_down; L.alpha[0] = alpha;
   return ffn_down_dgrad_impl(grad_y, w_down, n_tok, hidden, inter, cache, group_size, c_gate,
-                             s_gate, c_up, s_up, grad_h_gate, grad_h_up, h_mid_hat, L, stream);
+                             s_gate, c_up, s_up, grad_h_gate, grad_h_up, h_mid_hat, OutlierArgs{},
+                             L, stream);
+}
+
+int cpt_ffn_down_dgrad_outlier(const void* grad_y, const void* w_down, int64_t n_tok,
+                               int64_t hidden, int64_t inter, int cache, int64_t group_size,
+                               const void* c_gate, const void* s_gate, const void* slot_gate,
+                               const void* o_gate, const void* c_up, const void* s_up,
+                               const void* slot_up, const void* o_up, int64_t k,
+                               void* grad_h_gate, void* grad_h_up, void* h_mid_hat,
+                               int64_t rank, int64_t ldp, const void* p, const void* a_down,
+                               float alpha, void* stream) {
+  if (k < 0 || rank < 0) return kErrShape;
+  OutlierArgs O;
+  O.slot_gate = slot_gate; O.o_gate = o_gate; O.slot_up = slot_up; O.o_up = o_up; O.k = k;
+  LoraTerms L;
+  if (rank > 0) {
+    L.rank = (int)rank; L.ldp = ldp; L.q_kmajor = 0; L.ldq = inter;
+    L.p[0] = p; L.q[0] = a_down; L.alpha[0] = alpha;
+  }
+  return ffn_down_dgrad_impl(grad_y, w_down, n_tok, hidden, inter, cache, group_size, c_gate,
+                             s_gate, c_up, s_up, grad_h_gate, grad_h_up, h_mid_hat, O, L, stream);
 }
 
 }  // extern "C"

@@ -42,6 +42,14 @@ def _bits(mode: str) -> int:
 _CACHE_CODE = {"int4": _lib.CACHE_INT4, "int8": _lib.CACHE_INT8, "bf16": _lib.CACHE_BF16,
                "recompute": _lib.CACHE_NONE}
 _FUSED_GROUPS = (32, 64, 128)
+# Group sizes whose dequantise + SwiGLU backward runs in the dgrad GEMM's
+# epilogue (G.ffn_down_dgrad) instead of the dgrad GEMM followed by the K2
+# kernel.  Empty: on MI355X the fused epilogue (VALU work and 540 MB of writes
+# while the block's MFMAs idle, one wavefront per SIMD) costs more than the
+# standalone K2 at full occupancy: C2 step 5.84 -> 5.77 ms, C3 4.83 -> 4.69 ms
+# unfused.  The fused kernel stays available and tested; add group sizes here
+# to route the Function through it.
+_FUSED_DGRAD_GROUPS = ()
 
 
 def _mfma(*ts) -> bool:
@@ -245,7 +253,9 @@ class FlashFFNv3Function(torch.autograd.Function):
         need_recon = need_gate_path or need_h_mid
         use_k2 = mode in ("int4", "int8") and ctx.use_triton and need_gate_path
         lora_d = _lora_ok((a_down, b_down))
-        fusable = _mfma(gy, w_down) and lora_d and gy.shape[0] > 0 and not outl
+        # the fused dgrad kernel restores outlier channels only for the
+        # quantised caches (K2's path); bf16 / recompute caches carry none
+        fusable = _mfma(gy, w_down) and lora_d and gy.shape[0] > 0 and (use_k2 or not outl)
         fusable_gu = (_mfma(x_2d, w_gate, w_up) and _lora_ok((a_gate, b_gate), (a_up, b_up))
                       and x_2d.shape[0] > 0)
 
@@ -284,11 +294,12 @@ class FlashFFNv3Function(torch.autograd.Function):
         dlora = (gyB_d, a_down, s_down) if (a_down is not None and lora_d) else None
         grad_h_gate = grad_h_up = h_mid_hat = None
         if need_gate_path:
-            if use_k2 and fusable and gs in _FUSED_GROUPS:                # :1525-1533
+            if use_k2 and fusable and gs in _FUSED_DGRAD_GROUPS:          # :1525-1533
                 # dgrad GEMM with dequantise + SwiGLU backward in its epilogue
                 grad_h_gate, grad_h_up, h_mid_hat = G.ffn_down_dgrad(
                     gy, w_down, _CACHE_CODE[mode], gs, c_gate, qs_gate, c_up, qs_up,
-                    need_h_mid, lora=dlora)
+                    need_h_mid, lora=dlora,
+                    outliers=(slot_gate, o_gate, slot_up, o_up) if outl else None)
                 _V3_COUNTERS["triton_dequant_bwd"] += 1
             elif (not use_k2) and fusable and hg is not None and _mfma(hg, hu):
                 grad_h_gate, grad_h_up, h_mid_hat = G.ffn_down_dgrad(
@@ -714,7 +725,7 @@ class FlashFFNv3AdapterFunction(torch.autograd.Function):
 
         grad_h_gate = grad_h_up = h_mid_hat = None
         if need_gate_path:
-            if use_k2 and fusable_d and gs in _FUSED_GROUPS:                    # :2101-2110
+            if use_k2 and fusable_d and gs in _FUSED_DGRAD_GROUPS:              # :2101-2110
                 grad_h_gate, grad_h_up, h_mid_hat = G.ffn_down_dgrad(
                     g_eff_y, w_down, _CACHE_CODE[mode], gs, cq_gate, qs_gate, cq_up, qs_up,
                     need_h_mid)

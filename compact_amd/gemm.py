@@ -317,11 +317,13 @@ def ffn_gate_up(x, w_gate, w_up, cache: int, group_size: int, want_h_mid: bool =
 
 
 def ffn_down_dgrad(grad_y, w_down, cache: int, group_size: int, c_gate, s_gate, c_up, s_up,
-                   want_h_mid: bool, lora=None):
+                   want_h_mid: bool, lora=None, outliers=None):
     """Fused grad_y @ w_down + dequantise + SwiGLU backward.
     Returns (grad_h_gate, grad_h_up, h_mid_hat | None).  lora = (gy B_d
     [n, r], A_d [r, inter], s): the down projection's LoRA term of
-    grad_h_mid."""
+    grad_h_mid.  outliers = (slot_gate, o_gate, slot_up, o_up): the C3
+    outlier channels (int16 slot maps [inter], bf16 blocks [n, k]) that
+    replace their dequantised columns."""
     _require_device(grad_y, w_down)
     _check_bf16(grad_y, w_down)
     n, hdim = grad_y.shape
@@ -333,10 +335,31 @@ def ffn_down_dgrad(grad_y, w_down, cache: int, group_size: int, c_gate, s_gate, 
     du = torch.empty((n, d), dtype=torch.bfloat16, device=dev)
     hm = torch.empty((n, d), dtype=torch.bfloat16, device=dev) if want_h_mid else None
 
-    def p(t):
-        return None if t is None else t.contiguous().data_ptr()
+    keep_in = [None if t is None else t.contiguous() for t in (c_gate, s_gate, c_up, s_up)]
+    c_gate, s_gate, c_up, s_up = keep_in
 
-    if lora is not None:
+    def p(t):
+        return None if t is None else t.data_ptr()
+
+    if outliers is not None:
+        slot_g, o_g, slot_u, o_u = [t.contiguous() for t in outliers]
+        k = o_g.shape[1]
+        assert o_u.shape[1] == k and slot_g.numel() == d and slot_u.numel() == d
+        rank, ldp, pp, qq, alpha, keep = 0, 0, None, None, 0.0, []
+        if lora is not None:
+            gyb, a_down, s = lora
+            a_down = a_down.contiguous()
+            rank, ldp, qk, ldq, t, keep = _lora_args([(gyb, a_down, s)], d)
+            assert qk == 0 and ldq == d
+            pp, qq, alpha = t[0]
+        with _timed("ffn_down_dgrad"):
+            rc = _lib.lib().cpt_ffn_down_dgrad_outlier(
+                grad_y.data_ptr(), w_down.data_ptr(), n, hdim, d, cache, group_size, p(c_gate),
+                p(s_gate), slot_g.data_ptr(), o_g.data_ptr(), p(c_up), p(s_up),
+                slot_u.data_ptr(), o_u.data_ptr(), k, dg.data_ptr(), du.data_ptr(), p(hm),
+                rank, ldp, pp, qq, alpha, _stream(grad_y))
+        del keep
+    elif lora is not None:
         gyb, a_down, s = lora
         a_down = a_down.contiguous()          # [r, inter] rows: the MN-major factor
         r, ldp, qk, ldq, t, keep = _lora_args([(gyb, a_down, s)], d)

@@ -249,6 +249,22 @@ int cpt_ffn_down_dgrad_lora(const void* grad_y, const void* w_down, int64_t n_to
                             void* h_mid_hat, int64_t rank, int64_t ldp, const void* p,
                             const void* a_down, float alpha, void* stream);
 
+/* cpt_ffn_down_dgrad (optionally with the LoRA term of cpt_ffn_down_dgrad_lora:
+ * rank 0 = none) for an int4/int8 cache with outlier channels (config C3;
+ * HyC-LoRA's zero-and-overwrite on the v3 codec, hyclora/operators/
+ * compress_function.py:147-174): columns with slot_gate[d] >= 0 take
+ * o_gate[m * k + slot] (bf16 [n_tok, k]) in place of their dequantised value,
+ * likewise for up, before the SwiGLU backward.  Bit-equal to the dgrad GEMM
+ * followed by cpt_dequant_swiglu_backward_outlier. */
+int cpt_ffn_down_dgrad_outlier(const void* grad_y, const void* w_down, int64_t n_tok,
+                               int64_t hidden, int64_t inter, int cache, int64_t group_size,
+                               const void* c_gate, const void* s_gate, const void* slot_gate,
+                               const void* o_gate, const void* c_up, const void* s_up,
+                               const void* slot_up, const void* o_up, int64_t k,
+                               void* grad_h_gate, void* grad_h_up, void* h_mid_hat,
+                               int64_t rank, int64_t ldp, const void* p, const void* a_down,
+                               float alpha, void* stream);
+
 /* ---------------- adapter families (DoRA magnitude) ---------------- */
 /* VeRA, AdaLoRA and DyLoRA reach the kernels above as composed or sliced thin
  * factors (src/flashffn.py:1850-1921); DoRA's per-output-channel magnitude

@@ -97,6 +97,42 @@ def test_outlier_k1_k2_equal_standalone(device, bits, group):
         assert torch.equal(x.view(torch.int16), y.view(torch.int16))
 
 
+@pytest.mark.parametrize("bits,group", [(4, 64), (8, 128)])
+@pytest.mark.parametrize("with_lora", [False, True])
+@pytest.mark.parametrize("want_h_mid", [True, False])
+def test_outlier_fused_dgrad_equals_unfused(device, bits, group, with_lora, want_h_mid):
+    """The dgrad GEMM with dequantise + outlier restore + SwiGLU backward in
+    its epilogue equals the GEMM (with the down projection's LoRA term) and
+    the standalone outlier K2, bit for bit."""
+    cpt, G = _cpt()
+    n, hdim, d = 384, 256, 1024
+    a, b = _hot(n, d, 11)
+    ga, gb = a.to(device), b.to(device)
+    k = int(d * 0.01)
+    sg_, _ = cpt.outlier_select(ga, k)
+    su_, _ = cpt.outlier_select(gb, k)
+    _, qg, sg, og, qu, su, ou = cpt.silu_mul_quant_outlier(ga, gb, bits, group, sg_, su_, k)
+    gen = torch.Generator(device=device).manual_seed(12)
+    gy = torch.randn(n, hdim, device=device, generator=gen).to(torch.bfloat16)
+    wd = (torch.randn(hdim, d, device=device, generator=gen) * 0.05).to(torch.bfloat16)
+    lora = None
+    if with_lora:
+        gyb = (torch.randn(n, 16, device=device, generator=gen) * 0.1).to(torch.bfloat16)
+        a_d = (torch.randn(16, d, device=device, generator=gen) * 0.05).to(torch.bfloat16)
+        lora = (gyb, a_d, 2.0)
+    dg, du, hm = G.ffn_down_dgrad(gy, wd, bits, group, qg, sg, qu, su, want_h_mid, lora=lora,
+                                  outliers=(sg_, og, su_, ou))
+    gmid = G.mm2(gy, wd, lora=[lora]) if with_lora else G.mm(gy, wd)
+    rdg, rdu, rhm = cpt.dequant_swiglu_backward_outlier(gmid, qg, sg, og, sg_, qu, su, ou, su_,
+                                                        bits, group, want_h_mid=want_h_mid)
+    assert torch.equal(dg.view(torch.int16), rdg.view(torch.int16))
+    assert torch.equal(du.view(torch.int16), rdu.view(torch.int16))
+    if want_h_mid:
+        assert torch.equal(hm.view(torch.int16), rhm.view(torch.int16))
+    else:
+        assert hm is None
+
+
 def _close(got, ref):
     got = got.float().cpu()
     tol = 1e-2 * ref.abs() + 1e-3 * ref.abs().max()
