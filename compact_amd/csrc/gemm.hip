@@ -273,10 +273,12 @@ struct Frags {
 // MFMA fragment of an MN-major tile: 8 consecutive k (sub-step s, lane half)
 // of mn row rowbase + lane % 32, as two transpose reads of 4 k each.
 __device__ __forceinline__ bf16x8 frag_mn(const uint16_t* t, int rowbase, int s, int lane) {
-  const int k = s * 16 + 8 * (lane >> 5) + ((lane & 15) >> 2);
-  const int mn = rowbase + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  const i16x4 lo = lds_read_tr(t + lds_mn(k, mn));
-  const i16x4 hi = lds_read_tr(t + lds_mn(k + 4, mn));
+  // lds_mn(k, mn) is affine in s and rowbase: one lane base, the rest immediates
+  const int lane_ofs = lds_mn(8 * (lane >> 5) + ((lane & 15) >> 2),
+                              16 * ((lane >> 4) & 1) + 4 * (lane & 3));
+  const uint16_t* p = t + lane_ofs + s * 16 * LDM + rowbase;
+  const i16x4 lo = lds_read_tr(p);
+  const i16x4 hi = lds_read_tr(p + 4 * LDM);
   return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
@@ -285,18 +287,22 @@ __device__ __forceinline__ void read_frags(const uint16_t* stage_base, int wn, i
                                            int s, Frags& f) {
   const uint16_t* sa = stage_base;
   const uint16_t* sb = stage_base + TILE_ELEMS;
-  const int chunk = s * 2 + (lane >> 5);
+  // K-major fragment (row R0 + 32 i, chunk 2 s + lane / 32) sits at
+  // lds_off(R0, lane / 32) + 2176 i + 16 s: one lane base, the rest immediates
+  constexpr int kRowBlk = 32 * 64 + 16 * 8;   // lds_off step of 32 rows
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if (BKM)
-      f.n[i] = *reinterpret_cast<const bf16x8*>(sb + lds_off(wn * 128 + i * 32 + (lane & 31), chunk));
+      f.n[i] = *reinterpret_cast<const bf16x8*>(
+          sb + lds_off(wn * 128 + (lane & 31), lane >> 5) + i * kRowBlk + s * 16);
     else
       f.n[i] = frag_mn(sb, wn * 128 + i * 32, s, lane);
   }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     if (AKM)
-      f.m[j] = *reinterpret_cast<const bf16x8*>(sa + lds_off(wm * 128 + j * 32 + (lane & 31), chunk));
+      f.m[j] = *reinterpret_cast<const bf16x8*>(
+          sa + lds_off(wm * 128 + (lane & 31), lane >> 5) + j * kRowBlk + s * 16);
     else
       f.m[j] = frag_mn(sa, wm * 128 + j * 32, s, lane);
   }
@@ -379,21 +385,23 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
     const __amdgpu_buffer_rsrc_t r = (DUAL && ((it >> 1) & 1)) ? L.rup : T.rb;
     return bload(r, L.ob[it] + T.db);
   };
+  const int wofs = lds_off(tid >> 3, tid & 7);
   // group g of tile kt: store the held registers into `stage`, reload them with tile T
   auto group = [&](int g, int stage, const TileLd& T) {
     uint16_t* sa = lds + stage * 2 * TILE_ELEMS;
     uint16_t* sb = sa + TILE_ELEMS;
+    // K-major chunk q = tid + 256 it sits at lds_off(tid / 8, tid % 8) + 2176 it
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int it = 2 * g + h, q = tid + NTHR * it;
-      if (AK) *reinterpret_cast<uint4*>(sa + lds_off(q >> 3, q & 7)) = va[it];
+      const int it = 2 * g + h;
+      if (AK) *reinterpret_cast<uint4*>(sa + wofs + it * 2176) = va[it];
       else sstore_mn_row(sa, tid, it, va[it]);
       va[it] = ldA(T, it);
     }
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const int it = 2 * g + h, q = tid + NTHR * it;
-      if (BK_) *reinterpret_cast<uint4*>(sb + lds_off(q >> 3, q & 7)) = vb[it];
+      const int it = 2 * g + h;
+      if (BK_) *reinterpret_cast<uint4*>(sb + wofs + it * 2176) = vb[it];
       else sstore_mn_row(sb, tid, it, vb[it]);
       vb[it] = ldB(T, it);
     }
