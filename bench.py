@@ -32,6 +32,9 @@ WORKLOADS = {
     "c2": dict(group=128, bits=8, mode="int8", lora_rank=0, outlier_ratio=0.0,
                desc="C2: SwiGLU FFN fwd+bwd, d_model=4096, d_ff=11008, 8x1024 tokens, bf16, "
                     "int8 per-group(128) cache, full-FT"),
+    "c2f": dict(group=128, bits=8, mode="int8", lora_rank=0, outlier_ratio=0.0, frozen=True,
+                desc="C2 frozen: C2 with the weights frozen and no adapter (grad_x only), the "
+                     "frozen-weight variant of C2"),
     "c3": dict(group=64, bits=4, mode="int4", lora_rank=16, outlier_ratio=0.01,
                desc="C3: C2 + LoRA r16 (alpha 32) on gate/up/down, frozen base, int4 "
                     "per-group(64) cache with top-1% outlier channels in bf16"),
@@ -124,12 +127,13 @@ def cpu_baseline(budget_tokens=512):
             "median_s": med}
 
 
-def library_arm(x, gy, wg, wu, wd, steps, warmup):
+def library_arm(x, gy, wg, wu, wd, steps, warmup, frozen=False):
     """The same C2 step in the reference's structure (src/flashffn.py:1409-1587)
     with every GEMM through torch.matmul (hipBLASLt on ROCm) and the codec as the
     standalone K1 / K2 kernels of this build: what the reference's composition
-    of library GEMMs and separate codec kernels gives on this GPU.  Returns
-    ms per step (HIP events around `steps` steps, mean)."""
+    of library GEMMs and separate codec kernels gives on this GPU.  `frozen`
+    drops the weight gradients and K2's h_mid^ (only grad_x is needed).
+    Returns ms per step (HIP events around `steps` steps, mean)."""
     import torch
     from compact_amd import kernels as K
 
@@ -142,11 +146,13 @@ def library_arm(x, gy, wg, wu, wd, steps, warmup):
         del h_mid, y
         ghm = gy @ wd
         dg, du, hmh = K.dequant_swiglu_backward(ghm, cg, sg, cu, su, BITS, GROUP,
-                                                want_h_mid=True)
+                                                want_h_mid=not frozen)
         del ghm
-        gwd = gy.t() @ hmh
         gx = dg @ wg
         gx = gx + du @ wu
+        if frozen:
+            return (gx,)
+        gwd = gy.t() @ hmh
         gwg = dg.t() @ x
         gwu = du.t() @ x
         return gx, gwg, gwu, gwd
@@ -313,7 +319,8 @@ def main():
     g = torch.Generator(device=dev).manual_seed(0)
     x = torch.randn(n, h, device=dev, generator=g).to(torch.bfloat16)
     gy = torch.randn(n, h, device=dev, generator=g).to(torch.bfloat16)
-    full_ft = wl["lora_rank"] == 0
+    frozen = wl.get("frozen", False)
+    full_ft = wl["lora_rank"] == 0 and not frozen
     wg = (torch.randn(d, h, device=dev, generator=g) * 0.02).to(torch.bfloat16)
     wu = (torch.randn(d, h, device=dev, generator=g) * 0.02).to(torch.bfloat16)
     wd = (torch.randn(h, d, device=dev, generator=g) * 0.02).to(torch.bfloat16)
@@ -322,6 +329,8 @@ def main():
     scale = 0.0
     if full_ft:
         params = tuple(w.requires_grad_() for w in (wg, wu, wd))
+    elif frozen:
+        params = ()
     else:
         # LoRA r16, alpha 32: A ~ kaiming-uniform(a=sqrt(5)) (bound 1/sqrt(in)), B ~ N(0, 0.01)
         r = wl["lora_rank"]
@@ -415,7 +424,7 @@ def main():
                     "traffic": measured_traffic(dom, args.workload),
                     "algorithmic_flops": amount}
     flops = gemm_flops_fwd_bwd(n, h, d, full_ft)
-    if not full_ft:   # thin adapter GEMMs: 18 * N * r * (H + D)
+    if wl["lora_rank"]:   # thin adapter GEMMs: 18 * N * r * (H + D)
         flops += 18 * n * wl["lora_rank"] * (h + d)
     out = {
         "metric": "FFN fwd+bwd tokens/sec + saved-activation MB, Llama-7B FFN shape, 1 MI355X",
@@ -424,16 +433,17 @@ def main():
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seed 0, X~N(0,1), W~N(0,0.02))",
         "config": {"workload": wl["desc"], "tokens": n, "d_model": h, "d_ff": d,
                    "cache_mode": MODE, "group_size": GROUP, "lora_rank": wl["lora_rank"],
-                   "outlier_ratio": wl["outlier_ratio"], "parallelism": "none (1 GPU)"},
+                   "outlier_ratio": wl["outlier_ratio"], "frozen_base": not full_ft,
+                   "parallelism": "none (1 GPU)"},
         "saved_activation_mb": sb / 1e6,
         "step_tflops": flops / (ms * 1e-3) / 1e12,
         "step_frac_mfma_bf16": flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
         "roofline": roofline,
         "kernels": kernels,
     }
-    if full_ft and not args.no_library_arm:
+    if (full_ft or frozen) and not args.no_library_arm:
         lib_ms = library_arm(x.detach(), gy, wg.detach(), wu.detach(), wd.detach(),
-                             args.steps, args.warmup)
+                             args.steps, args.warmup, frozen)
         out["library_arm"] = {
             "ms_per_step": lib_ms, "tokens_per_s": n / (lib_ms * 1e-3),
             "speedup_of_this_build": lib_ms / ms,
