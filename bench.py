@@ -316,6 +316,7 @@ def main():
 
     dev = torch.device("cuda:0")
     n, h, d = args.tokens, HID, INTER
+    batch = 8 if n % 8 == 0 else 1          # 8 sequences of 1024 tokens at the default size
     g = torch.Generator(device=dev).manual_seed(0)
     x = torch.randn(n, h, device=dev, generator=g).to(torch.bfloat16)
     gy = torch.randn(n, h, device=dev, generator=g).to(torch.bfloat16)
@@ -344,16 +345,18 @@ def main():
         params = tuple(lora.values())
 
     def fwd():
+        # [batch, seq, H] as a LlamaMLP receives it: the first sequence ranks
+        # the C3 outlier channels (HyC-LoRA's x_[0] statistics)
         return cpt.FlashFFNv3Function.apply(
-            x, wg, lora.get("a_gate"), lora.get("b_gate"), wu, lora.get("a_up"),
-            lora.get("b_up"), wd, lora.get("a_down"), lora.get("b_down"),
+            x.view(batch, n // batch, h), wg, lora.get("a_gate"), lora.get("b_gate"),
+            wu, lora.get("a_up"), lora.get("b_up"), wd, lora.get("a_down"), lora.get("b_down"),
             scale, scale, scale, MODE, GROUP, True, wl["outlier_ratio"])
 
     def step():
         for p in params + (x,):
             p.grad = None
         y = fwd()
-        y.backward(gy)
+        y.backward(gy.view_as(y))
 
     if args.probe:
         # calibration: torch's copy kernel reads and writes exactly PROBE_COPY_BYTES
@@ -431,7 +434,8 @@ def main():
         "value": n / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seed 0, X~N(0,1), W~N(0,0.02))",
-        "config": {"workload": wl["desc"], "tokens": n, "d_model": h, "d_ff": d,
+        "config": {"workload": wl["desc"], "tokens": n, "batch": batch, "seq_len": n // batch,
+                   "d_model": h, "d_ff": d,
                    "cache_mode": MODE, "group_size": GROUP, "lora_rank": wl["lora_rank"],
                    "outlier_ratio": wl["outlier_ratio"], "frozen_base": not full_ft,
                    "parallelism": "none (1 GPU)"},

@@ -542,8 +542,9 @@ inline int glu_dispatch(int op, int dt, const void* a, const void* g, const void
 }
 
 // ---------------------------------------------------------------------------
-// outlier channel selection: the k columns with the largest L2 norm over all
-// rows (HyC-LoRA's get_statistics_channel_base, compress_function.py:80-88),
+// outlier channel selection: the k columns with the largest L2 norm over the
+// rows given (the caller passes the first sample's rows, as HyC-LoRA's
+// get_statistics_channel_base ranks x_[0], compress_function.py:80-88),
 // ties to the lower column index, slots in ascending column order.
 // Deterministic: fp64 sums in a fixed order.
 // ---------------------------------------------------------------------------
@@ -563,8 +564,7 @@ __global__ __launch_bounds__(64) void colsumsq_partial_kernel(
   double acc[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) acc[e] = 0.0;
-  for (int64_t r = r0; r < r1; ++r) {
-    float v[8];
+  auto load = [&](int64_t r, float (&v)[8]) {
     if constexpr (DT == kF32) {
       const float4* p = reinterpret_cast<const float4*>(reinterpret_cast<const float*>(t) + r * d + col);
       const float4 a = p[0], b = p[1];
@@ -572,6 +572,22 @@ __global__ __launch_bounds__(64) void colsumsq_partial_kernel(
     } else {
       Vec8<DT>::ld(reinterpret_cast<const typename E::T*>(t) + r * d + col, 0, v);
     }
+  };
+  // 8 rows' loads in flight before their (row-ordered) accumulation
+  constexpr int kU = 8;
+  int64_t r = r0;
+  for (; r + kU <= r1; r += kU) {
+    float v[kU][8];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) load(r + u, v[u]);
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += (double)v[u][e] * (double)v[u][e];
+  }
+  for (; r < r1; ++r) {
+    float v[8];
+    load(r, v);
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[e] += (double)v[e] * (double)v[e];
   }
@@ -623,7 +639,7 @@ __global__ __launch_bounds__(kPickThreads) void outlier_pick_kernel(const double
   }
   __shared__ int hist[256];
   __shared__ unsigned long long sh_prefix;
-  __shared__ int sh_rem;
+  __shared__ int sh_rem, sh_done;
   __shared__ int sh_cnt[kPickWaves][2];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -679,6 +695,9 @@ __global__ __launch_bounds__(kPickThreads) void outlier_pick_kernel(const double
             if (before + c[q] >= remaining) {
               sh_prefix = prefix | ((unsigned long long)(255 - 4 * lane - q) << shift);
               sh_rem = remaining - before;
+              // the digit's whole bucket is needed: every key in it is
+              // picked, so the lower bytes need not be resolved
+              sh_done = before + c[q] == remaining;
               break;
             }
             before += c[q];
@@ -688,10 +707,17 @@ __global__ __launch_bounds__(kPickThreads) void outlier_pick_kernel(const double
       __syncthreads();
       prefix = sh_prefix;
       remaining = sh_rem;
+      const int done = sh_done;
       mask |= 0xFFull << shift;
       __syncthreads();
+      if (done) break;
     }
   }
+  // thr: the k-th largest key, or (early exit) the bucket's prefix with the
+  // unresolved low bytes zero.  Keys above thr are picked, and the first
+  // need_eq keys equal to it in column order; after an early exit every key
+  // of the bucket is > thr or == thr and need_eq covers them all, so the
+  // pick is the same k columns.
   const unsigned long long thr = prefix;
   const int need_eq = remaining;
   const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));

@@ -99,6 +99,20 @@ def _lora_ok(*pairs) -> bool:
             and all(_mfma(a, b) for a, b in pairs if a is not None))
 
 
+def outlier_stat_rows(shape) -> int:
+    """Rows of the [N, D] activations whose column norms pick the outlier
+    channels.  HyC-LoRA takes the norm over the first sample,
+    `x_[0].abs().norm(dim=-2)` on a [B, S, D] tensor
+    (src/hyclora/operators/compress_function.py:85): the first N / B rows for
+    an input of 3 or more dims.  A 2-D input [N, D] is one sample: all rows."""
+    n = 1
+    for s in shape[:-1]:
+        n *= int(s)
+    if len(shape) >= 3 and int(shape[0]) > 0:
+        return n // int(shape[0])
+    return n
+
+
 def _proj(x_2d, w, a, b, s, name):
     """out = x W^T (+ s * (x A^T) B^T) in PEFT op order (src/flashffn.py:1410-1420).
     Returns (out, xA | None)."""
@@ -185,8 +199,9 @@ class FlashFFNv3Function(torch.autograd.Function):
                 h_gate, xa_g = _proj(x_2d, w_gate, a_gate, b_gate, s_gate, "gemm_fwd_gate")
                 h_up, xa_u = _proj(x_2d, w_up, a_up, b_up, s_up, "gemm_fwd_up")
             if k_out > 0:
-                slot_gate, _ = K.outlier_select(h_gate, k_out)
-                slot_up, _ = K.outlier_select(h_up, k_out)
+                rows = outlier_stat_rows(orig_shape)
+                slot_gate, _ = K.outlier_select(h_gate, k_out, rows)
+                slot_up, _ = K.outlier_select(h_up, k_out, rows)
             if fused_quant and k_out > 0:
                 h_mid, c_gate, qs_gate, o_gate, c_up, qs_up, o_up = K.silu_mul_quant_outlier(
                     h_gate, h_up, _bits(cache_mode), group_size, slot_gate, slot_up, k_out)

@@ -305,13 +305,19 @@ triton_dequant_swiglu_backward = dequant_swiglu_backward
 # hyclora/operators/compress_function.py:80-174)
 # ---------------------------------------------------------------------------
 
-def outlier_select(t: torch.Tensor, k: int):
-    """The k columns of t [N, D] with the largest L2 norm over all rows (ties to
-    the lower column).  Returns (slot int16 [D]: -1 or the column's position
-    among the selected in ascending order, idx int32 [k] ascending)."""
+def outlier_select(t: torch.Tensor, k: int, rows: int | None = None):
+    """The k columns of t [N, D] with the largest L2 norm over the first `rows`
+    rows (all rows when None; ties to the lower column).  HyC-LoRA takes the
+    norm over the first sample's tokens, `x_[0].abs().norm(dim=-2)`
+    (src/hyclora/operators/compress_function.py:85-86): pass that sample's
+    row count.  Returns (slot int16 [D]: -1 or the column's position among the
+    selected in ascending order, idx int32 [k] ascending)."""
     _require_device(t)
     t = t.contiguous()
     n, d = t.shape
+    if rows is not None:
+        assert 0 <= rows <= n, f"rows={rows} outside [0, {n}]"
+        n = rows
     dev = t.device
     chunks = max(1, (n + 63) // 64)            # 64-row fp64 partial sums
     partial = torch.empty((chunks, d), dtype=torch.float64, device=dev)

@@ -98,8 +98,10 @@ int cpt_dequant_swiglu_backward(const void* grad_h_mid, const void* q_gate, cons
  * aligned rows. */
 
 /* Select the k outlier columns of t [n, d]: fp64 column sums of squares in a
- * fixed order (partial: fp64 [ceil(n/256), d]; sumsq: fp64 [d]), rank with
- * ties to the lower column, write slot [d] and idx int32 [k] (ascending). */
+ * fixed order (partial: fp64 [ceil(n/64), d]; sumsq: fp64 [d]), rank with
+ * ties to the lower column, write slot [d] and idx int32 [k] (ascending).
+ * n is the number of leading rows that rank the channels: HyC-LoRA ranks on
+ * the first sample, x_[0] of a [B, S, d] tensor (S rows). */
 int cpt_outlier_select(const void* t, int dtype, int64_t n, int64_t d, int64_t k,
                        void* partial, void* sumsq, void* slot, void* idx, void* stream);
 

@@ -219,17 +219,21 @@ def dequant_swiglu_backward(gmid: np.ndarray, qg, sg, qu, su, bits: int,
 # ---------------------------------------------------------------------------
 
 
-def outlier_channels(h: np.ndarray, ratio: float) -> np.ndarray:
+def outlier_channels(h: np.ndarray, ratio: float, rows: int | None = None) -> np.ndarray:
     """Channel selection after HyC-LoRA's `get_statistics_channel_base`
     (hyclora/operators/compress_function.py:80-88): the int(D*ratio) channels
-    with the largest L2 norm over tokens.  Spec of this build: the norm is
-    taken over all N rows in float64; ties go to the lower channel index; the
-    result is sorted ascending (slot i of the outlier buffer holds channel
-    idx[i])."""
+    with the largest L2 norm over the first sample's tokens,
+    `x_[0].abs().norm(dim=-2)` (:85).  h is the [N, D] matrix; `rows` is the
+    first sample's row count (None: all rows, a 2-D input being one sample).
+    Spec of this build where HyC-LoRA leaves it open: the norm is taken in
+    float64; ties go to the lower channel index; the result is sorted
+    ascending (slot i of the outlier buffer holds channel idx[i])."""
     h = np.asarray(h, dtype=np.float64)
     k = int(h.shape[1] * ratio)
     if k == 0:
         return np.zeros((0,), np.int32)
+    if rows is not None:
+        h = h[:rows]
     norms = np.sqrt((h * h).sum(axis=0))
     order = np.lexsort((np.arange(h.shape[1]), -norms))
     return np.sort(order[:k]).astype(np.int32)

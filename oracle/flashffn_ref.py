@@ -116,9 +116,18 @@ def triton_dequant_swiglu_backward(grad_h_mid, q_gate, s_gate, q_up, s_up, bits,
     return from_f32(dg, dt), from_f32(du, dt), (from_f32(hm, dt) if want_h_mid else None)
 
 
-def outlier_select(h, ratio):
-    """Outlier columns of the bf16 tensor h (codec.outlier_channels spec)."""
-    return codec.outlier_channels(to_f32(h), ratio)
+def outlier_select(h, ratio, rows=None):
+    """Outlier columns of the bf16 tensor h (codec.outlier_channels spec),
+    ranked by the column norms of its first `rows` rows."""
+    return codec.outlier_channels(to_f32(h), ratio, rows)
+
+
+def stat_rows(shape):
+    """The first sample's row count: HyC-LoRA ranks channels on x_[0] of a
+    [B, S, D] input (compress_function.py:85), i.e. N / B rows; a 2-D input is
+    a single sample."""
+    n = int(np.prod([int(s) for s in shape[:-1]])) if len(shape) > 1 else 1
+    return n // int(shape[0]) if len(shape) >= 3 and int(shape[0]) > 0 else n
 
 
 def v3_quantize_outlier(h, bits, group_size, idx):
@@ -178,7 +187,9 @@ class OracleFlashFFNv3Function(torch.autograd.Function):
         if k_out > 0:
             # this build's C3 extension: HyC-LoRA outlier channels on the v3 codec
             bits = 4 if cache_mode == "int4" else 8
-            idx_gate, idx_up = outlier_select(h_gate, outlier_ratio), outlier_select(h_up, outlier_ratio)
+            rows = stat_rows(orig_shape)
+            idx_gate = outlier_select(h_gate, outlier_ratio, rows)
+            idx_up = outlier_select(h_up, outlier_ratio, rows)
             c_gate, qs_gate, o_gate = v3_quantize_outlier(h_gate, bits, group_size, idx_gate)
             c_up, qs_up, o_up = v3_quantize_outlier(h_up, bits, group_size, idx_up)
             h_mid = triton_silu_mul(h_gate, h_up)

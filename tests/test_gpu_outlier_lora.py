@@ -39,13 +39,18 @@ def _hot(n, d, seed, hot=(3, 100, 257, 1000)):
 
 
 @pytest.mark.parametrize("ratio", [0.005, 0.01, 0.05])
-def test_outlier_select_matches_oracle(device, ratio):
+@pytest.mark.parametrize("rows", [None, 128, 1])
+def test_outlier_select_matches_oracle(device, ratio, rows):
+    """rows: the first sample's row count that ranks the channels (None: all)."""
     cpt, _ = _cpt()
     a, b = _hot(384, 2048, 5)
+    if rows is not None:
+        # later rows carry other hot channels: ranking all rows would differ
+        a[rows:, 1500:1600] *= 60
     for t in (a, b):
         k = int(t.shape[1] * ratio)
-        slot, idx = cpt.outlier_select(t.to(device), k)
-        want = codec.outlier_channels(to_f32(t), ratio)
+        slot, idx = cpt.outlier_select(t.to(device), k, rows)
+        want = codec.outlier_channels(to_f32(t), ratio, rows)
         assert idx.cpu().numpy().tolist() == want.tolist()
         s = slot.cpu().numpy()
         assert (s >= 0).sum() == k
@@ -171,16 +176,19 @@ def test_splitk_matches_fp32(device, mnk):
 H, D, RANK, S, N = 256, 768, 16, 2.0, 256
 
 
-@pytest.mark.parametrize("ratio", [0.0, 0.01])
-def test_c3_function_vs_oracle(device, ratio):
+@pytest.mark.parametrize("ratio,batch", [(0.0, None), (0.01, None), (0.01, 2)])
+def test_c3_function_vs_oracle(device, ratio, batch):
     """C3 shape in miniature: LoRA r16 (s=2) on gate/up/down, frozen base,
-    int4 g64 cache, top-1% outlier channels."""
+    int4 g64 cache, top-1% outlier channels.  batch: x as [batch, N / batch, H],
+    whose first sample ranks the outlier channels."""
     cpt, _ = _cpt()
     ps = R.synthetic_param_set("all", H, D, RANK, S, seed=21, dtype=torch.bfloat16,
                                peft_init=True, b_std=0.01)
     gen = torch.Generator().manual_seed(22)
     x = torch.randn(N, H, generator=gen).to(torch.bfloat16)
     gy = torch.randn(N, H, generator=gen).to(torch.bfloat16)
+    if batch:
+        x, gy = x.view(batch, N // batch, H), gy.view(batch, N // batch, H)
     psd = {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in ps.items()}
     got, y = R.run_function_grads(cpt.FlashFFNv3Function.apply, psd, x.to(device), gy.to(device),
                                   "int4", 64, True, ratio)

@@ -223,3 +223,37 @@ def test_outlier_codec_spec():
         *codec.quantize_group_absmax(v, 4, 64), 4, 64))
     with_o = codec.bf16_bits_to_f32(deq)
     assert np.linalg.norm(with_o - v) < np.linalg.norm(plain - v)
+
+
+@pytest.mark.parametrize("b,s,d,ratio", [(2, 64, 512, 0.01), (4, 32, 1024, 0.05), (1, 48, 256, 0.02)])
+def test_outlier_channels_rank_the_first_sample(b, s, d, ratio):
+    """Channel selection follows HyC-LoRA's `get_statistics_channel_base`
+    (src/hyclora/operators/compress_function.py:85-86): the top int(D*ratio)
+    of `x_[0].abs().norm(dim=-2)` on the [B, S, D] tensor, i.e. the first
+    sample's S rows of the [N, D] matrix.  The later samples carry other hot
+    channels, so ranking all rows would pick a different set."""
+    g = torch.Generator().manual_seed(b * 1000 + d)
+    x = torch.randn(b, s, d, generator=g)
+    k = int(d * ratio)
+    hot0 = torch.randperm(d, generator=g)[:k]
+    x[0][:, hot0] *= 8.0
+    if b > 1:
+        other = torch.randperm(d, generator=g)[:k]
+        x[1:][:, :, other] *= 80.0
+    v = x.reshape(-1, d).numpy()
+    got = codec.outlier_channels(v, ratio, rows=s)
+    want = torch.topk(x[0].abs().norm(dim=-2), k, largest=True).indices
+    assert got.tolist() == sorted(want.tolist())
+    assert sorted(got.tolist()) == sorted(hot0.tolist())
+    if b > 1:
+        assert codec.outlier_channels(v, ratio).tolist() != got.tolist()
+    # a 2-D input is one sample: rows=None ranks every row
+    assert codec.outlier_channels(v[:s], ratio).tolist() == got.tolist()
+
+
+def test_outlier_stat_rows_product_equals_oracle():
+    from compact_amd.flashffn import outlier_stat_rows
+    from oracle.flashffn_ref import stat_rows
+    for shape, want in (((256, 64), 256), ((2, 128, 64), 128), ((4, 2, 8, 64), 16),
+                        ((0, 5, 64), 0), ((1, 7, 64), 7), ((0, 64), 0)):
+        assert outlier_stat_rows(shape) == want == stat_rows(shape), shape
