@@ -193,13 +193,18 @@ struct Acc {
 // the strided direction (rows for K-major, k for MN-major), so rows past the
 // edge read as zero in hardware; the remaining edge (k for K-major, mn for
 // MN-major) is handled by pushing the offset past num_records (kOOB).
-// Offsets are 32-bit: each operand must span < 2 GiB (checked on the host).
+// Offsets are 32-bit, so every resource starts where the block's reads start:
+// a K-major operand at the tile's first row (its 256 rows are all the block
+// reads), an MN-major operand at the block's first k row (the start of its
+// split-K range).  A K-major operand of any size works; an MN-major one as
+// long as one block's k range spans < 2 GiB (the host checks both and splits
+// K when needed).  num_records still ends at the operand's last row.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kOOB = 0x80000000u;
 constexpr int kRsrcWord3 = 0x00020000;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
-  const uint32_t n = bytes > 0x7FFFFFFF ? 0x7FFFFFFFu : (uint32_t)bytes;
+  const uint32_t n = bytes > 0x7FFFFFFF ? 0x7FFFFFFFu : bytes < 0 ? 0u : (uint32_t)bytes;
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)n, kRsrcWord3);
 }
 
@@ -211,29 +216,42 @@ __device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 template <bool AK, bool BKM, bool DUAL>
 struct Loader {
   __amdgpu_buffer_rsrc_t ra[2], rb[2], rup;
-  uint32_t oa[8], ob[8];   // per-thread byte offsets at k = 0 (kOOB if the row/mn is out)
+  uint32_t oa[8], ob[8];   // per-thread byte offsets at the resource start (kOOB if out)
   int64_t K[2];
+  int64_t kbase[2];        // k row an MN-major resource starts at (per pair)
   int nk0;
   int64_t lda, ldb;
 
-  __device__ __forceinline__ void init(const KArgs& A, int64_t m0, int64_t n0, int tid) {
+  // kt0: the block's first k-tile (split-K), within pair 0
+  __device__ __forceinline__ void init(const KArgs& A, int64_t m0, int64_t n0, int tid, int kt0) {
     lda = A.a[0].ld;
     ldb = A.b[0].ld;
     K[0] = A.K[0];
     K[1] = A.npairs > 1 ? A.K[1] : 0;
     nk0 = (int)((A.K[0] + BK - 1) / BK);
+    kbase[0] = kt0 < nk0 ? (int64_t)kt0 * BK : 0;
+    kbase[1] = 0;
+    constexpr bool BK_ = BKM || DUAL;
+    const int64_t nb0 = DUAL ? (n0 >> 1) : n0;   // dual: the tile's first weight row
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       if (p == 1 && A.npairs < 2) { ra[1] = ra[0]; rb[1] = rb[0]; continue; }
-      // m-side: K-major spans M rows; MN-major spans K rows
-      ra[p] = make_rsrc(A.a[p].p, (AK ? A.M : A.K[p]) * lda * 2);
-      rb[p] = make_rsrc(A.b[p].p, (DUAL ? A.D : (BKM ? A.N : A.K[p])) * ldb * 2);
+      const char* pa = reinterpret_cast<const char*>(A.a[p].p);
+      const char* pb = reinterpret_cast<const char*>(A.b[p].p);
+      // K-major: rows [m0, M) from the tile's first row; MN-major: k rows
+      // [kbase, K) from the block's first k row
+      ra[p] = AK ? make_rsrc(pa + m0 * lda * 2, (A.M - m0) * lda * 2)
+                 : make_rsrc(pa + kbase[p] * lda * 2, (K[p] - kbase[p]) * lda * 2);
+      rb[p] = BK_ ? make_rsrc(pb + nb0 * ldb * 2, ((DUAL ? A.D : A.N) - nb0) * ldb * 2)
+                  : make_rsrc(pb + kbase[p] * ldb * 2, (K[p] - kbase[p]) * ldb * 2);
     }
-    rup = DUAL ? make_rsrc(A.b_up, A.D * ldb * 2) : rb[0];
+    rup = DUAL ? make_rsrc(reinterpret_cast<const char*>(A.b_up) + nb0 * ldb * 2,
+                           (A.D - nb0) * ldb * 2)
+               : rb[0];
     if (AK) {
 #pragma unroll
       for (int it = 0; it < 8; ++it) {
-        const int64_t row = m0 + (tid >> 3) + 32 * it;
+        const int64_t row = (tid >> 3) + 32 * it;
         oa[it] = (uint32_t)((row * lda + (tid & 7) * 8) * 2);
       }
     } else {
@@ -243,17 +261,16 @@ struct Loader {
         oa[r] = mn < A.M ? (uint32_t)((((tid >> 5) * 8 + r) * lda + mn) * 2) : kOOB;
     }
     if (DUAL) {
-      const int64_t d0 = n0 >> 1;
 #pragma unroll
       for (int it = 0; it < 8; ++it) {
         const int blk = it >> 1;
-        const int64_t d = d0 + ((blk >> 1) << 6) + (tid >> 3) + 32 * (it & 1);
+        const int64_t d = ((blk >> 1) << 6) + (tid >> 3) + 32 * (it & 1);
         ob[it] = (uint32_t)((d * ldb + (tid & 7) * 8) * 2);
       }
     } else if (BKM) {
 #pragma unroll
       for (int it = 0; it < 8; ++it) {
-        const int64_t row = n0 + (tid >> 3) + 32 * it;
+        const int64_t row = (tid >> 3) + 32 * it;
         ob[it] = (uint32_t)((row * ldb + (tid & 7) * 8) * 2);
       }
     } else {
@@ -349,7 +366,7 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc.v[i][j][r] = 0.0f;
   Loader<AK, BKM, DUAL> L;
-  L.init(A, m0, n0, tid);
+  L.init(A, m0, n0, tid, kt0);
   int nk_all = L.nk0;
   if (A.npairs > 1) nk_all += (int)((A.K[1] + BK - 1) / BK);
   if (kt_end < 0 || kt_end > nk_all) kt_end = nk_all;
@@ -376,8 +393,10 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
     T.ra = p ? L.ra[1] : L.ra[0];
     T.rb = p ? L.rb[1] : L.rb[0];
     const bool kok = k0 + (tid & 7) * 8 < Kp;
-    T.da = AK ? (kok ? (uint32_t)(k0 * 2) : kOOB) : (uint32_t)(k0 * L.lda * 2);
-    T.db = BK_ ? (kok ? (uint32_t)(k0 * 2) : kOOB) : (uint32_t)(k0 * L.ldb * 2);
+    // MN-major: rows from the resource's first k row (rows past Kp read zero)
+    const int64_t kr = k0 - (p ? L.kbase[1] : L.kbase[0]);
+    T.da = AK ? (kok ? (uint32_t)(k0 * 2) : kOOB) : (uint32_t)(kr * L.lda * 2);
+    T.db = BK_ ? (kok ? (uint32_t)(k0 * 2) : kOOB) : (uint32_t)(kr * L.ldb * 2);
     return T;
   };
   auto ldA = [&](const TileLd& T, int it) -> uint4 { return bload(T.ra, L.oa[it] + T.da); };
@@ -1131,11 +1150,18 @@ inline bool operand_ok(const void* p, int64_t ld, bool kmajor, int64_t mn, int64
   return (mn & 7) == 0 && ld >= mn;
 }
 
-// 32-bit buffer offsets: the strided extent plus one tile of overhang must
-// stay below 2 GiB.
+// 32-bit buffer offsets from where each block's reads start (Loader): a
+// K-major operand spans one 256-row panel of any operand size; an MN-major
+// one the block's k range, here all of K plus the prefetch overhang (split-K
+// launches check their ranges with operand_fits_k).
 inline bool operand_fits(int64_t ld, bool kmajor, int64_t mn, int64_t K) {
-  const int64_t rows = (kmajor ? mn : K) + 256;
+  (void)mn;
+  const int64_t rows = kmajor ? 256 + 1 : K + 256;
   return rows * ld * 2 < ((int64_t)1 << 31);
+}
+
+inline bool operand_fits_k(int64_t ld, bool kmajor, int64_t k_range) {
+  return operand_fits(ld, kmajor, 0, k_range);
 }
 
 template <int EPI, int CACHE, int LT>
@@ -1437,7 +1463,8 @@ int cpt_gemm_bf16_ex(const void* a, int64_t lda, int a_kmajor, const void* b, in
   if (!c || (mode != 1 && (!al16(c) || (ldc & 3))) || ldc < N) return kErrAlign;
   if (K > 0 && (!operand_ok(a, lda, a_kmajor, M, K) || !operand_ok(b, ldb, b_kmajor, N, K)))
     return kErrAlign;
-  if (!operand_fits(lda, a_kmajor, M, K) || !operand_fits(ldb, b_kmajor, N, K))
+  // split-K blocks read one k range each: mode 2 checks the range below
+  if (mode != 2 && (!operand_fits(lda, a_kmajor, M, K) || !operand_fits(ldb, b_kmajor, N, K)))
     return kErrTooLarge;
   KArgs A{};
   A.a[0] = {(const uint16_t*)a, lda};
@@ -1494,6 +1521,9 @@ int cpt_gemm_bf16_ex(const void* a, int64_t lda, int a_kmajor, const void* b, in
   A.ws = (float*)workspace;
   A.ksplit = splits;
   A.kt_per_split = (nk + splits - 1) / splits;
+  const int64_t k_range = (int64_t)A.kt_per_split * BK;
+  if (!operand_fits_k(lda, a_kmajor, k_range) || !operand_fits_k(ldb, b_kmajor, k_range))
+    return kErrTooLarge;
   int rc;
   if (a_kmajor && b_kmajor) rc = launch<true, true, EPI_F32, 0, 0>(A, st);
   else if (a_kmajor && !b_kmajor) rc = launch<true, false, EPI_F32, 0, 0>(A, st);

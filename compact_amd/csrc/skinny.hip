@@ -40,8 +40,11 @@ constexpr int kRowBlocks = CPT_SKINNY_RB;      // 16-row blocks per wavefront (s
 constexpr int kRowsPerBlock = 4 * 16 * kRowBlocks;   // 4 wavefronts per block
 constexpr int kUnroll = CPT_SKINNY_UNROLL;     // k32 steps in flight per wavefront
 
+// records clamped to [0, 2^31 - 1]: resources start where a block's reads
+// start, so offsets stay 32-bit for operands of any size
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, int64_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcWord3);
+  const int n = bytes > 0x7FFFFFFF ? 0x7FFFFFFF : bytes < 0 ? 0 : (int)bytes;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, n, kRsrcWord3);
 }
 
 __device__ __forceinline__ bf16x8 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
@@ -61,19 +64,20 @@ __global__ __launch_bounds__(256) void skinny_proj_kernel(
     int64_t ldc, float alpha) {
   constexpr int RB = kRowBlocks;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t m0 = ((int64_t)blockIdx.x * 4 + wave) * 16 * RB;
   if (m0 >= M) return;   // whole wavefront
   const int s = blockIdx.y;
   const int64_t k_begin = (int64_t)s * kchunk;
   const int64_t k_end = min(K, k_begin + kchunk);
-  // rows of A past M and rows of Q past R read zero through the records
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(a, M * lda * 2);
+  // A from the wavefront's first row: rows past M and rows of Q past R read
+  // zero through the records
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(a + m0 * lda, (M - m0) * lda * 2);
   const __amdgpu_buffer_rsrc_t rq = make_rsrc(q, (int64_t)R * ldq * 2);
   const int kq = 8 * (lane >> 4);
   uint32_t oa[RB];
 #pragma unroll
-  for (int b = 0; b < RB; ++b) oa[b] = (uint32_t)(((m0 + 16 * b + (lane & 15)) * lda + kq) * 2);
+  for (int b = 0; b < RB; ++b) oa[b] = (uint32_t)((((int64_t)16 * b + (lane & 15)) * lda + kq) * 2);
   uint32_t oq[NB];
 #pragma unroll
   for (int t = 0; t < NB; ++t) oq[t] = (uint32_t)(((int64_t)(t * 16 + (lane & 15)) * ldq + kq) * 2);
@@ -195,10 +199,11 @@ __global__ __launch_bounds__(256) void skinny_red_kernel(
   const int s = blockIdx.y;
   const int64_t t_begin = (int64_t)s * tchunk;
   const int64_t t_end = min(T, t_begin + tchunk);
-  // tokens past T read zero through the records; columns past N / R are
-  // masked per 8-wide chunk (N % 8 == 0, R % 8 == 0)
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, T * ldx * 2);
-  const __amdgpu_buffer_rsrc_t rp = make_rsrc(p, T * ldp * 2);
+  // both from the split's first token (offsets relative to t_begin); tokens
+  // past T read zero through the records; columns past N / R are masked per
+  // 8-wide chunk (N % 8 == 0, R % 8 == 0)
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + t_begin * ldx, (T - t_begin) * ldx * 2);
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(p + t_begin * ldp, (T - t_begin) * ldp * 2);
   // X piece: thread loads rows tid / 8 and tid / 8 + 32, columns 8 (tid % 8)
   const int xr = tid >> 3, xc = (tid & 7) * 8;
   const bool xok = n0 + xc < N;
@@ -213,9 +218,10 @@ __global__ __launch_bounds__(256) void skinny_red_kernel(
   uint4 vx0, vx1, vp;
   auto load = [&](int64_t t0) {
     const bool in = t0 < t_end;
-    const uint32_t ox0 = (uint32_t)(((t0 + xr) * ldx + n0 + xc) * 2);
-    const uint32_t ox1 = (uint32_t)(((t0 + xr + 32) * ldx + n0 + xc) * 2);
-    const uint32_t op = (uint32_t)(((t0 + pr) * ldp + pc) * 2);
+    const int64_t tr = t0 - t_begin;
+    const uint32_t ox0 = (uint32_t)(((tr + xr) * ldx + n0 + xc) * 2);
+    const uint32_t ox1 = (uint32_t)(((tr + xr + 32) * ldx + n0 + xc) * 2);
+    const uint32_t op = (uint32_t)(((tr + pr) * ldp + pc) * 2);
     auto v0 = __builtin_amdgcn_raw_buffer_load_b128(rx, (in && xok && t0 + xr < t_end) ? ox0 : kOOB, 0, 0);
     auto v1 = __builtin_amdgcn_raw_buffer_load_b128(rx, (in && xok && t0 + xr + 32 < t_end) ? ox1 : kOOB, 0, 0);
     auto v2 = __builtin_amdgcn_raw_buffer_load_b128(rp, (in && pok && t0 + pr < t_end) ? op : kOOB, 0, 0);
@@ -295,8 +301,9 @@ int cpt_gemm_bf16_skinny(const void* a, int64_t lda, const void* q, int64_t ldq,
   if (!a || !q || !c || !al16(a) || !al16(q) || (lda & 7) || (ldq & 7) || (K & 7) || lda < K ||
       ldq < K || ldc < R)
     return kErrAlign;
-  // 32-bit buffer offsets: A spans M rows (plus a wavefront's overhang), Q 32
-  if ((M + kRowsPerBlock) * lda * 2 >= ((int64_t)1 << 31) || 32 * ldq * 2 >= ((int64_t)1 << 31))
+  // 32-bit buffer offsets from each wavefront's first row: 16 * kRowBlocks
+  // rows of A, 32 of Q
+  if ((16 * kRowBlocks + 1) * lda * 2 >= ((int64_t)1 << 31) || 32 * ldq * 2 >= ((int64_t)1 << 31))
     return kErrTooLarge;
   const int64_t kchunk = ((K + splits - 1) / splits + 31) / 32 * 32;
   splits = (int)(kchunk > 0 ? (K + kchunk - 1) / kchunk : 1);
@@ -333,11 +340,14 @@ int cpt_gemm_bf16_skinny_t(const void* x, int64_t ldx, const void* p, int64_t ld
       (N & 7) || (R & 7) || ldx < N || ldp < R || ldo < (out_trans ? N : R) ||
       ((uintptr_t)workspace & 3))
     return kErrAlign;
-  if ((T + kRedTok) * ldx * 2 >= ((int64_t)1 << 31) || (T + kRedTok) * ldp * 2 >= ((int64_t)1 << 31))
-    return kErrTooLarge;
   const int64_t tchunk = ((T + splits - 1) / splits + kRedTok - 1) / kRedTok * kRedTok;
   splits = (int)(tchunk > 0 ? (T + tchunk - 1) / tchunk : 1);
   if (splits < 1) splits = 1;
+  // 32-bit buffer offsets from each split's first token: its tokens plus the
+  // prefetched piece past its end
+  if ((tchunk + 2 * kRedTok) * ldx * 2 >= ((int64_t)1 << 31) ||
+      (tchunk + 2 * kRedTok) * ldp * 2 >= ((int64_t)1 << 31))
+    return kErrTooLarge;
   const int64_t blocks = (N + kRedCols - 1) / kRedCols;
   if (blocks > 0x7FFFFFFF || splits > 65535) return kErrTooLarge;
   hipStream_t st = (hipStream_t)stream;

@@ -118,6 +118,11 @@ def _lora_args(terms, n_q):
 
 SKINNY_MAX_RANK = 32
 
+# Buffer offsets are 32-bit.  Every kernel's resource starts where a block's
+# reads start (a tile's first row, a split's first token or k row), so an
+# operand of any size works as long as one block's range spans less than this.
+_SPAN_BYTES = 1 << 31
+
 
 def skinny(a: torch.Tensor, q: torch.Tensor, alpha: float = 1.0,
            name: str = "gemm_skinny") -> torch.Tensor:
@@ -170,6 +175,10 @@ def skinny_t(x: torch.Tensor, p: torch.Tensor, alpha: float = 1.0, trans: bool =
         p = p.contiguous()
     blocks = (N + 63) // 64
     splits = max(1, min(max(T // 256, 1), (768 + blocks - 1) // blocks))
+    # each split reads its tokens (plus 128 of prefetch) within 32-bit offsets
+    per = (_SPAN_BYTES // (2 * max(x.stride(0), p.stride(0))) - 129) // 64 * 64
+    assert per >= 64, "operand rows too long for 32-bit buffer offsets"
+    splits = max(splits, (T + per - 1) // per)
     out = torch.empty((R, N) if trans else (N, R), dtype=torch.bfloat16, device=x.device)
     ws = torch.empty((splits * N * R,), dtype=torch.float32, device=x.device)
     with _timed(name):
@@ -181,11 +190,35 @@ def skinny_t(x: torch.Tensor, p: torch.Tensor, alpha: float = 1.0, trans: bool =
     return out
 
 
+def _max_k_rows(ld: int) -> int:
+    """k rows one block may read from an MN-major operand with rows ld apart
+    (prefetch overhang of 256 rows included)."""
+    return _SPAN_BYTES // (2 * ld) - 257
+
+
+def _min_splits(K: int, lda: int, ak: int, ldb: int, bk: int) -> int:
+    """Fewest k ranges that keep every block of a product within 32-bit
+    offsets, given its operand layouts (1 for everything but products over
+    very long k, e.g. the weight gradients of ~100k+ tokens whose operands
+    exceed 2 GiB)."""
+    lim = K
+    if not ak:
+        lim = min(lim, _max_k_rows(lda))       # A MN-major: [K][lda]
+    if not bk:
+        lim = min(lim, _max_k_rows(ldb))       # B MN-major: [K][ldb]
+    if lim >= K:
+        return 1
+    assert lim >= 64, "operand rows too long for 32-bit buffer offsets"
+    nk, per = (K + 63) // 64, lim // 64
+    return (nk + per - 1) // per
+
+
 def mm(a: torch.Tensor, b: torch.Tensor, name: str = "gemm") -> torch.Tensor:
     """a [M, K] @ b [K, N] -> bf16 [M, N] on the MFMA engine.  Tall products
     with N <= 32 (the adapter terms' x A^T, grad_y B, ...) go to the skinny
     kernel; other products with too few 256x256 output tiles to fill the chip
-    (N or M = rank) split K across blocks instead."""
+    (N or M = rank) split K across blocks instead, as do products whose
+    transposed operands are too long for one block's 32-bit offsets."""
     M, K = a.shape
     N = b.shape[1]
     if (N <= SKINNY_MAX_RANK and K >= 256 and K % 8 == 0 and M >= 256
@@ -193,6 +226,10 @@ def mm(a: torch.Tensor, b: torch.Tensor, name: str = "gemm") -> torch.Tensor:
         return skinny(a, b.t(), 1.0, name)
     tiles = ((M + 255) // 256) * ((N + 255) // 256)
     if tiles < 128 and K >= 1024:
+        return mm_splitk(a, b, 1.0, name=name)
+    a, lda, ak = _layout_a(a)
+    b, ldb, bk = _layout_b(b)
+    if _min_splits(K, lda, ak, ldb, bk) > 1:
         return mm_splitk(a, b, 1.0, name=name)
     return mm2(a, b, None, None, name)
 
@@ -421,6 +458,7 @@ def mm_splitk(a: torch.Tensor, b: torch.Tensor, alpha: float = 1.0, splits: int 
     if splits is None:
         tiles = ((M + 255) // 256) * ((N + 255) // 256)
         splits = max(1, min((K + 63) // 64, (512 + tiles - 1) // tiles))
+    splits = max(splits, _min_splits(K, lda, ak, ldb, bk))
     ldc = (N + 7) // 8 * 8
     c = torch.empty((M, ldc), dtype=torch.bfloat16, device=a.device)
     ws = torch.empty((splits * M * N,), dtype=torch.float32, device=a.device)

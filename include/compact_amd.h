@@ -27,7 +27,9 @@ enum {
   CPT_ERR_DTYPE = 5,       /* dtype code not supported by this entry point */
   CPT_ERR_LAUNCH = 6,      /* the HIP launch failed */
   CPT_ERR_ALIGN = 7,       /* a pointer misses the alignment the kernel needs */
-  CPT_ERR_TOO_LARGE = 8    /* size beyond what the kernel indexes */
+  CPT_ERR_TOO_LARGE = 8    /* size beyond what the kernel indexes (GEMM: a transposed
+                              operand whose k range in one block spans >= 2 GiB; the
+                              Python host splits k before that) */
 };
 
 enum { CPT_F32 = 0, CPT_F16 = 1, CPT_BF16 = 2 };
