@@ -81,3 +81,24 @@ def test_measured_traffic_reads_profiles():
     # a pair no summary covers gives None
     assert bench.measured_traffic("ffn_gate_up", "c2") == 2573000000
     assert bench.measured_traffic("ffn_gate_up", "no_such_workload") is None
+
+
+def test_v4_harness_model():
+    """The V4 speed-gate harness builds the reference gate's MLP: TinyLlama
+    dims, LoRA r8 / alpha 16 on gate, up and down with only the adapters
+    trainable, and the v2 arm's merged weight W + s B A."""
+    import torch
+    from compact_amd import bench_v4
+    mlp = bench_v4.build_mlp("cpu")
+    assert mlp.gate_proj.in_features == 2048 and mlp.gate_proj.out_features == 5632
+    trainable = [n for n, p in mlp.named_parameters() if p.requires_grad]
+    assert len(trainable) == 6 and all("lora_" in n for n in trainable)
+    p = mlp.up_proj
+    a, b = p.lora_A["default"].weight.detach(), p.lora_B["default"].weight.detach()
+    assert a.shape == (8, 2048) and b.shape == (5632, 8) and p.scaling["default"] == 2.0
+    assert float(b.float().std()) > 0.01            # re-drawn N(0, 0.02), not PEFT's zeros
+    w = p.get_base_layer().weight
+    want = (w.float() + 2.0 * (b.float() @ a.float())).to(torch.bfloat16)
+    got = bench_v4.lora_eff_weight(p).detach()
+    assert got.dtype == torch.bfloat16
+    assert (got.float() - want.float()).abs().max() <= 2 ** -7 * want.float().abs().max()
