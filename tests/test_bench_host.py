@@ -102,3 +102,19 @@ def test_v4_harness_model():
     got = bench_v4.lora_eff_weight(p).detach()
     assert got.dtype == torch.bfloat16
     assert (got.float() - want.float()).abs().max() <= 2 ** -7 * want.float().abs().max()
+
+
+def test_v5_bigram_batches():
+    """The V5 harness's synthetic text: each token is followed by one of 4
+    fixed successors, so every observed transition comes from the table."""
+    from compact_amd import bench_v5
+    bs = bench_v5.bigram_batches(3, 4, 64, 1000, succ=4, seed=1)
+    assert len(bs) == 3 and tuple(bs[0].shape) == (4, 64)
+    succ = {}
+    for b in bs:
+        for row in b.tolist():
+            for t0, t1 in zip(row, row[1:]):
+                succ.setdefault(t0, set()).add(t1)
+    assert max(len(v) for v in succ.values()) <= 4
+    again = bench_v5.bigram_batches(3, 4, 64, 1000, succ=4, seed=1)
+    assert all((x == y).all() for x, y in zip(bs, again))
