@@ -810,18 +810,20 @@ __device__ __forceinline__ void epi_glu(const KArgs& A, const Acc& acc, int64_t 
         if (!ok) continue;
         if ((tid & (GS / 8 - 1)) == 0) (t ? A.s_up : A.s_gate)[m * G + d / GS] = sh;
         uint8_t* qp = t ? A.q_up : A.q_gate;
+        int code[8];
+        quant_codes8<BITS>(v, safe, rs, code);
         if constexpr (BITS == 8) {
           uint32_t w0 = 0, w1 = 0;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            w0 |= ((uint32_t)quant_code<8>(v[e], safe, rs) & 0xFFu) << (8 * e);
-            w1 |= ((uint32_t)quant_code<8>(v[e + 4], safe, rs) & 0xFFu) << (8 * e);
+            w0 |= ((uint32_t)code[e] & 0xFFu) << (8 * e);
+            w1 |= ((uint32_t)code[e + 4] & 0xFFu) << (8 * e);
           }
           *reinterpret_cast<uint2*>(qp + off) = make_uint2(w0, w1);
         } else {
           uint32_t w = 0;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) w |= (uint32_t)(quant_code<4>(v[e], safe, rs) + 8) << (4 * e);
+          for (int e = 0; e < 8; ++e) w |= (uint32_t)(code[e] + 8) << (4 * e);
           *reinterpret_cast<uint32_t*>(qp + m * (D >> 1) + (d >> 1)) = w;
         }
       }

@@ -40,10 +40,23 @@ template <int BITS> struct QMax;
 template <> struct QMax<4> { static constexpr float v = 7.0f; };
 template <> struct QMax<8> { static constexpr float v = 127.0f; };
 
-// scale = fp16(fp32(absmax / qmax))  (absmax given as the bits of |x|)
+// scale = fp16(fp32(absmax / qmax))  (absmax given as the bits of |x|).
+// Fast path: y = absmax * fp32(1/qmax) and the correctly rounded quotient are
+// each within 1 fp32 ulp of the exact one, so within 2 ulp of each other.
+// They round to the same fp16 unless an fp16 rounding midpoint lies between
+// them: in fp16's normal range, where the 13 fp32 mantissa bits below fp16's
+// read 0x1000 at a midpoint, y more than 4 ulp from that pattern decides.
+// Elsewhere (fp16 subnormal or overflow range, NaN) and near a midpoint
+// (about one group in a thousand) the division decides.
 template <int BITS>
 __device__ __forceinline__ uint16_t scale_bits(uint32_t absmax_bits) {
-  return f32_to_f16_bits(__uint_as_float(absmax_bits) / QMax<BITS>::v);
+  const float a = __uint_as_float(absmax_bits);
+  float y = a * (1.0f / QMax<BITS>::v);
+  const uint32_t b = __float_as_uint(y);
+  const uint32_t ex = b >> 23;                      // y >= 0: the biased exponent
+  const int low = (int)(b & 0x1FFFu) - 0x1000;
+  if (!(ex >= 113u && ex <= 142u && (low > 4 || low < -4))) y = a / QMax<BITS>::v;
+  return f32_to_f16_bits(y);
 }
 
 // safe = scale > 0 ? scale : 1
@@ -66,6 +79,31 @@ __device__ __forceinline__ int quant_code(float v, float safe, float rsafe) {
   if (__builtin_fabsf(q - r) > 0.5f - 0.000244140625f) r = __builtin_rintf(v / safe);
   r = fminf(fmaxf(r, -QMax<BITS>::v), QMax<BITS>::v);
   return (int)r;
+}
+
+// quant_code for the 8 values a thread owns in one group, with one branch for
+// all eight: when any fast-path quotient lies near a half-integer, all eight
+// are recomputed from the correctly rounded division, which equals the fast
+// path wherever that one is valid.  Same codes as quant_code, element for
+// element.
+template <int BITS>
+__device__ __forceinline__ void quant_codes8(const float v[8], float safe, float rsafe,
+                                             int code[8]) {
+  float r[8];
+  float worst = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float q = v[e] * rsafe;
+    r[e] = __builtin_rintf(q);
+    worst = fmaxf(worst, __builtin_fabsf(q - r[e]));
+  }
+  if (worst > 0.5f - 0.000244140625f) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) r[e] = __builtin_rintf(v[e] / safe);
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+    code[e] = (int)fminf(fmaxf(r[e], -QMax<BITS>::v), QMax<BITS>::v);
 }
 
 }  // namespace cpt
