@@ -30,20 +30,18 @@ constexpr int kBlock = 256;
 template <int BITS>
 __device__ __forceinline__ void store_codes8(uint8_t* q, int64_t c, const float v[8], float safe) {
   const float rs = __builtin_amdgcn_rcpf(safe);
-  int code[8];
-  quant_codes8<BITS>(v, safe, rs, code);
   if (BITS == 8) {
     uint32_t w0 = 0, w1 = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      w0 |= ((uint32_t)code[j] & 0xFFu) << (8 * j);
-      w1 |= ((uint32_t)code[4 + j] & 0xFFu) << (8 * j);
+      w0 |= ((uint32_t)quant_code<8>(v[j], safe, rs) & 0xFFu) << (8 * j);
+      w1 |= ((uint32_t)quant_code<8>(v[4 + j], safe, rs) & 0xFFu) << (8 * j);
     }
     reinterpret_cast<uint2*>(q)[c] = make_uint2(w0, w1);
   } else {
     uint32_t w = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) w |= (uint32_t)(code[j] + 8) << (4 * j);
+    for (int j = 0; j < 8; ++j) w |= (uint32_t)(quant_code<4>(v[j], safe, rs) + 8) << (4 * j);
     reinterpret_cast<uint32_t*>(q)[c] = w;
   }
 }
