@@ -69,9 +69,7 @@ __device__ __forceinline__ uint32_t group_absmax8(const float v[8]) {
   uint32_t am = 0;
 #pragma unroll
   for (int j = 0; j < 8; ++j) am = max(am, __float_as_uint(v[j]) & 0x7FFFFFFFu);
-#pragma unroll
-  for (int off = 1; off < LPG; off <<= 1) am = max(am, (uint32_t)__shfl_xor((int)am, off));
-  return am;
+  return group_max_u32<LPG>(am);
 }
 
 // Quantise the 8 elements this thread owns; lane 0 of each group writes the scale.

@@ -801,9 +801,7 @@ __device__ __forceinline__ void epi_glu(const KArgs& A, const Acc& acc, int64_t 
         uint32_t am = 0;
 #pragma unroll
         for (int e = 0; e < 8; ++e) am = max(am, absbits(v[e]));
-#pragma unroll
-        for (int off_l = 1; off_l < GS / 8; off_l <<= 1)
-          am = max(am, (uint32_t)__shfl_xor((int)am, off_l));
+        am = group_max_u32<GS / 8>(am);
         const uint16_t sh = scale_bits<BITS>(am);
         const float safe = safe_scale(sh);
         const float rs = __builtin_amdgcn_rcpf(safe);

@@ -7,6 +7,8 @@
 // bf16 round trip of the dequantised cache :1251-1253.
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace cpt {
@@ -34,6 +36,29 @@ __device__ __forceinline__ void swiglu_bwd1(float dh, float g, float u, float& d
   du = dh * hact;
   const float dsilu = sig * (1.0f + g * (1.0f - sig));
   dg = grad_h_act * dsilu;
+}
+
+// Max over each aligned group of LPG lanes (LPG a power of two <= 64), every
+// lane of a group receiving it.  Up to 16 lanes it is a DPP butterfly inside
+// the 16-lane row, VALU only: swap neighbours, swap pairs (quad_perm
+// [1,0,3,2], [2,3,0,1]), then mirror within 8 and within 16 lanes
+// (row_half_mirror, row_mirror), each step pairing every lane with one from
+// the other half of its growing group.  Wider groups add ds_bpermute
+// exchanges (__shfl_xor) across rows.
+template <int LPG>
+__device__ __forceinline__ uint32_t group_max_u32(uint32_t v) {
+  static_assert(LPG >= 1 && LPG <= 64 && (LPG & (LPG - 1)) == 0, "group of 1..64 lanes");
+  auto dpp_max = [](uint32_t x, auto ctrl) {
+    return max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, decltype(ctrl)::value, 0xF,
+                                                        0xF, false));
+  };
+  if constexpr (LPG >= 2) v = dpp_max(v, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
+  if constexpr (LPG >= 4) v = dpp_max(v, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
+  if constexpr (LPG >= 8) v = dpp_max(v, std::integral_constant<int, 0x141>{});  // row_half_mirror
+  if constexpr (LPG >= 16) v = dpp_max(v, std::integral_constant<int, 0x140>{}); // row_mirror
+#pragma unroll
+  for (int off = 16; off < LPG; off <<= 1) v = max(v, (uint32_t)__shfl_xor((int)v, off));
+  return v;
 }
 
 template <int BITS> struct QMax;
