@@ -434,11 +434,12 @@ def synthetic_param_set(config: str, h: int, d: int, rank: int, scaling: float,
 
 
 def tensor_cos(a, b) -> float:
+    a, b = a.detach(), b.detach()
     return float(F.cosine_similarity(a.double().flatten(), b.double().flatten(), dim=0))
 
 
 def rel_frob(a, b) -> float:
-    b64 = b.double()
+    a, b64 = a.detach(), b.detach().double()
     den = b64.norm()
     return float((a.double() - b64).norm() / den) if den > 0 else float((a.double()).norm())
 
