@@ -53,12 +53,21 @@ _FUSED_DGRAD_GROUPS = ()
 
 
 def _mfma(*ts) -> bool:
-    """The MFMA engine runs bf16 operands whose dims are multiples of 8."""
+    """The MFMA engine takes bf16 matrices with 16-byte aligned rows: the
+    contiguous extent and the row stride multiples of 8.  The other extent
+    (the token count of an activation, or of a transposed one) is free: the
+    kernels mask rows and k past the edge."""
     for t in ts:
         if t is None:
             continue
-        if t.dtype != torch.bfloat16 or any(d % 8 for d in t.shape):
+        if t.dtype != torch.bfloat16 or t.dim() != 2:
             return False
+        rows, cols = t.shape
+        if t.stride(1) == 1 and cols % 8 == 0 and t.stride(0) % 8 == 0:
+            continue
+        if t.stride(0) == 1 and rows % 8 == 0 and t.stride(1) % 8 == 0:
+            continue
+        return False
     return True
 
 

@@ -172,3 +172,48 @@ def test_unknown_wrapper_raises():
     mlp.gate_proj = Weird()
     with pytest.raises(NotImplementedError):
         cpt.make_v3_forward(mlp)
+
+
+@pytest.mark.parametrize("config,mode,ratio", [("fullft", "int8", 0.0), ("all", "int4", 0.0),
+                                               ("all", "int4", 0.01), ("fullft", "recompute", 0.0)])
+@pytest.mark.parametrize("shape", [(0, H), (2, 0, H)])
+def test_empty_token_batch(device, config, mode, ratio, shape):
+    """No tokens: y keeps x's (empty) shape, grad_x is empty and every weight
+    or adapter gradient is zero, as the oracle (torch GEMMs over zero rows)
+    gives."""
+    ps = R.synthetic_param_set(config, H, D, RANK, S, seed=5, dtype=torch.bfloat16)
+    x = torch.zeros(shape, dtype=torch.bfloat16)
+    gy = torch.zeros(shape, dtype=torch.bfloat16)
+    got, y = R.run_function_grads(_cpt().FlashFFNv3Function.apply, _to(ps, device),
+                                  x.to(device), gy.to(device), mode, 64, True, ratio)
+    ora, y_o = R.run_function_grads(R.OracleFlashFFNv3Function.apply, ps, x, gy, mode, 64,
+                                    True, ratio)
+    assert tuple(y.shape) == tuple(shape) == tuple(y_o.shape)
+    assert set(got) == set(ora)
+    for k in ora:
+        assert tuple(got[k].shape) == tuple(ora[k].shape), k
+        assert not got[k].float().abs().any(), k
+
+
+@pytest.mark.parametrize("n", [1, 7, 100, 259])
+@pytest.mark.parametrize("config,mode,group", [("all", "int4", 64), ("fullft", "int8", 128),
+                                               ("gateup", "bf16", 64),
+                                               ("fullft", "recompute", 64)])
+def test_function_odd_token_counts(device, n, config, mode, group):
+    """Token counts that are not multiples of 8 (or of the 256-row tile) run
+    on the same kernels: rows and the token reduction are masked at the
+    edge.  Same bars as the N = 256 parity test."""
+    cpt = _cpt()
+    ps = R.synthetic_param_set(config, H, D, RANK, S, seed=6, dtype=torch.bfloat16)
+    gen = torch.Generator().manual_seed(n)
+    x = torch.randn(n, H, generator=gen).to(torch.bfloat16)
+    gy = torch.randn(n, H, generator=gen).to(torch.bfloat16)
+    cpt.v3_reset_counters()
+    got, y = _run(_to(ps, device), x.to(device), gy.to(device), mode, group)
+    if mode in ("int4", "int8"):
+        assert cpt._V3_COUNTERS["triton_quant_fwd"] == 1     # the fused device codec ran
+    ora, y_o = R.run_function_grads(R.OracleFlashFFNv3Function.apply, ps, x, gy, mode, group)
+    assert R.rel_frob(y.cpu(), y_o) < 1e-2
+    assert set(got) == set(ora)
+    for k in ora:
+        assert R.rel_frob(got[k].cpu(), ora[k]) < 2e-2, k

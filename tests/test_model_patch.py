@@ -69,3 +69,20 @@ def test_bamboo_mlp_refused():
     holder.mlp = mlp
     with pytest.raises(ValueError):
         MP.apply_flash_ffn_v3(holder, "int8")
+
+
+def test_mfma_layout_rule():
+    """The engine takes 16-byte aligned rows: contiguous extent and row stride
+    multiples of 8, the other extent free; degenerate rank-1 columns and
+    ragged contiguous extents go elsewhere."""
+    import torch
+    from compact_amd.flashffn import _mfma
+    bf = torch.bfloat16
+    assert _mfma(torch.zeros(7, 256, dtype=bf))              # any token count
+    assert _mfma(torch.zeros(7, 256, dtype=bf).t())          # transposed activation
+    assert _mfma(torch.zeros(1, 256, dtype=bf))
+    assert not _mfma(torch.zeros(256, 1, dtype=bf))          # a rank-1 factor
+    assert not _mfma(torch.zeros(256, 4, dtype=bf))
+    assert not _mfma(torch.zeros(256, 12, dtype=bf)[:, :8])  # rows 12 elements apart
+    assert not _mfma(torch.zeros(8, 8, dtype=torch.float32))
+    assert _mfma(torch.zeros(16, 768, dtype=bf)[:4])         # a row slice of a weight
