@@ -48,7 +48,10 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int BM = 256, BN = 256, BK = 64, NTHR = 256;
 constexpr int TILE_ELEMS = 256 * 72 + 32 * 8;  // one operand stage in LDS (padded rows)
 constexpr int LDS_BYTES = 4 * TILE_ELEMS * 2;   // 2 stages x 2 operands (146 KiB)
-constexpr int GROUP_ROWS = 8;                  // tile-rows per L2 group
+#ifndef CPT_GROUP_ROWS
+#define CPT_GROUP_ROWS 4
+#endif
+constexpr int GROUP_ROWS = CPT_GROUP_ROWS;     // tile-rows per L2 group
 
 // K-major tiles: row r (m or n) at r * 64 + (r / 2) * 8 elements, 8-element
 // (16-byte) k chunks.  LDS is 64 banks of 4 bytes on gfx950 and a 128-bit
