@@ -131,6 +131,23 @@ def test_adapter_function_vs_oracle_bf16(device, kind, mode, group):
 
 
 @pytest.mark.parametrize("kind", R.ADAPTER_KINDS)
+@pytest.mark.parametrize("n", [7, 100])
+def test_adapter_function_odd_token_counts(device, kind, n):
+    """Token counts that are not multiples of 8 run on the same kernels for
+    every adapter family (int4 g64 cache), against the oracle."""
+    ps = R.synthetic_adapter_set(kind, H, D, RANK, ALPHA, seed=23)
+    gen = torch.Generator().manual_seed(n)
+    x = torch.randn(n, H, generator=gen).to(torch.bfloat16)
+    gy = torch.randn(n, H, generator=gen).to(torch.bfloat16)
+    got, y = _run_both(ps, x, gy, "int4", 64, device)
+    ora, y_o = R.run_adapter_grads(R.OracleFlashFFNv3AdapterFunction.apply, ps, x, gy, "int4", 64)
+    assert R.rel_frob(y, y_o) < 1e-2
+    assert set(got) == set(ora)
+    for k in ora:
+        assert R.rel_frob(got[k], ora[k]) < 2e-2, k
+
+
+@pytest.mark.parametrize("kind", R.ADAPTER_KINDS)
 @pytest.mark.parametrize("mode", ["int4", "recompute", "bf16"])
 def test_adapter_function_gates_vs_fp32(device, kind, mode):
     """The reference's V2-style gates against float32 autograd of the family's
