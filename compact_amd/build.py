@@ -5,7 +5,7 @@ HIP source with hipcc and links them into compact_amd/_build/libcompact_amd.so.
 Cross-compiles without a GPU.  Flags that decide numerics:
   -fhip-fp32-correctly-rounded-divide-sqrt   IEEE division (codec bit-exactness)
   -fno-gpu-flush-denormals-to-zero           keep fp32 denormals
-  -ffp-contract=off                          (codec, gemm, adapters) no FMA contraction
+  -ffp-contract=off                          (codec, gemm*, adapters) no FMA contraction
   -Xclang -target-feature -Xclang -packed-fp32-ops   no packed-fp32 instructions
 """
 
@@ -31,8 +31,8 @@ COMMON = [
     "-Wall", "-Wno-unused-function",
     f"-I{CSRC}", f"-I{os.path.join(ROOT, 'include')}",
 ]
-PER_FILE = {"codec.hip": ["-ffp-contract=off"], "gemm.hip": ["-ffp-contract=off"],
-            "adapters.hip": ["-ffp-contract=off"]}
+# no FMA contraction in the codec, GEMM (every gemm*.hip unit) and adapter kernels
+NO_CONTRACT = ("codec", "gemm", "adapters")
 
 
 def hipcc() -> str:
@@ -44,7 +44,9 @@ def hipcc() -> str:
 
 def _compile(src: str) -> str:
     obj = os.path.join(OUT_DIR, os.path.basename(src) + ".o")
-    cmd = [hipcc(), "-c", src, "-o", obj] + COMMON + PER_FILE.get(os.path.basename(src), [])
+    cmd = [hipcc(), "-c", src, "-o", obj] + COMMON
+    if os.path.basename(src).startswith(NO_CONTRACT):
+        cmd.append("-ffp-contract=off")
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
