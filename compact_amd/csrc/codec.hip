@@ -275,15 +275,16 @@ __global__ __launch_bounds__(kBlock) void dequantize_generic_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// K2: dequantise through bf16, SwiGLU backward, optional h_mid^
+// K2: dequantise through bf16, SwiGLU backward, optional h_mid^.
+// grad_h_gate may be written over grad_h_mid (the caller's private buffer):
+// each thread reads its 8 elements of gmid before it stores the same 8 of
+// dg, so gmid, dg, du and hm carry no __restrict__.
 // ---------------------------------------------------------------------------
 template <int BITS, bool WANT_HM, bool OUTL>
 __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_kernel(
-    const uint16_t* __restrict__ gmid, const uint8_t* __restrict__ qg,
-    const uint16_t* __restrict__ sg, const uint8_t* __restrict__ qu,
-    const uint16_t* __restrict__ su, uint16_t* __restrict__ dg, uint16_t* __restrict__ du,
-    uint16_t* __restrict__ hm, int64_t nchunk, int gs_shift, int64_t d, Outliers outg,
-    Outliers outu) {
+    const uint16_t* gmid, const uint8_t* __restrict__ qg, const uint16_t* __restrict__ sg,
+    const uint8_t* __restrict__ qu, const uint16_t* __restrict__ su, uint16_t* dg, uint16_t* du,
+    uint16_t* hm, int64_t nchunk, int gs_shift, int64_t d, Outliers outg, Outliers outu) {
   const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (c >= nchunk) return;
   float cg[8], cu[8], dh[8], og[8], ou[8], oh[8], hg[8], hu[8];
@@ -317,10 +318,9 @@ __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_kernel(
 // generic K2 (group sizes below 8, misaligned pointers): one thread per element
 template <int BITS, bool WANT_HM>
 __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_generic_kernel(
-    const uint16_t* __restrict__ gmid, const uint8_t* __restrict__ qg,
-    const uint16_t* __restrict__ sg, const uint8_t* __restrict__ qu,
-    const uint16_t* __restrict__ su, uint16_t* __restrict__ dg, uint16_t* __restrict__ du,
-    uint16_t* __restrict__ hm, int64_t n_el, int64_t gs) {
+    const uint16_t* gmid, const uint8_t* __restrict__ qg, const uint16_t* __restrict__ sg,
+    const uint8_t* __restrict__ qu, const uint16_t* __restrict__ su, uint16_t* dg, uint16_t* du,
+    uint16_t* hm, int64_t n_el, int64_t gs) {
   const int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (e >= n_el) return;
   float code_g, code_u;

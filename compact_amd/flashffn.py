@@ -39,6 +39,13 @@ def _bits(mode: str) -> int:
     return 4 if mode == "int4" else 8
 
 
+def _private(mode: str, hg, hu) -> bool:
+    """The backward's h_gate / h_up are its own buffers (recomputed or
+    dequantised, not the saved bf16 cache), contiguous, so the SwiGLU
+    backward may write its gradients over them."""
+    return mode != "bf16" and hg.is_contiguous() and hu.is_contiguous()
+
+
 _CACHE_CODE = {"int4": _lib.CACHE_INT4, "int8": _lib.CACHE_INT8, "bf16": _lib.CACHE_BF16,
                "recompute": _lib.CACHE_NONE}
 _FUSED_GROUPS = (32, 64, 128)
@@ -53,14 +60,15 @@ _FUSED_DGRAD_GROUPS = ()
 
 
 def _mfma(*ts) -> bool:
-    """The MFMA engine takes bf16 matrices with 16-byte aligned rows: the
-    contiguous extent and the row stride multiples of 8.  The other extent
-    (the token count of an activation, or of a transposed one) is free: the
-    kernels mask rows and k past the edge."""
+    """The bf16 MFMA engine takes bf16 matrices with 16-byte aligned rows: the
+    base address 16-byte aligned, the contiguous extent and the row stride
+    multiples of 8.  The other extent (the token count of an activation, or
+    of a transposed one) is free: the kernels mask rows and k past the edge.
+    Everything else runs on the general-layout kernel (G.mm_any)."""
     for t in ts:
         if t is None:
             continue
-        if t.dtype != torch.bfloat16 or t.dim() != 2:
+        if t.dtype != torch.bfloat16 or t.dim() != 2 or t.data_ptr() % 16:
             return False
         rows, cols = t.shape
         if t.stride(1) == 1 and cols % 8 == 0 and t.stride(0) % 8 == 0:
@@ -72,32 +80,40 @@ def _mfma(*ts) -> bool:
 
 
 def _mm(a, b, name):
-    """a @ b: the MFMA engine for bf16, the library GEMM otherwise."""
+    """a @ b: the bf16 MFMA engine, or the general-layout kernel for other
+    dtypes and layouts."""
     if _mfma(a, b) and a.shape[0] > 0:
         return G.mm(a, b, name)
-    return a @ b
+    return G.mm_any(a, b, name=name)
 
 
 def _linear(x, w, name):
-    if _mfma(x, w) and x.shape[0] > 0:
-        return G.linear(x, w, name)
-    return F.linear(x, w)
+    return _mm(x, w.t(), name)
 
 
 def _addmm(c, a, b, s, name):
-    """c + s * (a @ b) in the reference's bf16 op order (product, scaling and
-    sum each rounded): in place on the engine for bf16."""
+    """c + s * (a @ b) in the reference's op order (product, scaling and sum
+    each rounded to the dtype), in place on c."""
     if _mfma(c, a, b) and a.shape[0] > 0 and c.stride(1) == 1:
         return G.addmm_(c, a, b, s, name)
-    return c + s * (a @ b)
+    return G.mm_any(a, b, s, G.ANY_ADD, out=c, name=name)
 
 
 def _mm_scaled(a, b, s, name):
     """s * (a @ b) for the thin adapter gradients, which reduce over all
-    tokens: split-K on the engine for bf16."""
+    tokens: split-K on the bf16 engine, or the general-layout kernel."""
     if _mfma(a, b) and a.shape[1] > 0:
         return G.mm_splitk(a, b, s, name=name)
-    return s * (a @ b)
+    return G.mm_any(a, b, s, G.ANY_SCALE, name=name)
+
+
+def _mm_sum(a, b, a2, b2, name):
+    """a @ b + a2 @ b2: one K-concatenated accumulation on the bf16 engine, or
+    the reference's two rounded products and their rounded sum."""
+    if _mfma(a, b, a2, b2):
+        return G.mm2(a, b, a2, b2, name)
+    out = G.mm_any(a, b, name=name)
+    return G.mm_any(a2, b2, 1.0, G.ANY_ADD, out=out, name=name)
 
 
 def _lora_ok(*pairs) -> bool:
@@ -150,11 +166,13 @@ class FlashFFNv3Function(torch.autograd.Function):
     """LoRA-factored SwiGLU FFN with a quantised GLU-cache backward
     (src/flashffn.py:1376-1602).  a_*/b_* may be None (pass s_*=0.0).
 
-    bf16 without gate/up adapters runs the fused MFMA kernels: the forward
-    gate/up GEMM carries SiLU*mul and the codec in its epilogue, the backward
-    down-projection GEMM carries the dequantisation and the SwiGLU backward.
-    Other cases compose the GEMM engine (or the library GEMM for non-bf16
-    dtypes) with the standalone elementwise kernels in the reference's order.
+    bf16 with 16-byte aligned rows runs the fused MFMA kernels: the forward
+    gate/up GEMM carries the LoRA terms, SiLU*mul and the codec in its
+    epilogue; the backward runs the dgrad GEMM, then the K2 kernel
+    (dequantise + SwiGLU backward), or for bf16 / recompute caches the dgrad
+    GEMM with the SwiGLU backward in its epilogue.  Other dtypes and layouts
+    compose the general-layout GEMM kernel with the standalone elementwise
+    kernels in the reference's order.
 
     outlier_ratio > 0 (int4/int8 caches, this build's extension for config C3):
     per call, the int(D * ratio) columns of h_gate and of h_up with the largest
@@ -326,9 +344,12 @@ class FlashFFNv3Function(torch.autograd.Function):
                     outliers=(slot_gate, o_gate, slot_up, o_up) if outl else None)
                 _V3_COUNTERS["triton_dequant_bwd"] += 1
             elif (not use_k2) and fusable and hg is not None and _mfma(hg, hu):
+                # grad_h_gate / grad_h_up are written over h_gate / h_up when
+                # those are this backward's own (recomputed or dequantised)
                 grad_h_gate, grad_h_up, h_mid_hat = G.ffn_down_dgrad(
                     gy, w_down, _lib.CACHE_BF16, gs, hg, None, hu, None, need_h_mid,
-                    lora=dlora)
+                    lora=dlora, inplace=_private(mode, hg, hu))
+                hg = hu = None
             else:
                 if dlora is not None and _mfma(gy, w_down) and gy.shape[0] > 0:
                     grad_h_mid = G.mm2(gy, w_down, name="gemm_dgrad_down", lora=[
@@ -338,17 +359,23 @@ class FlashFFNv3Function(torch.autograd.Function):
                     if a_down is not None:
                         grad_h_mid = _addmm(grad_h_mid, gyB_d, a_down, s_down,
                                             "gemm_dgrad_down_lora")
+                # grad_h_mid is private: K2 writes grad_h_gate over it, and
+                # the GLU backward writes over h_gate / h_up too when those
+                # are private (3 live [N, D] buffers instead of 6,
+                # src/flashffn.py:129-198)
                 if use_k2 and outl:
                     grad_h_gate, grad_h_up, h_mid_hat = K.dequant_swiglu_backward_outlier(
                         grad_h_mid, c_gate, qs_gate, o_gate, slot_gate, c_up, qs_up, o_up,
-                        slot_up, _bits(mode), gs, want_h_mid=need_h_mid)
+                        slot_up, _bits(mode), gs, want_h_mid=need_h_mid, inplace=True)
                 elif use_k2:
                     grad_h_gate, grad_h_up, h_mid_hat = K.dequant_swiglu_backward(
                         grad_h_mid, c_gate, qs_gate, c_up, qs_up, _bits(mode), gs,
-                        want_h_mid=need_h_mid)
+                        want_h_mid=need_h_mid, inplace=True)
                 else:
                     grad_h_gate, grad_h_up, h_mid_hat = K.swiglu_backward_glu(
-                        grad_h_mid, hg, hu, need_h_mid)
+                        grad_h_mid, hg, hu, need_h_mid,
+                        inplace=_private(mode, hg, hu) and grad_h_mid.is_contiguous())
+                    hg = hu = None
                 del grad_h_mid
 
         if need_h_mid:                                                    # :1536-1543
@@ -381,10 +408,7 @@ class FlashFFNv3Function(torch.autograd.Function):
                     grad_x = G.mm2(grad_h_gate, w_gate, grad_h_up, w_up, "gemm_dgrad_x",
                                    lora=[t for t in xl if t is not None] or None)
                 else:
-                    if _mfma(grad_h_gate, w_gate, grad_h_up, w_up):
-                        grad_x = G.mm2(grad_h_gate, w_gate, grad_h_up, w_up, "gemm_dgrad_x")
-                    else:
-                        grad_x = grad_h_gate @ w_gate + grad_h_up @ w_up
+                    grad_x = _mm_sum(grad_h_gate, w_gate, grad_h_up, w_up, "gemm_dgrad_x")
                     if a_gate is not None:
                         grad_x = _addmm(grad_x, ghgB, a_gate, s_gate, "gemm_dgrad_x_lora_gate")
                     if a_up is not None:
@@ -747,6 +771,10 @@ class FlashFFNv3AdapterFunction(torch.autograd.Function):
             gyB_d = _mm(g_eff_y, b_down, "gemm_gyB_down")
         fusable_d = a_down is None and _mfma(g_eff_y, w_down) and g_eff_y.shape[0] > 0
 
+        # the SwiGLU backward may write over h_gate / h_up when they are this
+        # backward's own and no magnitude gradient reads them afterwards
+        own = (hg is not None and hu is not None and m_gate is None and m_up is None
+               and _private(mode, hg, hu))
         grad_h_gate = grad_h_up = h_mid_hat = None
         if need_gate_path:
             if use_k2 and fusable_d and gs in _FUSED_DGRAD_GROUPS:              # :2101-2110
@@ -757,7 +785,8 @@ class FlashFFNv3AdapterFunction(torch.autograd.Function):
             elif (not use_k2) and fusable_d and hg is not None and hu is not None \
                     and _mfma(hg, hu):
                 grad_h_gate, grad_h_up, h_mid_hat = G.ffn_down_dgrad(
-                    g_eff_y, w_down, _lib.CACHE_BF16, gs, hg, None, hu, None, need_h_mid)
+                    g_eff_y, w_down, _lib.CACHE_BF16, gs, hg, None, hu, None, need_h_mid,
+                    inplace=own)
             else:
                 grad_h_mid = _mm(g_eff_y, w_down, "gemm_dgrad_down")
                 if a_down is not None:
@@ -765,10 +794,11 @@ class FlashFFNv3AdapterFunction(torch.autograd.Function):
                 if use_k2:
                     grad_h_gate, grad_h_up, h_mid_hat = K.dequant_swiglu_backward(
                         grad_h_mid, cq_gate, qs_gate, cq_up, qs_up, _bits(mode), gs,
-                        want_h_mid=need_h_mid)
+                        want_h_mid=need_h_mid, inplace=True)
                 else:
                     grad_h_gate, grad_h_up, h_mid_hat = K.swiglu_backward_glu(
-                        grad_h_mid, hg, hu, need_h_mid)
+                        grad_h_mid, hg, hu, need_h_mid,
+                        inplace=own and grad_h_mid.is_contiguous())
                 del grad_h_mid
 
         grad_w_down = grad_a_down = grad_b_down = grad_m_down = None
@@ -810,10 +840,7 @@ class FlashFFNv3AdapterFunction(torch.autograd.Function):
             if a_up is not None and (need_x or need_au):
                 ghuB = _mm(g_eff_u, b_up, "gemm_ghuB")
             if need_x:
-                if _mfma(g_eff_g, w_gate, g_eff_u, w_up):
-                    grad_x = G.mm2(g_eff_g, w_gate, g_eff_u, w_up, "gemm_dgrad_x")
-                else:
-                    grad_x = g_eff_g @ w_gate + g_eff_u @ w_up
+                grad_x = _mm_sum(g_eff_g, w_gate, g_eff_u, w_up, "gemm_dgrad_x")
                 if a_gate is not None:
                     grad_x = _addmm(grad_x, ghgB, a_gate, s_gate, "gemm_dgrad_x_lora_gate")
                 if a_up is not None:
@@ -868,7 +895,7 @@ def make_v3_adapter_forward(mlp: nn.Module, cache_mode: str = "int4", group_size
 
 def _gate_up(x_2d, w_gate, w_up, keep: bool):
     """(h_mid, h_gate | None, h_up | None): the fused dual GEMM + GLU on the
-    engine for bf16, the library GEMMs + the GLU kernel otherwise."""
+    engine for bf16, the general-layout GEMMs + the GLU kernel otherwise."""
     if _mfma(x_2d, w_gate, w_up) and x_2d.shape[0] > 0:
         h_mid, hg, hu, *_ = G.ffn_gate_up(x_2d, w_gate, w_up,
                                           _lib.CACHE_BF16 if keep else _lib.CACHE_NONE, 64)
@@ -878,18 +905,22 @@ def _gate_up(x_2d, w_gate, w_up, keep: bool):
     return K.silu_mul(hg, hu), (hg if keep else None), (hu if keep else None)
 
 
-def _glu_backward(gy, w_down, hg, hu):
-    """(grad_h_gate, grad_h_up) of h_mid = SiLU(hg) * hu through y = h_mid W_d^T."""
+def _glu_backward(gy, w_down, hg, hu, inplace=False):
+    """(grad_h_gate, grad_h_up) of h_mid = SiLU(hg) * hu through y = h_mid W_d^T;
+    `inplace` writes them over hg / hu (private, contiguous)."""
     if _mfma(gy, w_down, hg, hu) and gy.shape[0] > 0:
-        dg, du, _ = G.ffn_down_dgrad(gy, w_down, _lib.CACHE_BF16, 64, hg, None, hu, None, False)
+        dg, du, _ = G.ffn_down_dgrad(gy, w_down, _lib.CACHE_BF16, 64, hg, None, hu, None, False,
+                                     inplace=inplace)
         return dg, du
-    return K.swiglu_backward(_mm(gy, w_down, "gemm_dgrad_down"), hg, hu)
+    ghm = _mm(gy, w_down, "gemm_dgrad_down")
+    if inplace and ghm.is_contiguous():
+        dg, du, _ = K.swiglu_backward_glu(ghm, hg, hu, False, inplace=True)
+        return dg, du
+    return K.swiglu_backward(ghm, hg, hu)
 
 
 def _dgrad_x(dg, w_gate, du, w_up):
-    if _mfma(dg, w_gate, du, w_up):
-        return G.mm2(dg, w_gate, du, w_up, "gemm_dgrad_x")
-    return dg @ w_gate + du @ w_up
+    return _mm_sum(dg, w_gate, du, w_up, "gemm_dgrad_x")
 
 
 class FlashFFNFunction(torch.autograd.Function):
@@ -905,7 +936,7 @@ class FlashFFNFunction(torch.autograd.Function):
           returns grad_x only.
     Device path: the fused dual GEMM + GLU forward and the fused dgrad GEMM +
     SwiGLU backward on the MFMA engine (bf16), the top-K select and scatter
-    kernels; library GEMMs + the GLU kernels for other dtypes."""
+    kernels; the general-layout GEMMs + the GLU kernels for other dtypes."""
 
     @staticmethod
     def forward(ctx, x, w_gate, w_up, w_down, k_fraction=0.3):
@@ -963,7 +994,8 @@ class FlashFFNFunction(torch.autograd.Function):
         grad_x = grad_w_gate = grad_w_up = None
         if need_x or need_wg or need_wu:
             _, hg, hu = _gate_up(x_2d, w_gate, w_up, keep=True)
-            dg, du = _glu_backward(gy, w_down, hg, hu)
+            dg, du = _glu_backward(gy, w_down, hg, hu,
+                                   inplace=hg.is_contiguous() and hu.is_contiguous())
             del hg, hu
             if need_wg:
                 grad_w_gate = _mm(dg.t(), x_2d, "gemm_wgrad_gate")

@@ -12,8 +12,11 @@ LoRA adapter terms (`lora=` / `lora_gate=`, `lora_up=`): PEFT's
 the reference does (src/flashffn.py:1414,1420,1439,1529,1558-1566), for ranks
 8 and 16.
 
+mm_any          any dtype and any strides (cpt_gemm_any, fp32 MFMA): float32
+                (config C1), float16, unaligned bf16 views, rank-1 factors.
+
 These replace the cuBLAS GEMMs the reference issues through F.linear / @
-(src/flashffn.py:1410-1439,1503-1587).  bf16 only: the MFMA path.
+(src/flashffn.py:1410-1439,1503-1587).
 """
 
 from __future__ import annotations
@@ -26,21 +29,25 @@ from .kernels import _require_device, _stream, _timed
 
 
 def _layout_a(a: torch.Tensor):
-    """(tensor, ld, kmajor) for a logical [M, K] operand."""
-    if a.stride(1) == 1 and a.stride(0) % 8 == 0 and a.stride(0) >= a.shape[1]:
-        return a, a.stride(0), 1
-    if a.stride(0) == 1 and a.stride(1) % 8 == 0 and a.stride(1) >= a.shape[0]:
-        return a, a.stride(1), 0
+    """(tensor, ld, kmajor) for a logical [M, K] operand: rows 16-byte aligned
+    in place, otherwise a contiguous copy."""
+    if a.data_ptr() % 16 == 0:
+        if a.stride(1) == 1 and a.stride(0) % 8 == 0 and a.stride(0) >= a.shape[1]:
+            return a, a.stride(0), 1
+        if a.stride(0) == 1 and a.stride(1) % 8 == 0 and a.stride(1) >= a.shape[0]:
+            return a, a.stride(1), 0
     a = a.contiguous()
     return a, a.stride(0), 1
 
 
 def _layout_b(b: torch.Tensor):
-    """(tensor, ld, kmajor) for a logical [K, N] operand (kmajor: stored [N][ld])."""
-    if b.stride(0) == 1 and b.stride(1) % 8 == 0 and b.stride(1) >= b.shape[0]:
-        return b, b.stride(1), 1
-    if b.stride(1) == 1 and b.stride(0) % 8 == 0 and b.stride(0) >= b.shape[1]:
-        return b, b.stride(0), 0
+    """(tensor, ld, kmajor) for a logical [K, N] operand (kmajor: stored [N][ld]):
+    rows 16-byte aligned in place, otherwise a contiguous copy."""
+    if b.data_ptr() % 16 == 0:
+        if b.stride(0) == 1 and b.stride(1) % 8 == 0 and b.stride(1) >= b.shape[0]:
+            return b, b.stride(1), 1
+        if b.stride(1) == 1 and b.stride(0) % 8 == 0 and b.stride(0) >= b.shape[1]:
+            return b, b.stride(0), 0
     b = b.contiguous()
     return b, b.stride(0), 0
 
@@ -354,13 +361,16 @@ def ffn_gate_up(x, w_gate, w_up, cache: int, group_size: int, want_h_mid: bool =
 
 
 def ffn_down_dgrad(grad_y, w_down, cache: int, group_size: int, c_gate, s_gate, c_up, s_up,
-                   want_h_mid: bool, lora=None, outliers=None):
+                   want_h_mid: bool, lora=None, outliers=None, inplace: bool = False):
     """Fused grad_y @ w_down + dequantise + SwiGLU backward.
     Returns (grad_h_gate, grad_h_up, h_mid_hat | None).  lora = (gy B_d
     [n, r], A_d [r, inter], s): the down projection's LoRA term of
     grad_h_mid.  outliers = (slot_gate, o_gate, slot_up, o_up): the C3
     outlier channels (int16 slot maps [inter], bf16 blocks [n, k]) that
-    replace their dequantised columns."""
+    replace their dequantised columns.  `inplace=True` (bf16 cache only)
+    writes grad_h_gate / grad_h_up over c_gate / c_up, which must be
+    contiguous and private to the caller (the in-place GLU backward,
+    src/flashffn.py:129-198)."""
     _require_device(grad_y, w_down)
     _check_bf16(grad_y, w_down)
     n, hdim = grad_y.shape
@@ -368,8 +378,13 @@ def ffn_down_dgrad(grad_y, w_down, cache: int, group_size: int, c_gate, s_gate, 
     assert w_down.shape == (hdim, d)
     grad_y, w_down = grad_y.contiguous(), w_down.contiguous()
     dev = grad_y.device
-    dg = torch.empty((n, d), dtype=torch.bfloat16, device=dev)
-    du = torch.empty((n, d), dtype=torch.bfloat16, device=dev)
+    if inplace:
+        assert cache == _lib.CACHE_BF16 and c_gate.is_contiguous() and c_up.is_contiguous()
+        assert tuple(c_gate.shape) == (n, d) and tuple(c_up.shape) == (n, d)
+        dg, du = c_gate, c_up
+    else:
+        dg = torch.empty((n, d), dtype=torch.bfloat16, device=dev)
+        du = torch.empty((n, d), dtype=torch.bfloat16, device=dev)
     hm = torch.empty((n, d), dtype=torch.bfloat16, device=dev) if want_h_mid else None
 
     keep_in = [None if t is None else t.contiguous() for t in (c_gate, s_gate, c_up, s_up)]
@@ -468,3 +483,35 @@ def mm_splitk(a: torch.Tensor, b: torch.Tensor, alpha: float = 1.0, splits: int 
                                          _stream(a))
     check(rc, name)
     return c if ldc == N else c[:, :N]
+
+
+# epilogues of the general-layout GEMM (cpt_gemm_any)
+ANY_STORE, ANY_ADD, ANY_SCALE = 0, 1, 2
+_ANY_DT = {torch.float32: _lib.F32, torch.float16: _lib.F16, torch.bfloat16: _lib.BF16}
+
+
+def mm_any(a: torch.Tensor, b: torch.Tensor, alpha: float = 1.0, mode: int = ANY_STORE,
+           out: torch.Tensor | None = None, name: str = "gemm_any") -> torch.Tensor:
+    """a [M, K] @ b [K, N] for float32 / float16 / bfloat16 operands of any
+    strides, on the fp32 MFMA (cpt_gemm_any): the products the bf16 engine
+    does not take (config C1's float32, unaligned views, rank-1 factors).
+    mode ANY_STORE: rd(a @ b); ANY_SCALE: rd(alpha * rd(a @ b)); ANY_ADD: in
+    place, out = rd(out + rd(alpha * rd(a @ b))), with rd the rounding to the
+    operands' dtype (the reference's eager op order)."""
+    _require_device(a, b)
+    assert a.dim() == 2 and b.dim() == 2, "2-D operands expected"
+    assert a.dtype == b.dtype and a.dtype in _ANY_DT, f"unsupported dtypes {a.dtype}, {b.dtype}"
+    M, K = a.shape
+    K_, N = b.shape
+    assert K == K_, f"inner dims differ: {tuple(a.shape)} @ {tuple(b.shape)}"
+    if mode == ANY_ADD:
+        assert out is not None and tuple(out.shape) == (M, N) and out.dtype == a.dtype
+    else:
+        out = torch.empty((M, N), dtype=a.dtype, device=a.device)
+    with _timed(name):
+        rc = _lib.lib().cpt_gemm_any(_ANY_DT[a.dtype], a.data_ptr(), a.stride(0), a.stride(1),
+                                     b.data_ptr(), b.stride(0), b.stride(1), out.data_ptr(),
+                                     out.stride(0), out.stride(1), M, N, K, float(alpha), mode,
+                                     _stream(a))
+    check(rc, name)
+    return out

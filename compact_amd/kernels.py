@@ -242,10 +242,12 @@ def silu_mul_quant(h_gate, h_up, bits, group_size=64):
 
 
 def dequant_swiglu_backward(grad_h_mid, q_gate, s_gate, q_up, s_up, bits, group_size=64,
-                            want_h_mid=False):
+                            want_h_mid=False, inplace=False):
     """K2 (src/flashffn.py:1343-1373): returns (grad_h_gate, grad_h_up,
     h_mid_hat | None), equal to dequantise-through-bf16 + swiglu_backward
-    (+ silu_mul) without materialising the dequantised caches."""
+    (+ silu_mul) without materialising the dequantised caches.
+    `inplace=True` writes grad_h_gate over grad_h_mid (which must be private
+    to the caller): one [N, D] buffer fewer at the backward's peak."""
     _require_device(grad_h_mid, q_gate, s_gate, q_up, s_up)
     assert grad_h_mid.dim() == 2 and grad_h_mid.is_contiguous()
     assert grad_h_mid.dtype == torch.bfloat16, \
@@ -261,7 +263,7 @@ def dequant_swiglu_backward(grad_h_mid, q_gate, s_gate, q_up, s_up, bits, group_
     assert tuple(q_gate.shape) == expect and tuple(q_up.shape) == expect, \
         f"payload shape {tuple(q_gate.shape)} != expected {expect}"
     q_gate, s_gate, q_up, s_up = (t.contiguous() for t in (q_gate, s_gate, q_up, s_up))
-    grad_h_gate = torch.empty_like(grad_h_mid)
+    grad_h_gate = grad_h_mid if inplace else torch.empty_like(grad_h_mid)
     grad_h_up = torch.empty_like(grad_h_mid)
     h_mid_hat = torch.empty_like(grad_h_mid) if want_h_mid else None
     with _timed("dequant_swiglu_backward"):
@@ -392,12 +394,14 @@ def silu_mul_quant_outlier(h_gate, h_up, bits, group_size, slot_gate, slot_up, k
 
 
 def dequant_swiglu_backward_outlier(grad_h_mid, q_gate, s_gate, o_gate, slot_gate, q_up, s_up,
-                                    o_up, slot_up, bits, group_size, want_h_mid=False):
-    """K2 with the outlier columns restored.  Returns (grad_h_gate, grad_h_up, h_mid^ | None)."""
+                                    o_up, slot_up, bits, group_size, want_h_mid=False,
+                                    inplace=False):
+    """K2 with the outlier columns restored.  Returns (grad_h_gate, grad_h_up,
+    h_mid^ | None); `inplace=True` writes grad_h_gate over grad_h_mid."""
     _require_device(grad_h_mid, q_gate, s_gate, o_gate, slot_gate, q_up, s_up, o_up, slot_up)
     assert grad_h_mid.dtype == torch.bfloat16 and grad_h_mid.is_contiguous()
     n, d = grad_h_mid.shape
-    dg = torch.empty_like(grad_h_mid)
+    dg = grad_h_mid if inplace else torch.empty_like(grad_h_mid)
     du = torch.empty_like(grad_h_mid)
     hm = torch.empty_like(grad_h_mid) if want_h_mid else None
     k = o_gate.shape[1]

@@ -83,7 +83,9 @@ int cpt_silu_mul_quant(const void* h_gate, const void* h_up, int64_t n, int64_t 
 
 /* Replaces triton_dequant_swiglu_backward / K2 _v3_dequant_swiglu_bwd_kernel
  * (src/flashffn.py:1256-1300,1343-1373): dequantise both caches through bf16,
- * SwiGLU backward, and h_mid^ when h_mid_hat is not NULL. */
+ * SwiGLU backward, and h_mid^ when h_mid_hat is not NULL.  grad_h_gate may
+ * be the same buffer as grad_h_mid (written over it); no other output may
+ * alias an input. */
 int cpt_dequant_swiglu_backward(const void* grad_h_mid, const void* q_gate, const void* s_gate,
                                 const void* q_up, const void* s_up, int64_t n, int64_t d,
                                 int bits, int64_t group_size, void* grad_h_gate,
@@ -126,7 +128,8 @@ int cpt_silu_mul_quant_outlier(const void* h_gate, const void* h_up, int64_t n, 
                                void* s_gate, void* o_gate, void* q_up, void* s_up, void* o_up,
                                void* stream);
 
-/* K2 with the outlier columns restored after the bf16 dequantisation. */
+/* K2 with the outlier columns restored after the bf16 dequantisation
+ * (grad_h_gate may be written over grad_h_mid, as in K2). */
 int cpt_dequant_swiglu_backward_outlier(const void* grad_h_mid, const void* q_gate,
                                         const void* s_gate, const void* slot_gate,
                                         const void* o_gate, const void* q_up, const void* s_up,
@@ -184,6 +187,23 @@ int cpt_gemm_bf16_ex(const void* a, int64_t lda, int a_kmajor, const void* b, in
                      int b_kmajor, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K,
                      float alpha, int mode, int splits, void* workspace, void* stream);
 
+/* General-layout GEMM for every product the bf16 engine above does not take:
+ * float32 (config C1) and float16 operands, bf16 views whose rows are not
+ * 16-byte aligned, ranks and widths that are not multiples of 8.  Replaces
+ * the library GEMMs the reference calls through F.linear / @ for those
+ * operands (src/flashffn.py:1410-1439,1503-1587).
+ *   A(m, k) = a[m*sam + k*sak], B(k, n) = b[k*sbk + n*sbn],
+ *   C(m, n) = c[m*scm + n*scn]; a, b, c all of `dtype`.
+ * fp32 accumulation on the fp32 MFMA (bf16 / fp16 products exact); with rd()
+ * the rounding to dtype:
+ *   mode 0: C = rd(A.B)
+ *   mode 1: C = rd(C + rd(alpha * rd(A.B)))   (h + s * F.linear(xa, b))
+ *   mode 2: C = rd(alpha * rd(A.B))           (s * (a @ b))
+ * Any strides (elements, not bytes); pointers aligned to the element size. */
+int cpt_gemm_any(int dtype, const void* a, int64_t sam, int64_t sak, const void* b, int64_t sbk,
+                 int64_t sbn, void* c, int64_t scm, int64_t scn, int64_t M, int64_t N,
+                 int64_t K, float alpha, int mode, void* stream);
+
 /* Low-rank adapter terms folded into a GEMM's output ahead of its epilogue,
  * in PEFT's op order `h + s * B(A(x))` (src/flashffn.py:1414,1420,1439,1529,
  * 1558-1566):
@@ -236,7 +256,9 @@ int cpt_ffn_gate_up_lora(const void* x, const void* w_gate, const void* w_up, in
  * cache (BF16: c_gate/c_up are h_gate/h_up bf16; INT4/INT8: codes + fp16
  * scales, dequantised through bf16) and writes grad_h_gate, grad_h_up and,
  * if h_mid_hat != NULL, h_mid^ = SiLU(hg^)*hu^ (bit-equal to
- * cpt_dequant_swiglu_backward on the same bf16 grad_h_mid). */
+ * cpt_dequant_swiglu_backward on the same bf16 grad_h_mid).  With a BF16
+ * cache, grad_h_gate / grad_h_up may be written over c_gate / c_up (each
+ * element is read before it is overwritten, by the same thread). */
 int cpt_ffn_down_dgrad(const void* grad_y, const void* w_down, int64_t n_tok, int64_t hidden,
                        int64_t inter, int cache, int64_t group_size, const void* c_gate,
                        const void* s_gate, const void* c_up, const void* s_up, void* grad_h_gate,

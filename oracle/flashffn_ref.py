@@ -156,12 +156,22 @@ class OracleFlashFFNv3Function(torch.autograd.Function):
             s_gate, s_up, s_down, cache_mode, group_size, use_triton)
     The Triton kernels are replaced by their oracle contracts; the GEMMs are
     torch CPU F.linear/@ in the tensors' dtype, as the reference runs them.
+
+    Two trailing arguments serve the tests that check a device run on a
+    sample of its rows or against its own cache (neither changes the
+    algorithm, only where one of its inputs comes from):
+      outlier_idx = (idx_gate, idx_up): the outlier channels to keep, instead
+          of ranking this call's rows (a row sample does not hold the first
+          sequence those channels are ranked on);
+      cache_override = (c_gate, qs_gate, c_up, qs_up): the int4/int8 cache to
+          save instead of quantising this call's h_gate / h_up (which a CPU
+          GEMM rounds differently from the device's).
     """
 
     @staticmethod
     def forward(ctx, x, w_gate, a_gate, b_gate, w_up, a_up, b_up, w_down, a_down, b_down,
                 s_gate=0.0, s_up=0.0, s_down=0.0, cache_mode="int4", group_size=64,
-                use_triton=True, outlier_ratio=0.0):
+                use_triton=True, outlier_ratio=0.0, outlier_idx=None, cache_override=None):
         assert cache_mode in ("int4", "int8", "bf16", "recompute"), cache_mode
         orig_shape = x.shape
         hidden_dim = x.shape[-1]
@@ -187,9 +197,12 @@ class OracleFlashFFNv3Function(torch.autograd.Function):
         if k_out > 0:
             # this build's C3 extension: HyC-LoRA outlier channels on the v3 codec
             bits = 4 if cache_mode == "int4" else 8
-            rows = stat_rows(orig_shape)
-            idx_gate = outlier_select(h_gate, outlier_ratio, rows)
-            idx_up = outlier_select(h_up, outlier_ratio, rows)
+            if outlier_idx is not None:
+                idx_gate, idx_up = (np.asarray(i, dtype=np.int64) for i in outlier_idx)
+            else:
+                rows = stat_rows(orig_shape)
+                idx_gate = outlier_select(h_gate, outlier_ratio, rows)
+                idx_up = outlier_select(h_up, outlier_ratio, rows)
             c_gate, qs_gate, o_gate = v3_quantize_outlier(h_gate, bits, group_size, idx_gate)
             c_up, qs_up, o_up = v3_quantize_outlier(h_up, bits, group_size, idx_up)
             h_mid = triton_silu_mul(h_gate, h_up)
@@ -213,6 +226,9 @@ class OracleFlashFFNv3Function(torch.autograd.Function):
                 c_up, qs_up = v3_quantize_group_absmax(h_up, bits, group_size)
             elif cache_mode == "bf16":
                 c_gate, c_up = h_gate, h_up
+        if cache_override is not None:
+            assert cache_mode in ("int4", "int8") and k_out == 0
+            c_gate, qs_gate, c_up, qs_up = cache_override
         ctx.save_for_backward(x, w_gate, a_gate, b_gate, w_up, a_up, b_up,
                               w_down, a_down, b_down, xa_g, xa_u, ha_d,
                               c_gate, qs_gate, c_up, qs_up)              # :1454-1458
@@ -375,9 +391,11 @@ def ref_grads_fp32(ps: dict, x: torch.Tensor, gy: torch.Tensor):
 
 
 def run_function_grads(fn_apply, ps: dict, x, gy, mode: str, group_size: int,
-                       use_triton: bool = True, outlier_ratio: float = 0.0):
+                       use_triton: bool = True, outlier_ratio: float = 0.0, *extra):
     """Run an FFN v3 Function (oracle or product) on leaf clones of `ps`.
-    Mirrors src/verify_flashffn_v3.py:259-291.  Returns ({name: grad}, y)."""
+    Mirrors src/verify_flashffn_v3.py:259-291.  `extra` are further trailing
+    arguments of the Function (the oracle's outlier_idx / cache_override).
+    Returns ({name: grad}, y)."""
     def leaf(t, rg):
         return None if t is None else t.detach().clone().requires_grad_(rg)
 
@@ -392,7 +410,7 @@ def run_function_grads(fn_apply, ps: dict, x, gy, mode: str, group_size: int,
                  t["w_up"], t["a_up"], t["b_up"],
                  t["w_down"], t["a_down"], t["b_down"],
                  ps["s_gate"], ps["s_up"], ps["s_down"], mode, group_size, use_triton,
-                 outlier_ratio)
+                 outlier_ratio, *extra)
     y.backward(gy)
     grads = {"grad_x": xl.grad}
     for k, tt in t.items():

@@ -149,24 +149,39 @@ def test_k2_vs_oracle_and_unfused(device, kind, bits, group):
 
 @pytest.mark.parametrize("n", [1, 7, 512, 2048, 8192])
 @pytest.mark.parametrize("d", [5632, 11008, 14336])
-@pytest.mark.parametrize("bits", [4, 8])
-def test_shape_sweep(device, n, d, bits):
+@pytest.mark.parametrize("bits,group", [(4, 64), (8, 64), (4, 128), (8, 128)])
+def test_shape_sweep(device, n, d, bits, group):
+    """The reference's G4 (src/verify_v3_kernels.py:357-414): K1 and K2 at
+    every shape, each bitwise against its unfused composition, and the
+    oracle on 16 sampled rows (rows are independent)."""
     cpt = _lib()
-    group = 64
-    gen = torch.Generator(device=device).manual_seed(n * 7 + d + bits)
+    gen = torch.Generator(device=device).manual_seed(n * 7 + d + bits + group)
     a = (torch.randn(n, d, device=device, generator=gen) * 3).to(torch.bfloat16)
     b = (torch.randn(n, d, device=device, generator=gen) * 2).to(torch.bfloat16)
+    gm = torch.randn(n, d, device=device, generator=gen).to(torch.bfloat16)
     hm, qg, sg, qu, su = cpt.silu_mul_quant(a, b, bits, group)
     q2, s2 = cpt.v3_quantize_group_absmax(a, bits, group)
     assert torch.equal(qg.view(torch.uint8), q2.view(torch.uint8))
     assert torch.equal(sg.view(torch.int16), s2.view(torch.int16))
     assert torch.equal(hm.view(torch.int16), cpt.silu_mul(a, b).view(torch.int16))
+    dg, du, hmh = cpt.dequant_swiglu_backward(gm, qg, sg, qu, su, bits, group, want_h_mid=True)
+    hg = cpt.v3_dequantize_group_absmax(qg, sg, bits, group)
+    hu = cpt.v3_dequantize_group_absmax(qu, su, bits, group)
+    ug, uu, uh = cpt.swiglu_backward_glu(gm, hg, hu, True)
+    for x, y in ((dg, ug), (du, uu), (hmh, uh)):
+        assert torch.equal(x.view(torch.int16), y.view(torch.int16))
     rows = torch.randperm(n, generator=torch.Generator().manual_seed(1))[:16]
     ra, rb = to_f32(a.cpu()[rows]), to_f32(b.cpu()[rows])
     rq, rs = codec.quantize_group_absmax(rb, bits, group)
     payload_equal(qu.cpu()[rows], rq)
     scales_equal(su.cpu()[rows], rs)
     close(hm.cpu()[rows], codec.round_bf16(codec.silu_mul(ra, rb)))
+    rdg, rdu, rhm = codec.dequant_swiglu_backward(
+        to_f32(gm.cpu()[rows]), qg.cpu()[rows].numpy(), sg.cpu()[rows].numpy(),
+        qu.cpu()[rows].numpy(), su.cpu()[rows].numpy(), bits, group, want_h_mid=True)
+    close(dg.cpu()[rows], codec.round_bf16(rdg))
+    close(du.cpu()[rows], codec.round_bf16(rdu))
+    close(hmh.cpu()[rows], codec.round_bf16(rhm))
 
 
 def test_ragged_group_raises(device):

@@ -86,3 +86,4 @@ def test_mfma_layout_rule():
     assert not _mfma(torch.zeros(256, 12, dtype=bf)[:, :8])  # rows 12 elements apart
     assert not _mfma(torch.zeros(8, 8, dtype=torch.float32))
     assert _mfma(torch.zeros(16, 768, dtype=bf)[:4])         # a row slice of a weight
+    assert not _mfma(torch.zeros(4, 264, dtype=bf)[:, 1:257])  # rows 2 bytes off 16-byte alignment

@@ -144,3 +144,35 @@ def test_outlier_cache_function_invariants():
     err_plain = sum(R.rel_frob(plain[k], ref[k]) for k in ref)
     err_outl = sum(R.rel_frob(outl[k], ref[k]) for k in ref)
     assert err_outl <= err_plain
+
+
+@pytest.mark.parametrize("dtype,mode,gs,ratio", [(torch.float32, "int8", 128, 0.0),
+                                                 (torch.bfloat16, "int4", 64, 0.0),
+                                                 (torch.bfloat16, "int4", 64, 0.05)])
+def test_oracle_injection_arguments_keep_the_algorithm(dtype, mode, gs, ratio):
+    """outlier_idx / cache_override given the values the oracle would compute
+    itself leave every output and gradient bit-identical, so a test that
+    injects the device's own channels or cache checks the same algorithm."""
+    ps = R.synthetic_param_set("all", 32, 128, 4, 2.0, seed=21, dtype=dtype)
+    g = torch.Generator().manual_seed(22)
+    x = torch.randn(2, 24, 32, generator=g).to(dtype)
+    gy = torch.randn(2, 24, 32, generator=g).to(dtype)
+    base, y0 = R.run_function_grads(R.OracleFlashFFNv3Function.apply, ps, x, gy, mode, gs,
+                                    True, ratio)
+    x2 = x.reshape(-1, 32)
+    hg = F.linear(x2, ps["w_gate"]) + ps["s_gate"] * F.linear(F.linear(x2, ps["a_gate"]),
+                                                            ps["b_gate"])
+    hu = F.linear(x2, ps["w_up"]) + ps["s_up"] * F.linear(F.linear(x2, ps["a_up"]), ps["b_up"])
+    bits = 4 if mode == "int4" else 8
+    if ratio > 0:
+        rows = R.stat_rows(x.shape)
+        extra = ((R.outlier_select(hg, ratio, rows), R.outlier_select(hu, ratio, rows)), None)
+    else:
+        qg, sg = R.v3_quantize_group_absmax(hg, bits, gs)
+        qu, su = R.v3_quantize_group_absmax(hu, bits, gs)
+        extra = (None, (qg, sg, qu, su))
+    got, y1 = R.run_function_grads(R.OracleFlashFFNv3Function.apply, ps, x, gy, mode, gs, True,
+                                   ratio, *extra)
+    assert torch.equal(y0, y1)
+    for k in base:
+        assert torch.equal(base[k], got[k]), k
