@@ -49,6 +49,8 @@ SIGNATURES = {
     "cpt_gemm_bf16_skinny": [_P, _L, _P, _L, _P, _L, _L, _L, _L, ctypes.c_float, _I, _P, _P],
     "cpt_gemm_bf16_skinny_t": [_P, _L, _P, _L, _P, _L, _I, _L, _L, _L, ctypes.c_float, _I, _P,
                                _P],
+    "cpt_gemm_bf16_skinny_t_noalloc": [_P, _L, _P, _L, _P, _L, _I, _L, _L, _L, ctypes.c_float,
+                                       _I, _P],
     "cpt_ffn_down_dgrad_outlier": [_P, _P, _L, _L, _L, _I, _L, _P, _P, _P, _P, _P, _P, _P, _P,
                                    _L, _P, _P, _P, _L, _L, _P, _P, ctypes.c_float, _P],
     "cpt_dora_scale": [_P, _P, _P, _L, _L, _I, _P, _P],
@@ -65,6 +67,8 @@ SIZE_QUERIES = {
 }
 
 CACHE_NONE, CACHE_BF16, CACHE_INT4, CACHE_INT8 = 0, 1, 4, 8
+
+NOALLOC_SCRATCH_BYTES = 16 << 20    # CPT_NOALLOC_SCRATCH_BYTES
 
 _lib = None
 

@@ -19,6 +19,8 @@
 // and B[8 (l / 16) + e][l % 16], e = 0..7; the result lane l holds
 // D[4 (l / 16) + i][l % 16], i = 0..3.
 
+#include <mutex>
+
 #include "common.h"
 #include "compact_amd.h"
 
@@ -284,6 +286,42 @@ __global__ __launch_bounds__(256) void skinny_red_reduce_kernel(const float* __r
 
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// ---------------------------------------------------------------------------
+// Scratch for cpt_gemm_bf16_skinny_t_noalloc: the split partials live in this
+// fixed device array instead of a caller workspace, for callers that cannot
+// allocate (HIP graph capture, serving loops).  Each GPU holds its own copy,
+// at its own address, for the life of the process; host code reaches it only
+// through the address hipGetSymbolAddress returns for the current device
+// (the array's name is a host-side stand-in, not a device address).  Every
+// call on a GPU shares that GPU's array: calls that overlap on one GPU race.
+// The kernels write every partial they later sum, so nothing needs clearing.
+// ---------------------------------------------------------------------------
+constexpr int64_t kScratchBytes = (int64_t)16 << 20;   // CPT_NOALLOC_SCRATCH_BYTES
+static __device__ __align__(256) float scratch[kScratchBytes / 4];
+
+constexpr int kMaxDevices = 64;
+
+// The current device's address of `scratch`, looked up once per device.
+inline int scratch_ptr(void** out) {
+  static std::mutex mu;
+  static void* ptrs[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return kErrLaunch;
+  if (dev < 0 || dev >= kMaxDevices) return kErrShape;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptrs[dev]) {
+    void* ptr = nullptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return kErrLaunch;
+    ptrs[dev] = ptr;
+  }
+  *out = ptrs[dev];
+  return kOk;
+}
+
+int skinny_t_impl(const void* x, int64_t ldx, const void* p, int64_t ldp, void* out,
+                  int64_t ldo, int out_trans, int64_t T, int64_t N, int64_t R, float alpha,
+                  int splits, void* workspace, int64_t workspace_bytes, void* stream);
+
 }  // namespace skinny
 }  // namespace cpt
 
@@ -330,9 +368,39 @@ int cpt_gemm_bf16_skinny(const void* a, int64_t lda, const void* q, int64_t ldq,
   return kOk;
 }
 
+}  // extern "C"
+
+extern "C" {
+
 int cpt_gemm_bf16_skinny_t(const void* x, int64_t ldx, const void* p, int64_t ldp, void* out,
                            int64_t ldo, int out_trans, int64_t T, int64_t N, int64_t R,
                            float alpha, int splits, void* workspace, void* stream) {
+  return skinny_t_impl(x, ldx, p, ldp, out, ldo, out_trans, T, N, R, alpha, splits, workspace, -1,
+                       stream);
+}
+
+int cpt_gemm_bf16_skinny_t_noalloc(const void* x, int64_t ldx, const void* p, int64_t ldp,
+                                   void* out, int64_t ldo, int out_trans, int64_t T, int64_t N,
+                                   int64_t R, float alpha, int splits, void* stream) {
+  if (T < 0 || N < 0 || R < 0 || splits < 1 || R > 32) return kErrShape;
+  if (N == 0 || R == 0) return kOk;
+  void* ws = nullptr;
+  if (const int rc = scratch_ptr(&ws)) return rc;
+  return skinny_t_impl(x, ldx, p, ldp, out, ldo, out_trans, T, N, R, alpha, splits, ws,
+                       kScratchBytes, stream);
+}
+
+}  // extern "C"
+
+namespace cpt {
+namespace skinny {
+
+// workspace_bytes < 0: the caller's workspace holds splits * N * R floats
+// (cpt_gemm_bf16_skinny_t's contract); otherwise the split partials must fit
+// in workspace_bytes.
+int skinny_t_impl(const void* x, int64_t ldx, const void* p, int64_t ldp, void* out,
+                  int64_t ldo, int out_trans, int64_t T, int64_t N, int64_t R, float alpha,
+                  int splits, void* workspace, int64_t workspace_bytes, void* stream) {
   if (T < 0 || N < 0 || R < 0 || splits < 1) return kErrShape;
   if (R > 32) return kErrShape;
   if (N == 0 || R == 0) return kOk;
@@ -350,6 +418,7 @@ int cpt_gemm_bf16_skinny_t(const void* x, int64_t ldx, const void* p, int64_t ld
     return kErrTooLarge;
   const int64_t blocks = (N + kRedCols - 1) / kRedCols;
   if (blocks > 0x7FFFFFFF || splits > 65535) return kErrTooLarge;
+  if (workspace_bytes >= 0 && (int64_t)splits * N * R * 4 > workspace_bytes) return kErrTooLarge;
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)blocks, (unsigned)splits);
   if (R <= 16)
@@ -366,4 +435,5 @@ int cpt_gemm_bf16_skinny_t(const void* x, int64_t ldx, const void* p, int64_t ld
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
-}  // extern "C"
+}  // namespace skinny
+}  // namespace cpt

@@ -180,8 +180,7 @@ def skinny_t(x: torch.Tensor, p: torch.Tensor, alpha: float = 1.0, trans: bool =
         x = x.contiguous()
     if not _row_major(p) or p.stride(0) < R:
         p = p.contiguous()
-    blocks = (N + 63) // 64
-    splits = max(1, min(max(T // 256, 1), (768 + blocks - 1) // blocks))
+    splits = skinny_t_splits(T, N)
     # each split reads its tokens (plus 128 of prefetch) within 32-bit offsets
     per = (_SPAN_BYTES // (2 * max(x.stride(0), p.stride(0))) - 129) // 64 * 64
     assert per >= 64, "operand rows too long for 32-bit buffer offsets"
@@ -194,6 +193,37 @@ def skinny_t(x: torch.Tensor, p: torch.Tensor, alpha: float = 1.0, trans: bool =
                                                1 if trans else 0, T, N, R, float(alpha), splits,
                                                ws.data_ptr(), _stream(x))
     check(rc, name)
+    return out
+
+
+def skinny_t_splits(T: int, N: int) -> int:
+    """Token splits of the token-reduction kernel: ~768 blocks of 64 columns."""
+    blocks = (N + 63) // 64
+    return max(1, min(max(T // 256, 1), (768 + blocks - 1) // blocks))
+
+
+def skinny_t_noalloc(x: torch.Tensor, p: torch.Tensor, out: torch.Tensor, alpha: float = 1.0,
+                     trans: bool = False, splits: int | None = None,
+                     name: str = "gemm_skinny_t_noalloc") -> torch.Tensor:
+    """skinny_t into a caller-provided `out` through the allocation-free entry
+    point: the split partials use the library's fixed per-GPU scratch, so the
+    call allocates nothing (x, p token-major rows 16-byte aligned; out [N, R],
+    or [R, N] with trans, rows `out.stride(0)` apart)."""
+    _require_device(x, p, out)
+    _check_bf16(x, p)
+    T, N = x.shape
+    R = p.shape[1]
+    assert p.shape[0] == T and out.dtype == torch.bfloat16 and out.stride(1) == 1
+    assert tuple(out.shape) == ((R, N) if trans else (N, R))
+    assert _row_major(x) and _row_major(p), "x and p must have 16-byte aligned rows"
+    if splits is None:
+        splits = skinny_t_splits(T, N)
+    with _timed(name):
+        rc = _lib.lib().cpt_gemm_bf16_skinny_t_noalloc(
+            x.data_ptr(), x.stride(0), p.data_ptr(), p.stride(0), out.data_ptr(), out.stride(0),
+            1 if trans else 0, T, N, R, float(alpha), splits, _stream(x))
+    check(rc, f"{name} (split partials beyond the {_lib.NOALLOC_SCRATCH_BYTES >> 20} MiB "
+              "scratch?)" if rc == _lib.ERR_TOO_LARGE else name)
     return out
 
 

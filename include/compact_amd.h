@@ -175,6 +175,20 @@ int cpt_gemm_bf16_skinny_t(const void* x, int64_t ldx, const void* p, int64_t ld
                            int64_t ldo, int out_trans, int64_t T, int64_t N, int64_t R,
                            float alpha, int splits, void* workspace, void* stream);
 
+/* No counterpart in the reference.  cpt_gemm_bf16_skinny_t for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc): the same kernels and result, with the
+ * split partials in a fixed device array of CPT_NOALLOC_SCRATCH_BYTES per GPU
+ * inside the library instead of a caller workspace.  The caller passes the
+ * inputs and the output.  splits * N * R * 4 bytes (after the split count is
+ * normalised as in cpt_gemm_bf16_skinny_t) must fit, else CPT_ERR_TOO_LARGE.
+ * The array persists until the process ends and every call on a GPU shares
+ * it: calls that overlap on one GPU (two streams, two threads) race. */
+#define CPT_NOALLOC_SCRATCH_BYTES (16 << 20)
+int cpt_gemm_bf16_skinny_t_noalloc(const void* x, int64_t ldx, const void* p, int64_t ldp,
+                                   void* out, int64_t ldo, int out_trans, int64_t T, int64_t N,
+                                   int64_t R, float alpha, int splits, void* stream);
+
 /* Extended GEMM for the adapter (LoRA) terms, one operand pair:
  *   mode 0: C = bf16(A.B)
  *   mode 1: C = bf16(C + bf16(alpha * bf16(A.B)))   (PEFT's h + s * B(A(x)),
