@@ -6,11 +6,16 @@ full fine-tune (dense weight grads), synthetic seeded inputs.
   python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
 
 Prints ONE JSON line.  A step is one forward + backward of the FFN block on
-the same resident inputs.  `roofline` is for the dominant HIP kernel of this
-build, timed live with HIP events on its launch stream inside the timed steps;
-`kernels` lists every timed kernel.  `cpu_baseline` times the CPU oracle (the
-restatement of the reference's FlashFFNv3Function; the reference itself
-cannot run on a CPU) on a bounded sample of the same workload.
+the same resident inputs.  The headline (`value`, `ms_per_step` = the mean
+over the K timed steps, plus their median / p10 / p90 from one HIP event
+pair per step) is timed with no per-kernel events.  A second pass over K
+more steps records HIP events around every kernel on its launch stream:
+`kernels` lists them and `roofline` is the dominant HIP kernel's rate from
+that pass.  The same line carries C3 (LoRA r16, int4 g64 + 1% outlier
+channels) under "c3", timed the same way.  `cpu_baseline` times the CPU
+oracle (the restatement of the reference's FlashFFNv3Function; the reference
+itself cannot run on a CPU) on a bounded sample of C2, and config C1 (the
+reference's own CPU case) at full size under "c1_full".
 """
 
 from __future__ import annotations
@@ -25,9 +30,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
-# workload C2; C3 with --workload c3
-N_TOK, HID, INTER, GROUP, BITS = 8 * 1024, 4096, 11008, 128, 8
-MODE = "int8"
+HID, INTER, N_TOK = 4096, 11008, 8 * 1024
 WORKLOADS = {
     "c2": dict(group=128, bits=8, mode="int8", lora_rank=0, outlier_ratio=0.0,
                desc="C2: SwiGLU FFN fwd+bwd, d_model=4096, d_ff=11008, 8x1024 tokens, bf16, "
@@ -56,15 +59,17 @@ def codec_bytes(n, d, bits, group, want_h_mid=True):
     return k1, k2
 
 
-def algorithmic_work(n, h, d):
+def algorithmic_work(n, h, d, bits, group):
     """Per-launch algorithmic work of every timed kernel: (amount, bound),
     FLOPs for the MFMA-bound GEMMs (2*M*N*K per product), bytes for the
     HBM-bound standalone codec kernels."""
-    k1_bytes, k2_bytes = codec_bytes(n, d, BITS, GROUP)
+    k1_bytes, k2_bytes = codec_bytes(n, d, bits, group)
     gemm = 2 * n * h * d
     return {
         "ffn_gate_up": (2 * gemm, "mfma"),          # x @ [Wg; Wu]^T (+ GLU + codec)
         "gemm_fwd_down": (gemm, "mfma"),            # h_mid @ Wd^T
+        "gemm_fwd_gate": (gemm, "mfma"),
+        "gemm_fwd_up": (gemm, "mfma"),
         "ffn_down_dgrad": (gemm, "mfma"),           # gy @ Wd (+ dequant + SwiGLU bwd)
         "gemm_dgrad_down": (gemm, "mfma"),          # gy @ Wd (K2 runs after it)
         "gemm_wgrad_down": (gemm, "mfma"),          # gy^T @ h_mid^
@@ -101,33 +106,62 @@ def saved_bytes(fn, exclude_ptrs):
     return total
 
 
-def cpu_baseline(budget_tokens=512):
-    """Times the CPU oracle's FlashFFNv3Function (fp32, int8 g128, full-FT)
-    on `budget_tokens` tokens of the C2 shape: 1 warmup + 3 reps, median."""
+def cpu_model() -> str:
+    """The host CPU's model name (what lscpu prints as 'Model name')."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.lower().startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _oracle_median(ps, x, gy, mode, group, reps=3):
+    """1 warmup + `reps` timed fwd+bwd of the CPU oracle Function: median s."""
+    from oracle import flashffn_ref as R
+    times = []
+    for rep in range(reps + 1):
+        t0 = time.perf_counter()
+        R.run_function_grads(R.OracleFlashFFNv3Function.apply, ps, x, gy, mode, group)
+        if rep:
+            times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def cpu_baseline(c2_tokens=2048):
+    """The CPU oracle's FlashFFNv3Function (the reference's algorithm restated;
+    the reference itself cannot run on a CPU) on the host's threads as the
+    environment sets them (torch's default, OMP_NUM_THREADS):
+      value   C2's shape (H 4096, D 11008, int8 g128, full-FT) on a bounded
+              sample of `c2_tokens` tokens, in fp32 (CPU bf16 GEMM support
+              varies by host);
+      c1_full config C1 exactly: fp32, 4 x 512 tokens, H 2048, D 5632, int8
+              g128, full-FT, seed 0.
+    1 warmup + 3 timed reps each, median; tokens/s = tokens / median."""
     import torch
     from oracle import flashffn_ref as R
-    torch.set_num_threads(os.cpu_count() or 1)
-    ps = R.synthetic_param_set("fullft", HID, INTER, 0, 0.0, seed=0, dtype=torch.float32)
-    g = torch.Generator().manual_seed(0)
-    x = torch.randn(budget_tokens, HID, generator=g)
-    gy = torch.randn(budget_tokens, HID, generator=g)
-    times = []
-    for rep in range(4):
-        t0 = time.perf_counter()
-        R.run_function_grads(R.OracleFlashFFNv3Function.apply, ps, x, gy, MODE, GROUP)
-        dt = time.perf_counter() - t0
-        if rep:
-            times.append(dt)
-    times.sort()
-    med = times[len(times) // 2]
-    return {"value": budget_tokens / med, "unit": "tokens/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"{budget_tokens} tokens of C2 (H={HID}, D={INTER}), fp32, int8 g{GROUP}, "
-                      f"full-FT fwd+bwd; oracle FlashFFNv3Function on CPU, median of 3",
-            "median_s": med}
+    out = {}
+    for key, (n, h, d) in (("c2", (c2_tokens, HID, INTER)), ("c1", (2048, 2048, 5632))):
+        ps = R.synthetic_param_set("fullft", h, d, 0, 0.0, seed=0, dtype=torch.float32)
+        g = torch.Generator().manual_seed(0)
+        x = torch.randn(n, h, generator=g)
+        gy = torch.randn(n, h, generator=g)
+        out[key] = (n, _oracle_median(ps, x, gy, "int8", 128))
+    (n2, t2), (n1, t1) = out["c2"], out["c1"]
+    return {"value": n2 / t2, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port", "cpu": cpu_model(),
+            "sample": f"{n2} tokens of C2 (H={HID}, D={INTER}), fp32, int8 g128, full-FT "
+                      "fwd+bwd; oracle FlashFFNv3Function on CPU, median of 3",
+            "median_s": t2,
+            "c1_full": {"value": n1 / t1, "unit": "tokens/s", "median_s": t1,
+                        "sample": "config C1 at full size: fp32, 4x512 tokens, d_model 2048, "
+                                  "d_ff 5632, int8 g128, full-FT fwd+bwd, seed 0"}}
 
 
-def library_arm(x, gy, wg, wu, wd, steps, warmup, frozen=False):
+def library_arm(x, gy, wg, wu, wd, steps, warmup, bits, group, frozen=False):
     """The same C2 step in the reference's structure (src/flashffn.py:1409-1587)
     with every GEMM through torch.matmul (hipBLASLt on ROCm) and the codec as the
     standalone K1 / K2 kernels of this build: what the reference's composition
@@ -140,12 +174,12 @@ def library_arm(x, gy, wg, wu, wd, steps, warmup, frozen=False):
     def lib_step():
         hg = x @ wg.t()
         hu = x @ wu.t()
-        h_mid, cg, sg, cu, su = K.silu_mul_quant(hg, hu, BITS, GROUP)
+        h_mid, cg, sg, cu, su = K.silu_mul_quant(hg, hu, bits, group)
         del hg, hu
         y = h_mid @ wd.t()
         del h_mid, y
         ghm = gy @ wd
-        dg, du, hmh = K.dequant_swiglu_backward(ghm, cg, sg, cu, su, BITS, GROUP,
+        dg, du, hmh = K.dequant_swiglu_backward(ghm, cg, sg, cu, su, bits, group,
                                                 want_h_mid=not frozen)
         del ghm
         gx = dg @ wg
@@ -169,6 +203,29 @@ def library_arm(x, gy, wg, wu, wd, steps, warmup, frozen=False):
         e1.record(stream)
         torch.cuda.synchronize()
     return e0.elapsed_time(e1) / steps
+
+
+def timed_steps(step, steps):
+    """`steps` calls of step() bracketed by synchronize, one HIP event pair
+    per step on the current stream.  Returns (total_ms, sorted per-step ms)."""
+    import torch
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for a, b in ev:
+        a.record(stream)
+        step()
+        b.record(stream)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1), sorted(a.elapsed_time(b) for a, b in ev)
+
+
+def _pct(sorted_ms, q):
+    return sorted_ms[min(len(sorted_ms) - 1, int(q * (len(sorted_ms) - 1) + 0.5))]
 
 
 def measured_traffic(kernel: str, workload: str):
@@ -247,11 +304,7 @@ def model_step_bench(args):
     assert cpt._V3_COUNTERS["forward"] == args.steps * cfg["layers"], cpt._V3_COUNTERS
     kern = kt.avg_ms()
     h, d = cfg["hidden"], cfg["inter"]
-    global GROUP, BITS
-    GROUP, BITS = cfg["group"], 4 if cfg["cache_mode"] == "int4" else 8
-    work = algorithmic_work(n_tok, h, d)
-    work["gemm_fwd_gate"] = work["gemm_fwd_up"] = work["gemm_dgrad_down"] = \
-        (2 * n_tok * h * d, "mfma")
+    work = algorithmic_work(n_tok, h, d, 4 if cfg["cache_mode"] == "int4" else 8, cfg["group"])
     dom_name = max((k for k in kern if k in work), key=lambda k: kern[k]["total_ms"])
     amount, bound = work[dom_name]
     rate = amount / (kern[dom_name]["avg_ms"] * 1e-3)
@@ -282,40 +335,12 @@ def model_step_bench(args):
     print(json.dumps(out))
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--tokens", type=int, default=N_TOK)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-tokens", type=int, default=512)
-    ap.add_argument("--no-library-arm", action="store_true",
-                    help="skip timing the hipBLASLt composition of the same step")
-    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["c4", "c5"], default="c2",
-                    help="c2 (default) / c3: the FFN block; c4 / c5: a whole-model training "
-                         "step (TinyLlama full-FT / Llama-7B LoRA) with every MLP on FlashFFN v3")
-    ap.add_argument("--probe", action="store_true",
-                    help="HBM-counter probe (run under rocprofv3 --pmc): a 1 GiB calibration "
-                         "copy, then --steps untimed steps; prints one status line")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
-                                   "(multi-GPU sharding is a design note, not a code path)"}))
-        sys.exit(2)
-    if args.workload in ("c4", "c5"):
-        model_step_bench(args)
-        return
-    wl = WORKLOADS[args.workload]
-    global GROUP, BITS, MODE
-    GROUP, BITS, MODE = wl["group"], wl["bits"], wl["mode"]
-
+def ffn_case(name, n, dev):
+    """Seeded C2 / C3 inputs on the device and the Function step over them."""
     import torch
     import compact_amd as cpt
-    from compact_amd.kernels import KernelTimer
-
-    dev = torch.device("cuda:0")
-    n, h, d = args.tokens, HID, INTER
+    wl = WORKLOADS[name]
+    h, d = HID, INTER
     batch = 8 if n % 8 == 0 else 1          # 8 sequences of 1024 tokens at the default size
     g = torch.Generator(device=dev).manual_seed(0)
     x = torch.randn(n, h, device=dev, generator=g).to(torch.bfloat16)
@@ -350,7 +375,7 @@ def main():
         return cpt.FlashFFNv3Function.apply(
             x.view(batch, n // batch, h), wg, lora.get("a_gate"), lora.get("b_gate"),
             wu, lora.get("a_up"), lora.get("b_up"), wd, lora.get("a_down"), lora.get("b_down"),
-            scale, scale, scale, MODE, GROUP, True, wl["outlier_ratio"])
+            scale, scale, scale, wl["mode"], wl["group"], True, wl["outlier_ratio"])
 
     def step():
         for p in params + (x,):
@@ -358,51 +383,43 @@ def main():
         y = fwd()
         y.backward(gy.view_as(y))
 
-    if args.probe:
-        # calibration: torch's copy kernel reads and writes exactly PROBE_COPY_BYTES
-        src = torch.ones(PROBE_COPY_BYTES // 2, device=dev, dtype=torch.bfloat16)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        del src, dst
-        for _ in range(args.steps):
-            step()
-        torch.cuda.synchronize()
-        print(json.dumps({"probe": args.workload, "steps": args.steps,
-                          "copy_bytes": PROBE_COPY_BYTES}))
-        return
+    return dict(wl=wl, n=n, batch=batch, x=x, gy=gy, wg=wg, wu=wu, wd=wd, params=params,
+                fwd=fwd, step=step, full_ft=full_ft, frozen=frozen)
 
-    for _ in range(args.warmup):
-        step()
+
+def run_ffn(name, n, steps, warmup, dev, library=True):
+    """Headline, per-kernel pass and saved bytes of one FFN workload."""
+    import torch
+    import compact_amd as cpt
+    from compact_amd.kernels import KernelTimer
+    c = ffn_case(name, n, dev)
+    wl, h, d = c["wl"], HID, INTER
+    for _ in range(warmup):
+        c["step"]()
     torch.cuda.synchronize()
     cpt.v3_reset_counters()
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    total_ms, per_step = timed_steps(c["step"], steps)
+    ms = total_ms / steps
+    assert cpt._V3_COUNTERS["triton_quant_fwd"] == steps, "the fused codec (K1) did not run"
+    assert cpt._V3_COUNTERS["triton_dequant_bwd"] == steps, "the fused dequant (K2) did not run"
+
+    # per-kernel pass: HIP events on each kernel's launch stream, separate steps
     with KernelTimer() as kt:
-        torch.cuda.synchronize()
-        e0.record(stream)
-        for _ in range(args.steps):
-            step()
-        e1.record(stream)
-        torch.cuda.synchronize()
-    total_ms = e0.elapsed_time(e1)
-    ms = total_ms / args.steps
-    assert cpt._V3_COUNTERS["triton_quant_fwd"] == args.steps, "fused codec (K1) did not run"
-    assert cpt._V3_COUNTERS["triton_dequant_bwd"] == args.steps, "fused dequant (K2) did not run"
+        timed_steps(c["step"], steps)
     kern = kt.avg_ms()
 
     # parameters (trainable or frozen) and x are excluded, x counted once
     # (src/verify_flashffn_v3.py:523-543,594-597)
-    all_params = set(params) | {wg, wu, wd}
-    sb = saved_bytes(fwd, {p.data_ptr() for p in all_params} | {x.data_ptr()}) + x.nbytes
+    x = c["x"]
+    all_params = set(c["params"]) | {c["wg"], c["wu"], c["wd"]}
+    sb = saved_bytes(c["fwd"], {p.data_ptr() for p in all_params} | {x.data_ptr()}) + x.nbytes
 
-    algo = algorithmic_work(n, h, d)
-    algo["gemm_fwd_gate"] = algo["gemm_fwd_up"] = algo["gemm_dgrad_down"] = (2 * n * h * d, "mfma")
+    algo = algorithmic_work(n, h, d, wl["bits"], wl["group"])
     kernels = {}
-    for name, st in kern.items():
+    for kname, st in kern.items():
         entry = dict(st)
-        if name in algo:
-            amount, bound = algo[name]
+        if kname in algo:
+            amount, bound = algo[kname]
             rate = amount / (st["avg_ms"] * 1e-3)
             if bound == "hbm":
                 entry["gbs"] = rate / 1e9
@@ -410,49 +427,120 @@ def main():
             else:
                 entry["tflops"] = rate / 1e12
                 entry["frac_mfma_bf16"] = entry["tflops"] / MFMA_BF16_PEAK_TFLOPS
-        kernels[name] = entry
-    # dominant HIP kernel of this build by total time in the timed steps
+        kernels[kname] = entry
+    # dominant HIP kernel of this build by total time in the per-kernel pass
     dom = max((k for k in kern if k in algo), key=lambda k: kern[k]["total_ms"])
     amount, bound = algo[dom]
     rate = amount / (kern[dom]["avg_ms"] * 1e-3)
+    traffic = measured_traffic(dom, name)
     if bound == "hbm":
         roofline = {"kernel": dom, "bound": "hbm", "achieved": rate / 1e9, "peak": HBM_PEAK_GBS,
-                    "unit": "GB/s", "frac": rate / 1e9 / HBM_PEAK_GBS,
-                    "traffic": measured_traffic(dom, args.workload),
+                    "unit": "GB/s", "frac": rate / 1e9 / HBM_PEAK_GBS, "traffic": traffic,
                     "algorithmic_bytes": amount}
     else:
         roofline = {"kernel": dom, "bound": "mfma", "achieved": rate / 1e12,
                     "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                    "frac": rate / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-                    "traffic": measured_traffic(dom, args.workload),
+                    "frac": rate / 1e12 / MFMA_BF16_PEAK_TFLOPS, "traffic": traffic,
                     "algorithmic_flops": amount}
-    flops = gemm_flops_fwd_bwd(n, h, d, full_ft)
+    roofline["timing"] = "mean of the per-kernel pass's HIP events on the launch stream"
+    roofline["traffic_source"] = ("profiles/ rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE summary of "
+                                  "bench.py --probe" if traffic is not None else None)
+    flops = gemm_flops_fwd_bwd(n, h, d, c["full_ft"])
     if wl["lora_rank"]:   # thin adapter GEMMs: 18 * N * r * (H + D)
         flops += 18 * n * wl["lora_rank"] * (h + d)
-    out = {
-        "metric": "FFN fwd+bwd tokens/sec + saved-activation MB, Llama-7B FFN shape, 1 MI355X",
-        "value": n / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
-        "vs_baseline": None, "dtype": "bf16", "data": "synthetic (seed 0, X~N(0,1), W~N(0,0.02))",
-        "config": {"workload": wl["desc"], "tokens": n, "batch": batch, "seq_len": n // batch,
-                   "d_model": h, "d_ff": d,
-                   "cache_mode": MODE, "group_size": GROUP, "lora_rank": wl["lora_rank"],
-                   "outlier_ratio": wl["outlier_ratio"], "frozen_base": not full_ft,
-                   "parallelism": "none (1 GPU)"},
+    res = {
+        "value": n / (ms * 1e-3), "ms_per_step": ms,
+        "ms_per_step_median": _pct(per_step, 0.5), "ms_per_step_p10": _pct(per_step, 0.1),
+        "ms_per_step_p90": _pct(per_step, 0.9),
+        "config": {"workload": wl["desc"], "tokens": n, "batch": c["batch"],
+                   "seq_len": n // c["batch"], "d_model": h, "d_ff": d,
+                   "cache_mode": wl["mode"], "group_size": wl["group"],
+                   "lora_rank": wl["lora_rank"], "outlier_ratio": wl["outlier_ratio"],
+                   "frozen_base": not c["full_ft"], "parallelism": "none (1 GPU)"},
         "saved_activation_mb": sb / 1e6,
         "step_tflops": flops / (ms * 1e-3) / 1e12,
         "step_frac_mfma_bf16": flops / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
         "roofline": roofline,
         "kernels": kernels,
     }
-    if (full_ft or frozen) and not args.no_library_arm:
-        lib_ms = library_arm(x.detach(), gy, wg.detach(), wu.detach(), wd.detach(),
-                             args.steps, args.warmup, frozen)
-        out["library_arm"] = {
+    if library and (c["full_ft"] or c["frozen"]):
+        lib_ms = library_arm(x.detach(), c["gy"], c["wg"].detach(), c["wu"].detach(),
+                             c["wd"].detach(), steps, warmup, wl["bits"], wl["group"],
+                             c["frozen"])
+        res["library_arm"] = {
             "ms_per_step": lib_ms, "tokens_per_s": n / (lib_ms * 1e-3),
             "speedup_of_this_build": lib_ms / ms,
             "what": "same step in the reference's structure: GEMMs through torch.matmul "
                     "(hipBLASLt), K1/K2 codec as standalone kernels, same inputs and box"}
+    return res, c
+
+
+def probe(name, n, steps, dev):
+    """HBM-counter probe (run under rocprofv3 --pmc): a 1 GiB calibration copy,
+    then `steps` untimed steps; prints one status line."""
+    import torch
+    c = ffn_case(name, n, dev)
+    # calibration: torch's copy kernel reads and writes exactly PROBE_COPY_BYTES
+    src = torch.ones(PROBE_COPY_BYTES // 2, device=dev, dtype=torch.bfloat16)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    del src, dst
+    for _ in range(steps):
+        c["step"]()
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": name, "steps": steps, "copy_bytes": PROBE_COPY_BYTES}))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--tokens", type=int, default=N_TOK)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-tokens", type=int, default=2048)
+    ap.add_argument("--no-library-arm", action="store_true",
+                    help="skip timing the hipBLASLt composition of the same step")
+    ap.add_argument("--no-c3", action="store_true",
+                    help="skip the C3 workload that the default C2 line carries under 'c3'")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["c4", "c5"], default="c2",
+                    help="c2 (default) / c3: the FFN block; c4 / c5: a whole-model training "
+                         "step (TinyLlama full-FT / Llama-7B LoRA) with every MLP on FlashFFN v3")
+    ap.add_argument("--probe", action="store_true",
+                    help="HBM-counter probe (run under rocprofv3 --pmc): a 1 GiB calibration "
+                         "copy, then --steps untimed steps; prints one status line")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1 "
+                                   "(multi-GPU sharding is a design note, not a code path)"}))
+        sys.exit(2)
+    if args.workload in ("c4", "c5"):
+        model_step_bench(args)
+        return
+
+    import torch
+    dev = torch.device("cuda:0")
+    if args.probe:
+        probe(args.workload, args.tokens, args.steps, dev)
+        return
+    res, case = run_ffn(args.workload, args.tokens, args.steps, args.warmup, dev,
+                        library=not args.no_library_arm)
+    del case
+    out = {
+        "metric": "FFN fwd+bwd tokens/sec + saved-activation MB, Llama-7B FFN shape, 1 MI355X",
+        "value": res.pop("value"), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": res.pop("ms_per_step"), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seed 0, X~N(0,1), W~N(0,0.02))",
+    }
+    out.update(res)
+    if args.workload == "c2" and not args.no_c3:
+        torch.cuda.empty_cache()
+        c3, case = run_ffn("c3", args.tokens, args.steps, args.warmup, dev, library=False)
+        del case
+        c3.pop("kernels")
+        out["c3"] = {"tokens_per_s": c3.pop("value"), **c3}
     if not args.no_cpu_baseline and args.workload == "c2":
         out["cpu_baseline"] = cpu_baseline(args.cpu_tokens)
     print(json.dumps(out))

@@ -49,7 +49,7 @@ def test_gemm_flops():
 
 
 def test_algorithmic_work_bounds():
-    w = bench.algorithmic_work(N, H, D)
+    w = bench.algorithmic_work(N, H, D, 8, 128)
     gemm = 2 * N * H * D
     assert w["ffn_gate_up"] == (2 * gemm, "mfma")
     assert w["gemm_dgrad_x"] == (2 * gemm, "mfma")
@@ -118,3 +118,18 @@ def test_v5_bigram_batches():
     assert max(len(v) for v in succ.values()) <= 4
     again = bench_v5.bigram_batches(3, 4, 64, 1000, succ=4, seed=1)
     assert all((x == y).all() for x, y in zip(bs, again))
+
+
+def test_step_percentiles_and_cpu_model():
+    assert bench._pct([1.0, 2.0, 3.0, 4.0, 5.0], 0.5) == 3.0
+    assert bench._pct([1.0, 2.0, 3.0, 4.0, 5.0], 0.1) == 1.0
+    assert bench._pct([7.0], 0.9) == 7.0
+    assert isinstance(bench.cpu_model(), str) and bench.cpu_model()
+
+
+def test_cpu_baseline_shapes_are_the_configs():
+    """The CPU baseline's C1 leg is config C1 exactly (BASELINE.json
+    configs[0]): 4 x 512 tokens, d_model 2048, d_ff 5632, int8 g128."""
+    import inspect
+    src = inspect.getsource(bench.cpu_baseline)
+    assert '("c1", (2048, 2048, 5632))' in src and '"int8", 128' in src
