@@ -87,6 +87,10 @@ __device__ __forceinline__ void quant_chunk(const float v[8], bool valid, int64_
 // out as bf16 into out[row * k + slot] and zeroed before the codec sees them
 // (HyC-LoRA's outlier extraction, hyclora/operators/compress_function.py:111-143,
 // on the v3 per-group codec).  v holds 8 consecutive elements of one row.
+// Outlier counts up to this take the one-block-per-row K2 kernel (its [2][k]
+// bf16 LDS block stays at 32 KiB or less).
+constexpr int64_t kRowOutliersMax = 8192;
+
 struct Outliers {
   const int16_t* slot;   // [D], -1 for ordinary columns
   uint16_t* out;         // [N, k] bf16
@@ -103,36 +107,66 @@ __device__ __forceinline__ void chunk_rc(int64_t c, int64_t d, const Outliers& o
   col = ((int64_t)((uint32_t)c - r * o.rows.d)) * 8;
 }
 
-__device__ __forceinline__ void extract_outliers8(float v[8], int64_t c, int64_t d,
-                                                  const Outliers& o, bool valid) {
-  if (!valid) return;
-  int64_t row, col;
-  chunk_rc(c, d, o, row, col);
-  const uint4 w = *reinterpret_cast<const uint4*>(o.slot + col);   // 8 x int16
-  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+// The outlier columns of one 8-column chunk: slot values (8 x int16, -1 for
+// ordinary columns) and the 8-bit mask of those with slot >= 0, from the sign
+// bits, branch-free.
+struct ChunkSlots {
+  uint32_t w[4];
+  uint32_t mask;
+  __device__ __forceinline__ int slot(int j) const {
+    return (int16_t)((w[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+  }
+};
+
+__device__ __forceinline__ ChunkSlots load_slots8(const Outliers& o, int64_t col, bool valid) {
+  ChunkSlots cs;
+  uint4 v = make_uint4(0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu);
+  if (valid) v = *reinterpret_cast<const uint4*>(o.slot + col);
+  cs.w[0] = v.x; cs.w[1] = v.y; cs.w[2] = v.z; cs.w[3] = v.w;
+  uint32_t m = 0;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int sl = (int16_t)((ws[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
-    if (sl >= 0) {
-      o.out[row * o.k + sl] = (uint16_t)f32_to_bf16_bits(v[j]);
-      v[j] = 0.0f;
-    }
+  for (int i = 0; i < 4; ++i) {
+    m |= ((~cs.w[i] >> 15) & 1u) << (2 * i);
+    m |= ((~cs.w[i] >> 31) & 1u) << (2 * i + 1);
+  }
+  cs.mask = m;
+  return cs;
+}
+
+// Copy the chunk's outlier columns out as bf16 and zero them in v.  The
+// stores run only in lanes whose chunk holds an outlier (~8% at 1% of d_ff).
+__device__ __forceinline__ void extract_outliers8(float v[8], int64_t row, const ChunkSlots& cs,
+                                                  const Outliers& o) {
+  if (cs.mask) {
+    uint16_t* dst = o.out + row * o.k;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if ((cs.mask >> j) & 1u) dst[cs.slot(j)] = (uint16_t)f32_to_bf16_bits(v[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = ((cs.mask >> j) & 1u) ? 0.0f : v[j];
+}
+
+// The stored bf16 values of the chunk's outlier columns (0 elsewhere),
+// fetched ahead of the dequantisation they replace.
+__device__ __forceinline__ void fetch_outliers8(float ov[8], int64_t row, const ChunkSlots& cs,
+                                                const Outliers& o) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ov[j] = 0.0f;
+  if (cs.mask) {
+    const uint16_t* src = o.out + row * o.k;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if ((cs.mask >> j) & 1u) ov[j] = bf16_to_f32(src[cs.slot(j)]);
   }
 }
 
 // Overwrite dequantised values of outlier columns with the stored bf16 values
 // (compress_function.py:147-174).
-__device__ __forceinline__ void restore_outliers8(float v[8], int64_t c, int64_t d,
-                                                  const Outliers& o) {
-  int64_t row, col;
-  chunk_rc(c, d, o, row, col);
-  const uint4 w = *reinterpret_cast<const uint4*>(o.slot + col);
-  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+__device__ __forceinline__ void restore_outliers8(float v[8], const float ov[8],
+                                                  const ChunkSlots& cs) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int sl = (int16_t)((ws[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
-    if (sl >= 0) v[j] = bf16_to_f32(o.out[row * o.k + sl]);
-  }
+  for (int j = 0; j < 8; ++j) v[j] = ((cs.mask >> j) & 1u) ? ov[j] : v[j];
 }
 
 // ---------------------------------------------------------------------------
@@ -146,9 +180,17 @@ __global__ __launch_bounds__(kBlock) void quantize_fast_kernel(
     int64_t nchunk, int64_t d, Outliers o) {
   const int64_t base = (int64_t)blockIdx.x * kBlock * kQuantCPT + threadIdx.x;
   float v[kQuantCPT][8];
+  ChunkSlots cs[kQuantCPT];
+  int64_t row[kQuantCPT];
 #pragma unroll
   for (int i = 0; i < kQuantCPT; ++i) {
     const int64_t c = base + i * kBlock;
+    if (OUTL) {
+      int64_t col = 0;
+      row[i] = 0;
+      if (c < nchunk) chunk_rc(c, d, o, row[i], col);
+      cs[i] = load_slots8(o, col, c < nchunk);
+    }
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[i][j] = 0.0f;
     if (c < nchunk) Vec8<DT>::ld(t, c, v[i]);
@@ -157,7 +199,7 @@ __global__ __launch_bounds__(kBlock) void quantize_fast_kernel(
   for (int i = 0; i < kQuantCPT; ++i) {
     const int64_t c = base + i * kBlock;
     const bool valid = c < nchunk;
-    if (OUTL) extract_outliers8(v[i], c, d, o, valid);
+    if (OUTL) extract_outliers8(v[i], row[i], cs[i], o);
     quant_chunk<BITS, LPG>(v[i], valid, c, q, s);
   }
 }
@@ -172,6 +214,14 @@ __global__ __launch_bounds__(kBlock) void silu_mul_quant_kernel(
     uint16_t* __restrict__ su, int64_t nchunk, int64_t d, Outliers og, Outliers ou) {
   const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   const bool valid = c < nchunk;
+  // the slot maps first: a small cached read, in flight with the payload
+  int64_t row = 0, col = 0;
+  ChunkSlots csg, csu;
+  if (OUTL) {
+    if (valid) chunk_rc(c, d, og, row, col);
+    csg = load_slots8(og, col, valid);
+    csu = load_slots8(ou, col, valid);
+  }
   float gv[8] = {0, 0, 0, 0, 0, 0, 0, 0}, uv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   if (valid) {
     Vec8<kBF16>::ld(g, c, gv);
@@ -182,8 +232,8 @@ __global__ __launch_bounds__(kBlock) void silu_mul_quant_kernel(
     Vec8<kBF16>::st(hm, c, h);
   }
   if (OUTL) {
-    extract_outliers8(gv, c, d, og, valid);
-    extract_outliers8(uv, c, d, ou, valid);
+    extract_outliers8(gv, row, csg, og);
+    extract_outliers8(uv, row, csu, ou);
   }
   quant_chunk<BITS, LPG>(gv, valid, c, qg, sg);
   quant_chunk<BITS, LPG>(uv, valid, c, qu, su);
@@ -244,15 +294,22 @@ __global__ __launch_bounds__(kBlock) void dequantize_fast_kernel(
     int64_t nchunk, int gs_shift, int64_t d, Outliers o) {
   const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (c >= nchunk) return;
-  float code[8], v[8];
+  float code[8], v[8], ov[8];
   load_codes8<BITS>(q, c, code);
   const float sc = f16_bits_to_f32(s[(c * 8) >> gs_shift]);
+  ChunkSlots cs;
+  if (OUTL) {
+    int64_t row, col;
+    chunk_rc(c, d, o, row, col);
+    cs = load_slots8(o, col, true);
+    fetch_outliers8(ov, row, cs, o);
+  }
 #pragma unroll
   for (int j = 0; j < 8; ++j) v[j] = code[j] * sc;
   if (OUTL) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = round_bf16(v[j]);
-    restore_outliers8(v, c, d, o);
+    restore_outliers8(v, ov, cs);
   }
   Vec8<OUT_DT>::st(out, c, v);
 }
@@ -288,6 +345,18 @@ __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_kernel(
   const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (c >= nchunk) return;
   float cg[8], cu[8], dh[8], og[8], ou[8], oh[8], hg[8], hu[8];
+  // outlier values first: their loads depend on the slot maps, so they are
+  // issued ahead of the payload loads and overlap them
+  float ovg[8], ovu[8];
+  ChunkSlots csg, csu;
+  if (OUTL) {
+    int64_t row, col;
+    chunk_rc(c, d, outg, row, col);
+    csg = load_slots8(outg, col, true);
+    csu = load_slots8(outu, col, true);
+    fetch_outliers8(ovg, row, csg, outg);
+    fetch_outliers8(ovu, row, csu, outu);
+  }
   load_codes8<BITS>(qg, c, cg);
   load_codes8<BITS>(qu, c, cu);
   Vec8<kBF16>::ld(gmid, c, dh);
@@ -301,8 +370,8 @@ __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_kernel(
     hu[j] = round_bf16(cu[j] * scu);
   }
   if (OUTL) {
-    restore_outliers8(hg, c, d, outg);
-    restore_outliers8(hu, c, d, outu);
+    restore_outliers8(hg, ovg, csg);
+    restore_outliers8(hu, ovu, csu);
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -339,6 +408,79 @@ __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_generic_kernel(
   dg[e] = (uint16_t)f32_to_bf16_bits(og);
   du[e] = (uint16_t)f32_to_bf16_bits(ou);
   if (WANT_HM) hm[e] = (uint16_t)f32_to_bf16_bits(hact * hu);
+}
+
+// ---------------------------------------------------------------------------
+// K2 with outlier channels, one block per row.  The block reads the row's
+// [k] outlier values into LDS in one coalesced pass before its threads
+// restore from it, so no thread issues an HBM load that waits on the slot
+// map (0.173 against 0.185 ms for the chunk-per-thread kernel at C3).  Thread
+// t owns chunks t, t + 256, ... of the row (D / 8 chunks).  The same layout
+// for K1 (outliers collected in LDS, written once per row) measured slower
+// than the chunk-per-thread K1 (0.153-0.175 against 0.137 ms), so K1 keeps
+// the per-chunk extraction.
+// ---------------------------------------------------------------------------
+// Chunks each thread has in flight per step of the row loop (loads of all of
+// them issued before any is used).
+constexpr int kRowUnroll = 2;
+
+template <int BITS, bool WANT_HM>
+__global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_outlier_rows_kernel(
+    const uint16_t* gmid, const uint8_t* __restrict__ qg, const uint16_t* __restrict__ sg,
+    const uint8_t* __restrict__ qu, const uint16_t* __restrict__ su, uint16_t* dg, uint16_t* du,
+    uint16_t* hm, int64_t cpr, int gs_shift, Outliers og, Outliers ou) {
+  extern __shared__ uint16_t so[];   // [2][k] bf16: gate, up
+  const int64_t row = blockIdx.x;
+  const int k = (int)og.k;
+  for (int i = threadIdx.x; i < k; i += kBlock) {
+    so[i] = og.out[row * k + i];
+    so[k + i] = ou.out[row * k + i];
+  }
+  __syncthreads();
+  for (int64_t j0 = 0; j0 < cpr; j0 += kBlock * kRowUnroll) {
+    ChunkSlots csg[kRowUnroll], csu[kRowUnroll];
+    float cg[kRowUnroll][8], cu[kRowUnroll][8], dh[kRowUnroll][8], scg[kRowUnroll],
+        scu[kRowUnroll];
+#pragma unroll
+    for (int t = 0; t < kRowUnroll; ++t) {
+      const int64_t jc = j0 + t * kBlock + threadIdx.x;
+      // a chunk past the row reads chunk 0 of the row again and stores nothing
+      const int64_t c = row * cpr + (jc < cpr ? jc : 0);
+      csg[t] = load_slots8(og, (jc < cpr ? jc : 0) * 8, true);
+      csu[t] = load_slots8(ou, (jc < cpr ? jc : 0) * 8, true);
+      load_codes8<BITS>(qg, c, cg[t]);
+      load_codes8<BITS>(qu, c, cu[t]);
+      Vec8<kBF16>::ld(gmid, c, dh[t]);
+      const int64_t si = (c * 8) >> gs_shift;
+      scg[t] = f16_bits_to_f32(sg[si]);
+      scu[t] = f16_bits_to_f32(su[si]);
+    }
+#pragma unroll
+    for (int t = 0; t < kRowUnroll; ++t) {
+      const int64_t jc = j0 + t * kBlock + threadIdx.x;
+      if (jc >= cpr) continue;
+      const int64_t c = row * cpr + jc;
+      float ogr[8], our[8], oh[8], hg[8], hu[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        // bf16 round trip of the dequantised cache (src/flashffn.py:1251-1253),
+        // then the stored value of an outlier column (compress_function.py:147-174)
+        hg[j] = round_bf16(cg[t][j] * scg[t]);
+        hu[j] = round_bf16(cu[t][j] * scu[t]);
+        if ((csg[t].mask >> j) & 1u) hg[j] = bf16_to_f32(so[csg[t].slot(j)]);
+        if ((csu[t].mask >> j) & 1u) hu[j] = bf16_to_f32(so[k + csu[t].slot(j)]);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        float hact;
+        swiglu_bwd1(dh[t][j], hg[j], hu[j], ogr[j], our[j], hact);
+        oh[j] = hact * hu[j];  // src/flashffn.py:1298-1300
+      }
+      Vec8<kBF16>::st(dg, c, ogr);
+      Vec8<kBF16>::st(du, c, our);
+      if (WANT_HM) Vec8<kBF16>::st(hm, c, oh);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1059,6 +1201,16 @@ int cpt_dequant_swiglu_backward_outlier(const void* grad_h_mid, const void* q_ga
   uint16_t* dg = (uint16_t*)grad_h_gate;
   uint16_t* du = (uint16_t*)grad_h_up;
   uint16_t* hm = (uint16_t*)h_mid_hat;
+  if (k <= kRowOutliersMax && n <= 0x7FFFFFFF) {
+    // one block per row, the row's outliers staged in LDS
+    const size_t lds = (size_t)(2 * k) * sizeof(uint16_t);
+    const int64_t cpr = d / 8;
+#define CPT_K2R(B, W) dequant_swiglu_bwd_outlier_rows_kernel<B, W><<<(unsigned)n, kBlock, lds, st>>>(gm, qg, sg, qu, su, dg, du, hm, cpr, sh, og, ou)
+    if (bits == 4) { if (hm) CPT_K2R(4, true); else CPT_K2R(4, false); }
+    else { if (hm) CPT_K2R(8, true); else CPT_K2R(8, false); }
+#undef CPT_K2R
+    return launch_status();
+  }
 #define CPT_K2O(B, W) dequant_swiglu_bwd_kernel<B, W, true><<<grid, kBlock, 0, st>>>(gm, qg, sg, qu, su, dg, du, hm, nchunk, sh, d, og, ou)
   if (bits == 4) { if (hm) CPT_K2O(4, true); else CPT_K2O(4, false); }
   else { if (hm) CPT_K2O(8, true); else CPT_K2O(8, false); }
