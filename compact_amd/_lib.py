@@ -38,6 +38,7 @@ SIGNATURES = {
     "cpt_gemm_bf16": [_P, _L, _I, _P, _L, _I, _P, _L, _P, _L, _L, _P, _L, _L, _L, _L, _P],
     "cpt_gemm_bf16_ex": [_P, _L, _I, _P, _L, _I, _P, _L, _L, _L, _L, ctypes.c_float, _I, _I, _P, _P],
     "cpt_gemm_any": [_I, _P, _L, _L, _P, _L, _L, _P, _L, _L, _L, _L, _L, ctypes.c_float, _I, _P],
+    "cpt_gemm_wgrad_glu": [_P, _L, _I, _L, _P, _P, _P, _P, _P, _L, _L, _L, _L, _P],
     "cpt_ffn_gate_up": [_P, _P, _P, _L, _L, _L, _I, _L, _P, _P, _P, _P, _P, _P, _P, _P],
     "cpt_ffn_down_dgrad": [_P, _P, _L, _L, _L, _I, _L, _P, _P, _P, _P, _P, _P, _P, _P],
     "cpt_gemm_bf16_lora": [_P, _L, _I, _P, _L, _I, _P, _L, _P, _L, _L, _P, _L, _L, _L, _L,

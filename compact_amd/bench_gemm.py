@@ -71,6 +71,24 @@ def main():
                      "library_tflops": flops / b / 1e9}
         print(f"{name:38s} engine {a:7.3f} ms {flops / a / 1e9:7.1f} TF/s | "
               f"library {b:7.3f} ms {flops / b / 1e9:7.1f} TF/s", flush=True)
+    # The down projection's weight gradient, both routes of this build: K2
+    # writing h_mid^ and the plain TN GEMM, against K2 without h_mid^ and the
+    # GEMM that rebuilds h^ from the int8 cache in its operand staging.
+    def k2_then_tn():
+        _, _, hmh = K.dequant_swiglu_backward(hm, qg, sg, qu, su, 8, gs, want_h_mid=True)
+        return G.mm(gy.t(), hmh)
+
+    def k2_then_glu():
+        K.dequant_swiglu_backward(hm, qg, sg, qu, su, 8, gs, want_h_mid=False)
+        return G.wgrad_glu(gy, 8, gs, qg, sg, qu, su)
+
+    a, b = _time(k2_then_tn, args.iters), _time(k2_then_glu, args.iters)
+    c = _time(lambda: G.wgrad_glu(gy, 8, gs, qg, sg, qu, su), args.iters)
+    out["dWd route"] = {"k2_h_mid_then_tn_ms": a, "k2_then_wgrad_glu_ms": b,
+                        "wgrad_glu_alone_ms": c, "wgrad_glu_tflops": fl / c / 1e9}
+    print(f"{'bwd dWd: K2 + h_mid^ + TN GEMM':38s} {a:7.3f} ms | K2 + GEMM with the GLU in its "
+          f"operand staging {b:7.3f} ms (that GEMM alone {c:7.3f} ms, {fl / c / 1e9:7.1f} TF/s)",
+          flush=True)
     if args.json:
         json.dump(out, open(args.json, "w"), indent=1)
 

@@ -418,6 +418,61 @@ int ffn_down_dgrad_impl(const void* grad_y, const void* w_down, int64_t n_tok, i
   }
 }
 
+// C[hidden, inter] = grad_y^T . h^ with h^ = bf16(SiLU(hg^) * hu^) formed from
+// the int cache in the B operand's staging (the weight gradient of the down
+// projection without K2's h_mid^ in HBM).
+int wgrad_glu_impl(const void* grad_y, int64_t ldg, int cache, int64_t gs, const void* q_gate,
+                   const void* s_gate, const void* q_up, const void* s_up, void* c, int64_t ldc,
+                   int64_t hidden, int64_t inter, int64_t n_tok, void* stream) {
+  if (hidden < 0 || inter < 0 || n_tok < 0) return kErrShape;
+  if (cache != CACHE_INT4 && cache != CACHE_INT8) return kErrBits;
+  if (gs <= 0 || inter % gs) return kErrRagged;
+  if (!is_pow2(gs)) return kErrGroupPow2;
+  if (gs != 32 && gs != 64 && gs != 128) return kErrGroupPow2;
+  if (hidden == 0 || inter == 0) return kOk;
+  if (!q_gate || !s_gate || !q_up || !s_up || !c) return kErrShape;
+  const uintptr_t qmask = cache == CACHE_INT8 ? 7u : 3u;
+  if ((inter & 7) || ((uintptr_t)q_gate & qmask) || ((uintptr_t)q_up & qmask) ||
+      ((uintptr_t)s_gate & 1u) || ((uintptr_t)s_up & 1u) || !al16(c) || (ldc & 3) ||
+      ldc < inter || (n_tok > 0 && !operand_ok(grad_y, ldg, false, hidden, n_tok)))
+    return kErrAlign;
+  // 32-bit offsets: grad_y's k rows and the cache's rows (plus a tile of prefetch)
+  const int64_t qrow = cache == CACHE_INT8 ? inter : inter / 2;
+  if (!operand_fits(ldg, false, hidden, n_tok) || (n_tok + 256) * qrow >= ((int64_t)1 << 31) ||
+      (n_tok + 256) * (inter / gs) * 2 >= ((int64_t)1 << 31))
+    return kErrTooLarge;
+  KArgs A{};
+  A.a[0] = {(const uint16_t*)grad_y, ldg};
+  A.b[0] = {nullptr, inter};
+  A.K[0] = n_tok;
+  A.npairs = 1;
+  A.M = hidden;
+  A.N = inter;
+  A.D = inter;
+  A.lgs = gs;
+  A.tiles_m = (int)((hidden + BM - 1) / BM);
+  A.tiles_n = (int)((inter + BN - 1) / BN);
+  A.C = (uint16_t*)c;
+  A.ldc = ldc;
+  A.q_gate = (uint8_t*)q_gate;
+  A.q_up = (uint8_t*)q_up;
+  A.s_gate = (uint16_t*)s_gate;
+  A.s_up = (uint16_t*)s_up;
+  hipStream_t st = (hipStream_t)stream;
+  if (cache == CACHE_INT8) {
+    switch (gs) {
+      case 32: return launch<false, false, EPI_STORE, CACHE_INT8, 32>(A, st);
+      case 64: return launch<false, false, EPI_STORE, CACHE_INT8, 64>(A, st);
+      default: return launch<false, false, EPI_STORE, CACHE_INT8, 128>(A, st);
+    }
+  }
+  switch (gs) {
+    case 32: return launch<false, false, EPI_STORE, CACHE_INT4, 32>(A, st);
+    case 64: return launch<false, false, EPI_STORE, CACHE_INT4, 64>(A, st);
+    default: return launch<false, false, EPI_STORE, CACHE_INT4, 128>(A, st);
+  }
+}
+
 }  // namespace gemm
 }  // namespace cpt
 
@@ -599,6 +654,14 @@ int cpt_ffn_down_dgrad_outlier(const void* grad_y, const void* w_down, int64_t n
   }
   return ffn_down_dgrad_impl(grad_y, w_down, n_tok, hidden, inter, cache, group_size, c_gate,
                              s_gate, c_up, s_up, grad_h_gate, grad_h_up, h_mid_hat, O, L, stream);
+}
+
+int cpt_gemm_wgrad_glu(const void* grad_y, int64_t ldg, int cache, int64_t group_size,
+                       const void* q_gate, const void* s_gate, const void* q_up,
+                       const void* s_up, void* c, int64_t ldc, int64_t hidden, int64_t inter,
+                       int64_t n_tok, void* stream) {
+  return wgrad_glu_impl(grad_y, ldg, cache, group_size, q_gate, s_gate, q_up, s_up, c, ldc,
+                        hidden, inter, n_tok, stream);
 }
 
 }  // extern "C"

@@ -155,6 +155,7 @@ struct KArgs {
   const uint16_t* o_g;
   const uint16_t* o_u;
   int64_t k_out;
+  int64_t lgs;             // group size of the int cache a BQ operand is the GLU of
   // low-rank adapter terms applied as the epilogue reads the accumulators
   // (acc_block); lrank == 0: none
   const uint16_t* lp[2];   // P_t [M, lrank], rows lldp apart (tokens x rank)
@@ -221,7 +222,7 @@ __device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return *reinterpret_cast<uint4*>(&v);
 }
 
-template <bool AK, bool BKM, bool DUAL>
+template <bool AK, bool BKM, bool DUAL, int BQ = 0>
 struct Loader {
   __amdgpu_buffer_rsrc_t ra[2], rb[2], rup;
   uint32_t oa[8], ob[8];   // per-thread byte offsets at the resource start (kOOB if out)
@@ -229,6 +230,11 @@ struct Loader {
   int64_t kbase[2];        // k row an MN-major resource starts at (per pair)
   int nk0;
   int64_t lda, ldb;
+  // BQ (B = the GLU of an int-BQ cache, MN-major [K][D]): the code and scale
+  // tensors of gate and up, and per-row byte offsets into them (kOOB if out)
+  __amdgpu_buffer_rsrc_t rqg, rqu, rsg, rsu;
+  uint32_t os[8];
+  int64_t qrow, srow;      // bytes per k row of the codes / of the scales
 
   // kt0: the block's first k-tile (split-K), within pair 0
   __device__ __forceinline__ void init(const KArgs& A, int64_t m0, int64_t n0, int tid, int kt0) {
@@ -268,7 +274,24 @@ struct Loader {
       for (int r = 0; r < 8; ++r)
         oa[r] = mn < A.M ? (uint32_t)((((tid >> 5) * 8 + r) * lda + mn) * 2) : kOOB;
     }
-    if (DUAL) {
+    if constexpr (BQ != 0) {
+      // codes [K][D] (int8) or [K][D/2] (int4 nibbles), scales fp16 [K][G];
+      // rows [kbase, K) from the block's first k row, as for MN-major bf16
+      qrow = BQ == 8 ? A.D : A.D / 2;
+      srow = (A.D / A.lgs) * 2;
+      const int64_t kb = kbase[0];
+      rqg = make_rsrc(A.q_gate + kb * qrow, (K[0] - kb) * qrow);
+      rqu = make_rsrc(A.q_up + kb * qrow, (K[0] - kb) * qrow);
+      rsg = make_rsrc(reinterpret_cast<const char*>(A.s_gate) + kb * srow, (K[0] - kb) * srow);
+      rsu = make_rsrc(reinterpret_cast<const char*>(A.s_up) + kb * srow, (K[0] - kb) * srow);
+      const int64_t mn = n0 + (tid & 31) * 8;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int64_t kr = (tid >> 5) * 8 + r;
+        ob[r] = mn < A.N ? (uint32_t)(kr * qrow + (BQ == 8 ? mn : mn / 2)) : kOOB;
+        os[r] = mn < A.N ? (uint32_t)(kr * srow + (mn / A.lgs) * 2) : kOOB;
+      }
+    } else if (DUAL) {
 #pragma unroll
       for (int it = 0; it < 8; ++it) {
         const int blk = it >> 1;
@@ -294,6 +317,36 @@ struct Frags {
   bf16x8 n[4];   // n-side fragments (MFMA A slot)
   bf16x8 m[4];   // m-side fragments (MFMA B slot)
 };
+
+// One k row of 8 columns of a B operand given as the GLU of an int cache:
+// the gate and up codes (int8: 8 bytes each; int4: 4 bytes of nibbles) and
+// their fp16 scales.
+struct RawQ {
+  uint32_t g0, g1, u0, u1;
+  uint32_t sg, su;
+};
+
+// h^ = bf16(SiLU(hg^) * hu^) of the 8 columns, hg^ / hu^ dequantised through
+// bf16: K2's h_mid^ (src/flashffn.py:1251-1253,1298-1300), bit for bit.
+template <int BITS>
+__device__ __forceinline__ uint4 deq_glu8(const RawQ& q) {
+  const float sg = f16_bits_to_f32((uint16_t)q.sg), su = f16_bits_to_f32((uint16_t)q.su);
+  float h[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float cg, cu;
+    if constexpr (BITS == 8) {
+      cg = (float)(int8_t)(((e < 4 ? q.g0 : q.g1) >> (8 * (e & 3))) & 0xFFu);
+      cu = (float)(int8_t)(((e < 4 ? q.u0 : q.u1) >> (8 * (e & 3))) & 0xFFu);
+    } else {
+      cg = (float)((q.g0 >> (4 * e)) & 0xFu) - 8.0f;
+      cu = (float)((q.u0 >> (4 * e)) & 0xFu) - 8.0f;
+    }
+    h[e] = silu_mul1(round_bf16(cg * sg), round_bf16(cu * su));
+  }
+  return make_uint4(pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]), pack_bf16x2(h[4], h[5]),
+                    pack_bf16x2(h[6], h[7]));
+}
 
 // MFMA fragment of an MN-major tile: 8 consecutive k (sub-step s, lane half)
 // of mn row rowbase + lane % 32, as two transpose reads of 4 k each.
@@ -360,9 +413,10 @@ __device__ __forceinline__ void sched_interleave() {
 // sub-steps, each group reloaded with tile kt+2 right after its write.  Loads
 // and LDS writes are spread evenly (no burst), and each load has a whole
 // k-tile to land.  Each operand goes 2 registers per group.
-template <bool AK, bool BKM, bool DUAL>
+template <bool AK, bool BKM, bool DUAL, int BQ = 0>
 __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t n0, uint16_t* lds,
                                             Acc& acc, int kt0 = 0, int kt_end = -1) {
+  static_assert(BQ == 0 || (!BKM && !DUAL), "the int-cache B operand is MN-major");
   constexpr bool BK_ = BKM || DUAL;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
@@ -373,7 +427,7 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc.v[i][j][r] = 0.0f;
-  Loader<AK, BKM, DUAL> L;
+  Loader<AK, BKM, DUAL, BQ> L;
   L.init(A, m0, n0, tid, kt0);
   int nk_all = L.nk0;
   if (A.npairs > 1) nk_all += (int)((A.K[1] + BK - 1) / BK);
@@ -382,7 +436,9 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
   // or reads zero past K
   const int nk = kt_end - kt0;
   if (nk <= 0) return;   // empty range: the accumulators stay zero
-  uint4 va[8], vb[8];
+  using BReg = std::conditional_t<BQ != 0, RawQ, uint4>;
+  uint4 va[8];
+  BReg vb[8];
   // Per-tile load state, computed once per k-tile: the pair's buffer and a
   // per-lane byte delta added to every fixed per-thread offset.  An offset at
   // or past kOOB reads zero (records < 2^31 and offsets + delta < 2^32), so
@@ -391,7 +447,7 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
   // operand per tile, not per load).
   struct TileLd {
     __amdgpu_buffer_rsrc_t ra, rb;
-    uint32_t da, db;
+    uint32_t da, db, ds;
   };
   auto tile = [&](int kt) -> TileLd {
     TileLd T;
@@ -405,12 +461,39 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
     const int64_t kr = k0 - (p ? L.kbase[1] : L.kbase[0]);
     T.da = AK ? (kok ? (uint32_t)(k0 * 2) : kOOB) : (uint32_t)(kr * L.lda * 2);
     T.db = BK_ ? (kok ? (uint32_t)(k0 * 2) : kOOB) : (uint32_t)(kr * L.ldb * 2);
+    if constexpr (BQ != 0) {
+      T.db = (uint32_t)(kr * L.qrow);
+      T.ds = (uint32_t)(kr * L.srow);
+    } else {
+      T.ds = 0;
+    }
     return T;
   };
   auto ldA = [&](const TileLd& T, int it) -> uint4 { return bload(T.ra, L.oa[it] + T.da); };
-  auto ldB = [&](const TileLd& T, int it) -> uint4 {
-    const __amdgpu_buffer_rsrc_t r = (DUAL && ((it >> 1) & 1)) ? L.rup : T.rb;
-    return bload(r, L.ob[it] + T.db);
+  auto ldB = [&](const TileLd& T, int it) -> BReg {
+    if constexpr (BQ != 0) {
+      RawQ q;
+      if constexpr (BQ == 8) {
+        const auto g = __builtin_amdgcn_raw_buffer_load_b64(L.rqg, L.ob[it] + T.db, 0, 0);
+        const auto u = __builtin_amdgcn_raw_buffer_load_b64(L.rqu, L.ob[it] + T.db, 0, 0);
+        q.g0 = g[0]; q.g1 = g[1]; q.u0 = u[0]; q.u1 = u[1];
+      } else {
+        q.g0 = __builtin_amdgcn_raw_buffer_load_b32(L.rqg, L.ob[it] + T.db, 0, 0);
+        q.u0 = __builtin_amdgcn_raw_buffer_load_b32(L.rqu, L.ob[it] + T.db, 0, 0);
+        q.g1 = q.u1 = 0;
+      }
+      q.sg = __builtin_amdgcn_raw_buffer_load_b16(L.rsg, L.os[it] + T.ds, 0, 0);
+      q.su = __builtin_amdgcn_raw_buffer_load_b16(L.rsu, L.os[it] + T.ds, 0, 0);
+      return q;
+    } else {
+      const __amdgpu_buffer_rsrc_t r = (DUAL && ((it >> 1) & 1)) ? L.rup : T.rb;
+      return bload(r, L.ob[it] + T.db);
+    }
+  };
+  // B registers -> LDS row (the int-cache operand is turned into h^ here)
+  auto stB_row = [&](uint16_t* sb, int it) {
+    if constexpr (BQ != 0) sstore_mn_row(sb, tid, it, deq_glu8<BQ>(vb[it]));
+    else sstore_mn_row(sb, tid, it, vb[it]);
   };
   const int wofs = lds_off(tid >> 3, tid & 7);
   // group g of tile kt: store the held registers into `stage`, reload them with tile T
@@ -428,8 +511,8 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int it = 2 * g + h;
-      if (BK_) *reinterpret_cast<uint4*>(sb + wofs + it * 2176) = vb[it];
-      else sstore_mn_row(sb, tid, it, vb[it]);
+      if constexpr (BK_) *reinterpret_cast<uint4*>(sb + wofs + it * 2176) = vb[it];
+      else stB_row(sb, it);
       vb[it] = ldB(T, it);
     }
   };
@@ -443,7 +526,12 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
     uint16_t* sa = lds;
     uint16_t* sb = sa + TILE_ELEMS;
     if (AK) sstore_kmajor(sa, tid, va); else sstore_mnmajor(sa, tid, va);
-    if (BK_) sstore_kmajor(sb, tid, vb); else sstore_mnmajor(sb, tid, vb);
+    if constexpr (BK_) {
+      sstore_kmajor(sb, tid, vb);
+    } else {
+#pragma unroll
+      for (int r = 0; r < 8; ++r) stB_row(sb, r);
+    }
   }
   {
     const TileLd T1 = tile(kt0 + 1);
@@ -998,7 +1086,11 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_kernel(KArgs A) {
     epi_f32(A, acc, m0, n0, split);
     return;
   } else {
-    mainloop_pp<AK, BKM, EPI == EPI_GLU>(A, m0, n0, lds, acc);
+    // a plain-store kernel instantiated with an int cache multiplies by the
+    // GLU of that cache (B = h^, the wgrad of the down projection)
+    constexpr int BQ = (EPI == EPI_STORE && CACHE == CACHE_INT8) ? 8
+                       : (EPI == EPI_STORE && CACHE == CACHE_INT4) ? 4 : 0;
+    mainloop_pp<AK, BKM, EPI == EPI_GLU, BQ>(A, m0, n0, lds, acc);
   }
   if constexpr (EPI == EPI_STORE) epi_store<LT>(A, acc, m0, n0);
   else if constexpr (EPI == EPI_ADD) epi_add(A, acc, m0, n0, lds);
@@ -1060,9 +1152,14 @@ int launch(KArgs& A, hipStream_t st) {
   X(true, false, EPI_DGLU, CACHE_INT8, 32, 0) X(true, false, EPI_DGLU, CACHE_INT8, 32, 1) \
   X(true, false, EPI_DGLU, CACHE_INT8, 64, 0) X(true, false, EPI_DGLU, CACHE_INT8, 64, 1) \
   X(true, false, EPI_DGLU, CACHE_INT8, 128, 0) X(true, false, EPI_DGLU, CACHE_INT8, 128, 1)
+#define CPT_GEMM_INST_WGLU(X)                                                \
+  X(false, false, EPI_STORE, CACHE_INT8, 32, 0) X(false, false, EPI_STORE, CACHE_INT8, 64, 0) \
+  X(false, false, EPI_STORE, CACHE_INT8, 128, 0) X(false, false, EPI_STORE, CACHE_INT4, 32, 0) \
+  X(false, false, EPI_STORE, CACHE_INT4, 64, 0) X(false, false, EPI_STORE, CACHE_INT4, 128, 0)
 #define CPT_GEMM_INST_ALL(X)                                                 \
   CPT_GEMM_INST_STORE(X) CPT_GEMM_INST_AUX(X) CPT_GEMM_INST_GLU_A(X)         \
-  CPT_GEMM_INST_GLU_B(X) CPT_GEMM_INST_DGLU_A(X) CPT_GEMM_INST_DGLU_B(X)
+  CPT_GEMM_INST_GLU_B(X) CPT_GEMM_INST_DGLU_A(X) CPT_GEMM_INST_DGLU_B(X)     \
+  CPT_GEMM_INST_WGLU(X)
 #define CPT_GEMM_DEFINE(AK, BKM, EPI, CACHE, GS, LT) \
   template int launch<AK, BKM, EPI, CACHE, GS, LT>(KArgs&, hipStream_t);
 #define CPT_GEMM_DECLARE(AK, BKM, EPI, CACHE, GS, LT) \

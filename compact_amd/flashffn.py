@@ -57,6 +57,13 @@ _FUSED_GROUPS = (32, 64, 128)
 # unfused.  The fused kernel stays available and tested; add group sizes here
 # to route the Function through it.
 _FUSED_DGRAD_GROUPS = ()
+# The weight gradient of the down projection with the GLU decompressed in the
+# GEMM's operand staging (G.wgrad_glu: h^ formed from the int cache as the TN
+# GEMM stages its B tiles) instead of K2 writing h_mid^ for a plain TN GEMM.
+# Off: each 256-column h^ tile is rebuilt by all hidden/256 = 16 row tiles,
+# so the kernel is VALU-bound and measures slower than K2's h_mid^ plus the
+# plain GEMM.  Both are bit-equal; set True to route the Function through it.
+_FUSED_WGRAD_GLU = False
 
 
 def _mfma(*ts) -> bool:
@@ -294,6 +301,11 @@ class FlashFFNv3Function(torch.autograd.Function):
         need_h_mid = need_wd or (a_down is not None and need_ad)          # :1490
         need_recon = need_gate_path or need_h_mid
         use_k2 = mode in ("int4", "int8") and ctx.use_triton and need_gate_path
+        # grad_w_down from the cache itself: K2 then skips h_mid^ unless the
+        # down adapter's gradient needs it
+        use_wglu = (_FUSED_WGRAD_GLU and use_k2 and need_wd and not outl and gs in _FUSED_GROUPS
+                    and _mfma(gy) and gy.shape[0] > 0)
+        need_hm = need_h_mid and ((a_down is not None and need_ad) or not use_wglu)
         lora_d = _lora_ok((a_down, b_down))
         # the fused dgrad kernel restores outlier channels only for the
         # quantised caches (K2's path); bf16 / recompute caches carry none
@@ -340,7 +352,7 @@ class FlashFFNv3Function(torch.autograd.Function):
                 # dgrad GEMM with dequantise + SwiGLU backward in its epilogue
                 grad_h_gate, grad_h_up, h_mid_hat = G.ffn_down_dgrad(
                     gy, w_down, _CACHE_CODE[mode], gs, c_gate, qs_gate, c_up, qs_up,
-                    need_h_mid, lora=dlora,
+                    need_hm, lora=dlora,
                     outliers=(slot_gate, o_gate, slot_up, o_up) if outl else None)
                 _V3_COUNTERS["triton_dequant_bwd"] += 1
             elif (not use_k2) and fusable and hg is not None and _mfma(hg, hu):
@@ -370,7 +382,7 @@ class FlashFFNv3Function(torch.autograd.Function):
                 elif use_k2:
                     grad_h_gate, grad_h_up, h_mid_hat = K.dequant_swiglu_backward(
                         grad_h_mid, c_gate, qs_gate, c_up, qs_up, _bits(mode), gs,
-                        want_h_mid=need_h_mid, inplace=True)
+                        want_h_mid=need_hm, inplace=True)
                 else:
                     grad_h_gate, grad_h_up, h_mid_hat = K.swiglu_backward_glu(
                         grad_h_mid, hg, hu, need_h_mid,
@@ -379,9 +391,12 @@ class FlashFFNv3Function(torch.autograd.Function):
                 del grad_h_mid
 
         if need_h_mid:                                                    # :1536-1543
-            if h_mid_hat is None:
+            if h_mid_hat is None and need_hm:
                 h_mid_hat = K.silu_mul(hg, hu)
-            if need_wd:
+            if need_wd and use_wglu:
+                grad_w_down = G.wgrad_glu(gy, _CACHE_CODE[mode], gs, c_gate, qs_gate, c_up, qs_up,
+                                          name="gemm_wgrad_down")
+            elif need_wd:
                 grad_w_down = _mm(gy.t(), h_mid_hat, "gemm_wgrad_down")
             if need_ad:
                 grad_a_down = _mm_scaled(gyB_d.t(), h_mid_hat, s_down, "gemm_grad_a_down")

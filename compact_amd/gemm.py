@@ -462,6 +462,35 @@ def ffn_down_dgrad(grad_y, w_down, cache: int, group_size: int, c_gate, s_gate, 
     return dg, du, hm
 
 
+def wgrad_glu(grad_y: torch.Tensor, cache: int, group_size: int, q_gate, s_gate, q_up, s_up,
+              name: str = "gemm_wgrad_down_glu") -> torch.Tensor:
+    """grad_y^T @ h^ -> bf16 [hidden, inter], h^ = bf16(SiLU(hg^) * hu^) formed
+    from the int4/int8 cache inside the GEMM's operand staging: the weight
+    gradient of the down projection without K2's h_mid^ (bit-equal to
+    mm(grad_y.t(), h_mid_hat), src/flashffn.py:1538-1543)."""
+    _require_device(grad_y, q_gate, s_gate, q_up, s_up)
+    _check_bf16(grad_y)
+    n, hdim = grad_y.shape
+    assert cache in (_lib.CACHE_INT4, _lib.CACHE_INT8), f"int4/int8 cache expected, got {cache}"
+    d = q_gate.shape[1] * (2 if cache == _lib.CACHE_INT4 else 1)
+    assert tuple(q_up.shape) == tuple(q_gate.shape) and q_gate.shape[0] == n
+    assert group_size > 0 and d % group_size == 0, \
+        f"D={d} not divisible by group_size={group_size}"
+    assert tuple(s_gate.shape) == (n, d // group_size) == tuple(s_up.shape), \
+        f"scales {tuple(s_gate.shape)} / {tuple(s_up.shape)} != {(n, d // group_size)}"
+    q_gate, s_gate, q_up, s_up = (t.contiguous() for t in (q_gate, s_gate, q_up, s_up))
+    if grad_y.stride(1) != 1 or grad_y.stride(0) % 8 or grad_y.data_ptr() % 16:
+        grad_y = grad_y.contiguous()
+    c = torch.empty((hdim, d), dtype=torch.bfloat16, device=grad_y.device)
+    with _timed(name):
+        rc = _lib.lib().cpt_gemm_wgrad_glu(grad_y.data_ptr(), grad_y.stride(0), cache, group_size,
+                                           q_gate.data_ptr(), s_gate.data_ptr(), q_up.data_ptr(),
+                                           s_up.data_ptr(), c.data_ptr(), c.stride(0), hdim, d, n,
+                                           _stream(grad_y))
+    check(rc, name)
+    return c
+
+
 def addmm_(c: torch.Tensor, a: torch.Tensor, b: torch.Tensor, alpha: float,
            name: str = "gemm_lora_add") -> torch.Tensor:
     """In place: c = bf16(c + bf16(alpha * bf16(a @ b))), PEFT's

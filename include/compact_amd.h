@@ -264,6 +264,18 @@ int cpt_ffn_gate_up_lora(const void* x, const void* w_gate, const void* w_up, in
                          const void* b_gate, float alpha_gate, const void* p_up,
                          const void* b_up, float alpha_up, void* stream);
 
+/* Weight gradient of the down projection with the GLU decompressed in the
+ * GEMM's operand staging (replaces K2's h_mid^ output and gy^T @ h_mid_hat,
+ * src/flashffn.py:1538-1543): C[hidden, inter] (bf16, rows ldc apart) =
+ * grad_y^T . h^, grad_y [n_tok, hidden] rows ldg apart, h^ = bf16(SiLU(hg^) *
+ * hu^) with hg^ / hu^ the int4/int8 cache (codes + fp16 scales of
+ * group_size 32/64/128) dequantised through bf16, bit-equal to the h_mid^
+ * of cpt_dequant_swiglu_backward, so C equals that GEMM bit for bit. */
+int cpt_gemm_wgrad_glu(const void* grad_y, int64_t ldg, int cache, int64_t group_size,
+                       const void* q_gate, const void* s_gate, const void* q_up,
+                       const void* s_up, void* c, int64_t ldc, int64_t hidden, int64_t inter,
+                       int64_t n_tok, void* stream);
+
 /* Fused backward of the down projection into the GLU (replaces gy @ w_down
  * and K2, src/flashffn.py:1525-1533): grad_h_mid = bf16(grad_y @ w_down)
  * with grad_y [n_tok, hidden], w_down [hidden, inter]; the epilogue reads the
