@@ -453,86 +453,114 @@ class FlashFFNv3Function(torch.autograd.Function):
 
 
 # ---------------------------------------------------------------------------
-# module-level API (src/flashffn.py:1605-1694)
+# module-level API (src/flashffn.py:1605-1694, 1798-1921, 2211-2230)
+#
+# A projection of an MLP is a plain nn.Linear or a PEFT-shaped adapter
+# wrapper (base_layer plus the family's own parameters).  The wrapper is
+# recognised by which adapter parameters it carries (_WRAPPER_TESTS), and a
+# per-family extractor (_EXTRACT) turns it into the factors the Functions
+# take, re-read on every call so training updates and DyLoRA's rank draws are
+# seen.  DoRA and AdaLoRA wrappers also carry LoRA's ModuleDicts, so the
+# families with extra parameters are tested before plain LoRA.
 # ---------------------------------------------------------------------------
 
-def _is_lora(proj: nn.Module) -> bool:
-    return (hasattr(proj, "base_layer")
-            and isinstance(getattr(proj, "lora_A", None), nn.ModuleDict)
-            and len(proj.lora_A) > 0)
+_MLP_PROJS = ("gate_proj", "up_proj", "down_proj")
+_FAMILY_NAME = {"dora": "DoRA", "adalora": "AdaLoRA", "vera": "VeRA", "dylora": "DyLoRA",
+                "lora": "LoRA"}
 
 
-def _v3_extract_proj(proj: nn.Module):
-    """(W, A, B, s) from a plain nn.Linear or a PEFT-LoRA-shaped wrapper
-    (src/flashffn.py:1605-1634).  Plain: (weight, None, None, 0.0).  Rejects
-    DoRA / AdaLoRA / several active adapters; warns that dropout is ignored."""
-    if not _is_lora(proj):
-        return proj.weight, None, None, 0.0
-    if len(getattr(proj, "lora_magnitude_vector", {}) or {}) > 0:
-        raise NotImplementedError("FlashFFNv3 fast path does not support DoRA")
-    if hasattr(proj, "lora_E"):
-        raise NotImplementedError("FlashFFNv3 fast path does not support AdaLoRA")
-    assert len(proj.active_adapters) == 1, "exactly one active adapter expected"
-    name = proj.active_adapters[0]
-    drop = proj.lora_dropout[name]
-    p = float(getattr(drop, "p", 0.0))
-    if p > 0.0:
-        warnings.warn(f"FlashFFNv3 ignores LoRA dropout (p={p}); results differ from PEFT "
-                      "forward when training with dropout.")
-    w = proj.get_base_layer().weight
-    return w, proj.lora_A[name].weight, proj.lora_B[name].weight, float(proj.scaling[name])
+def _holds_entries(proj: nn.Module, attr: str) -> bool:
+    v = getattr(proj, attr, None)
+    return v is not None and len(v) > 0
+
+
+_WRAPPER_TESTS = (
+    ("dora", lambda p: _holds_entries(p, "lora_magnitude_vector")),
+    ("adalora", lambda p: _holds_entries(p, "lora_E")),
+    ("vera", lambda p: _holds_entries(p, "vera_lambda_d")),
+    # DyLoRA keeps its factors as bare Parameters with a rank bound r
+    ("dylora", lambda p: all(isinstance(getattr(p, a, None), nn.Parameter)
+                             for a in ("lora_A", "lora_B"))
+     and hasattr(p, "r") and hasattr(p, "scaling")),
+    ("lora", lambda p: isinstance(getattr(p, "lora_A", None), nn.ModuleDict)
+     and len(p.lora_A) > 0),
+)
 
 
 def _v3_proj_kind(proj: nn.Module) -> str:
-    """Structural (duck-typed) classification of one MLP projection
-    (src/flashffn.py:1798-1821): 'dora' | 'adalora' | 'vera' | 'dylora' |
-    'lora' | 'plain' | 'unknown'."""
-    if hasattr(proj, "base_layer"):
-        if len(getattr(proj, "lora_magnitude_vector", None) or {}) > 0:
-            return "dora"
-        if len(getattr(proj, "lora_E", None) or {}) > 0:
-            return "adalora"
-        if len(getattr(proj, "vera_lambda_d", None) or {}) > 0:
-            return "vera"
-        if (isinstance(getattr(proj, "lora_A", None), nn.Parameter)
-                and isinstance(getattr(proj, "lora_B", None), nn.Parameter)
-                and hasattr(proj, "r") and hasattr(proj, "scaling")):
-            return "dylora"
-        if isinstance(getattr(proj, "lora_A", None), nn.ModuleDict) and len(proj.lora_A) > 0:
-            return "lora"
-        return "unknown"
-    if hasattr(proj, "weight"):
-        return "plain"
+    """Structural classification of one MLP projection (src/flashffn.py:
+    1798-1821): 'dora' | 'adalora' | 'vera' | 'dylora' | 'lora' | 'plain' |
+    'unknown'."""
+    if not hasattr(proj, "base_layer"):
+        return "plain" if hasattr(proj, "weight") else "unknown"
+    for kind, test in _WRAPPER_TESTS:
+        if test(proj):
+            return kind
     return "unknown"
+
+
+def _active_adapter(proj: nn.Module) -> str:
+    names = list(proj.active_adapters)
+    assert len(names) == 1, "exactly one active adapter expected"
+    return names[0]
+
+
+def _warn_dropout(family: str, drop: nn.Module):
+    """The fused path applies no adapter dropout: say so when it is on."""
+    p = float(getattr(drop, "p", 0.0))
+    if p > 0.0:
+        warnings.warn(f"FlashFFNv3 ignores {family} dropout (p={p}); results differ from the "
+                      f"reference forward when training with dropout.")
+
+
+def _lora_factors(proj: nn.Module, family: str = "LoRA"):
+    """(W, A, B, s) of a PEFT LoRA-style wrapper's active adapter."""
+    name = _active_adapter(proj)
+    _warn_dropout(family, proj.lora_dropout[name])
+    return (proj.get_base_layer().weight, proj.lora_A[name].weight, proj.lora_B[name].weight,
+            float(proj.scaling[name]))
+
+
+def _v3_extract_proj(proj: nn.Module):
+    """(W, A, B, s) from a plain nn.Linear (A = B = None, s = 0.0) or a PEFT
+    LoRA wrapper (src/flashffn.py:1605-1634).  Other adapter families raise
+    NotImplementedError: FlashFFNv3Function takes LoRA factors only."""
+    kind = _v3_proj_kind(proj)
+    if kind == "plain":
+        return proj.weight, None, None, 0.0
+    if kind != "lora":
+        raise NotImplementedError(
+            f"FlashFFNv3 fast path does not support {_FAMILY_NAME.get(kind, type(proj).__name__)}")
+    return _lora_factors(proj)
+
+
+def _to_dtype(t, dt):
+    """Cast through autograd (gradients flow back to the stored parameter)."""
+    return t if (t is None or t.dtype == dt) else t.to(dt)
 
 
 def make_v3_forward(mlp: nn.Module, cache_mode: str = "int4", group_size: int = 64,
                     use_triton: bool = True, outlier_ratio: float = 0.0):
     """Drop-in replacement for a LLaMA-style MLP forward (src/flashffn.py:1637-1678).
-    `mlp` exposes gate_proj / up_proj / down_proj, each a plain nn.Linear or a
-    PEFT-LoRA-shaped wrapper; factors are re-extracted on every call and cast
-    to x's dtype through autograd.  Unknown wrappers raise NotImplementedError."""
-    kinds = tuple(_v3_proj_kind(getattr(mlp, p)) for p in ("gate_proj", "up_proj", "down_proj"))
-    if any(k == "unknown" for k in kinds):
+    `mlp` exposes gate_proj / up_proj / down_proj, each a plain nn.Linear or an
+    adapter wrapper.  Plain and LoRA projections run FlashFFNv3Function; any
+    DoRA / AdaLoRA / VeRA / DyLoRA projection sends the MLP to the adapter
+    Function (src/flashffn.py:1660-1661).  Unknown wrappers raise
+    NotImplementedError."""
+    projs = [getattr(mlp, name) for name in _MLP_PROJS]
+    kinds = tuple(_v3_proj_kind(p) for p in projs)
+    if "unknown" in kinds:
         raise NotImplementedError(f"FlashFFNv3: unsupported projection wrapper(s) on MLP: {kinds}")
-    if any(k not in ("plain", "lora") for k in kinds):
-        # DoRA / AdaLoRA / VeRA / DyLoRA (possibly mixed with plain/LoRA) take
-        # the sibling Function (src/flashffn.py:1660-1661)
+    if not set(kinds) <= {"plain", "lora"}:
         assert outlier_ratio == 0.0, "outlier channels are not defined for the adapter Function"
         return make_v3_adapter_forward(mlp, cache_mode, group_size, use_triton)
 
     def v3_forward(x):
-        wg, ag, bg, sg = _v3_extract_proj(mlp.gate_proj)
-        wu, au, bu, su = _v3_extract_proj(mlp.up_proj)
-        wd, ad, bd, sd = _v3_extract_proj(mlp.down_proj)
-        dt = x.dtype
-
-        def cast(t):
-            return t if (t is None or t.dtype == dt) else t.to(dt)
-
-        return FlashFFNv3Function.apply(x, cast(wg), cast(ag), cast(bg), cast(wu), cast(au),
-                                        cast(bu), cast(wd), cast(ad), cast(bd), sg, su, sd,
-                                        cache_mode, group_size, use_triton, outlier_ratio)
+        factors = [_v3_extract_proj(p) for p in projs]
+        tensors = [_to_dtype(t, x.dtype) for f in factors for t in f[:3]]
+        scales = [f[3] for f in factors]
+        return FlashFFNv3Function.apply(x, *tensors, *scales, cache_mode, group_size, use_triton,
+                                        outlier_ratio)
     return v3_forward
 
 
@@ -566,61 +594,65 @@ def _v3_dora_col_norm(w: torch.Tensor, a: torch.Tensor, b: torch.Tensor, s: floa
         return K.dora_col_norm(w.detach(), a.detach(), b.detach(), s, out_dtype)
 
 
-def _v3_warn_dropout(kind: str, p: float):
-    if p > 0.0:
-        warnings.warn(f"FlashFFNv3 ignores {kind} dropout (p={p}); results differ from the "
-                      "reference forward when training with dropout.")
+# Per-family factor extraction: proj -> (W, A, B, s, m, nu) in the stored
+# dtype (the caller casts).  AdaLoRA's A*E and VeRA's lambda-scaled frozen
+# factors are composed here, in autograd, so their chain rules run on [r, in]
+# / [out, r] tensors; DyLoRA passes rank-b slices (b uniform in 1..r in
+# training, r in eval); DoRA adds its magnitude m and the detached norm nu.
+
+def _plain_adapter(proj):
+    return proj.weight, None, None, 0.0, None, None
+
+
+def _lora_adapter(proj):
+    return _lora_factors(proj) + (None, None)
+
+
+def _dylora_adapter(proj):
+    _warn_dropout("DyLoRA", proj.dropout)
+    rank = _rng_randint(1, proj.r) if proj.training else proj.r
+    return (proj.base_layer.weight, proj.lora_A[:rank, :], proj.lora_B[:, :rank],
+            float(proj.scaling), None, None)
+
+
+def _adalora_adapter(proj):
+    name = _active_adapter(proj)
+    _warn_dropout("AdaLoRA", proj.lora_dropout[name])
+    s_eff = float(proj.scaling[name]) / (float(proj.ranknum[name]) + 1e-5)
+    return (proj.get_base_layer().weight, proj.lora_A[name] * proj.lora_E[name],
+            proj.lora_B[name], s_eff, None, None)
+
+
+def _vera_adapter(proj):
+    name = _active_adapter(proj)
+    _warn_dropout("VeRA", proj.vera_dropout[name])
+    a_frozen = proj.vera_A[name][:, : proj.in_features]
+    b_frozen = proj.vera_B[name][: proj.out_features, :]
+    return (proj.get_base_layer().weight, proj.vera_lambda_d[name].unsqueeze(-1) * a_frozen,
+            proj.vera_lambda_b[name].unsqueeze(-1) * b_frozen, 1.0, None, None)
+
+
+def _dora_adapter(proj):
+    w, a, b, s = _lora_factors(proj, "DoRA")
+    return w, a, b, s, proj.lora_magnitude_vector[_active_adapter(proj)].weight, None
+
+
+_EXTRACT = {"plain": _plain_adapter, "lora": _lora_adapter, "dylora": _dylora_adapter,
+            "adalora": _adalora_adapter, "vera": _vera_adapter, "dora": _dora_adapter}
 
 
 def _v3_extract_proj_adapter(proj: nn.Module, dt: torch.dtype):
-    """(w, a, b, s, m, nu) of one projection, re-extracted per forward
-    (src/flashffn.py:1850-1921).  AdaLoRA's A*E and VeRA's lambda-scaled
-    frozen factors are composed here, in autograd, so their thin chain rules
-    run on [r, in] / [out, r] tensors; DyLoRA passes rank-b slices (b uniform
-    in 1..r in training, r in eval); DoRA adds m [out] and the detached norm
-    nu [out].  Everything is cast to dt through autograd."""
+    """(w, a, b, s, m, nu) of one projection in dtype dt, re-extracted per
+    forward (src/flashffn.py:1850-1921).  DoRA's nu is computed from the
+    cast factors; everything else is cast through autograd."""
     kind = _v3_proj_kind(proj)
-
-    def cast(t):
-        return t if (t is None or t.dtype == dt) else t.to(dt)
-
-    if kind == "plain":
-        return cast(proj.weight), None, None, 0.0, None, None
-    if kind == "lora":
-        w, a, b, s = _v3_extract_proj(proj)
-        return cast(w), cast(a), cast(b), s, None, None
-    if kind == "dylora":
-        _v3_warn_dropout("DyLoRA", float(getattr(proj.dropout, "p", 0.0)))
-        b_rank = _rng_randint(1, proj.r) if proj.training else proj.r
-        return (cast(proj.base_layer.weight), cast(proj.lora_A[:b_rank, :]),
-                cast(proj.lora_B[:, :b_rank]), float(proj.scaling), None, None)
-    if kind == "adalora":
-        name = proj.active_adapters[0]
-        _v3_warn_dropout("AdaLoRA", float(getattr(proj.lora_dropout[name], "p", 0.0)))
-        a_eff = proj.lora_A[name] * proj.lora_E[name]
-        s_eff = float(proj.scaling[name]) / (float(proj.ranknum[name]) + 1e-5)
-        return (cast(proj.get_base_layer().weight), cast(a_eff), cast(proj.lora_B[name]),
-                s_eff, None, None)
-    if kind == "vera":
-        name = proj.active_adapters[0]
-        _v3_warn_dropout("VeRA", float(getattr(proj.vera_dropout[name], "p", 0.0)))
-        a_frozen = proj.vera_A[name][:, : proj.in_features]
-        b_frozen = proj.vera_B[name][: proj.out_features, :]
-        a_eff = proj.vera_lambda_d[name].unsqueeze(-1) * a_frozen
-        b_eff = proj.vera_lambda_b[name].unsqueeze(-1) * b_frozen
-        return cast(proj.get_base_layer().weight), cast(a_eff), cast(b_eff), 1.0, None, None
-    if kind == "dora":
-        name = proj.active_adapters[0]
-        _v3_warn_dropout("DoRA", float(getattr(proj.lora_dropout[name], "p", 0.0)))
-        w = cast(proj.get_base_layer().weight)
-        a = cast(proj.lora_A[name].weight)
-        b = cast(proj.lora_B[name].weight)
-        s = float(proj.scaling[name])
-        m = cast(proj.lora_magnitude_vector[name].weight)
-        nu = _v3_dora_col_norm(w, a, b, s, out_dtype=dt)
-        return w, a, b, s, m, nu
-    raise NotImplementedError(
-        f"FlashFFNv3 adapter path: unsupported projection wrapper ({type(proj).__name__}).")
+    if kind not in _EXTRACT:
+        raise NotImplementedError(
+            f"FlashFFNv3 adapter path: unsupported projection wrapper ({type(proj).__name__}).")
+    w, a, b, s, m, _ = _EXTRACT[kind](proj)
+    w, a, b, m = (_to_dtype(t, dt) for t in (w, a, b, m))
+    nu = _v3_dora_col_norm(w, a, b, s, out_dtype=dt) if m is not None else None
+    return w, a, b, s, m, nu
 
 
 def _rng_randint(lo: int, hi: int) -> int:
@@ -892,14 +924,14 @@ def make_v3_adapter_forward(mlp: nn.Module, cache_mode: str = "int4", group_size
     AdaLoRA / VeRA / DyLoRA wrapped, mixed with plain or LoRA ones
     (src/flashffn.py:2211-2230).  Factors, the DoRA norm and DyLoRA's rank
     are re-extracted on every call."""
+    projs = [getattr(mlp, name) for name in _MLP_PROJS]
+
     def v3_adapter_forward(x):
-        dt = x.dtype
-        wg, ag, bg, sg, mg, nug = _v3_extract_proj_adapter(mlp.gate_proj, dt)
-        wu, au, bu, su, mu, nuu = _v3_extract_proj_adapter(mlp.up_proj, dt)
-        wd, ad, bd, sd, md, nud = _v3_extract_proj_adapter(mlp.down_proj, dt)
-        return FlashFFNv3AdapterFunction.apply(x, wg, ag, bg, mg, nug, wu, au, bu, mu, nuu,
-                                               wd, ad, bd, md, nud, sg, su, sd, cache_mode,
-                                               group_size, use_triton)
+        per = [_v3_extract_proj_adapter(p, x.dtype) for p in projs]
+        tensors = [t for w, a, b, _, m, nu in per for t in (w, a, b, m, nu)]
+        scales = [f[3] for f in per]
+        return FlashFFNv3AdapterFunction.apply(x, *tensors, *scales, cache_mode, group_size,
+                                               use_triton)
     return v3_adapter_forward
 
 
