@@ -75,12 +75,16 @@ def test_outlier_codec_bit_exact(device, bits, group):
     assert np.array_equal(deq.cpu().view(torch.int16).numpy().view(np.uint16), rdeq)
 
 
-@pytest.mark.parametrize("bits,group", [(4, 64), (8, 128)])
-def test_outlier_k1_k2_equal_standalone(device, bits, group):
+@pytest.mark.parametrize("bits,group,n,d", [(4, 64, 256, 1024), (8, 128, 256, 1024),
+                                            (4, 64, 7, 1024), (8, 512, 258, 2048),
+                                            (4, 8, 1, 1024), (8, 32, 5, 1024)])
+def test_outlier_k1_k2_equal_standalone(device, bits, group, n, d):
+    """K1 takes kK1Rows rows per thread: row counts that are not a multiple
+    of it, one row, and groups of 1 to 64 lanes."""
     cpt, _ = _cpt()
-    a, b = _hot(256, 1024, 9)
+    a, b = _hot(n, d, 9)
     ga, gb = a.to(device), b.to(device)
-    k = int(1024 * 0.01)
+    k = int(d * 0.01)
     sg_, _ = cpt.outlier_select(ga, k)
     su_, _ = cpt.outlier_select(gb, k)
     hm, qg, sg, og, qu, su, ou = cpt.silu_mul_quant_outlier(ga, gb, bits, group, sg_, su_, k)
@@ -92,7 +96,7 @@ def test_outlier_k1_k2_equal_standalone(device, bits, group):
     assert torch.equal(og.view(torch.int16), o2.view(torch.int16))
     assert torch.equal(ou.view(torch.int16), o3.view(torch.int16))
     assert torch.equal(hm.view(torch.int16), cpt.silu_mul(ga, gb).view(torch.int16))
-    gm = torch.randn(256, 1024, device=device).to(torch.bfloat16)
+    gm = torch.randn(n, d, device=device).to(torch.bfloat16)
     dg, du, h = cpt.dequant_swiglu_backward_outlier(gm, qg, sg, og, sg_, qu, su, ou, su_, bits,
                                                     group, want_h_mid=True)
     hg = cpt.v3_dequantize_outlier(qg, sg, og, sg_, bits, group)
