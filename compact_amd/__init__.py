@@ -12,8 +12,8 @@ from .kernels import (  # noqa: F401
     v3_quantize_group_absmax, v3_dequantize_group_absmax,
     triton_silu_mul, triton_swiglu_backward, triton_swiglu_backward_glu,
     triton_silu_mul_quant, triton_dequant_swiglu_backward,
-    outlier_select, v3_quantize_outlier, v3_dequantize_outlier, silu_mul_quant_outlier,
-    dequant_swiglu_backward_outlier, dora_scale, col_dot_div, dora_col_norm,
+    outlier_select, outlier_select_pair, v3_quantize_outlier, v3_dequantize_outlier,
+    silu_mul_quant_outlier, dequant_swiglu_backward_outlier, dora_scale, col_dot_div, dora_col_norm,
     topk_abs, topk_scatter,
 )
 from .flashffn import (  # noqa: F401

@@ -691,12 +691,26 @@ inline int glu_dispatch(int op, int dt, const void* a, const void* g, const void
 constexpr int kColRows = 64;    // rows per partial sum
 
 // partial[chunk][col] = sum over rows [chunk*kColRows, +kColRows) of t^2 (fp64)
+// Outlier selection runs on one tensor or on two of one shape (gate and up)
+// in the same launches: blockIdx.z picks the tensor's pointers.
+struct SelectOne {
+  const void* t;          // [n(+), d] activations (the first n rows rank)
+  double* partial;        // [chunks, d] fp64 partial sums
+  double* sumsq;          // [d]
+  int16_t* slot;          // [d]
+  int32_t* idx;           // [k]
+};
+struct SelectSet {
+  SelectOne s[2];
+};
+
 template <int DT>
-__global__ __launch_bounds__(64) void colsumsq_partial_kernel(
-    const void* __restrict__ t, double* __restrict__ partial, int64_t n, int64_t d) {
+__global__ __launch_bounds__(64) void colsumsq_partial_kernel(SelectSet S, int64_t n, int64_t d) {
   // one wavefront per 512-column strip and kColRows rows; 8 columns per lane
   // (one 128-bit load of bf16/fp16), fp64 accumulation in row order
   using E = Elem<DT>;
+  const void* __restrict__ t = S.s[blockIdx.z].t;
+  double* __restrict__ partial = S.s[blockIdx.z].partial;
   const int64_t col = ((int64_t)blockIdx.x * 64 + threadIdx.x) * 8;
   const int64_t r0 = (int64_t)blockIdx.y * kColRows;
   if (col >= d) return;
@@ -736,11 +750,13 @@ __global__ __launch_bounds__(64) void colsumsq_partial_kernel(
   for (int e = 0; e < 8; ++e) out[e] = acc[e];
 }
 
-__global__ __launch_bounds__(kBlock) void colsumsq_reduce_kernel(
-    const double* __restrict__ partial, double* __restrict__ sumsq, int64_t d, int chunks) {
+__global__ __launch_bounds__(kBlock) void colsumsq_reduce_kernel(SelectSet S, int64_t d,
+                                                                  int chunks) {
   // 64 columns per block; wave w sums chunks w, w + 4, ...; the four wave
   // sums are added in wave order (fixed order, deterministic)
   __shared__ double part[kBlock / 64][64];
+  const double* __restrict__ partial = S.s[blockIdx.z].partial;
+  double* __restrict__ sumsq = S.s[blockIdx.z].sumsq;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t col = (int64_t)blockIdx.x * 64 + lane;
   double acc = 0.0;
@@ -764,12 +780,13 @@ constexpr int64_t kPickStagedMax = 16384;  // 128 KiB of fp64 sums staged in LDS
 constexpr int kPickWaves = kPickThreads / 64;
 
 template <bool STAGED>
-__global__ __launch_bounds__(kPickThreads) void outlier_pick_kernel(const double* __restrict__ vg,
-                                                                    int64_t d, int64_t k,
-                                                                    int16_t* __restrict__ slot,
-                                                                    int32_t* __restrict__ idx) {
+__global__ __launch_bounds__(kPickThreads) void outlier_pick_kernel(SelectSet S, int64_t d,
+                                                                    int64_t k) {
   // STAGED: the d sums are copied to LDS once and every pass reads them there
   extern __shared__ __align__(16) unsigned char pick_smem[];
+  const double* __restrict__ vg = S.s[blockIdx.z].sumsq;
+  int16_t* __restrict__ slot = S.s[blockIdx.z].slot;
+  int32_t* __restrict__ idx = S.s[blockIdx.z].idx;
   const double* v = vg;
   if constexpr (STAGED) {
     double* sv = reinterpret_cast<double*>(pick_smem);
@@ -1065,24 +1082,19 @@ int cpt_dequant_swiglu_backward(const void* grad_h_mid, const void* q_gate, cons
   return launch_status();
 }
 
-int cpt_outlier_select(const void* t, int dtype, int64_t n, int64_t d, int64_t k,
-                       void* partial, void* sumsq, void* slot, void* idx, void* stream) {
-  if (n < 0 || d < 0 || k < 0 || k > d || k >= 32768) return kErrShape;
-  if (dtype != kF32 && dtype != kF16 && dtype != kBF16) return kErrDType;
-  if (d == 0) return kOk;
-  if (!slot || !sumsq || (n > 0 && (!t || !partial)) || (k > 0 && !idx)) return kErrShape;
-  if (n > 0 && ((d % 8) || !aligned16(t))) return kErrAlign;   // 8-column vector loads
-  hipStream_t st = (hipStream_t)stream;
+namespace {
+// ntensor (1 or 2) selections of one shape, in three launches
+int outlier_select_set(const SelectSet& S, int ntensor, int dtype, int64_t n, int64_t d,
+                       int64_t k, hipStream_t st) {
   const int chunks = (int)((n + kColRows - 1) / kColRows);
-  const unsigned gx = grid_for(d);
+  const unsigned z = (unsigned)ntensor;
   if (chunks > 0) {
-    dim3 grid((unsigned)((d + 511) / 512), (unsigned)chunks);
-    if (dtype == kBF16) colsumsq_partial_kernel<kBF16><<<grid, 64, 0, st>>>(t, (double*)partial, n, d);
-    else if (dtype == kF16) colsumsq_partial_kernel<kF16><<<grid, 64, 0, st>>>(t, (double*)partial, n, d);
-    else colsumsq_partial_kernel<kF32><<<grid, 64, 0, st>>>(t, (double*)partial, n, d);
+    dim3 grid((unsigned)((d + 511) / 512), (unsigned)chunks, z);
+    if (dtype == kBF16) colsumsq_partial_kernel<kBF16><<<grid, 64, 0, st>>>(S, n, d);
+    else if (dtype == kF16) colsumsq_partial_kernel<kF16><<<grid, 64, 0, st>>>(S, n, d);
+    else colsumsq_partial_kernel<kF32><<<grid, 64, 0, st>>>(S, n, d);
   }
-  colsumsq_reduce_kernel<<<(unsigned)((d + 63) / 64), kBlock, 0, st>>>((const double*)partial,
-                                                                        (double*)sumsq, d, chunks);
+  colsumsq_reduce_kernel<<<dim3((unsigned)((d + 63) / 64), 1, z), kBlock, 0, st>>>(S, d, chunks);
   static bool staged_attr = false;
   if (!staged_attr) {
     staged_attr = hipFuncSetAttribute((const void*)outlier_pick_kernel<true>,
@@ -1090,12 +1102,50 @@ int cpt_outlier_select(const void* t, int dtype, int64_t n, int64_t d, int64_t k
                                       (int)(kPickStagedMax * sizeof(double))) == hipSuccess;
   }
   if (staged_attr && d <= kPickStagedMax)
-    outlier_pick_kernel<true><<<1, kPickThreads, (size_t)d * sizeof(double), st>>>(
-        (const double*)sumsq, d, k, (int16_t*)slot, (int32_t*)idx);
+    outlier_pick_kernel<true><<<dim3(1, 1, z), kPickThreads, (size_t)d * sizeof(double), st>>>(
+        S, d, k);
   else
-    outlier_pick_kernel<false><<<1, kPickThreads, 0, st>>>((const double*)sumsq, d, k,
-                                                           (int16_t*)slot, (int32_t*)idx);
+    outlier_pick_kernel<false><<<dim3(1, 1, z), kPickThreads, 0, st>>>(S, d, k);
   return launch_status();
+}
+
+int select_args_ok(const void* t, int64_t n, int64_t d, int64_t k, const void* partial,
+                   const void* sumsq, const void* slot, const void* idx) {
+  if (!slot || !sumsq || (n > 0 && (!t || !partial)) || (k > 0 && !idx)) return kErrShape;
+  if (n > 0 && ((d % 8) || !aligned16(t))) return kErrAlign;   // 8-column vector loads
+  return kOk;
+}
+}  // namespace
+
+int cpt_outlier_select(const void* t, int dtype, int64_t n, int64_t d, int64_t k,
+                       void* partial, void* sumsq, void* slot, void* idx, void* stream) {
+  if (n < 0 || d < 0 || k < 0 || k > d || k >= 32768) return kErrShape;
+  if (dtype != kF32 && dtype != kF16 && dtype != kBF16) return kErrDType;
+  if (d == 0) return kOk;
+  const int rc = select_args_ok(t, n, d, k, partial, sumsq, slot, idx);
+  if (rc) return rc;
+  SelectSet S{};
+  S.s[0] = {t, (double*)partial, (double*)sumsq, (int16_t*)slot, (int32_t*)idx};
+  S.s[1] = S.s[0];
+  return outlier_select_set(S, 1, dtype, n, d, k, (hipStream_t)stream);
+}
+
+int cpt_outlier_select_pair(const void* t0, const void* t1, int dtype, int64_t n, int64_t d,
+                            int64_t k, void* partial, void* sumsq, void* slot0, void* idx0,
+                            void* slot1, void* idx1, void* stream) {
+  if (n < 0 || d < 0 || k < 0 || k > d || k >= 32768) return kErrShape;
+  if (dtype != kF32 && dtype != kF16 && dtype != kBF16) return kErrDType;
+  if (d == 0) return kOk;
+  const int64_t chunks = (n + kColRows - 1) / kColRows;
+  double* p1 = partial ? (double*)partial + chunks * d : nullptr;
+  double* q1 = sumsq ? (double*)sumsq + d : nullptr;
+  int rc = select_args_ok(t0, n, d, k, partial, sumsq, slot0, idx0);
+  if (!rc) rc = select_args_ok(t1, n, d, k, p1, q1, slot1, idx1);
+  if (rc) return rc;
+  SelectSet S{};
+  S.s[0] = {t0, (double*)partial, (double*)sumsq, (int16_t*)slot0, (int32_t*)idx0};
+  S.s[1] = {t1, p1, q1, (int16_t*)slot1, (int32_t*)idx1};
+  return outlier_select_set(S, 2, dtype, n, d, k, (hipStream_t)stream);
 }
 
 int cpt_v3_quantize_outlier(const void* t, int dtype, int64_t n, int64_t d, int bits,

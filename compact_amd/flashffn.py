@@ -159,11 +159,25 @@ def _proj(x_2d, w, a, b, s, name):
     return h, xa
 
 
+def _stackable(p, q) -> bool:
+    """Two rank-r factors that one skinny product can take stacked: ranks up to
+    32 together, the first a multiple of 8 (so the second's columns start on a
+    16-byte boundary)."""
+    return (p is not None and q is not None and p.dtype == q.dtype
+            and p.shape[0] % 8 == 0 and p.shape[0] + q.shape[0] <= G.SKINNY_MAX_RANK)
+
+
 def _gate_up_lora(x_2d, a_gate, b_gate, s_gate, a_up, b_up, s_up):
     """(xa_g | None, xa_u | None, ffn_gate_up keyword terms) for the fused
-    gate/up GEMM."""
-    xa_g = _mm(x_2d, a_gate.t(), "gemm_fwd_gate_xa") if a_gate is not None else None
-    xa_u = _mm(x_2d, a_up.t(), "gemm_fwd_up_xa") if a_up is not None else None
+    gate/up GEMM.  With both adapters, x [A_g; A_u]^T is one pass over x: its
+    column halves equal the two products bit for bit."""
+    if _stackable(a_gate, a_up) and x_2d.shape[0] >= 256 and x_2d.shape[1] >= 256:
+        r = a_gate.shape[0]
+        xa = _mm(x_2d, torch.cat([a_gate, a_up]).t(), "gemm_fwd_gate_up_xa")
+        xa_g, xa_u = xa[:, :r], xa[:, r:]
+    else:
+        xa_g = _mm(x_2d, a_gate.t(), "gemm_fwd_gate_xa") if a_gate is not None else None
+        xa_u = _mm(x_2d, a_up.t(), "gemm_fwd_up_xa") if a_up is not None else None
     kw = dict(lora_gate=None if a_gate is None else (xa_g, b_gate, s_gate),
               lora_up=None if a_up is None else (xa_u, b_up, s_up))
     return xa_g, xa_u, kw
@@ -234,8 +248,7 @@ class FlashFFNv3Function(torch.autograd.Function):
                 h_up, xa_u = _proj(x_2d, w_up, a_up, b_up, s_up, "gemm_fwd_up")
             if k_out > 0:
                 rows = outlier_stat_rows(orig_shape)
-                slot_gate, _ = K.outlier_select(h_gate, k_out, rows)
-                slot_up, _ = K.outlier_select(h_up, k_out, rows)
+                (slot_gate, _), (slot_up, _) = K.outlier_select_pair(h_gate, h_up, k_out, rows)
             if fused_quant and k_out > 0:
                 h_mid, c_gate, qs_gate, o_gate, c_up, qs_up, o_up = K.silu_mul_quant_outlier(
                     h_gate, h_up, _bits(cache_mode), group_size, slot_gate, slot_up, k_out)
@@ -408,12 +421,26 @@ class FlashFFNv3Function(torch.autograd.Function):
         grad_w_gate = grad_a_gate = grad_b_gate = None
         grad_w_up = grad_a_up = grad_b_up = None
         if need_gate_path:                                                # :1551-1587
-            ghgB = None
-            if a_gate is not None and (need_x or need_ag):
-                ghgB = _mm(grad_h_gate, b_gate, "gemm_ghgB")
-            ghuB = None
-            if a_up is not None and (need_x or need_au):
-                ghuB = _mm(grad_h_up, b_up, "gemm_ghuB")
+            ghgB = ghuB = ghB = None
+            # dg B_g and du B_u side by side in one [N, r_g + r_u] buffer, so
+            # one token reduction over x gives both A gradients below
+            stack = (_stackable(b_gate.t() if b_gate is not None else None,
+                                b_up.t() if b_up is not None else None)
+                     and (need_x or need_ag or need_au) and grad_h_gate.shape[0] >= 256
+                     and _mfma(grad_h_gate, b_gate, grad_h_up, b_up)
+                     and grad_h_gate.shape[1] >= 256)
+            if stack:
+                r = b_gate.shape[1]
+                ghB = torch.empty((grad_h_gate.shape[0], r + b_up.shape[1]),
+                                  dtype=grad_h_gate.dtype, device=grad_h_gate.device)
+                G.skinny(grad_h_gate, b_gate.t(), 1.0, "gemm_ghgB", out=ghB[:, :r])
+                G.skinny(grad_h_up, b_up.t(), 1.0, "gemm_ghuB", out=ghB[:, r:])
+                ghgB, ghuB = ghB[:, :r], ghB[:, r:]
+            else:
+                if a_gate is not None and (need_x or need_ag):
+                    ghgB = _mm(grad_h_gate, b_gate, "gemm_ghgB")
+                if a_up is not None and (need_x or need_au):
+                    ghuB = _mm(grad_h_up, b_up, "gemm_ghuB")
             if need_x:
                 xl = [(ghgB, a_gate, s_gate) if a_gate is not None else None,
                       (ghuB, a_up, s_up) if a_up is not None else None]
@@ -430,12 +457,18 @@ class FlashFFNv3Function(torch.autograd.Function):
                         grad_x = _addmm(grad_x, ghuB, a_up, s_up, "gemm_dgrad_x_lora_up")
             if need_bg:
                 grad_b_gate = _mm_scaled(grad_h_gate.t(), xa_g, s_gate, "gemm_grad_b_gate")
-            if need_ag:
-                grad_a_gate = _mm_scaled(ghgB.t(), x_2d, s_gate, "gemm_grad_a_gate")
+            if ghB is not None and need_ag and need_au and s_gate == s_up:
+                # s [dg B_g | du B_u]^T x: its row halves equal the two
+                # reductions bit for bit (same token order per row)
+                ga = _mm_scaled(ghB.t(), x_2d, s_gate, "gemm_grad_a_gate_up")
+                grad_a_gate, grad_a_up = ga[:ghgB.shape[1]], ga[ghgB.shape[1]:]
+            else:
+                if need_ag:
+                    grad_a_gate = _mm_scaled(ghgB.t(), x_2d, s_gate, "gemm_grad_a_gate")
+                if need_au:
+                    grad_a_up = _mm_scaled(ghuB.t(), x_2d, s_up, "gemm_grad_a_up")
             if need_bu:
                 grad_b_up = _mm_scaled(grad_h_up.t(), xa_u, s_up, "gemm_grad_b_up")
-            if need_au:
-                grad_a_up = _mm_scaled(ghuB.t(), x_2d, s_up, "gemm_grad_a_up")
             if need_wg:
                 grad_w_gate = _mm(grad_h_gate.t(), x_2d, "gemm_wgrad_gate")
             if need_wu:

@@ -132,10 +132,14 @@ _SPAN_BYTES = 1 << 31
 
 
 def skinny(a: torch.Tensor, q: torch.Tensor, alpha: float = 1.0,
-           name: str = "gemm_skinny") -> torch.Tensor:
+           name: str = "gemm_skinny", out: torch.Tensor | None = None) -> torch.Tensor:
     """bf16(alpha * a [M, K] @ q[R, K].T) for a rank R <= 32: the tall-skinny
     adapter products (x A^T, grad_y B, ...), streamed once through HBM with K
-    split across blocks (fp32 partials summed in a fixed order)."""
+    split across blocks (fp32 partials summed in a fixed order).  Each output
+    column's sum runs in the same order whatever R is, so stacked factors
+    give the columns of separate products bit for bit.  out: a bf16 [M, R]
+    view with unit column stride and 16-byte aligned rows (e.g. the column
+    half of a wider buffer) to write into."""
     _require_device(a, q)
     _check_bf16(a, q)
     M, K = a.shape
@@ -150,12 +154,18 @@ def skinny(a: torch.Tensor, q: torch.Tensor, alpha: float = 1.0,
     # M = 8192, K = 4096 / 11008: 3.6 / 4.9 TB/s)
     blocks = (M + 127) // 128
     splits = max(1, min(K // 256, (512 + blocks - 1) // blocks))
-    c = torch.empty((M, R), dtype=torch.bfloat16, device=a.device)
+    if out is None:
+        c = torch.empty((M, R), dtype=torch.bfloat16, device=a.device)
+    else:
+        c = out
+        assert (tuple(c.shape) == (M, R) and c.dtype == torch.bfloat16 and c.stride(1) == 1
+                and c.stride(0) % 8 == 0 and c.data_ptr() % 16 == 0), "skinny out layout"
     ws = (torch.empty((splits * M * R,), dtype=torch.float32, device=a.device)
           if splits > 1 else None)
     with _timed(name):
         rc = _lib.lib().cpt_gemm_bf16_skinny(a.data_ptr(), a.stride(0), q.data_ptr(),
-                                             q.stride(0), c.data_ptr(), R, M, R, K, float(alpha),
+                                             q.stride(0), c.data_ptr(), c.stride(0), M, R, K,
+                                             float(alpha),
                                              splits, None if ws is None else ws.data_ptr(),
                                              _stream(a))
     check(rc, name)

@@ -332,6 +332,31 @@ def outlier_select(t: torch.Tensor, k: int, rows: int | None = None):
     return slot, idx[:k]
 
 
+def outlier_select_pair(t0: torch.Tensor, t1: torch.Tensor, k: int, rows: int | None = None):
+    """outlier_select of t0 and of t1 (same shape and dtype) in the same
+    launches.  Returns ((slot0, idx0), (slot1, idx1)), each equal to
+    outlier_select on that tensor."""
+    _require_device(t0, t1)
+    t0, t1 = t0.contiguous(), t1.contiguous()
+    assert t0.shape == t1.shape and t0.dtype == t1.dtype, \
+        f"pair of {tuple(t0.shape)} {t0.dtype} and {tuple(t1.shape)} {t1.dtype}"
+    n, d = t0.shape
+    if rows is not None:
+        assert 0 <= rows <= n, f"rows={rows} outside [0, {n}]"
+        n = rows
+    dev = t0.device
+    chunks = max(1, (n + 63) // 64)            # 64-row fp64 partial sums
+    partial = torch.empty((2, chunks, d), dtype=torch.float64, device=dev)
+    sumsq = torch.empty((2, d), dtype=torch.float64, device=dev)
+    slot = torch.empty((2, d), dtype=torch.int16, device=dev)
+    idx = torch.empty((2, max(k, 1)), dtype=torch.int32, device=dev)
+    check(_lib.lib().cpt_outlier_select_pair(
+        t0.data_ptr(), t1.data_ptr(), _dtype_code(t0), n, d, k, partial.data_ptr(),
+        sumsq.data_ptr(), slot[0].data_ptr(), idx[0].data_ptr(), slot[1].data_ptr(),
+        idx[1].data_ptr(), _stream(t0)), "outlier_select_pair")
+    return (slot[0], idx[0, :k]), (slot[1], idx[1, :k])
+
+
 def _outlier_buf(n, k, dev):
     return torch.empty((n, k), dtype=torch.bfloat16, device=dev)
 

@@ -109,6 +109,17 @@ int cpt_dequant_swiglu_backward(const void* grad_h_mid, const void* q_gate, cons
 int cpt_outlier_select(const void* t, int dtype, int64_t n, int64_t d, int64_t k,
                        void* partial, void* sumsq, void* slot, void* idx, void* stream);
 
+/* cpt_outlier_select on two tensors of one shape, t0 and t1 (the gate and up
+ * activations), in the same three launches, so the two single-block ranking
+ * passes run side by side.  Each tensor's results equal a cpt_outlier_select
+ * call on it.  Workspace: partial fp64 [2, ceil(n/64), d] and sumsq fp64
+ * [2, d], tensor i using block i.  No counterpart in the reference, which
+ * ranks each tensor on its own (compress_function.py:80-88); for callers that
+ * select the gate and up channels of one forward together. */
+int cpt_outlier_select_pair(const void* t0, const void* t1, int dtype, int64_t n, int64_t d,
+                            int64_t k, void* partial, void* sumsq, void* slot0, void* idx0,
+                            void* slot1, void* idx1, void* stream);
+
 /* v3_quantize_group_absmax with the slot columns extracted (copied to
  * outliers, zeroed) before quantisation. */
 int cpt_v3_quantize_outlier(const void* t, int dtype, int64_t n, int64_t d, int bits,

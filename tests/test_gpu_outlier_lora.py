@@ -57,6 +57,33 @@ def test_outlier_select_matches_oracle(device, ratio, rows):
         assert s[want].tolist() == list(range(k))
 
 
+@pytest.mark.parametrize("n,d,ratio,rows", [(384, 2048, 0.01, 128), (384, 2048, 0.05, None),
+                                            (1, 1024, 0.01, None), (300, 11008, 0.01, 100),
+                                            (64, 512, 0.0, None)])
+def test_outlier_select_pair_equals_singles(device, n, d, ratio, rows):
+    """Both tensors selected in the same launches: each result bit-equal to
+    its own single selection and to the oracle."""
+    cpt, _ = _cpt()
+    a, b = _hot(n, d, 15)
+    ga, gb = a.to(device), b.to(device)
+    k = int(d * ratio)
+    (s0, i0), (s1, i1) = cpt.outlier_select_pair(ga, gb, k, rows)
+    for t, s, i in ((ga, s0, i0), (gb, s1, i1)):
+        rs, ri = cpt.outlier_select(t, k, rows)
+        assert torch.equal(s, rs) and torch.equal(i, ri)
+        want = codec.outlier_channels(to_f32(t.cpu()), ratio, rows)
+        assert i.cpu().numpy().tolist() == want.tolist()
+
+
+def test_outlier_select_pair_rejects_mismatch(device):
+    cpt, _ = _cpt()
+    a = torch.zeros(8, 64, dtype=torch.bfloat16, device=device)
+    with pytest.raises(AssertionError):
+        cpt.outlier_select_pair(a, torch.zeros(8, 128, dtype=torch.bfloat16, device=device), 1)
+    with pytest.raises(AssertionError):
+        cpt.outlier_select_pair(a, a.float(), 1)
+
+
 @pytest.mark.parametrize("bits,group", [(4, 64), (8, 128), (4, 32)])
 def test_outlier_codec_bit_exact(device, bits, group):
     cpt, _ = _cpt()
@@ -228,3 +255,34 @@ def test_c3_saved_bytes(device):
     k = int(D * 0.01)
     want = R.saved_bytes_closed_form(N, H, D, 4, 64, n_thin=3, rank=RANK, n_outlier=k)
     assert got == want + 2 * D * 2, entries     # + the two int16 slot tables
+
+
+@pytest.mark.parametrize("ratio,rank,s_up,mode", [(0.01, 16, 2.0, "int4"), (0.0, 16, 2.0, "int8"),
+                                                  (0.0, 8, 2.0, "bf16"), (0.01, 16, 1.0, "int4")])
+def test_stacked_adapter_products_bitwise(device, monkeypatch, ratio, rank, s_up, mode):
+    """Gate and up adapters stacked into one skinny product: x [A_g; A_u]^T in
+    the forward, [dg B_g | du B_u] and its one token reduction over x in the
+    backward (when s_gate == s_up).  Every output and gradient equals the
+    unstacked route bit for bit."""
+    cpt, _ = _cpt()
+    from compact_amd import flashffn as F
+    n, h, d = 512, 256, 768
+    ps = R.synthetic_param_set("all", h, d, rank, 2.0, seed=31, dtype=torch.bfloat16,
+                               peft_init=True, b_std=0.05)
+    ps["s_up"] = s_up
+    psd = {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in ps.items()}
+    gen = torch.Generator().manual_seed(32)
+    x = torch.randn(2, n // 2, h, generator=gen).to(torch.bfloat16).to(device)
+    gy = torch.randn(2, n // 2, h, generator=gen).to(torch.bfloat16).to(device)
+    calls = []
+    real = F._stackable
+    monkeypatch.setattr(F, "_stackable", lambda p, q: calls.append(1) or real(p, q))
+    got, y = R.run_function_grads(cpt.FlashFFNv3Function.apply, psd, x, gy, mode, 64, True, ratio)
+    assert calls and real(psd["a_gate"], psd["a_up"])
+    monkeypatch.setattr(F, "_stackable", lambda p, q: False)
+    want, y2 = R.run_function_grads(cpt.FlashFFNv3Function.apply, psd, x, gy, mode, 64, True,
+                                    ratio)
+    assert torch.equal(y.view(torch.int16), y2.view(torch.int16))
+    assert set(got) == set(want)
+    for k in want:
+        assert torch.equal(got[k].view(torch.int16), want[k].view(torch.int16)), k
