@@ -534,9 +534,26 @@ __device__ __forceinline__ void mainloop_pp(const KArgs& A, int64_t m0, int64_t 
     }
   }
   {
+    // Tile 1's loads go out in the order the loop's groups reissue them (per
+    // group: A 2g, 2g+1, then B 2g, 2g+1), pinned by scheduling barriers.  The
+    // loop header joins this path and the back edge, and the compiler's wait
+    // before each LDS write must cover both: with the same order on both,
+    // the first write of a k-tile waits for its own (oldest) load only, not
+    // for most of the 16 in flight.
     const TileLd T1 = tile(kt0 + 1);
 #pragma unroll
-    for (int it = 0; it < 8; ++it) { va[it] = ldA(T1, it); vb[it] = ldB(T1, it); }
+    for (int g = 0; g < 4; ++g) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        va[2 * g + h] = ldA(T1, 2 * g + h);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        vb[2 * g + h] = ldB(T1, 2 * g + h);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
   }
   __syncthreads();
   Frags f0, f1;
