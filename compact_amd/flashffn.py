@@ -124,11 +124,13 @@ def _mm_sum(a, b, a2, b2, name):
 
 
 def _lora_ok(*pairs) -> bool:
-    """The adapter terms (a, b) present ride in the GEMM epilogues: bf16 on the
-    engine, one shared rank of 8 or 16."""
+    """The adapter terms (a, b) present ride in the GEMM epilogues: bf16
+    factors of one shared rank up to 16 (G.lora_fusable; the GEMM wrapper
+    re-lays and zero-pads them for the kernel's 8-wide k chunks)."""
     ranks = {a.shape[0] for a, b in pairs if a is not None}
     return (len(ranks) <= 1 and all(G.lora_fusable(r) for r in ranks)
-            and all(_mfma(a, b) for a, b in pairs if a is not None))
+            and all(t.dtype == torch.bfloat16 and t.dim() == 2
+                    for a, b in pairs if a is not None for t in (a, b)))
 
 
 def outlier_stat_rows(shape) -> int:

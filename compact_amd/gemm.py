@@ -80,22 +80,39 @@ def _check_bf16(*ts):
         assert t.dim() == 2
 
 
-LORA_RANKS = (8, 16)
+LORA_MAX_RANK = 16
 
 
 def lora_fusable(rank: int) -> bool:
-    """Adapter terms of this rank ride in the GEMM epilogues."""
-    return rank in LORA_RANKS
+    """Adapter terms of this rank ride in the GEMM epilogues: one
+    v_mfma_f32_32x32x16_bf16 per 32 x 32 block and term covers ranks up to 16."""
+    return 1 <= rank <= LORA_MAX_RANK
 
 
 def _lora_args(terms, n_q):
     """(rank, ldp, q_kmajor, ldq, [(p, q, alpha) x 2], keep) for up to two
     terms (p [M, r], q the logical [r, N] factor, alpha); `keep` holds any
-    re-laid copies alive until the launch."""
+    re-laid copies alive until the launch.  The kernels fetch P and K-major Q
+    in 16-byte chunks of 8 k, so a rank that is not a multiple of 8 is
+    zero-padded to the next one (8 or 16): the padded k add exact zeros to
+    each fp32 dot product."""
     terms = [t for t in terms if t is not None]
     assert 1 <= len(terms) <= 2
     r = terms[0][0].shape[1]
-    assert lora_fusable(r), f"adapter rank {r} not in {LORA_RANKS}"
+    assert lora_fusable(r), f"adapter rank {r} above {LORA_MAX_RANK}"
+    if r % 8:
+        rp = (r + 7) // 8 * 8
+        pad = torch.nn.functional.pad
+        padded = []
+        for pm, q, al in terms:
+            # a factor given as [r, N] rows (an A weight) gains zero rows; one
+            # stored [N, r] (a B weight, q its transposed view) zero columns
+            if q.stride(1) == 1 and q.stride(0) != 1:
+                q = pad(q, (0, 0, 0, rp - r))
+            else:
+                q = pad(q.t(), (0, rp - r)).t()
+            padded.append((pad(pm, (0, rp - r)), q, al))
+        terms, r = padded, rp
     keep, ps, qs = [], [], []
     for pm, q, _ in terms:
         _check_bf16(pm, q)
@@ -124,6 +141,8 @@ def _lora_args(terms, n_q):
 
 
 SKINNY_MAX_RANK = 32
+# blocks of 128 rows x one K range the skinny projection aims for
+SKINNY_BLOCKS = 512
 
 # Buffer offsets are 32-bit.  Every kernel's resource starts where a block's
 # reads start (a tile's first row, a split's first token or k row), so an
@@ -153,7 +172,7 @@ def skinny(a: torch.Tensor, q: torch.Tensor, alpha: float = 1.0,
     # ranges cost more partials than they gain in parallelism (measured at
     # M = 8192, K = 4096 / 11008: 3.6 / 4.9 TB/s)
     blocks = (M + 127) // 128
-    splits = max(1, min(K // 256, (512 + blocks - 1) // blocks))
+    splits = max(1, min(K // 256, (SKINNY_BLOCKS + blocks - 1) // blocks))
     if out is None:
         c = torch.empty((M, R), dtype=torch.bfloat16, device=a.device)
     else:
@@ -382,7 +401,8 @@ def ffn_gate_up(x, w_gate, w_up, cache: int, group_size: int, want_h_mid: bool =
     if lora_gate is not None or lora_up is not None:
         # term 0 on the gate columns, term 1 on the up columns (absent: no-op)
         present = [t for t in (lora_gate, lora_up) if t is not None]
-        r, ldp, _, _, t, keep = _lora_args([(xa, bw.t(), s) for xa, bw, s in present], d)
+        r, ldp, qk, _, t, keep = _lora_args([(xa, bw.t(), s) for xa, bw, s in present], d)
+        assert qk == 1, "the gate/up adapter B factors go K-major"
         if lora_gate is None:
             t = [(None, None, 0.0), t[0]]
         with _timed("ffn_gate_up"):
