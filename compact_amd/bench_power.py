@@ -6,7 +6,9 @@ Runs every GEMM of a C2 fwd+bwd step (8192 tokens, d_model 4096, d_ff 11008,
 bf16) on this build's engine and through torch's `@` (hipBLASLt), each in a
 loop for --secs seconds, while a thread reads the GPU's metrics table through
 amdsmi (read-only queries: socket power, current gfx clock) every 10 ms.
-Prints, per product: time per launch, TFLOP/s, mean power (W) and clock (MHz)
+The first two lines are the register-only MFMA probe (v_mfma_f32_32x32x16_bf16,
+then v_mfma_f32_16x16x32_bf16, on every SIMD, no memory traffic): the MFMA
+rate the power cap allows when nothing else draws power.  Prints, per product: time per launch, TFLOP/s, mean power (W) and clock (MHz)
 over the loop (the first 0.8 s dropped), TFLOP/s per GHz (work per clock) and
 energy per FLOP (pJ).  The board's power cap is printed first.
 """
@@ -19,7 +21,9 @@ import time
 
 import torch
 
+from . import _lib
 from . import gemm as G
+from ._lib import check
 
 
 class PowerSampler:
@@ -84,6 +88,21 @@ def sustained(fn, secs: float, sampler: PowerSampler | None):
     return ms, pw, ck
 
 
+def mfma_probe(shape: int):
+    """One launch of the register-only MFMA probe (no memory traffic) with
+    shape 0 (32x32x16: 512 registers a lane, one block of 4 waves per CU,
+    256 blocks) or 1 (16x16x32: 132 registers, three blocks per CU, 768
+    blocks); about 1 ms each.  Returns (callable, FLOPs per launch)."""
+    blocks, iters, per = (256, 4096, 32768) if shape == 0 else (768, 2730, 16384)
+    out = torch.empty(blocks * 4, dtype=torch.float32, device="cuda")
+    lib = _lib.lib()
+
+    def run():
+        check(lib.cpt_probe_mfma_rate(shape, blocks, iters, 0.5, out.data_ptr(),
+                                      torch.cuda.current_stream().cuda_stream), "probe_mfma_rate")
+    return run, blocks * iters * 64 * per
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--secs", type=float, default=3.0)
@@ -109,7 +128,11 @@ def main():
     if sampler:
         pw, ck = sampler.mean(idle0 + 0.5, time.time())
         print(f"{'idle':40s} {'':>9s} {'':>12s} {pw:7.0f} W {ck:6.0f} MHz", flush=True)
+    p32, p32_fl = mfma_probe(0)
+    p16, p16_fl = mfma_probe(1)
     cases = [
+        ("MFMA 32x32x16 only, registers", p32, None, p32_fl),
+        ("MFMA 16x16x32 only, registers", p16, None, p16_fl),
         ("NT x.Wg^T, K 4096", lambda: G.linear(x, wg), lambda: x @ wg.t(), fl),
         ("NT h_mid.Wd^T, K 11008", lambda: G.linear(hm, wd), lambda: hm @ wd.t(), fl),
         ("NN gy.Wd, K 4096", lambda: G.mm(gy, wd), lambda: gy @ wd, fl),

@@ -60,10 +60,14 @@ constexpr int GROUP_ROWS = CPT_GROUP_ROWS;     // tile-rows per L2 group
 
 // K-major tiles: row r (m or n) at r * 64 + (r / 2) * 8 elements, 8-element
 // (16-byte) k chunks.  LDS is 64 banks of 4 bytes on gfx950 and a 128-bit
-// access is served 16 lanes at a time, so 16 lanes must cover 64 distinct
-// banks: fragment reads take 16 consecutive rows at one chunk, stores take 2
-// rows x 8 chunks, both 1-way.  The address stays affine in the chunk, so
-// fragment addresses are immediate offsets.
+// access takes 4 cycles of 16 lanes, so each 16-lane set must cover 64
+// distinct banks.  Measured with SQ_LDS_BANK_CONFLICT on one wave's patterns:
+// a read serves lanes {0-7, 24-31}, {8-15, 16-23}, {32-39, 56-63} and
+// {40-47, 48-55} together; a write serves 16 consecutive lanes.  The
+// 32x32x16 fragment read (lanes 0-31 take rows 0-31 at one chunk) then puts
+// rows 0-7 and 24-31 together, 1-way in this layout; the stores (2 rows x 8
+// chunks per 16 lanes) are 1-way too.  The address stays affine in the
+// chunk, so fragment addresses are immediate offsets.
 __device__ __forceinline__ int lds_off(int row, int chunk) {
   return row * 64 + ((row >> 1) << 3) + (chunk << 3);
 }

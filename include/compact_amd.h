@@ -380,6 +380,27 @@ int cpt_topk_abs(const void* t, int dtype, int64_t n, int64_t d, int64_t k, void
 int cpt_topk_scatter(const void* values, const void* indices, int dtype, int64_t n, int64_t d,
                      int64_t k, void* out, void* stream);
 
+/* ---------------- measurement ---------------- */
+
+/* No counterpart in the reference: a probe for the sustained bf16 MFMA rate
+ * the part reaches under its power cap, the achievable peak that the GEMM
+ * roofline figures are read against.  `blocks` blocks of 4 wavefronts each
+ * issue iters * 16 independent MFMAs on register operands (no memory
+ * traffic): shape 0 v_mfma_f32_32x32x16_bf16 (32768 FLOPs each), shape 1
+ * v_mfma_f32_16x16x32_bf16 (16384).  out [blocks * 4] fp32 receives one
+ * partial sum per wavefront.  FLOPs per launch = blocks * iters * 64 *
+ * (FLOPs per MFMA). */
+int cpt_probe_mfma_rate(int shape, int blocks, int iters, float seed, void* out, void* stream);
+
+/* No counterpart in the reference: a probe for the LDS bank-conflict cost of
+ * one 128-bit access pattern, which the GEMM's LDS layouts are chosen by.
+ * `blocks` blocks of one wavefront each read (write == 0) or write (write !=
+ * 0) 16 bytes per lane at LDS byte offset offs[lane] & 0xfff0 (offs: 64
+ * int32 on the device), `iters` times.  out [blocks * 64] fp32 receives one
+ * value per lane.  Read SQ_LDS_BANK_CONFLICT / SQ_INSTS_LDS under a PMC run. */
+int cpt_probe_lds_pattern(const void* offs, int write, int blocks, int iters, void* out,
+                          void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -205,3 +205,44 @@ def test_mm_splitk_routes_adapter_gradients(device):
     got2 = G.mm_splitk(x.t(), gb, 0.5)
     assert torch.equal(got2.view(torch.int16), G.skinny_t(x, gb, 0.5).view(torch.int16))
     assert_gemm_close(got2, 0.5 * ref_mm(x.t(), gb))
+
+
+@pytest.mark.parametrize("shape", [0, 1])
+def test_mfma_probe_runs_and_scales_with_iters(device, shape):
+    """The register-only MFMA probe behind the achievable-peak figure: each
+    wavefront's partial grows linearly with the round count (the rounds
+    repeat the same products), and invalid arguments are rejected."""
+    from compact_amd import _lib
+    lib = _lib.lib()
+    out1 = torch.empty(8 * 4, dtype=torch.float32, device=device)
+    out3 = torch.empty_like(out1)
+    s = torch.cuda.current_stream().cuda_stream
+    assert lib.cpt_probe_mfma_rate(shape, 8, 1, 0.5, out1.data_ptr(), s) == 0
+    assert lib.cpt_probe_mfma_rate(shape, 8, 3, 0.5, out3.data_ptr(), s) == 0
+    torch.cuda.synchronize()
+    assert torch.isfinite(out1).all() and out1.abs().sum() > 0
+    torch.testing.assert_close(out3, 3 * out1, rtol=1e-4, atol=1e-3)
+    assert lib.cpt_probe_mfma_rate(shape, 0, 1, 0.5, out1.data_ptr(), s) != 0
+    assert lib.cpt_probe_mfma_rate(shape, 8, 0, 0.5, out1.data_ptr(), s) != 0
+    assert lib.cpt_probe_mfma_rate(2, 8, 1, 0.5, out1.data_ptr(), s) != 0
+
+
+def test_lds_pattern_probe_reads_what_it_addresses(device):
+    """The LDS probe behind the layout measurements: lane l reads the four
+    dwords at offs[l] & 0xfff0 of an array holding i at dword i, `iters` times,
+    so its value is iters * (offs[l] + 6); a write pass reads back its own last
+    store (lane, iters, 2, 3)."""
+    from compact_amd import _lib
+    lib = _lib.lib()
+    s = torch.cuda.current_stream().cuda_stream
+    offs = torch.tensor([(16 * l * 37) % 65536 for l in range(64)], dtype=torch.int32, device=device)
+    out = torch.empty(2 * 64, dtype=torch.float32, device=device)
+    assert lib.cpt_probe_lds_pattern(offs.data_ptr(), 0, 2, 3, out.data_ptr(), s) == 0
+    torch.cuda.synchronize()
+    want = (3 * (offs.cpu().double() + 6)).float()
+    assert torch.equal(out.cpu()[:64], want) and torch.equal(out.cpu()[64:], want)
+    assert lib.cpt_probe_lds_pattern(offs.data_ptr(), 1, 2, 3, out.data_ptr(), s) == 0
+    torch.cuda.synchronize()
+    lane = torch.arange(64, dtype=torch.float32)
+    assert torch.equal(out.cpu()[:64], lane + 3 + 2 + 3)
+    assert lib.cpt_probe_lds_pattern(offs.data_ptr(), 0, 0, 3, out.data_ptr(), s) != 0

@@ -145,9 +145,24 @@ def test_down_dgrad_lora_fused_equals_composed(device, cache, bits, group, want_
         assert torch.equal(bits16(hm), bits16(rhm))
 
 
+def test_rank_below_16_is_zero_padded(device):
+    """A rank that is not a multiple of 8 is passed to the epilogue
+    zero-padded to 8 or 16: the extra products are exact zeros, so the
+    result equals the caller-padded call bit for bit."""
+    _, G, _ = _cpt()
+    a, b = rnd((64, 64), 60, device), rnd((64, 64), 61, device)
+    for r, rp in ((4, 8), (12, 16)):
+        p, q = rnd((64, r), 62, device), rnd((r, 64), 63, device)
+        pp = torch.nn.functional.pad(p, (0, rp - r))
+        qp = torch.nn.functional.pad(q, (0, 0, 0, rp - r))
+        got = G.mm2(a, b, lora=[(p, q, 1.0)])
+        ref = G.mm2(a, b, lora=[(pp, qp, 1.0)])
+        assert torch.equal(bits16(got), bits16(ref))
+
+
 def test_rank_outside_epilogue_set_raises(device):
     _, G, _ = _cpt()
     a, b = rnd((64, 64), 60, device), rnd((64, 64), 61, device)
-    p, q = rnd((64, 4), 62, device), rnd((4, 64), 63, device)
+    p, q = rnd((64, 32), 62, device), rnd((32, 64), 63, device)
     with pytest.raises(AssertionError):
         G.mm2(a, b, lora=[(p, q, 1.0)])
