@@ -12,7 +12,10 @@ pair per step) is timed with no per-kernel events.  A second pass over K
 more steps records HIP events around every kernel on its launch stream:
 `kernels` lists them and `roofline` is the dominant HIP kernel's rate from
 that pass.  The same line carries C3 (LoRA r16, int4 g64 + 1% outlier
-channels) under "c3", timed the same way.  `cpu_baseline` times the CPU
+channels) under "c3", timed the same way, and the whole-model training
+steps C4 (TinyLlama-1.1B full fine-tune) and C5 (Llama-7B LoRA) under "c4"
+and "c5" (HIP events around each step, no per-kernel events; --no-e2e skips
+them).  `cpu_baseline` times the CPU
 oracle (the restatement of the reference's FlashFFNv3Function; the reference
 itself cannot run on a CPU) on a bounded sample of C2, and config C1 (the
 reference's own CPU case) at full size under "c1_full".
@@ -246,6 +249,44 @@ def measured_traffic(kernel: str, workload: str):
                     and parts[1] == kernel and parts[2] == workload:
                 return float(parts[3])
     return None
+
+
+def model_step_summary(workload: str, steps: int, warmup: int) -> dict:
+    """Tokens/s of a whole-model training step (C4 / C5), timed with HIP
+    events around `steps` steps after `warmup` untimed ones, no per-kernel
+    events inside: ms per step (mean of the timed region and median of the
+    per-step events), the last loss.  For the default line's extra keys."""
+    import gc
+    import torch
+    import compact_amd as cpt
+    from compact_amd import e2e
+
+    cfg = e2e.CONFIGS[workload]
+    dev = torch.device("cuda:0")
+    model, opt = e2e.prepare(cfg, dev, flash=True)
+    ids = e2e.random_batch(cfg, dev)
+    n_tok = cfg["batch"] * cfg["seq"]
+    for _ in range(warmup):
+        e2e.train_step(model, opt, ids)
+    torch.cuda.synchronize()
+    cpt.v3_reset_counters()
+    stream = torch.cuda.current_stream()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record(stream)
+    for i in range(steps):
+        loss = e2e.train_step(model, opt, ids)
+        ev[i + 1].record(stream)
+    torch.cuda.synchronize()
+    per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+    ms = ev[0].elapsed_time(ev[steps]) / steps
+    assert cpt._V3_COUNTERS["forward"] == steps * cfg["layers"], cpt._V3_COUNTERS
+    out = {"workload": cfg["desc"], "tokens_per_s": n_tok / (ms * 1e-3), "ms_per_step": ms,
+           "ms_per_step_median": per[len(per) // 2], "steps": steps, "warmup": warmup,
+           "tokens": n_tok, "layers": cfg["layers"], "loss": float(loss)}
+    del model, opt, ids, loss
+    gc.collect()
+    torch.cuda.empty_cache()
+    return out
 
 
 def model_step_bench(args):
@@ -504,6 +545,9 @@ def main():
                     help="skip timing the hipBLASLt composition of the same step")
     ap.add_argument("--no-c3", action="store_true",
                     help="skip the C3 workload that the default C2 line carries under 'c3'")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="skip the C4 and C5 whole-model steps that the default C2 line "
+                         "carries under 'c4' and 'c5'")
     ap.add_argument("--workload", choices=sorted(WORKLOADS) + ["c4", "c5"], default="c2",
                     help="c2 (default) / c3: the FFN block; c4 / c5: a whole-model training "
                          "step (TinyLlama full-FT / Llama-7B LoRA) with every MLP on FlashFFN v3")
@@ -541,6 +585,16 @@ def main():
         del case
         c3.pop("kernels")
         out["c3"] = {"tokens_per_s": c3.pop("value"), **c3}
+    if args.workload == "c2" and not args.no_e2e:
+        # whole-model steps, fewer steps than the FFN (each is 0.1-0.4 s); a
+        # failure here is recorded and does not cost the headline line
+        for wl, (w, k) in (("c4", (3, 10)), ("c5", (2, 5))):
+            print(f"bench: {wl} whole-model step", file=sys.stderr, flush=True)
+            try:
+                out[wl] = model_step_summary(wl, k, w)
+            except Exception as e:  # noqa: BLE001 - reported in the line itself
+                out[wl] = {"error": f"{type(e).__name__}: {e}"}
+                torch.cuda.empty_cache()
     if not args.no_cpu_baseline and args.workload == "c2":
         out["cpu_baseline"] = cpu_baseline(args.cpu_tokens)
     print(json.dumps(out))
