@@ -161,6 +161,25 @@ def test_skinny_matches_reference(device, m, r, k):
     assert torch.equal(got.view(torch.int16), G.skinny(a, q, 2.0).view(torch.int16))
 
 
+@pytest.mark.parametrize("m,r,k,splits", [(777, 24, 1096, 3), (8192, 16, 4160, 5), (130, 16, 96, 1),
+                                          (300, 32, 2080, 2), (64, 8, 8, 1), (1000, 8, 328, 1)])
+def test_skinny_splits_cover_every_k_pass(device, m, r, k, splits):
+    """Explicit split counts through the C ABI: each block's k range runs
+    k-256 passes through LDS, then single k-64 steps, then k-32 steps whose
+    last 8-wide chunks may fall past K (they read zero).  Every shape here
+    leaves a different mix of the three, for ranks up to 16 and above."""
+    from compact_amd import _lib
+    a = rnd((m, k), 72, device)
+    q = rnd((r, k), 73, device, 0.05)
+    c = torch.empty((m, r), dtype=torch.bfloat16, device=device)
+    ws = torch.empty(splits * m * r + 16, dtype=torch.float32, device=device)
+    rc = _lib.lib().cpt_gemm_bf16_skinny(a.data_ptr(), k, q.data_ptr(), k, c.data_ptr(), r, m, r, k,
+                                         0.5, splits, ws.data_ptr(),
+                                         torch.cuda.current_stream().cuda_stream)
+    assert rc == 0
+    assert_gemm_close(c, 0.5 * (a.float().cpu() @ q.float().cpu().t()))
+
+
 def test_mm_routes_thin_products_to_skinny(device):
     """mm() with N <= 32 on a row-major A gives the skinny kernel's result,
     including a transposed [K, r] weight view (B = W^T of an [r, K] weight)
