@@ -707,33 +707,52 @@ __device__ __forceinline__ f32x16 acc_block(const KArgs& A, const Acc& acc, cons
 }
 
 // ---------------------------------------------------------------------------
-// epilogue: plain bf16 store
+// epilogue: plain bf16 store.  bf16(acc) (adapter terms added) is staged
+// through LDS as a row-major tile, rows 264 elements apart; 32 consecutive
+// threads then store one 512-byte row, so every store instruction writes
+// whole 128-byte lines.  Stored straight from the accumulator layout, each
+// instruction wrote 16 bytes into each of 32 rows.  The staged stores took a
+// K = 64 product (1376 tiles, almost all epilogue) from 87 to 78 us and a C2
+// step from 5.625 to 5.604 ms, bit-identical.
 // ---------------------------------------------------------------------------
 template <int LT>
-__device__ __forceinline__ void epi_store(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+__device__ __forceinline__ void epi_store(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0,
+                                          uint16_t* lds) {
+  constexpr int LD = 264;
+  static_assert(BM * LD * 2 <= LDS_BYTES, "the staged tile must fit the main loop's LDS");
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave & 1, wm = wave >> 1;
   LoraFr F;
   if constexpr (LT > 0) lora_load<false, LT>(A, m0, n0, F);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t m = m0 + wm * 128 + j * 32 + (lane & 31);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
+  static_for<0, 4>([&](auto j) {
+    const int ml = wm * 128 + j * 32 + (lane & 31);
+    static_for<0, 4>([&](auto i) {
       const f32x16 a = acc_block<false, LT>(A, acc, F, i, j);
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int64_t n = n0 + wn * 128 + i * 32 + g * 8 + (lane >> 5) * 4;
-        if (m >= A.M) continue;
-        if (n + 3 < A.N) {
-          *reinterpret_cast<uint2*>(A.C + m * A.ldc + n) =
-              make_uint2(pack_bf16x2(a[g * 4 + 0], a[g * 4 + 1]),
-                         pack_bf16x2(a[g * 4 + 2], a[g * 4 + 3]));
-        } else {
-          for (int e = 0; e < 4; ++e)
-            if (n + e < A.N) A.C[m * A.ldc + n + e] = (uint16_t)f32_to_bf16_bits(a[g * 4 + e]);
-        }
-      }
+      static_for<0, 4>([&](auto g) {
+        const int nl = wn * 128 + i * 32 + g * 8 + (lane >> 5) * 4;
+        *reinterpret_cast<uint2*>(lds + ml * LD + nl) =
+            make_uint2(pack_bf16x2(a[g * 4 + 0], a[g * 4 + 1]), pack_bf16x2(a[g * 4 + 2], a[g * 4 + 3]));
+      });
+    });
+  });
+  __syncthreads();
+  const int cl = (tid & 31) * 8;
+  const int64_t n = n0 + cl;
+  const bool vec = ((A.ldc & 7) == 0) && ((reinterpret_cast<uintptr_t>(A.C) & 15) == 0);
+#pragma unroll 4
+  for (int p = 0; p < 32; ++p) {
+    const int r = p * 8 + (tid >> 5);
+    const int64_t m = m0 + r;
+    if (m >= A.M || n >= A.N) continue;
+    const uint4 w = *reinterpret_cast<const uint4*>(lds + r * LD + cl);
+    uint16_t* cp = A.C + m * A.ldc + n;
+    if (vec && n + 7 < A.N) {
+      *reinterpret_cast<uint4*>(cp) = w;
+    } else {
+      const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
+      for (int e = 0; e < 8 && n + e < A.N; ++e)
+        cp[e] = (uint16_t)(e & 1 ? ww[e >> 1] >> 16 : ww[e >> 1] & 0xFFFFu);
     }
   }
 }
@@ -1113,7 +1132,7 @@ __global__ __launch_bounds__(NTHR, 1) void gemm_kernel(KArgs A) {
                        : (EPI == EPI_STORE && CACHE == CACHE_INT4) ? 4 : 0;
     mainloop_pp<AK, BKM, EPI == EPI_GLU, BQ>(A, m0, n0, lds, acc);
   }
-  if constexpr (EPI == EPI_STORE) epi_store<LT>(A, acc, m0, n0);
+  if constexpr (EPI == EPI_STORE) epi_store<LT>(A, acc, m0, n0, lds);
   else if constexpr (EPI == EPI_ADD) epi_add(A, acc, m0, n0, lds);
   else if constexpr (EPI == EPI_GLU) epi_glu<CACHE, GS, LT>(A, acc, m0, n0, lds);
   else if constexpr (EPI == EPI_DGLU) epi_dglu<CACHE, GS, LT>(A, acc, m0, n0, lds);
