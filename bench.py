@@ -11,7 +11,9 @@ over the K timed steps, plus their median / p10 / p90 from one HIP event
 pair per step) is timed with no per-kernel events.  A second pass over K
 more steps records HIP events around every kernel on its launch stream:
 `kernels` lists them and `roofline` is the dominant HIP kernel's rate from
-that pass.  The same line carries C3 (LoRA r16, int4 g64 + 1% outlier
+that pass, with `frac` against the 2.5 PF/s spec peak and
+`frac_of_achievable` against `achievable_peak`, the register-only MFMA rate
+(cpt_probe_mfma_rate) timed in the same run.  The same line carries C3 (LoRA r16, int4 g64 + 1% outlier
 channels) under "c3", timed the same way, and the whole-model training
 steps C4 (TinyLlama-1.1B full fine-tune) and C5 (Llama-7B LoRA) under "c4"
 and "c5" (HIP events around each step, no per-kernel events; --no-e2e skips
@@ -428,6 +430,45 @@ def ffn_case(name, n, dev):
                 fwd=fwd, step=step, full_ft=full_ft, frozen=frozen)
 
 
+_ACHIEVABLE = {}
+
+
+def achievable_mfma_peak(launches: int = 200) -> dict:
+    """The bf16 MFMA rate this part sustains with nothing else running:
+    cpt_probe_mfma_rate (v_mfma_f32_32x32x16_bf16 back to back on register
+    operands, one wavefront per SIMD, no memory traffic), timed over
+    `launches` back-to-back launches of about 1.2 ms.  Measured once per
+    process; the spec peak (2.5 PF/s) assumes a clock this part does not hold
+    under MFMA load."""
+    if "v" in _ACHIEVABLE:
+        return _ACHIEVABLE["v"]
+    import torch
+    from compact_amd import _lib
+    from compact_amd._lib import check
+    blocks, iters = 256, 4096
+    out = torch.empty(blocks * 4, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+    lib = _lib.lib()
+
+    def launch():
+        check(lib.cpt_probe_mfma_rate(0, blocks, iters, 0.5, out.data_ptr(), stream.cuda_stream),
+              "probe_mfma_rate")
+    for _ in range(20):
+        launch()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(launches):
+        launch()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / launches
+    flops = blocks * iters * 64 * 32768
+    _ACHIEVABLE["v"] = {"value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s",
+                        "source": "cpt_probe_mfma_rate: v_mfma_f32_32x32x16_bf16 back to back on "
+                                  "register operands, no memory traffic, timed in this run"}
+    return _ACHIEVABLE["v"]
+
+
 def run_ffn(name, n, steps, warmup, dev, library=True):
     """Headline, per-kernel pass and saved bytes of one FFN workload."""
     import torch
@@ -486,6 +527,10 @@ def run_ffn(name, n, steps, warmup, dev, library=True):
     roofline["timing"] = "mean of the per-kernel pass's HIP events on the launch stream"
     roofline["traffic_source"] = ("profiles/ rocprofv3 --pmc FETCH_SIZE + WRITE_SIZE summary of "
                                   "bench.py --probe" if traffic is not None else None)
+    if bound != "hbm":
+        ach = achievable_mfma_peak()
+        roofline["achievable_peak"] = ach
+        roofline["frac_of_achievable"] = rate / 1e12 / ach["value"]
     flops = gemm_flops_fwd_bwd(n, h, d, c["full_ft"])
     if wl["lora_rank"]:   # thin adapter GEMMs: 18 * N * r * (H + D)
         flops += 18 * n * wl["lora_rank"] * (h + d)
