@@ -49,6 +49,16 @@ def _private(mode: str, hg, hu) -> bool:
 _CACHE_CODE = {"int4": _lib.CACHE_INT4, "int8": _lib.CACHE_INT8, "bf16": _lib.CACHE_BF16,
                "recompute": _lib.CACHE_NONE}
 _FUSED_GROUPS = (32, 64, 128)
+# Cache formats whose codec runs in the gate/up dual GEMM's epilogue (K1 fused,
+# only codes and h_mid leave the kernel).  The other formats take the same
+# dual GEMM with a bf16 epilogue and then the standalone K1; the two paths are
+# bit-identical.  Measured on MI355X, fused against bf16 out + K1: int8 g128
+# at C2 1256 against 1272 us (fused kept); int4 g64 1268 against 1254 us at
+# the C2 dims, 401 against 388 us at TinyLlama dims with 8192 tokens and 126
+# against 112 us with 2048 (the int4 epilogue's smaller groups and half-line
+# code stores cost more inside the power-limited GEMM than K1 does at HBM
+# speed).
+_F1_CODEC_CACHES = ("int8",)
 # Group sizes whose dequantise + SwiGLU backward runs in the dgrad GEMM's
 # epilogue (G.ffn_down_dgrad) instead of the dgrad GEMM followed by the K2
 # kernel.  Empty: on MI355X the fused epilogue (VALU work and 540 MB of writes
@@ -230,7 +240,8 @@ class FlashFFNv3Function(torch.autograd.Function):
         if fusable:
             xa_g, xa_u, lkw = _gate_up_lora(x_2d, a_gate, b_gate, s_gate, a_up, b_up, s_up)
         fused_quant = (quant and use_triton and x.dtype == torch.bfloat16)   # :1424-1426
-        if fusable and fused_quant and k_out == 0 and group_size in _FUSED_GROUPS:
+        if (fusable and fused_quant and k_out == 0 and group_size in _FUSED_GROUPS
+                and cache_mode in _F1_CODEC_CACHES):
             # dual GEMM + GLU + codec in one kernel (K1 fused into the epilogue)
             h_mid, _, _, c_gate, qs_gate, c_up, qs_up = G.ffn_gate_up(
                 x_2d, w_gate, w_up, _CACHE_CODE[cache_mode], group_size, **lkw)
@@ -741,10 +752,17 @@ class FlashFFNv3AdapterFunction(torch.autograd.Function):
 
         c_gate = qs_gate = c_up = qs_up = None
         h_gate = h_up = xa_g = xa_u = None
-        if fusable and fused_quant and group_size in _FUSED_GROUPS:
+        if fusable and fused_quant and group_size in _FUSED_GROUPS and cache_mode in _F1_CODEC_CACHES:
             h_mid, _, _, c_gate, qs_gate, c_up, qs_up = G.ffn_gate_up(
                 x_2d, w_gate, w_up, _CACHE_CODE[cache_mode], group_size)
             _V3_COUNTERS["triton_quant_fwd"] += 1
+        elif fusable and fused_quant:
+            # the dual GEMM with a bf16 epilogue, then the standalone K1
+            _, h_gate, h_up, *_ = G.ffn_gate_up(x_2d, w_gate, w_up, _lib.CACHE_BF16, group_size,
+                                                want_h_mid=False)
+            h_mid, c_gate, qs_gate, c_up, qs_up = K.silu_mul_quant(
+                h_gate, h_up, _bits(cache_mode), group_size)
+            h_gate = h_up = None
         elif fusable and not fused_quant:
             keep = cache_mode != "recompute"
             h_mid, h_gate, h_up, *_ = G.ffn_gate_up(
