@@ -16,7 +16,9 @@ Patterns:
   (row l % 16, chunk l / 16) and the stores (row l / 8, chunk l % 8);
 - a layout made for the 16x16x32 read: 64-element rows, chunk XOR (row & 6);
 - pair tests: lane l at byte 16 l (every 16-lane set covers the 64 banks once), then lane j
-  moved onto lane i's banks at another address. A conflict means i and j share a cycle.
+  moved onto lane i's banks at another address. A conflict means i and j share a cycle;
+- 64-bit reads, plain and transposing (ds_read_b64_tr_b16), at the engine's MN-major fragment
+  addresses (rows 288 elements apart, and 256 for comparison) and lane-linear.
 
 Lane-group model for reads (fits every read pattern measured): a 128-bit read takes 4 cycles
 serving lanes {0-7, 24-31}, {8-15, 16-23}, {32-39, 56-63} and {40-47, 48-55}.  A 128-bit write
@@ -58,14 +60,26 @@ def _swz(r: int, c: int) -> int:
     return (r * 64 + ((c ^ (r & 6)) * 8)) * 2
 
 
-def patterns() -> dict[str, tuple[bool, list[int]]]:
-    pat: dict[str, tuple[bool, list[int]]] = {}
+def patterns() -> dict[str, tuple[int, list[int]]]:
+    """name -> (mode, byte offset per lane); mode False / True: 128-bit read /
+    write, 2: ds_read_b64, 3: ds_read_b64_tr_b16."""
+    pat: dict[str, tuple[int, list[int]]] = {}
     for name, f in (("engine layout", _engine), ("16x16 layout", _swz)):
         pat[f"{name}: 32x32x16 fragment read"] = (False, [f(l & 31, l >> 5) for l in range(64)])
         pat[f"{name}: 16x16x32 fragment read, k 0-31"] = (False, [f(l & 15, l >> 4) for l in range(64)])
         pat[f"{name}: 16x16x32 fragment read, k 32-63"] = (False, [f(l & 15, (l >> 4) + 4)
                                                                   for l in range(64)])
         pat[f"{name}: stores"] = (True, [f(l >> 3, l & 7) for l in range(64)])
+    # 64-bit reads (mode 2 plain, 3 transposing): the engine's MN-major fragment read,
+    # lane l at k-row 8 (l / 32) + (l % 16) / 4, mn 16 ((l / 16) % 2) + 4 (l % 4) of a
+    # [64 k][LDM] tile, LDM 288 (the engine) or 256 (no row skew)
+    for ldm in (288, 256):
+        mn = [((8 * (l >> 5) + ((l & 15) >> 2)) * ldm + 16 * ((l >> 4) & 1) + 4 * (l & 3)) * 2
+              for l in range(64)]
+        pat[f"MN-major fragment, LDM {ldm}: ds_read_b64_tr_b16"] = (3, mn)
+        pat[f"MN-major fragment, LDM {ldm}: ds_read_b64"] = (2, mn)
+    pat["lane-linear ds_read_b64"] = (2, [8 * l for l in range(64)])
+    pat["lane-linear ds_read_b64_tr_b16"] = (3, [8 * l for l in range(64)])
     pat["lane-linear read"] = (False, [16 * l for l in range(64)])
     pat["lane-linear write"] = (True, [16 * l for l in range(64)])
     for write in (False, True):
@@ -88,7 +102,8 @@ def run(iters: int = 2000, blocks: int = 1024):
     lib = _lib.lib()
     out = torch.empty(blocks * 64, device="cuda")
     for name, (write, offs) in patterns().items():
-        assert len(offs) == 64 and all(0 <= o <= 0xfff0 and o % 16 == 0 for o in offs), name
+        align = 8 if write >= 2 else 16
+        assert len(offs) == 64 and all(0 <= o <= 0xfff8 and o % align == 0 for o in offs), name
         t = torch.tensor(offs, dtype=torch.int32, device="cuda")
         print(f"dispatch {name}", flush=True)
         check(lib.cpt_probe_lds_pattern(t.data_ptr(), int(write), blocks, iters, out.data_ptr(),
@@ -110,7 +125,7 @@ def summarize(csv_path: str, log_path: str):
         n = c["SQ_INSTS_LDS"]
         write, offs = pat[name]
         print(f"| {name} | {c['SQ_LDS_BANK_CONFLICT'] / n:.2f} | {c['SQ_LDS_IDX_ACTIVE'] / n:.2f} | "
-              f"{'-' if write else model_conflicts(offs)} |")
+              f"{model_conflicts(offs) if write is False else '-'} |")
 
 
 def main():

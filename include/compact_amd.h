@@ -394,9 +394,10 @@ int cpt_probe_mfma_rate(int shape, int blocks, int iters, float seed, void* out,
 
 /* No counterpart in the reference: a probe for the LDS bank-conflict cost of
  * one 128-bit access pattern, which the GEMM's LDS layouts are chosen by.
- * `blocks` blocks of one wavefront each read (write == 0) or write (write !=
- * 0) 16 bytes per lane at LDS byte offset offs[lane] & 0xfff0 (offs: 64
- * int32 on the device), `iters` times.  out [blocks * 64] fp32 receives one
+ * `blocks` blocks of one wavefront each read (write == 0) or write (write ==
+ * 1) 16 bytes per lane at LDS byte offset offs[lane] & 0xfff0 (offs: 64
+ * int32 on the device), or read 8 bytes at offs[lane] & 0xfff8 with
+ * ds_read_b64 (write == 2) or ds_read_b64_tr_b16 (write == 3), `iters` times.  out [blocks * 64] fp32 receives one
  * value per lane.  Read SQ_LDS_BANK_CONFLICT / SQ_INSTS_LDS under a PMC run. */
 int cpt_probe_lds_pattern(const void* offs, int write, int blocks, int iters, void* out,
                           void* stream);

@@ -264,4 +264,13 @@ def test_lds_pattern_probe_reads_what_it_addresses(device):
     torch.cuda.synchronize()
     lane = torch.arange(64, dtype=torch.float32)
     assert torch.equal(out.cpu()[:64], lane + 3 + 2 + 3)
+    # 64-bit plain read: dwords a / 4 and a / 4 + 1 (a = offs & 0xfff8), each summed iters times
+    assert lib.cpt_probe_lds_pattern(offs.data_ptr(), 2, 2, 3, out.data_ptr(), s) == 0
+    torch.cuda.synchronize()
+    a8 = (offs.cpu().double() // 8) * 8
+    assert torch.equal(out.cpu()[:64], (3 * (a8 / 2 + 1)).float())
+    # the transposing read runs (its values are a 4 x 16 transpose across lanes)
+    assert lib.cpt_probe_lds_pattern(offs.data_ptr(), 3, 2, 3, out.data_ptr(), s) == 0
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
     assert lib.cpt_probe_lds_pattern(offs.data_ptr(), 0, 0, 3, out.data_ptr(), s) != 0
