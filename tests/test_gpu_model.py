@@ -12,7 +12,6 @@ unpatched, on the same weights and tokens.
 """
 
 import pytest
-import torch
 
 from compact_amd import e2e
 from compact_amd.kernels import _V3_COUNTERS, v3_reset_counters
