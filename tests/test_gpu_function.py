@@ -79,6 +79,32 @@ def test_function_vs_oracle_fp32(device, config, mode):
         assert R.rel_frob(got[k].cpu(), ora[k]) < tol, k
 
 
+@pytest.mark.parametrize("config", ["all", "fullft"])
+@pytest.mark.parametrize("mode,group", [("int4", 64), ("int8", 128), ("bf16", 64),
+                                        ("recompute", 64)])
+def test_function_vs_oracle_fp16(device, config, mode, group):
+    """fp16 activations and weights: the reference's fused kernels take bf16
+    only, so this is its eager path (the general-layout GEMM, the standalone
+    codec and GLU kernels in fp16).  y within 5e-3 of the oracle, grads within
+    5e-3 (unquantised) or 2e-2 (a code on a rounding tie may flip between the
+    CPU and GPU products), and the V2 cosines against fp32 autograd."""
+    ps = R.synthetic_param_set(config, H, D, RANK, S, seed=6, dtype=torch.float16)
+    gen = torch.Generator().manual_seed(14)
+    x = torch.randn(N, H, generator=gen).to(torch.float16)
+    gy = torch.randn(N, H, generator=gen).to(torch.float16)
+    got, y = _run(_to(ps, device), x.to(device), gy.to(device), mode, group)
+    assert y.dtype == torch.float16
+    ora, y_o = R.run_function_grads(R.OracleFlashFFNv3Function.apply, ps, x, gy, mode, group)
+    ref, _ = R.ref_grads_fp32(ps, x, gy)
+    assert R.rel_frob(y.cpu().float(), y_o.float()) < 5e-3
+    tol = 2e-2 if mode in ("int4", "int8") else 5e-3
+    for k in ref:
+        g = got[k].cpu().float()
+        assert R.rel_frob(g, ora[k].float()) < tol, k
+        floor = 0.98 if mode == "int4" else 0.999
+        assert R.tensor_cos(g, ref[k]) >= floor, k
+
+
 @pytest.mark.parametrize("config", ["all", "fullft", "none"])
 @pytest.mark.parametrize("mode", ["int4", "int8"])
 def test_fused_equals_unfused_bitwise(device, mode, config):
