@@ -261,7 +261,15 @@ int gemm_bf16_impl(const void* a, int64_t lda, int a_kmajor, const void* b, int6
     return b_kmajor ? launch<true, true, EPI_STORE, 0, 0, 2>(A, st)
                     : launch<true, false, EPI_STORE, 0, 0, 2>(A, st);
   }
-  if (a_kmajor && b_kmajor) return launch<true, true, EPI_STORE, 0, 0>(A, st);
+  if (a_kmajor && b_kmajor) {
+    // one NT pair on whole 256 x 256 tiles: the 16x16x32 loop (a different
+    // fp32 summation order from the engine's; cpt_gemm_bf16_ex mode 0 keeps
+    // the engine's)
+    if (!two && nt16_fits(M, N, K, c, ldc))
+      return launch_nt16((const uint16_t*)a, lda, (const uint16_t*)b, ldb, (uint16_t*)c, ldc, M, N,
+                         K, st);
+    return launch<true, true, EPI_STORE, 0, 0>(A, st);
+  }
   if (a_kmajor && !b_kmajor) return launch<true, false, EPI_STORE, 0, 0>(A, st);
   if (!a_kmajor && !b_kmajor) return launch<false, false, EPI_STORE, 0, 0>(A, st);
   return launch<false, true, EPI_STORE, 0, 0>(A, st);

@@ -1158,6 +1158,12 @@ int launch(KArgs& A, hipStream_t st) {
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
+// The plain-store NT product on the 16x16x32 direct-to-LDS main loop
+// (gemm16.hip): M, N multiples of 256, K of 64, C rows 16-byte aligned.
+bool nt16_fits(int64_t M, int64_t N, int64_t K, const void* c, int64_t ldc);
+int launch_nt16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c,
+                int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t st);
+
 // ---------------------------------------------------------------------------
 // Instantiations of launch<AK, BKM, EPI, CACHE, GS, LT>.  Each group is
 // compiled in its own translation unit (gemm_inst_*.hip) so the kernels

@@ -356,6 +356,28 @@ def mm2(a, b, a2=None, b2=None, name: str = "gemm", lora=None) -> torch.Tensor:
     return c if ldc == N else c[:, :N]
 
 
+def mm_engine(a: torch.Tensor, b: torch.Tensor, name: str = "gemm_engine") -> torch.Tensor:
+    """a [M, K] @ b [K, N] -> bf16 [M, N] on the 32x32x16 engine loop for
+    every shape: the fp32 summation order of the fused FFN kernels, so a
+    fused kernel equals its unfused composition through this product bit for
+    bit.  mm runs NT products on whole 256 x 256 tiles on the 16x16x32 loop
+    instead (same bf16 rounding of the fp32 sum, another summation order)."""
+    _require_device(a, b)
+    _check_bf16(a, b)
+    M, K = a.shape
+    K_, N = b.shape
+    assert K == K_, f"inner dims differ: {tuple(a.shape)} @ {tuple(b.shape)}"
+    a, lda, ak = _layout_a(a)
+    b, ldb, bk = _layout_b(b)
+    ldc = (N + 7) // 8 * 8
+    c = torch.empty((M, ldc), dtype=torch.bfloat16, device=a.device)
+    with _timed(name):
+        rc = _lib.lib().cpt_gemm_bf16_ex(a.data_ptr(), lda, ak, b.data_ptr(), ldb, bk, c.data_ptr(),
+                                         ldc, M, N, K, 1.0, 0, 1, None, _stream(a))
+    check(rc, name)
+    return c if ldc == N else c[:, :N]
+
+
 def linear(x: torch.Tensor, w: torch.Tensor, name: str = "gemm") -> torch.Tensor:
     """x [M, K] @ w[N, K].T -> [M, N] (F.linear without bias)."""
     return mm(x, w.t(), name)

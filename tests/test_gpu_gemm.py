@@ -6,6 +6,8 @@ reference); the bar is the bf16 rounding of the output: elementwise
 |got - ref| <= 1e-2 |ref| + 1e-3 max|ref|.  Fused kernels must equal their
 unfused composition (the same GEMM engine with a plain bf16 store, then the
 standalone K1 / K2 kernel) bit for bit: the accumulation order is the same.
+NT products on whole 256 x 256 tiles run on a second main loop (16x16x32
+MFMAs, another fp32 summation order); the compositions use G.mm_engine.
 """
 
 import pytest
@@ -66,6 +68,28 @@ def test_mm_deterministic_and_k_tail(device):
     assert_gemm_close(c1, ref_mm(a, b))
 
 
+# NT products on whole 256 x 256 tiles (M, N multiples of 256, K of 64) run
+# on the 16x16x32 direct-to-LDS loop (mm sends products of < 128 tiles with
+# K >= 1024 to split-K instead): one k-tile, two (the prologue's pair only),
+# odd tile counts, a last group of fewer than 4 tile rows (M 2560), and
+# operands whose rows are longer than K (sub-views of wider tensors).
+@pytest.mark.parametrize("m,n,k,pad", [(256, 256, 64, 0), (256, 512, 128, 0), (768, 256, 192, 8),
+                                       (2560, 2304, 960, 0), (4096, 2048, 4096, 64)])
+def test_mm_nt16_loop(device, m, n, k, pad):
+    _, G = _cpt()
+    a = rnd((m, k + pad), 40, device)[:, :k]
+    w = rnd((n, k + pad), 41, device, 0.05)[:, :k]
+    got = G.linear(a, w)
+    assert_gemm_close(got, ref_mm(a, w.t()))
+    assert torch.equal(got, G.linear(a, w))
+    # the engine's product of the same operands: same bf16 rounding of an
+    # fp32 sum in another order, so all but a few elements agree exactly
+    eng = G.mm_engine(a, w.t())
+    assert_gemm_close(eng, ref_mm(a, w.t()))
+    diff = (got.view(torch.int16) != eng.view(torch.int16)).float().mean().item()
+    assert diff < 0.05, diff
+
+
 @pytest.mark.parametrize("cache,bits,group", [("int4", 4, 64), ("int8", 8, 128), ("int8", 8, 64),
                                               ("int4", 4, 32), ("bf16", 0, 64),
                                               ("none", 0, 64)])
@@ -79,8 +103,9 @@ def test_gate_up_fused_equals_unfused(device, cache, bits, group, n_tok, hid, in
     wg = rnd((inter, hid), 11, device, 0.05)
     wu = rnd((inter, hid), 12, device, 0.05)
     hm, hg, hu, qg, sg, qu, su = G.ffn_gate_up(x, wg, wu, code, group)
-    hg_ref = G.linear(x, wg)
-    hu_ref = G.linear(x, wu)
+    # the engine's plain product: the fused kernel's summation order
+    hg_ref = G.mm_engine(x, wg.t())
+    hu_ref = G.mm_engine(x, wu.t())
     assert_gemm_close(hg_ref, ref_mm(x, wg.t()))
     hm_ref = cpt.silu_mul(hg_ref, hu_ref)
     assert torch.equal(hm.view(torch.int16), hm_ref.view(torch.int16))
@@ -143,6 +168,12 @@ def test_c2_shapes_gemm_numerics(device):
     cols = torch.arange(0, d, 1009, device=device)
     ref2 = gy.float().t() @ y[:, cols].float()
     assert_gemm_close(dw[:, cols], ref2.cpu())
+    # the forward down projection, K = 11008 (the 16x16x32 NT loop)
+    hm = rnd((n, d), 33, device)
+    wd = rnd((h, d), 34, device, 0.02)
+    yd = G.linear(hm, wd)
+    ref3 = hm[rows].float() @ wd.float().t()
+    assert_gemm_close(yd[rows], ref3.cpu())
 
 
 @pytest.mark.parametrize("m,r,k", [(8192, 16, 4096), (8192, 16, 11008), (300, 8, 264),

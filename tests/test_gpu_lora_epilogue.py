@@ -90,8 +90,8 @@ def test_gate_up_lora_fused_equals_composed(device, cache, bits, group, which, r
     lg = (xa_g, bg, 2.0) if which in ("both", "gate") else None
     lu = (xa_u, bu, 2.0) if which in ("both", "up") else None
     hm, hg, hu, qg, sg, qu, su = G.ffn_gate_up(x, wg, wu, code, group, lora_gate=lg, lora_up=lu)
-    hg_ref = G.mm2(x, wg.t(), lora=[(xa_g, bg.t(), 2.0)]) if lg else G.linear(x, wg)
-    hu_ref = G.mm2(x, wu.t(), lora=[(xa_u, bu.t(), 2.0)]) if lu else G.linear(x, wu)
+    hg_ref = G.mm2(x, wg.t(), lora=[(xa_g, bg.t(), 2.0)]) if lg else G.mm_engine(x, wg.t())
+    hu_ref = G.mm2(x, wu.t(), lora=[(xa_u, bu.t(), 2.0)]) if lu else G.mm_engine(x, wu.t())
     assert torch.equal(bits16(hm), bits16(cpt.silu_mul(hg_ref, hu_ref)))
     if cache == "bf16":
         assert torch.equal(bits16(hg), bits16(hg_ref))
