@@ -8,6 +8,7 @@ namespace cpt {
 namespace gemm {
 
 CPT_GEMM_INST_ALL(CPT_GEMM_DECLARE)
+CPT_NT16_INST_ALL(CPT_NT16_DECLARE)
 
 // out[m, n] = bf16(alpha * sum_s ws[s][m][n])  (split-K reduction, fixed order)
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws,
@@ -265,14 +266,20 @@ int gemm_bf16_impl(const void* a, int64_t lda, int a_kmajor, const void* b, int6
     // one NT pair on whole 256 x 256 tiles: the 16x16x32 loop (a different
     // fp32 summation order from the engine's; cpt_gemm_bf16_ex mode 0 keeps
     // the engine's)
-    if (!two && nt16_fits(M, N, K, c, ldc))
-      return launch_nt16((const uint16_t*)a, lda, (const uint16_t*)b, ldb, (uint16_t*)c, ldc, M, N,
-                         K, st);
+    if (!two && nt16_fits(M, N, K, c, ldc)) return launch_nt16<EPI_STORE, 0, 0>(A, st);
     return launch<true, true, EPI_STORE, 0, 0>(A, st);
   }
   if (a_kmajor && !b_kmajor) return launch<true, false, EPI_STORE, 0, 0>(A, st);
   if (!a_kmajor && !b_kmajor) return launch<false, false, EPI_STORE, 0, 0>(A, st);
   return launch<false, true, EPI_STORE, 0, 0>(A, st);
+}
+
+// F1 on the 16x16x32 loop: whole 256-token x 128-column tiles, K of 64
+inline bool ffn_nt16_fits(int64_t n_tok, int64_t inter, int64_t hidden) {
+  constexpr int64_t kIntMax = 0x7FFFFFFF;
+  return n_tok > 0 && inter > 0 && hidden > 0 && n_tok <= kIntMax && inter <= kIntMax &&
+         hidden <= kIntMax && n_tok % 256 == 0 && inter % 128 == 0 && hidden % 64 == 0 &&
+         (n_tok / 256) * (inter / 128) <= kIntMax;
 }
 
 int ffn_gate_up_impl(const void* x, const void* w_gate, const void* w_up, int64_t n_tok,
@@ -322,6 +329,23 @@ int ffn_gate_up_impl(const void* x, const void* w_gate, const void* w_up, int64_
   int terms = 0;
   if (const int rc = set_lora(A, L, n_tok, inter, terms)) return rc;
   hipStream_t st = (hipStream_t)stream;
+  // whole 256-token x 128-column tiles without adapter terms: the 16x16x32
+  // loop (its summation order is that of cpt_gemm_bf16's NT products on whole
+  // tiles, not of cpt_gemm_bf16_ex mode 0)
+  if (!terms && ffn_nt16_fits(n_tok, inter, hidden)) {
+    switch (cache) {
+      case CACHE_NONE: return launch_nt16<EPI_GLU, CACHE_NONE, 64>(A, st);
+      case CACHE_BF16: return launch_nt16<EPI_GLU, CACHE_BF16, 64>(A, st);
+      case CACHE_INT4:
+        return group_size == 32   ? launch_nt16<EPI_GLU, CACHE_INT4, 32>(A, st)
+               : group_size == 64 ? launch_nt16<EPI_GLU, CACHE_INT4, 64>(A, st)
+                                  : launch_nt16<EPI_GLU, CACHE_INT4, 128>(A, st);
+      default:
+        return group_size == 32   ? launch_nt16<EPI_GLU, CACHE_INT8, 32>(A, st)
+               : group_size == 64 ? launch_nt16<EPI_GLU, CACHE_INT8, 64>(A, st)
+                                  : launch_nt16<EPI_GLU, CACHE_INT8, 128>(A, st);
+    }
+  }
   // the dual kernel carries both terms (gate, up); an absent one is a no-op
   switch (cache) {
     case CACHE_NONE:

@@ -1,0 +1,283 @@
+// NT bf16 GEMM on v_mfma_f32_16x16x32_bf16 with direct-to-LDS operand loads:
+//   C[M, N] = A[M, K] . B[N, K]^T, both operands K-major, fp32 accumulate.
+// Two epilogues:
+//   EPI_STORE  C = bf16(acc): the plain NT product of cpt_gemm_bf16 when M and
+//              N are multiples of 256 and K of 64 (the forward down
+//              projection h_mid . W_d^T and other nn.Linear products);
+//   EPI_GLU    F1 (x . [W_gate; W_up]^T, the GLU and the cache codec of
+//              glu_finish) when M is a multiple of 256, d_ff of 128, K of 64
+//              and no adapter terms ride in the epilogue.
+// Every other product runs on the 32x32x16 engine in gemm_kernel.h.  The
+// instantiations live in gemm16*.hip.
+//
+// Why a second main loop.  At the 1400 W board limit the MFMA work per joule
+// sets the rate: 16x16x32 spends 0.63 pJ per FLOP against 0.71 for 32x32x16
+// (register-only probe), and loading the operands straight into LDS
+// (buffer_load ... lds) drops the engine's 16 ds_write_b128 per thread and
+// k-tile and the 64 VGPRs that hold a tile in flight.
+//
+// Block: 256 threads (4 waves, one per SIMD), a 256 x 256 output tile, k
+// steps of 64; wave w owns C rows 128 (w / 2) .. +127 and columns
+// 128 (w % 2) .. +127 as 8 x 8 MFMA blocks of 16 x 16.
+//
+// LDS: 2 stages x 2 operands x [256 rows][64 k] bf16, unpadded, 128 KiB.
+// Row r keeps its 8 chunks of 8 k-values at chunk position c ^ (r & 6): a
+// 16x16x32 fragment read (lane l: row l % 16, chunk l / 16 or l / 16 + 4)
+// then touches every bank once per 16 lanes (conflict-free under gfx950's
+// 128-bit read grouping).  A direct-to-LDS load writes 64 lanes x 16 bytes
+// contiguously, so the swizzle is applied on the global side: lane l of a
+// load fetches row 8 q + l / 8, chunk (l % 8) ^ (row & 6) into LDS row
+// 8 q + l / 8, chunk position l % 8.
+//
+// Schedule of one k-tile kt (stage s = kt & 1) over its 128 MFMA slots t:
+//   t < 64   sub-step 0 (k 0..31) on fragment set F0, in triangular (i, j)
+//            order so the first MFMAs need only the first fragments read;
+//   t >= 64  sub-step 1 (k 32..63) on F1;
+//   t = 2q   (q < 16) F1 reads of tile kt from stage s;
+//   t = 33   barrier A (after lgkmcnt(0)): every wave has read stage s;
+//   t = 34 + 6p (p < 16)  load p of tile kt + 2 into stage s;
+//   t = 95   barrier B (after this wave's loads of tile kt + 1 have landed:
+//            vmcnt = the loads of tile kt + 2 issued since);
+//   t = 96 + 2q  F0 reads of tile kt + 1 from stage s ^ 1.
+// Spreading the 16 loads over 90 slots matters: issued in one burst after a
+// single barrier the loop ran at 0.57 TF/GHz, spread this way at 0.82-0.85
+// (the engine 0.81-0.86), and at the board's power cap 8-9% faster than the
+// engine at K 11008 and 0-4% at K 4096.  Both barriers are plain s_barrier:
+// __syncthreads()'s release fence makes the compiler wait for every load in
+// flight, the direct-to-LDS ones included, which drains the pipeline.
+
+#pragma once
+
+#include "gemm_kernel.h"
+
+namespace cpt {
+namespace gemm {
+namespace nt16 {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+constexpr int kBK = 64;
+constexpr int kThreads = 256;
+constexpr int kStage = 256 * kBK;                 // elements of one operand in one stage
+constexpr int kMainLds = 4 * kStage * 2;          // 2 stages x 2 operands: 128 KiB
+constexpr int kLdOut = 264;                       // staged output rows (elements)
+constexpr int kOutLds = 256 * kLdOut * 2;         // 132 KiB
+constexpr int kMax2 = kMainLds > kOutLds ? kMainLds : kOutLds;
+constexpr int kLds = kMax2 > kGluLdsBytes ? kMax2 : kGluLdsBytes;
+static_assert(kLds <= 160 * 1024, "LDS per block");
+
+constexpr int kBarA = 34;                         // first slot after barrier A
+constexpr int kLdEvery = 6;                       // slots between loads of one tile
+constexpr int kBarB = 96;                         // first slot after barrier B
+constexpr int kLoadsBeforeB = (kBarB - 1 - kBarA) / kLdEvery + 1;
+static_assert(kBarA - 1 > 2 * 15, "barrier A follows the last F1 read");
+static_assert(kBarA + kLdEvery * 15 < 128, "every load of a tile inside the tile");
+static_assert(kBarB + 2 * 15 < 128, "F0 reads inside the tile");
+static_assert(kLoadsBeforeB <= 16, "vmcnt of barrier B");
+
+// sub-step 0 order: (i, j) over 8 x 8 blocks, block n = max(i, j) ascending
+struct Order {
+  uint8_t i[64], j[64];
+  constexpr Order() : i(), j() {
+    int t = 0;
+    for (int n = 0; n < 8; ++n) {
+      for (int q = 0; q < n; ++q) { i[t] = n; j[t] = q; ++t; }
+      for (int q = 0; q < n; ++q) { i[t] = q; j[t] = n; ++t; }
+      i[t] = n; j[t] = n; ++t;
+    }
+  }
+};
+
+__device__ __forceinline__ int lds_off(int row, int chunk) {
+  return row * kBK + ((chunk ^ (row & 6)) << 3);
+}
+
+// The accumulator is tied in place ("+a"): with the builtin, LLVM rotates the
+// 64 four-register blocks through copies.
+__device__ __forceinline__ void mfma(f32x4& c, const bf16x8& a, const bf16x8& b) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+
+// 16 bytes per lane from the buffer at voff into LDS at lds + 16 * lane bytes
+__device__ __forceinline__ void load_lds(__amdgpu_buffer_rsrc_t r, uint16_t* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, voff, 0, 0, 0);
+}
+
+template <int EPI, int CACHE, int GS>
+__global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
+  static_assert(EPI == EPI_STORE || EPI == EPI_GLU, "epilogues of the 16x16x32 loop");
+  constexpr bool DUAL = EPI == EPI_GLU;
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave & 1, wm = wave >> 1;
+  int tm, tn;
+  tile_coords(A.tiles_m, A.tiles_n, tm, tn);
+  const int64_t m0 = (int64_t)tm * 256, n0 = (int64_t)tn * 256;
+  const int nk = (int)(A.K[0] / kBK);
+  const int64_t lda = A.a[0].ld, ldb = A.b[0].ld;
+
+  // K-major operands at the tile's first row (the host keeps 257 rows < 2 GiB).
+  // DUAL: the tile's 256 B rows are gate rows d0 .. d0 + 63, up rows d0 .. +63,
+  // gate rows d0 + 64 .. +127, up rows d0 + 64 .. +127 (d0 = n0 / 2), so each
+  // wave's 128 columns hold 64 gate and the same 64 up columns.
+  const __amdgpu_buffer_rsrc_t ra =
+      make_rsrc(A.a[0].p + m0 * lda, (int64_t)(A.M - m0) * lda * 2);
+  const int64_t nb0 = DUAL ? n0 / 2 : n0;
+  const int64_t nrows = DUAL ? A.D : A.N;
+  const __amdgpu_buffer_rsrc_t rb =
+      make_rsrc(A.b[0].p + nb0 * ldb, (nrows - nb0) * ldb * 2);
+  const __amdgpu_buffer_rsrc_t rbu =
+      DUAL ? make_rsrc(A.b_up + nb0 * ldb, (nrows - nb0) * ldb * 2) : rb;
+  // load i of an operand fills LDS rows 8 q .. 8 q + 7, q = 4 i + wave; lane l
+  // row 8 q + l / 8 (so row & 6 = (l / 8) & 6) from source row r (DUAL B:
+  // block i of its weight's 128 rows as above)
+  const int chunk = (lane & 7) ^ ((lane >> 3) & 6);
+  uint32_t oa[8], ob[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 8 * (4 * i + wave) + (lane >> 3);
+    const int rw = DUAL ? 64 * (i >> 2) + 8 * (4 * (i & 1) + wave) + (lane >> 3) : r;
+    oa[i] = (uint32_t)(((int64_t)r * lda + chunk * 8) * 2);
+    ob[i] = (uint32_t)(((int64_t)rw * ldb + chunk * 8) * 2);
+  }
+  // byte offset of k-tile kt; past the end an offset beyond num_records (the
+  // loads return zeros and read no memory)
+  auto kofs = [&](int kt) -> uint32_t { return kt < nk ? (uint32_t)(kt * kBK * 2) : kOOB; };
+  // load p (0..15) of a tile into stage st: even p -> A block p / 2, odd -> B
+  auto issue = [&](int p, int st, uint32_t kb) {
+    const int i = p >> 1;
+    uint16_t* dst = lds + (st * 2 + (p & 1)) * kStage + (4 * i + wave) * 512;
+    if (p & 1) load_lds(DUAL && ((i >> 1) & 1) ? rbu : rb, dst, ob[i] + kb);
+    else load_lds(ra, dst, oa[i] + kb);
+  };
+
+  f32x4 acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // fragment q of a sub-step: even q -> B (n block q / 2), odd q -> A (m block q / 2)
+  const int nofs0 = lds_off(wn * 128 + (lane & 15), lane >> 4);
+  const int mofs0 = lds_off(wm * 128 + (lane & 15), lane >> 4);
+  const int nofs1 = lds_off(wn * 128 + (lane & 15), (lane >> 4) + 4);
+  const int mofs1 = lds_off(wm * 128 + (lane & 15), (lane >> 4) + 4);
+  bf16x8 f0[16], f1[16];
+  auto rd = [&](int st, int s, int q) -> bf16x8 {
+    const uint16_t* base = lds + st * 2 * kStage;
+    const int o = (q & 1) ? (s ? mofs1 : mofs0) : kStage + (s ? nofs1 : nofs0);
+    return *reinterpret_cast<const bf16x8*>(base + o + (q >> 1) * 16 * kBK);
+  };
+
+  // prologue: tile 0 -> stage 0, tile 1 -> stage 1; tile 0 landed; F0 of tile 0
+  {
+    const uint32_t k0 = kofs(0), k1 = kofs(1);
+#pragma unroll
+    for (int p = 0; p < 16; ++p) issue(p, 0, k0);
+#pragma unroll
+    for (int p = 0; p < 16; ++p) issue(p, 1, k1);
+  }
+  asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  // read order pinned so the loop header's merged waits stay counts, not lgkmcnt(0)
+#pragma unroll
+  for (int q = 0; q < 16; ++q) {
+    f0[q] = rd(0, 0, q);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  constexpr Order ord;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int stage = kt & 1;
+    const uint32_t kb2 = kofs(kt + 2);
+    static_for<0, 128>([&](auto tc) {
+      constexpr int t = decltype(tc)::value;
+      if constexpr (t < 64) {
+        constexpr int i = ord.i[t], j = ord.j[t];
+        mfma(acc[i][j], f0[2 * i], f0[2 * j + 1]);
+      } else {
+        constexpr int i = (t - 64) >> 3, j = (t - 64) & 7;
+        mfma(acc[i][j], f1[2 * i], f1[2 * j + 1]);
+      }
+      if constexpr (t % 2 == 0 && t / 2 < 16) f1[t / 2] = rd(stage, 1, t / 2);
+      if constexpr (t == kBarA - 1) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      if constexpr (t >= kBarA && (t - kBarA) % kLdEvery == 0 && (t - kBarA) / kLdEvery < 16)
+        issue((t - kBarA) / kLdEvery, stage, kb2);
+      if constexpr (t == kBarB - 1)
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kLoadsBeforeB) : "memory");
+      if constexpr (t >= kBarB && (t - kBarB) % 2 == 0 && (t - kBarB) / 2 < 16)
+        f0[(t - kBarB) / 2] = rd(stage ^ 1, 0, (t - kBarB) / 2);
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  }
+  // the loads past the last tile write zeros into LDS: land them (every wave)
+  // before the output is staged there
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  // lane holds tile column (n side) 128 wn + 16 i + 4 (lane / 16) + 0..3 of
+  // tile row (m side) 128 wm + 16 j + lane % 16 in acc[i][j]
+  if constexpr (EPI == EPI_STORE) {
+    // bf16(acc) is staged as a row-major tile (rows kLdOut apart: 32 lanes of
+    // one 8-byte write cover the 64 banks once), then 32 threads store each
+    // 512-byte row.
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int ml = wm * 128 + 16 * j + (lane & 15);
+        const int nl = wn * 128 + 16 * i + 4 * (lane >> 4);
+        *reinterpret_cast<uint2*>(lds + ml * kLdOut + nl) =
+            make_uint2(pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3]));
+      }
+    __syncthreads();
+    const int cl = (tid & 31) * 8;
+#pragma unroll 4
+    for (int p = 0; p < 32; ++p) {
+      const int r = p * 8 + (tid >> 5);
+      const uint4 w = *reinterpret_cast<const uint4*>(lds + r * kLdOut + cl);
+      *reinterpret_cast<uint4*>(A.C + (m0 + r) * A.ldc + n0 + cl) = w;
+    }
+  } else {
+    // F1: blocks i < 4 are gate columns d = 64 wn + 16 i + ..., i >= 4 the
+    // same up columns; staged as glu_finish's two tiles (rows kGluLd apart:
+    // 32 lanes of one 8-byte write cover the 64 banks once)
+    uint16_t* sg = lds;
+    uint16_t* su = lds + 256 * kGluLd;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int ml = wm * 128 + 16 * j + (lane & 15);
+        const int dl = wn * 64 + 16 * (i & 3) + 4 * (lane >> 4);
+        *reinterpret_cast<uint2*>((i < 4 ? sg : su) + ml * kGluLd + dl) =
+            make_uint2(pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3]));
+      }
+    __syncthreads();
+    glu_finish<CACHE, GS>(A, m0, n0, lds);
+  }
+}
+
+}  // namespace nt16
+
+template <int EPI, int CACHE, int GS>
+int launch_nt16(const KArgs& A, hipStream_t st) {
+  auto kern = nt16::nt16_kernel<EPI, CACHE, GS>;
+  static bool attr_set = false;   // per instantiation
+  if (!attr_set) {
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            nt16::kLds) != hipSuccess)
+      return kErrLaunch;
+    attr_set = true;
+  }
+  const int64_t tiles = (int64_t)A.tiles_m * A.tiles_n;
+  if (tiles <= 0) return kOk;
+  if (tiles > 0x7FFFFFFF) return kErrTooLarge;
+  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(nt16::kThreads), nt16::kLds, st, A);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+}  // namespace gemm
+}  // namespace cpt

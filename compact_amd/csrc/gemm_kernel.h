@@ -847,42 +847,25 @@ __device__ __forceinline__ void epi_f32(const KArgs& A, const Acc& acc, int64_t 
 // Wave (wn, wm) holds gate in acc[0..1][j] and up in acc[2..3][j] for
 // d = d0 + 64 wn + 32 i + 8 q + 4 (lane/32) + e, m = m0 + 128 wm + 32 j + lane%32.
 // ---------------------------------------------------------------------------
-template <int CACHE, int GS, int LT>
-__device__ __forceinline__ void epi_glu(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0,
-                                        uint16_t* lds) {
-  // F1: h_gate = bf16(acc gate half), h_up = bf16(acc up half) are staged
-  // through LDS as two row-major 256 x 128 bf16 tiles; then 16 consecutive
-  // threads own one row (8 columns each): h_mid, the bf16 cache or the codes
-  // go out as contiguous row segments, and a quantisation group is GS / 8
-  // consecutive lanes (shuffle-xor max).
+// F1 epilogue, second half (shared by both main loops): h_gate and h_up of the
+// tile sit in LDS as two row-major 256 x 128 bf16 tiles, rows kGluLd apart
+// (gate at lds, up at lds + 256 kGluLd), written by the caller's staging and a
+// block barrier.  16 consecutive threads own one row (8 columns each): h_mid,
+// the bf16 cache or the codes go out as contiguous row segments, and a
+// quantisation group is GS / 8 consecutive lanes (shuffle-xor max).
+constexpr int kGluLd = 136;               // LDS row stride in bf16 (272 bytes)
+constexpr int kGluLdsBytes = 2 * 256 * kGluLd * 2;
+
+template <int CACHE, int GS>
+__device__ __forceinline__ void glu_finish(const KArgs& A, int64_t m0, int64_t n0,
+                                           const uint16_t* lds) {
   static_assert(GS >= 8 && GS <= 128 && 128 % GS == 0, "group must divide the 128-column tile");
   constexpr int BITS = CACHE == CACHE_INT4 ? 4 : 8;
   constexpr bool QUANT = CACHE == CACHE_INT4 || CACHE == CACHE_INT8;
-  constexpr int LD = 136;                  // LDS row stride in bf16 (272 bytes)
+  constexpr int LD = kGluLd;
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wn = wave & 1, wm = wave >> 1;
-  const int half = lane >> 5;
-  uint16_t* sg = lds;
-  uint16_t* su = lds + 256 * LD;
-  LoraFr F;
-  if constexpr (LT > 0) lora_load<true, LT>(A, m0, n0, F);
-  // acc[i][j] (i = 0, 1 gate; i = 2, 3 up) -> d = 64 wn + 32 (i & 1) + 8 q + 4 half + e
-  static_for<0, 4>([&](auto j) {
-    const int ml = wm * 128 + j * 32 + (lane & 31);
-    static_for<0, 2>([&](auto i) {
-      const f32x16 ag = acc_block<true, LT>(A, acc, F, i, j);
-      const f32x16 au = acc_block<true, LT>(A, acc, F, i + 2, j);
-      static_for<0, 4>([&](auto q) {
-        const int dl = wn * 64 + i * 32 + q * 8 + half * 4;
-        *reinterpret_cast<uint2*>(sg + ml * LD + dl) =
-            make_uint2(pack_bf16x2(ag[q * 4 + 0], ag[q * 4 + 1]), pack_bf16x2(ag[q * 4 + 2], ag[q * 4 + 3]));
-        *reinterpret_cast<uint2*>(su + ml * LD + dl) =
-            make_uint2(pack_bf16x2(au[q * 4 + 0], au[q * 4 + 1]), pack_bf16x2(au[q * 4 + 2], au[q * 4 + 3]));
-      });
-    });
-  });
-  __syncthreads();
+  const uint16_t* sg = lds;
+  const uint16_t* su = lds + 256 * LD;
   const int64_t D = A.D;
   const int64_t G = D / GS;
   const int cl = (tid & 15) * 8;
@@ -951,6 +934,40 @@ __device__ __forceinline__ void epi_glu(const KArgs& A, const Acc& acc, int64_t 
       }
     }
   }
+}
+
+template <int CACHE, int GS, int LT>
+__device__ __forceinline__ void epi_glu(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0,
+                                        uint16_t* lds) {
+  // F1: h_gate = bf16(acc gate half), h_up = bf16(acc up half) are staged
+  // through LDS (glu_finish's layout), then glu_finish writes the outputs.
+  static_assert(BM * kGluLd * 2 * 2 <= LDS_BYTES, "the staged tiles must fit the main loop's LDS");
+  constexpr int LD = kGluLd;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wn = wave & 1, wm = wave >> 1;
+  const int half = lane >> 5;
+  uint16_t* sg = lds;
+  uint16_t* su = lds + 256 * LD;
+  LoraFr F;
+  if constexpr (LT > 0) lora_load<true, LT>(A, m0, n0, F);
+  // acc[i][j] (i = 0, 1 gate; i = 2, 3 up) -> d = 64 wn + 32 (i & 1) + 8 q + 4 half + e
+  static_for<0, 4>([&](auto j) {
+    const int ml = wm * 128 + j * 32 + (lane & 31);
+    static_for<0, 2>([&](auto i) {
+      const f32x16 ag = acc_block<true, LT>(A, acc, F, i, j);
+      const f32x16 au = acc_block<true, LT>(A, acc, F, i + 2, j);
+      static_for<0, 4>([&](auto q) {
+        const int dl = wn * 64 + i * 32 + q * 8 + half * 4;
+        *reinterpret_cast<uint2*>(sg + ml * LD + dl) =
+            make_uint2(pack_bf16x2(ag[q * 4 + 0], ag[q * 4 + 1]), pack_bf16x2(ag[q * 4 + 2], ag[q * 4 + 3]));
+        *reinterpret_cast<uint2*>(su + ml * LD + dl) =
+            make_uint2(pack_bf16x2(au[q * 4 + 0], au[q * 4 + 1]), pack_bf16x2(au[q * 4 + 2], au[q * 4 + 3]));
+      });
+    });
+  });
+  __syncthreads();
+  glu_finish<CACHE, GS>(A, m0, n0, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -1158,11 +1175,13 @@ int launch(KArgs& A, hipStream_t st) {
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
-// The plain-store NT product on the 16x16x32 direct-to-LDS main loop
-// (gemm16.hip): M, N multiples of 256, K of 64, C rows 16-byte aligned.
+// NT products on the 16x16x32 direct-to-LDS main loop (gemm16_kernel.h), one
+// operand pair, K a multiple of 64, no adapter terms: EPI_STORE with M, N
+// multiples of 256 and C rows 16-byte aligned (nt16_fits); EPI_GLU (F1) with
+// M a multiple of 256 and d_ff of 128.
 bool nt16_fits(int64_t M, int64_t N, int64_t K, const void* c, int64_t ldc);
-int launch_nt16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c,
-                int64_t ldc, int64_t M, int64_t N, int64_t K, hipStream_t st);
+template <int EPI, int CACHE, int GS>
+int launch_nt16(const KArgs& A, hipStream_t st);
 
 // ---------------------------------------------------------------------------
 // Instantiations of launch<AK, BKM, EPI, CACHE, GS, LT>.  Each group is
@@ -1206,6 +1225,16 @@ int launch_nt16(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, 
   CPT_GEMM_INST_STORE(X) CPT_GEMM_INST_AUX(X) CPT_GEMM_INST_GLU_A(X)         \
   CPT_GEMM_INST_GLU_B(X) CPT_GEMM_INST_DGLU_A(X) CPT_GEMM_INST_DGLU_B(X)     \
   CPT_GEMM_INST_WGLU(X)
+#define CPT_NT16_INST_STORE(X) X(EPI_STORE, 0, 0)
+#define CPT_NT16_INST_GLU_A(X)                                               \
+  X(EPI_GLU, CACHE_NONE, 64) X(EPI_GLU, CACHE_BF16, 64) X(EPI_GLU, CACHE_INT4, 32) \
+  X(EPI_GLU, CACHE_INT4, 64) X(EPI_GLU, CACHE_INT4, 128)
+#define CPT_NT16_INST_GLU_B(X)                                               \
+  X(EPI_GLU, CACHE_INT8, 32) X(EPI_GLU, CACHE_INT8, 64) X(EPI_GLU, CACHE_INT8, 128)
+#define CPT_NT16_INST_ALL(X) CPT_NT16_INST_STORE(X) CPT_NT16_INST_GLU_A(X) CPT_NT16_INST_GLU_B(X)
+#define CPT_NT16_DEFINE(EPI, CACHE, GS) template int launch_nt16<EPI, CACHE, GS>(const KArgs&, hipStream_t);
+#define CPT_NT16_DECLARE(EPI, CACHE, GS) \
+  extern template int launch_nt16<EPI, CACHE, GS>(const KArgs&, hipStream_t);
 #define CPT_GEMM_DEFINE(AK, BKM, EPI, CACHE, GS, LT) \
   template int launch<AK, BKM, EPI, CACHE, GS, LT>(KArgs&, hipStream_t);
 #define CPT_GEMM_DECLARE(AK, BKM, EPI, CACHE, GS, LT) \

@@ -157,7 +157,12 @@ int cpt_dequant_swiglu_backward_outlier(const void* grad_h_mid, const void* q_ga
  * bf16 in and out.  a_kmajor: A stored [M][lda] (1) or [K][lda] (0);
  * b_kmajor: B stored [N][ldb] (1, the nn.Linear weight) or [K][ldb] (0).
  * Pointers 16-byte aligned, leading dims multiples of 8, the contiguous
- * extent of each operand a multiple of 8, N and ldc multiples of 4. */
+ * extent of each operand a multiple of 8, N and ldc multiples of 4.
+ * One NT pair (both operands K-major) with M, N multiples of 256, K of 64
+ * and ldc of 8 runs on a 16x16x32 MFMA loop; every other product on the
+ * 32x32x16 loop of the fused FFN kernels.  Both round the fp32 sum to bf16
+ * once; their summation orders differ (cpt_gemm_bf16_ex mode 0 is always
+ * the 32x32x16 loop). */
 int cpt_gemm_bf16(const void* a, int64_t lda, int a_kmajor, const void* b, int64_t ldb,
                   int b_kmajor, const void* a2, int64_t lda2, const void* b2, int64_t ldb2,
                   int64_t K2, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream);
@@ -201,7 +206,8 @@ int cpt_gemm_bf16_skinny_t_noalloc(const void* x, int64_t ldx, const void* p, in
                                    int64_t R, float alpha, int splits, void* stream);
 
 /* Extended GEMM for the adapter (LoRA) terms, one operand pair:
- *   mode 0: C = bf16(A.B)
+ *   mode 0: C = bf16(A.B) on the 32x32x16 loop for every shape: the
+ *           summation order of the fused FFN kernels' GEMMs
  *   mode 1: C = bf16(C + bf16(alpha * bf16(A.B)))   (PEFT's h + s * B(A(x)),
  *           src/flashffn.py:1414,1420,1439,1529; C read and written in place)
  *   mode 2: C = bf16(alpha * sum of `splits` fp32 partials of A.B over K

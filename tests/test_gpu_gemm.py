@@ -6,8 +6,9 @@ reference); the bar is the bf16 rounding of the output: elementwise
 |got - ref| <= 1e-2 |ref| + 1e-3 max|ref|.  Fused kernels must equal their
 unfused composition (the same GEMM engine with a plain bf16 store, then the
 standalone K1 / K2 kernel) bit for bit: the accumulation order is the same.
-NT products on whole 256 x 256 tiles run on a second main loop (16x16x32
-MFMAs, another fp32 summation order); the compositions use G.mm_engine.
+NT products on whole tiles (and F1 on whole 256-token tiles) run on a second
+main loop (16x16x32 MFMAs, another fp32 summation order); each composition
+uses the plain product of the same loop (plain_like_f1, G.mm_engine).
 """
 
 import pytest
@@ -90,10 +91,27 @@ def test_mm_nt16_loop(device, m, n, k, pad):
     assert diff < 0.05, diff
 
 
+def plain_like_f1(G, x, w):
+    """x . w^T in the summation order of F1 without adapter terms: the
+    16x16x32 loop when F1 runs on it (ffn_nt16_fits in gemm.hip: tokens a
+    multiple of 256, d_ff of 128, d_model of 64), else the engine.  The plain
+    NT product reaches that loop on whole 256-column tiles, so zero rows pad
+    w (the other columns' sums are unchanged)."""
+    n, k = x.shape
+    d = w.shape[0]
+    if n % 256 == 0 and d % 128 == 0 and k % 64 == 0:
+        dp = -(-d // 256) * 256
+        assert k < 1024 or (n // 256) * (dp // 256) >= 128, "mm would split K"
+        wp = torch.nn.functional.pad(w, (0, 0, 0, dp - d))
+        return G.linear(x, wp)[:, :d].contiguous()
+    return G.mm_engine(x, w.t())
+
+
 @pytest.mark.parametrize("cache,bits,group", [("int4", 4, 64), ("int8", 8, 128), ("int8", 8, 64),
                                               ("int4", 4, 32), ("bf16", 0, 64),
                                               ("none", 0, 64)])
-@pytest.mark.parametrize("n_tok,hid,inter", [(512, 256, 512), (300, 128, 384), (7, 64, 256)])
+@pytest.mark.parametrize("n_tok,hid,inter", [(512, 256, 512), (512, 128, 384), (300, 128, 384),
+                                             (7, 64, 256)])
 def test_gate_up_fused_equals_unfused(device, cache, bits, group, n_tok, hid, inter):
     cpt, G = _cpt()
     from compact_amd import _lib
@@ -103,9 +121,9 @@ def test_gate_up_fused_equals_unfused(device, cache, bits, group, n_tok, hid, in
     wg = rnd((inter, hid), 11, device, 0.05)
     wu = rnd((inter, hid), 12, device, 0.05)
     hm, hg, hu, qg, sg, qu, su = G.ffn_gate_up(x, wg, wu, code, group)
-    # the engine's plain product: the fused kernel's summation order
-    hg_ref = G.mm_engine(x, wg.t())
-    hu_ref = G.mm_engine(x, wu.t())
+    # the plain product in the fused kernel's summation order
+    hg_ref = plain_like_f1(G, x, wg)
+    hu_ref = plain_like_f1(G, x, wu)
     assert_gemm_close(hg_ref, ref_mm(x, wg.t()))
     hm_ref = cpt.silu_mul(hg_ref, hu_ref)
     assert torch.equal(hm.view(torch.int16), hm_ref.view(torch.int16))
