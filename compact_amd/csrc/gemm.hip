@@ -262,13 +262,16 @@ int gemm_bf16_impl(const void* a, int64_t lda, int a_kmajor, const void* b, int6
     return b_kmajor ? launch<true, true, EPI_STORE, 0, 0, 2>(A, st)
                     : launch<true, false, EPI_STORE, 0, 0, 2>(A, st);
   }
-  if (a_kmajor && b_kmajor) {
-    // one NT pair on whole 256 x 256 tiles: the 16x16x32 loop (a different
-    // fp32 summation order from the engine's; cpt_gemm_bf16_ex mode 0 keeps
-    // the engine's)
-    if (!two && nt16_fits(M, N, K, c, ldc)) return launch_nt16<EPI_STORE, 0, 0>(A, st);
-    return launch<true, true, EPI_STORE, 0, 0>(A, st);
+  // whole 256 x 256 tiles, K of each pair a multiple of 64: the 16x16x32 loop
+  // (another fp32 summation order than the engine's; cpt_gemm_bf16_ex mode 0
+  // keeps the engine's)
+  if (nt16_fits(M, N, K, c, ldc) && (!two || (K2 > 0 && K2 % 64 == 0 && K2 <= 0x7FFFFFFF))) {
+    if (a_kmajor && b_kmajor) return launch_nt16<true, true, EPI_STORE, 0, 0>(A, st);
+    if (a_kmajor && !b_kmajor) return launch_nt16<true, false, EPI_STORE, 0, 0>(A, st);
+    if (!a_kmajor && !b_kmajor) return launch_nt16<false, false, EPI_STORE, 0, 0>(A, st);
+    return launch_nt16<false, true, EPI_STORE, 0, 0>(A, st);
   }
+  if (a_kmajor && b_kmajor) return launch<true, true, EPI_STORE, 0, 0>(A, st);
   if (a_kmajor && !b_kmajor) return launch<true, false, EPI_STORE, 0, 0>(A, st);
   if (!a_kmajor && !b_kmajor) return launch<false, false, EPI_STORE, 0, 0>(A, st);
   return launch<false, true, EPI_STORE, 0, 0>(A, st);
@@ -334,16 +337,16 @@ int ffn_gate_up_impl(const void* x, const void* w_gate, const void* w_up, int64_
   // tiles, not of cpt_gemm_bf16_ex mode 0)
   if (!terms && ffn_nt16_fits(n_tok, inter, hidden)) {
     switch (cache) {
-      case CACHE_NONE: return launch_nt16<EPI_GLU, CACHE_NONE, 64>(A, st);
-      case CACHE_BF16: return launch_nt16<EPI_GLU, CACHE_BF16, 64>(A, st);
+      case CACHE_NONE: return launch_nt16<true, true, EPI_GLU, CACHE_NONE, 64>(A, st);
+      case CACHE_BF16: return launch_nt16<true, true, EPI_GLU, CACHE_BF16, 64>(A, st);
       case CACHE_INT4:
-        return group_size == 32   ? launch_nt16<EPI_GLU, CACHE_INT4, 32>(A, st)
-               : group_size == 64 ? launch_nt16<EPI_GLU, CACHE_INT4, 64>(A, st)
-                                  : launch_nt16<EPI_GLU, CACHE_INT4, 128>(A, st);
+        return group_size == 32   ? launch_nt16<true, true, EPI_GLU, CACHE_INT4, 32>(A, st)
+               : group_size == 64 ? launch_nt16<true, true, EPI_GLU, CACHE_INT4, 64>(A, st)
+                                  : launch_nt16<true, true, EPI_GLU, CACHE_INT4, 128>(A, st);
       default:
-        return group_size == 32   ? launch_nt16<EPI_GLU, CACHE_INT8, 32>(A, st)
-               : group_size == 64 ? launch_nt16<EPI_GLU, CACHE_INT8, 64>(A, st)
-                                  : launch_nt16<EPI_GLU, CACHE_INT8, 128>(A, st);
+        return group_size == 32   ? launch_nt16<true, true, EPI_GLU, CACHE_INT8, 32>(A, st)
+               : group_size == 64 ? launch_nt16<true, true, EPI_GLU, CACHE_INT8, 64>(A, st)
+                                  : launch_nt16<true, true, EPI_GLU, CACHE_INT8, 128>(A, st);
     }
   }
   // the dual kernel carries both terms (gate, up); an absent one is a no-op

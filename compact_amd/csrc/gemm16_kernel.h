@@ -99,15 +99,39 @@ __device__ __forceinline__ void mfma(f32x4& c, const bf16x8& a, const bf16x8& b)
   asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
 }
 
-// 16 bytes per lane from the buffer at voff into LDS at lds + 16 * lane bytes
-__device__ __forceinline__ void load_lds(__amdgpu_buffer_rsrc_t r, uint16_t* lds, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, voff, 0, 0, 0);
+// Buffer descriptor as four SGPRs (the inline-asm form of make_rsrc).
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 rsrc_sgpr(const void* p, int64_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(p);
+  const uint32_t n = bytes > 0x7FFFFFFF ? 0x7FFFFFFFu : bytes < 0 ? 0u : (uint32_t)bytes;
+  return i32x4{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xFFFFu), (int)n, kRsrcWord3};
 }
 
-template <int EPI, int CACHE, int GS>
+// 16 bytes per lane from the buffer at voff + soff into LDS at dst + 16 * lane
+// bytes.  Inline asm, not the builtin: the compiler counts a builtin load as a
+// pending LDS write and then puts vmcnt(0) (every load in flight, the next
+// tiles' included) before the transposing LDS reads.  Every wait these loads
+// need is explicit in the schedule (barrier B's vmcnt, the epilogue's vmcnt(0)).
+// voff is the loop-invariant per-lane offset, soff the uniform k-tile delta.
+__device__ __forceinline__ void load_lds(const i32x4& r, uint16_t* dst, uint32_t voff,
+                                         uint32_t soff) {
+  const uint32_t m0v = (uint32_t)(uintptr_t)(lds_void_t*)dst;
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :: "s"(m0v), "v"(voff), "s"(r), "s"(soff) : "memory", "m0");
+}
+
+// MN-major tile: [64 k][256 mn] rows of 512 bytes; the 16-byte chunk c of
+// row k sits at position c ^ mn_swz(k).  A 32-lane pass of the transposing
+// fragment read covers rows k0 + 0..3 and k0 + 8..11 (lanes 0-15, 16-31) at
+// two chunks each; the XOR gives those 8 rows 8 different chunk pairs, so the
+// pass touches each of the 64 banks once.
+__device__ __forceinline__ int mn_swz(int k) { return 2 * ((k & 3) | ((k & 8) >> 1)); }
+
+template <bool AK, bool BK, int EPI, int CACHE, int GS>
 __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
   static_assert(EPI == EPI_STORE || EPI == EPI_GLU, "epilogues of the 16x16x32 loop");
   constexpr bool DUAL = EPI == EPI_GLU;
+  static_assert(!DUAL || (AK && BK), "F1's operands are K-major");
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -116,42 +140,72 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
   int tm, tn;
   tile_coords(A.tiles_m, A.tiles_n, tm, tn);
   const int64_t m0 = (int64_t)tm * 256, n0 = (int64_t)tn * 256;
-  const int nk = (int)(A.K[0] / kBK);
-  const int64_t lda = A.a[0].ld, ldb = A.b[0].ld;
+  // k-tiles [0, nk0) come from pair 0, [nk0, nk) from pair 1 (K-concatenated)
+  const int nk0 = (int)(A.K[0] / kBK);
+  const int nk = nk0 + (A.npairs == 2 ? (int)(A.K[1] / kBK) : 0);
+  const int64_t lda = A.a[0].ld, ldb = A.b[0].ld;   // pair 1 shares them (host check)
 
-  // K-major operands at the tile's first row (the host keeps 257 rows < 2 GiB).
+  // Buffers: a K-major operand at the tile's first row (257 rows < 2 GiB), an
+  // MN-major one at the tile's first column (K + 256 rows < 2 GiB; host checks).
   // DUAL: the tile's 256 B rows are gate rows d0 .. d0 + 63, up rows d0 .. +63,
   // gate rows d0 + 64 .. +127, up rows d0 + 64 .. +127 (d0 = n0 / 2), so each
   // wave's 128 columns hold 64 gate and the same 64 up columns.
-  const __amdgpu_buffer_rsrc_t ra =
-      make_rsrc(A.a[0].p + m0 * lda, (int64_t)(A.M - m0) * lda * 2);
   const int64_t nb0 = DUAL ? n0 / 2 : n0;
   const int64_t nrows = DUAL ? A.D : A.N;
-  const __amdgpu_buffer_rsrc_t rb =
-      make_rsrc(A.b[0].p + nb0 * ldb, (nrows - nb0) * ldb * 2);
-  const __amdgpu_buffer_rsrc_t rbu =
-      DUAL ? make_rsrc(A.b_up + nb0 * ldb, (nrows - nb0) * ldb * 2) : rb;
-  // load i of an operand fills LDS rows 8 q .. 8 q + 7, q = 4 i + wave; lane l
-  // row 8 q + l / 8 (so row & 6 = (l / 8) & 6) from source row r (DUAL B:
-  // block i of its weight's 128 rows as above)
-  const int chunk = (lane & 7) ^ ((lane >> 3) & 6);
+  auto rsrc_a = [&](int pr) {
+    return AK ? rsrc_sgpr(A.a[pr].p + m0 * lda, (A.M - m0) * lda * 2)
+              : rsrc_sgpr(A.a[pr].p + m0, (A.K[pr] * lda - m0) * 2);
+  };
+  auto rsrc_b = [&](int pr, const uint16_t* p) {
+    return BK ? rsrc_sgpr(p + nb0 * ldb, (nrows - nb0) * ldb * 2)
+              : rsrc_sgpr(p + n0, (A.K[pr] * ldb - n0) * 2);
+  };
+  const bool two = A.npairs == 2;
+  const i32x4 ra0 = rsrc_a(0), rb0 = rsrc_b(0, A.b[0].p);
+  const i32x4 ra1 = two ? rsrc_a(1) : ra0;
+  const i32x4 rb1 = two ? rsrc_b(1, A.b[1].p) : rb0;
+  const i32x4 rbu = DUAL ? rsrc_b(0, A.b_up) : rb0;
+  // Load i of an operand fills LDS block q = 4 i + wave (1 KiB):
+  //   K-major: rows 8 q .. 8 q + 7; lane l row 8 q + l / 8 (row & 6 = (l / 8) & 6),
+  //            16-byte k chunk (l % 8) ^ (row & 6) (DUAL B: source row per block as above);
+  //   MN-major: k-rows 2 q, 2 q + 1; lane l k-row 2 q + l / 32, mn chunk
+  //            (l % 32) ^ mn_swz(k-row).
   uint32_t oa[8], ob[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const int r = 8 * (4 * i + wave) + (lane >> 3);
+    const int q = 4 * i + wave;
+    const int r = 8 * q + (lane >> 3);
+    const int ck = (lane & 7) ^ ((lane >> 3) & 6);
+    const int kr = 2 * q + (lane >> 5);
+    const int cm = (lane & 31) ^ mn_swz(kr);
     const int rw = DUAL ? 64 * (i >> 2) + 8 * (4 * (i & 1) + wave) + (lane >> 3) : r;
-    oa[i] = (uint32_t)(((int64_t)r * lda + chunk * 8) * 2);
-    ob[i] = (uint32_t)(((int64_t)rw * ldb + chunk * 8) * 2);
+    oa[i] = AK ? (uint32_t)(((int64_t)r * lda + ck * 8) * 2) : (uint32_t)(((int64_t)kr * lda + cm * 8) * 2);
+    ob[i] = BK ? (uint32_t)(((int64_t)rw * ldb + ck * 8) * 2) : (uint32_t)(((int64_t)kr * ldb + cm * 8) * 2);
   }
-  // byte offset of k-tile kt; past the end an offset beyond num_records (the
-  // loads return zeros and read no memory)
-  auto kofs = [&](int kt) -> uint32_t { return kt < nk ? (uint32_t)(kt * kBK * 2) : kOOB; };
+  // per k-tile: the pair's buffers and each operand's byte delta (k0 * 2 for a
+  // K-major operand, k0 * ld * 2 for an MN-major one); past the last tile a
+  // delta beyond num_records (the loads return zeros and read no memory)
+  struct TileLd {
+    i32x4 a, b;
+    uint32_t da, db;
+  };
+  // bytes per k-tile, 32-bit (an MN-major operand's K + 256 rows are < 2 GiB):
+  // a 64-bit product here is VALU work, and the buffers selected with it then
+  // land in VGPRs (a readfirstlane loop around every load)
+  const uint32_t stepa = AK ? (uint32_t)(kBK * 2) : (uint32_t)(kBK * lda * 2);
+  const uint32_t stepb = BK ? (uint32_t)(kBK * 2) : (uint32_t)(kBK * ldb * 2);
+  auto tile = [&](int kt) -> TileLd {
+    const bool p1 = kt >= nk0;
+    const uint32_t lk = (uint32_t)(kt - (p1 ? nk0 : 0));
+    const bool in = kt < nk;
+    return TileLd{p1 ? ra1 : ra0, p1 ? rb1 : rb0, in ? lk * stepa : kOOB, in ? lk * stepb : kOOB};
+  };
   // load p (0..15) of a tile into stage st: even p -> A block p / 2, odd -> B
-  auto issue = [&](int p, int st, uint32_t kb) {
+  auto issue = [&](int p, int st, const TileLd& T) {
     const int i = p >> 1;
     uint16_t* dst = lds + (st * 2 + (p & 1)) * kStage + (4 * i + wave) * 512;
-    if (p & 1) load_lds(DUAL && ((i >> 1) & 1) ? rbu : rb, dst, ob[i] + kb);
-    else load_lds(ra, dst, oa[i] + kb);
+    if (p & 1) load_lds(DUAL && ((i >> 1) & 1) ? rbu : T.b, dst, ob[i], T.db);
+    else load_lds(T.a, dst, oa[i], T.da);
   };
 
   f32x4 acc[8][8];
@@ -160,25 +214,42 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // fragment q of a sub-step: even q -> B (n block q / 2), odd q -> A (m block q / 2)
+  // Fragment q of a sub-step s (k 32 s .. 32 s + 31): even q -> B (n block q / 2),
+  // odd q -> A (m block q / 2).  Lane l holds 8 consecutive k (8 (l / 16) ..)
+  // of row l % 16 of the block:
+  //   K-major: one 16-byte read;
+  //   MN-major: two transposing reads (4 k each).  In a 16-lane group lane l'
+  //     reads k-row 8 (l / 16) + (l' % 16) / 4 (+ 4), columns 4 (l' % 4) .. + 3 of
+  //     the block; the chunk position is 16 w + 2 (block ^ f') + (l % 4) / 2 with
+  //     f' = mn_swz(k-row) / 2, the same for both reads and both sub-steps.
   const int nofs0 = lds_off(wn * 128 + (lane & 15), lane >> 4);
   const int mofs0 = lds_off(wm * 128 + (lane & 15), lane >> 4);
   const int nofs1 = lds_off(wn * 128 + (lane & 15), (lane >> 4) + 4);
   const int mofs1 = lds_off(wm * 128 + (lane & 15), (lane >> 4) + 4);
+  const int mn_lane = (8 * (lane >> 4) + ((lane & 15) >> 2)) * 256 + ((lane & 3) >> 1) * 8 + (lane & 1) * 4;
+  const int mn_fx = 8 * mn_swz(8 * (lane >> 4) + ((lane & 15) >> 2));   // 16 f'
   bf16x8 f0[16], f1[16];
   auto rd = [&](int st, int s, int q) -> bf16x8 {
     const uint16_t* base = lds + st * 2 * kStage;
-    const int o = (q & 1) ? (s ? mofs1 : mofs0) : kStage + (s ? nofs1 : nofs0);
-    return *reinterpret_cast<const bf16x8*>(base + o + (q >> 1) * 16 * kBK);
+    const bool bside = (q & 1) == 0;
+    if ((bside && BK) || (!bside && AK)) {
+      const int o = bside ? kStage + (s ? nofs1 : nofs0) : (s ? mofs1 : mofs0);
+      return *reinterpret_cast<const bf16x8*>(base + o + (q >> 1) * 16 * kBK);
+    }
+    const uint16_t* p = base + (bside ? kStage + 128 * wn : 128 * wm) + mn_lane + s * 32 * 256 +
+                        ((16 * (q >> 1)) ^ mn_fx);
+    const i16x4 lo = lds_read_tr(p);
+    const i16x4 hi = lds_read_tr(p + 4 * 256);
+    return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   };
 
   // prologue: tile 0 -> stage 0, tile 1 -> stage 1; tile 0 landed; F0 of tile 0
   {
-    const uint32_t k0 = kofs(0), k1 = kofs(1);
+    const TileLd T0 = tile(0), T1 = tile(1);
 #pragma unroll
-    for (int p = 0; p < 16; ++p) issue(p, 0, k0);
+    for (int p = 0; p < 16; ++p) issue(p, 0, T0);
 #pragma unroll
-    for (int p = 0; p < 16; ++p) issue(p, 1, k1);
+    for (int p = 0; p < 16; ++p) issue(p, 1, T1);
   }
   asm volatile("s_waitcnt vmcnt(16)\n\ts_barrier" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
@@ -192,7 +263,7 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
   constexpr Order ord;
   for (int kt = 0; kt < nk; ++kt) {
     const int stage = kt & 1;
-    const uint32_t kb2 = kofs(kt + 2);
+    const TileLd T2 = tile(kt + 2);
     static_for<0, 128>([&](auto tc) {
       constexpr int t = decltype(tc)::value;
       if constexpr (t < 64) {
@@ -205,7 +276,7 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
       if constexpr (t % 2 == 0 && t / 2 < 16) f1[t / 2] = rd(stage, 1, t / 2);
       if constexpr (t == kBarA - 1) asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       if constexpr (t >= kBarA && (t - kBarA) % kLdEvery == 0 && (t - kBarA) / kLdEvery < 16)
-        issue((t - kBarA) / kLdEvery, stage, kb2);
+        issue((t - kBarA) / kLdEvery, stage, T2);
       if constexpr (t == kBarB - 1)
         asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kLoadsBeforeB) : "memory");
       if constexpr (t >= kBarB && (t - kBarB) % 2 == 0 && (t - kBarB) / 2 < 16)
@@ -262,9 +333,9 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
 
 }  // namespace nt16
 
-template <int EPI, int CACHE, int GS>
+template <bool AK, bool BK, int EPI, int CACHE, int GS>
 int launch_nt16(const KArgs& A, hipStream_t st) {
-  auto kern = nt16::nt16_kernel<EPI, CACHE, GS>;
+  auto kern = nt16::nt16_kernel<AK, BK, EPI, CACHE, GS>;
   static bool attr_set = false;   // per instantiation
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,

@@ -1175,12 +1175,13 @@ int launch(KArgs& A, hipStream_t st) {
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
-// NT products on the 16x16x32 direct-to-LDS main loop (gemm16_kernel.h), one
-// operand pair, K a multiple of 64, no adapter terms: EPI_STORE with M, N
-// multiples of 256 and C rows 16-byte aligned (nt16_fits); EPI_GLU (F1) with
-// M a multiple of 256 and d_ff of 128.
+// Products on the 16x16x32 direct-to-LDS main loop (gemm16_kernel.h), K of
+// each pair a multiple of 64, no adapter terms: EPI_STORE in every operand
+// layout with M, N multiples of 256 and C rows 16-byte aligned (nt16_fits);
+// EPI_GLU (F1, both operands K-major, one pair) with M a multiple of 256 and
+// d_ff of 128.
 bool nt16_fits(int64_t M, int64_t N, int64_t K, const void* c, int64_t ldc);
-template <int EPI, int CACHE, int GS>
+template <bool AK, bool BK, int EPI, int CACHE, int GS>
 int launch_nt16(const KArgs& A, hipStream_t st);
 
 // ---------------------------------------------------------------------------
@@ -1225,16 +1226,21 @@ int launch_nt16(const KArgs& A, hipStream_t st);
   CPT_GEMM_INST_STORE(X) CPT_GEMM_INST_AUX(X) CPT_GEMM_INST_GLU_A(X)         \
   CPT_GEMM_INST_GLU_B(X) CPT_GEMM_INST_DGLU_A(X) CPT_GEMM_INST_DGLU_B(X)     \
   CPT_GEMM_INST_WGLU(X)
-#define CPT_NT16_INST_STORE(X) X(EPI_STORE, 0, 0)
+#define CPT_NT16_INST_STORE(X)                                               \
+  X(true, true, EPI_STORE, 0, 0) X(true, false, EPI_STORE, 0, 0)             \
+  X(false, false, EPI_STORE, 0, 0) X(false, true, EPI_STORE, 0, 0)
 #define CPT_NT16_INST_GLU_A(X)                                               \
-  X(EPI_GLU, CACHE_NONE, 64) X(EPI_GLU, CACHE_BF16, 64) X(EPI_GLU, CACHE_INT4, 32) \
-  X(EPI_GLU, CACHE_INT4, 64) X(EPI_GLU, CACHE_INT4, 128)
+  X(true, true, EPI_GLU, CACHE_NONE, 64) X(true, true, EPI_GLU, CACHE_BF16, 64) \
+  X(true, true, EPI_GLU, CACHE_INT4, 32) X(true, true, EPI_GLU, CACHE_INT4, 64) \
+  X(true, true, EPI_GLU, CACHE_INT4, 128)
 #define CPT_NT16_INST_GLU_B(X)                                               \
-  X(EPI_GLU, CACHE_INT8, 32) X(EPI_GLU, CACHE_INT8, 64) X(EPI_GLU, CACHE_INT8, 128)
+  X(true, true, EPI_GLU, CACHE_INT8, 32) X(true, true, EPI_GLU, CACHE_INT8, 64) \
+  X(true, true, EPI_GLU, CACHE_INT8, 128)
 #define CPT_NT16_INST_ALL(X) CPT_NT16_INST_STORE(X) CPT_NT16_INST_GLU_A(X) CPT_NT16_INST_GLU_B(X)
-#define CPT_NT16_DEFINE(EPI, CACHE, GS) template int launch_nt16<EPI, CACHE, GS>(const KArgs&, hipStream_t);
-#define CPT_NT16_DECLARE(EPI, CACHE, GS) \
-  extern template int launch_nt16<EPI, CACHE, GS>(const KArgs&, hipStream_t);
+#define CPT_NT16_DEFINE(AK, BK, EPI, CACHE, GS) \
+  template int launch_nt16<AK, BK, EPI, CACHE, GS>(const KArgs&, hipStream_t);
+#define CPT_NT16_DECLARE(AK, BK, EPI, CACHE, GS) \
+  extern template int launch_nt16<AK, BK, EPI, CACHE, GS>(const KArgs&, hipStream_t);
 #define CPT_GEMM_DEFINE(AK, BKM, EPI, CACHE, GS, LT) \
   template int launch<AK, BKM, EPI, CACHE, GS, LT>(KArgs&, hipStream_t);
 #define CPT_GEMM_DECLARE(AK, BKM, EPI, CACHE, GS, LT) \

@@ -74,21 +74,49 @@ def test_mm_deterministic_and_k_tail(device):
 # K >= 1024 to split-K instead): one k-tile, two (the prologue's pair only),
 # odd tile counts, a last group of fewer than 4 tile rows (M 2560), and
 # operands whose rows are longer than K (sub-views of wider tensors).
+@pytest.mark.parametrize("ak", [True, False])
+@pytest.mark.parametrize("bk", [True, False])
 @pytest.mark.parametrize("m,n,k,pad", [(256, 256, 64, 0), (256, 512, 128, 0), (768, 256, 192, 8),
                                        (2560, 2304, 960, 0), (4096, 2048, 4096, 64)])
-def test_mm_nt16_loop(device, m, n, k, pad):
+def test_mm_nt16_loop(device, ak, bk, m, n, k, pad):
+    """Every operand layout (K-major: rows of K; MN-major: rows of M or N,
+    transposing LDS reads); pad > 0 makes rows longer than their extent."""
     _, G = _cpt()
-    a = rnd((m, k + pad), 40, device)[:, :k]
-    w = rnd((n, k + pad), 41, device, 0.05)[:, :k]
-    got = G.linear(a, w)
-    assert_gemm_close(got, ref_mm(a, w.t()))
-    assert torch.equal(got, G.linear(a, w))
+    a = rnd((m, k + pad), 40, device)[:, :k] if ak else rnd((k, m + pad), 40, device)[:, :m].t()
+    b = rnd((n, k + pad), 41, device, 0.05)[:, :k].t() if bk else \
+        rnd((k, n + pad), 41, device, 0.05)[:, :n]
+    got = G.mm(a, b)
+    assert_gemm_close(got, ref_mm(a, b))
+    assert torch.equal(got, G.mm(a, b))
     # the engine's product of the same operands: same bf16 rounding of an
     # fp32 sum in another order, so all but a few elements agree exactly
-    eng = G.mm_engine(a, w.t())
-    assert_gemm_close(eng, ref_mm(a, w.t()))
+    eng = G.mm_engine(a, b)
+    assert_gemm_close(eng, ref_mm(a, b))
     diff = (got.view(torch.int16) != eng.view(torch.int16)).float().mean().item()
     assert diff < 0.05, diff
+
+
+@pytest.mark.parametrize("ak,bk", [(True, False), (True, True), (False, False)])
+@pytest.mark.parametrize("k1,k2", [(64, 64), (192, 320), (1024, 2048)])
+def test_mm2_nt16_two_pairs(device, ak, bk, k1, k2):
+    """A K-concatenated pair (dg W_g + du W_u) on the 16x16x32 loop: the
+    k-tiles switch operand pairs at k1, and the sum is one fp32 accumulation."""
+    _, G = _cpt()
+    m, n = 512, 768
+
+    def op_a(k, seed):
+        return rnd((m, k), seed, device) if ak else rnd((k, m), seed, device).t()
+
+    def op_b(k, seed):
+        return rnd((n, k), seed, device, 0.05).t() if bk else rnd((k, n), seed, device, 0.05)
+
+    a, b, a2, b2 = op_a(k1, 50), op_b(k1, 51), op_a(k2, 52), op_b(k2, 53)
+    got = G.mm2(a, b, a2, b2)
+    ref = ref_mm(a, b) + ref_mm(a2, b2)
+    assert_gemm_close(got, ref)
+    # the same sum as one product over the concatenated K
+    cat = G.mm2(torch.cat([a, a2], 1), torch.cat([b, b2], 0))
+    assert torch.equal(got.view(torch.int16), cat.view(torch.int16))
 
 
 def plain_like_f1(G, x, w):
@@ -154,12 +182,12 @@ def test_down_dgrad_fused_equals_unfused(device, cache, bits, group, want_h_mid,
     if bits:
         _, qg, sg, qu, su = cpt.silu_mul_quant(hg, hu, bits, group)
         dg, du, hm = G.ffn_down_dgrad(gy, wd, code, group, qg, sg, qu, su, want_h_mid)
-        gmid = G.mm(gy, wd)
+        gmid = G.mm_engine(gy, wd)   # B1 runs on the engine
         rdg, rdu, rhm = cpt.dequant_swiglu_backward(gmid, qg, sg, qu, su, bits, group,
                                                     want_h_mid=want_h_mid)
     else:
         dg, du, hm = G.ffn_down_dgrad(gy, wd, code, group, hg, None, hu, None, want_h_mid)
-        gmid = G.mm(gy, wd)
+        gmid = G.mm_engine(gy, wd)   # B1 runs on the engine
         rdg, rdu, rhm = cpt.swiglu_backward_glu(gmid, hg, hu, want_h_mid)
     assert_gemm_close(gmid, ref_mm(gy, wd))
     assert torch.equal(dg.view(torch.int16), rdg.view(torch.int16))
