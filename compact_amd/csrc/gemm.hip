@@ -253,23 +253,31 @@ int gemm_bf16_impl(const void* a, int64_t lda, int a_kmajor, const void* b, int6
   int terms = 0;
   if (const int rc = set_lora(A, L, M, N, terms)) return rc;
   hipStream_t st = (hipStream_t)stream;
+  // whole 256 x 256 tiles, K of each pair a multiple of 64: the 16x16x32 loop
+  // (another fp32 summation order than the engine's; cpt_gemm_bf16_ex mode 0
+  // keeps the engine's)
+  const bool nt16 =
+      nt16_fits(M, N, K, c, ldc) && (!two || (K2 > 0 && K2 % 64 == 0 && K2 <= 0x7FFFFFFF));
   if (terms) {
     // adapter terms are carried by the layouts that need them: K-major A
     if (!a_kmajor) return kErrShape;
+    if (nt16 && terms == 1)
+      return b_kmajor ? launch_nt16<true, true, EPI_STORE, 0, 0, 1>(A, st)
+                      : launch_nt16<true, false, EPI_STORE, 0, 0, 1>(A, st);
+    if (nt16)
+      return b_kmajor ? launch_nt16<true, true, EPI_STORE, 0, 0, 2>(A, st)
+                      : launch_nt16<true, false, EPI_STORE, 0, 0, 2>(A, st);
     if (terms == 1)
       return b_kmajor ? launch<true, true, EPI_STORE, 0, 0, 1>(A, st)
                       : launch<true, false, EPI_STORE, 0, 0, 1>(A, st);
     return b_kmajor ? launch<true, true, EPI_STORE, 0, 0, 2>(A, st)
                     : launch<true, false, EPI_STORE, 0, 0, 2>(A, st);
   }
-  // whole 256 x 256 tiles, K of each pair a multiple of 64: the 16x16x32 loop
-  // (another fp32 summation order than the engine's; cpt_gemm_bf16_ex mode 0
-  // keeps the engine's)
-  if (nt16_fits(M, N, K, c, ldc) && (!two || (K2 > 0 && K2 % 64 == 0 && K2 <= 0x7FFFFFFF))) {
-    if (a_kmajor && b_kmajor) return launch_nt16<true, true, EPI_STORE, 0, 0>(A, st);
-    if (a_kmajor && !b_kmajor) return launch_nt16<true, false, EPI_STORE, 0, 0>(A, st);
-    if (!a_kmajor && !b_kmajor) return launch_nt16<false, false, EPI_STORE, 0, 0>(A, st);
-    return launch_nt16<false, true, EPI_STORE, 0, 0>(A, st);
+  if (nt16) {
+    if (a_kmajor && b_kmajor) return launch_nt16<true, true, EPI_STORE, 0, 0, 0>(A, st);
+    if (a_kmajor && !b_kmajor) return launch_nt16<true, false, EPI_STORE, 0, 0, 0>(A, st);
+    if (!a_kmajor && !b_kmajor) return launch_nt16<false, false, EPI_STORE, 0, 0, 0>(A, st);
+    return launch_nt16<false, true, EPI_STORE, 0, 0, 0>(A, st);
   }
   if (a_kmajor && b_kmajor) return launch<true, true, EPI_STORE, 0, 0>(A, st);
   if (a_kmajor && !b_kmajor) return launch<true, false, EPI_STORE, 0, 0>(A, st);
@@ -332,22 +340,26 @@ int ffn_gate_up_impl(const void* x, const void* w_gate, const void* w_up, int64_
   int terms = 0;
   if (const int rc = set_lora(A, L, n_tok, inter, terms)) return rc;
   hipStream_t st = (hipStream_t)stream;
-  // whole 256-token x 128-column tiles without adapter terms: the 16x16x32
-  // loop (its summation order is that of cpt_gemm_bf16's NT products on whole
-  // tiles, not of cpt_gemm_bf16_ex mode 0)
-  if (!terms && ffn_nt16_fits(n_tok, inter, hidden)) {
+  // whole 256-token x 128-column tiles: the 16x16x32 loop (its summation
+  // order is that of cpt_gemm_bf16's products on whole tiles, not of
+  // cpt_gemm_bf16_ex mode 0); the dual kernel carries both adapter terms
+  if (ffn_nt16_fits(n_tok, inter, hidden)) {
+#define CPT_F1_NT16(CACHE, GS) \
+  (terms ? launch_nt16<true, true, EPI_GLU, CACHE, GS, 2>(A, st) \
+         : launch_nt16<true, true, EPI_GLU, CACHE, GS, 0>(A, st))
     switch (cache) {
-      case CACHE_NONE: return launch_nt16<true, true, EPI_GLU, CACHE_NONE, 64>(A, st);
-      case CACHE_BF16: return launch_nt16<true, true, EPI_GLU, CACHE_BF16, 64>(A, st);
+      case CACHE_NONE: return CPT_F1_NT16(CACHE_NONE, 64);
+      case CACHE_BF16: return CPT_F1_NT16(CACHE_BF16, 64);
       case CACHE_INT4:
-        return group_size == 32   ? launch_nt16<true, true, EPI_GLU, CACHE_INT4, 32>(A, st)
-               : group_size == 64 ? launch_nt16<true, true, EPI_GLU, CACHE_INT4, 64>(A, st)
-                                  : launch_nt16<true, true, EPI_GLU, CACHE_INT4, 128>(A, st);
+        return group_size == 32   ? CPT_F1_NT16(CACHE_INT4, 32)
+               : group_size == 64 ? CPT_F1_NT16(CACHE_INT4, 64)
+                                  : CPT_F1_NT16(CACHE_INT4, 128);
       default:
-        return group_size == 32   ? launch_nt16<true, true, EPI_GLU, CACHE_INT8, 32>(A, st)
-               : group_size == 64 ? launch_nt16<true, true, EPI_GLU, CACHE_INT8, 64>(A, st)
-                                  : launch_nt16<true, true, EPI_GLU, CACHE_INT8, 128>(A, st);
+        return group_size == 32   ? CPT_F1_NT16(CACHE_INT8, 32)
+               : group_size == 64 ? CPT_F1_NT16(CACHE_INT8, 64)
+                                  : CPT_F1_NT16(CACHE_INT8, 128);
     }
+#undef CPT_F1_NT16
   }
   // the dual kernel carries both terms (gate, up); an absent one is a no-op
   switch (cache) {

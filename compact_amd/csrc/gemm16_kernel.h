@@ -7,8 +7,9 @@
 //   EPI_GLU    F1 (x . [W_gate; W_up]^T, the GLU and the cache codec of
 //              glu_finish) when M is a multiple of 256, d_ff of 128, K of 64
 //              and no adapter terms ride in the epilogue.
-// Every other product runs on the 32x32x16 engine in gemm_kernel.h.  The
-// instantiations live in gemm16*.hip.
+// Adapter terms (LT = 1, 2) are added in either epilogue.  Every other product
+// runs on the 32x32x16 engine in gemm_kernel.h.  The instantiations live in
+// gemm16*.hip.
 //
 // Why a second main loop.  At the 1400 W board limit the MFMA work per joule
 // sets the rate: 16x16x32 spends 0.63 pJ per FLOP against 0.71 for 32x32x16
@@ -127,8 +128,92 @@ __device__ __forceinline__ void load_lds(const i32x4& r, uint16_t* dst, uint32_t
 // pass touches each of the 64 banks once.
 __device__ __forceinline__ int mn_swz(int k) { return 2 * ((k & 3) | ((k & 8) >> 1)); }
 
-template <bool AK, bool BK, int EPI, int CACHE, int GS>
+// ---------------------------------------------------------------------------
+// Adapter (LoRA) terms in the epilogue: out = bf16(bf16(acc) + bf16(alpha *
+// bf16(P_t Q_t^T))) per term, PEFT's order.  The rank-sized product of each
+// 16 x 16 block is one v_mfma_f32_16x16x16_bf16: lane l supplies k
+// 4 (l / 16) .. + 3 of row l % 16 of a block (Q for the n side, P for the m
+// side); k past the rank, rows past an operand's end and an absent term's null
+// P read zero through the buffer range check.  An absent term also has
+// alpha = -0.0, and x + bf16(-0.0 * 0) == x for every x: no branch.
+// ---------------------------------------------------------------------------
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ s16x4 lora4_km(__amdgpu_buffer_rsrc_t rs, int64_t ld, int64_t row, int r,
+                                          int lane) {
+  const int k0 = (lane >> 4) * 4;
+  const uint32_t off = k0 < r ? (uint32_t)((row * ld + k0) * 2) : kOOB;
+  return __builtin_bit_cast(s16x4, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
+}
+
+// Q stored [r][ld] (n contiguous): 4 k of column n, one 2-byte load each
+__device__ __forceinline__ s16x4 lora4_mn(__amdgpu_buffer_rsrc_t rs, int64_t ld, int64_t n, int r,
+                                          int lane) {
+  const int k0 = (lane >> 4) * 4;
+  s16x4 v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t off = k0 + e < r ? (uint32_t)(((int64_t)(k0 + e) * ld + n) * 2) : kOOB;
+    v[e] = (short)__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+  }
+  return v;
+}
+
+// One wave's adapter fragments: p[t][j] the m-side rows of P_t (block j),
+// q[t][i] the n-side rows of Q_t (block i; DUAL: term t's blocks only, gate
+// i < 4 and up i >= 4).
+struct Lora16 {
+  s16x4 p[2][8];
+  s16x4 q[2][8];
+};
+
+template <bool DUAL, int LT>
+__device__ __forceinline__ void lora16_load(const KArgs& A, int64_t m0, int64_t n0, int wm, int wn,
+                                            int lane, Lora16& F) {
+  const int r = A.lrank;
+#pragma unroll
+  for (int t = 0; t < LT; ++t) {
+    const __amdgpu_buffer_rsrc_t rp = make_rsrc(A.lp[t], A.lp[t] ? A.M * A.lldp * 2 : 0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      F.p[t][j] = lora4_km(rp, A.lldp, m0 + wm * 128 + 16 * j + (lane & 15), r, lane);
+    if constexpr (DUAL) {
+      const __amdgpu_buffer_rsrc_t rq = make_rsrc(A.lq[t], A.lq[t] ? A.D * r * 2 : 0);
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii)
+        F.q[t][4 * t + ii] = lora4_km(rq, r, (n0 >> 1) + wn * 64 + 16 * ii + (lane & 15), r, lane);
+    } else {
+      const int64_t qbytes = A.lq_km ? A.N * r * 2 : (int64_t)r * A.lldq * 2;
+      const __amdgpu_buffer_rsrc_t rq = make_rsrc(A.lq[t], qbytes);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int64_t n = n0 + wn * 128 + 16 * i + (lane & 15);
+        F.q[t][i] = A.lq_km ? lora4_km(rq, r, n, r, lane) : lora4_mn(rq, A.lldq, n, r, lane);
+      }
+    }
+  }
+}
+
+// accumulator block (i, j) with the kernel's LT adapter terms applied
+template <bool DUAL, int LT>
+__device__ __forceinline__ f32x4 acc16(const KArgs& A, const f32x4& a, const Lora16& F, int i,
+                                       int j) {
+  f32x4 v = a;
+#pragma unroll
+  for (int t = 0; t < LT; ++t) {
+    if (DUAL && (i >> 2) != t) continue;
+    const f32x4 l = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(F.q[t][i], F.p[t][j],
+                                                             f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      v[r] = round_bf16(round_bf16(v[r]) + round_bf16(A.lalpha[t] * round_bf16(l[r])));
+  }
+  return v;
+}
+
+template <bool AK, bool BK, int EPI, int CACHE, int GS, int LT>
 __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
+  static_assert(LT == 0 || AK, "adapter terms ride with a K-major A (P's rows are tokens)");
   static_assert(EPI == EPI_STORE || EPI == EPI_GLU, "epilogues of the 16x16x32 loop");
   constexpr bool DUAL = EPI == EPI_GLU;
   static_assert(!DUAL || (AK && BK), "F1's operands are K-major");
@@ -290,6 +375,8 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
 
   // lane holds tile column (n side) 128 wn + 16 i + 4 (lane / 16) + 0..3 of
   // tile row (m side) 128 wm + 16 j + lane % 16 in acc[i][j]
+  Lora16 F;
+  if constexpr (LT > 0) lora16_load<DUAL, LT>(A, m0, n0, wm, wn, lane, F);
   if constexpr (EPI == EPI_STORE) {
     // bf16(acc) is staged as a row-major tile (rows kLdOut apart: 32 lanes of
     // one 8-byte write cover the 64 banks once), then 32 threads store each
@@ -300,8 +387,9 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
       for (int j = 0; j < 8; ++j) {
         const int ml = wm * 128 + 16 * j + (lane & 15);
         const int nl = wn * 128 + 16 * i + 4 * (lane >> 4);
+        const f32x4 v = LT > 0 ? acc16<false, LT>(A, acc[i][j], F, i, j) : acc[i][j];
         *reinterpret_cast<uint2*>(lds + ml * kLdOut + nl) =
-            make_uint2(pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3]));
+            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
       }
     __syncthreads();
     const int cl = (tid & 31) * 8;
@@ -323,8 +411,9 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
       for (int j = 0; j < 8; ++j) {
         const int ml = wm * 128 + 16 * j + (lane & 15);
         const int dl = wn * 64 + 16 * (i & 3) + 4 * (lane >> 4);
+        const f32x4 v = LT > 0 ? acc16<true, LT>(A, acc[i][j], F, i, j) : acc[i][j];
         *reinterpret_cast<uint2*>((i < 4 ? sg : su) + ml * kGluLd + dl) =
-            make_uint2(pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3]));
+            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
       }
     __syncthreads();
     glu_finish<CACHE, GS>(A, m0, n0, lds);
@@ -333,9 +422,9 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
 
 }  // namespace nt16
 
-template <bool AK, bool BK, int EPI, int CACHE, int GS>
+template <bool AK, bool BK, int EPI, int CACHE, int GS, int LT>
 int launch_nt16(const KArgs& A, hipStream_t st) {
-  auto kern = nt16::nt16_kernel<AK, BK, EPI, CACHE, GS>;
+  auto kern = nt16::nt16_kernel<AK, BK, EPI, CACHE, GS, LT>;
   static bool attr_set = false;   // per instantiation
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,

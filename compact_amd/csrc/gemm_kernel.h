@@ -1176,12 +1176,12 @@ int launch(KArgs& A, hipStream_t st) {
 }
 
 // Products on the 16x16x32 direct-to-LDS main loop (gemm16_kernel.h), K of
-// each pair a multiple of 64, no adapter terms: EPI_STORE in every operand
-// layout with M, N multiples of 256 and C rows 16-byte aligned (nt16_fits);
-// EPI_GLU (F1, both operands K-major, one pair) with M a multiple of 256 and
-// d_ff of 128.
+// each pair a multiple of 64, adapter terms (LT) with a K-major A: EPI_STORE
+// in every operand layout with M, N multiples of 256 and C rows 16-byte
+// aligned (nt16_fits); EPI_GLU (F1, both operands K-major, one pair) with M a
+// multiple of 256 and d_ff of 128.
 bool nt16_fits(int64_t M, int64_t N, int64_t K, const void* c, int64_t ldc);
-template <bool AK, bool BK, int EPI, int CACHE, int GS>
+template <bool AK, bool BK, int EPI, int CACHE, int GS, int LT>
 int launch_nt16(const KArgs& A, hipStream_t st);
 
 // ---------------------------------------------------------------------------
@@ -1227,20 +1227,27 @@ int launch_nt16(const KArgs& A, hipStream_t st);
   CPT_GEMM_INST_GLU_B(X) CPT_GEMM_INST_DGLU_A(X) CPT_GEMM_INST_DGLU_B(X)     \
   CPT_GEMM_INST_WGLU(X)
 #define CPT_NT16_INST_STORE(X)                                               \
-  X(true, true, EPI_STORE, 0, 0) X(true, false, EPI_STORE, 0, 0)             \
-  X(false, false, EPI_STORE, 0, 0) X(false, true, EPI_STORE, 0, 0)
+  X(true, true, EPI_STORE, 0, 0, 0) X(true, false, EPI_STORE, 0, 0, 0)       \
+  X(false, false, EPI_STORE, 0, 0, 0) X(false, true, EPI_STORE, 0, 0, 0)     \
+  X(true, true, EPI_STORE, 0, 0, 1) X(true, false, EPI_STORE, 0, 0, 1)       \
+  X(true, true, EPI_STORE, 0, 0, 2) X(true, false, EPI_STORE, 0, 0, 2)
 #define CPT_NT16_INST_GLU_A(X)                                               \
-  X(true, true, EPI_GLU, CACHE_NONE, 64) X(true, true, EPI_GLU, CACHE_BF16, 64) \
-  X(true, true, EPI_GLU, CACHE_INT4, 32) X(true, true, EPI_GLU, CACHE_INT4, 64) \
-  X(true, true, EPI_GLU, CACHE_INT4, 128)
+  X(true, true, EPI_GLU, CACHE_NONE, 64, 0) X(true, true, EPI_GLU, CACHE_NONE, 64, 2) \
+  X(true, true, EPI_GLU, CACHE_BF16, 64, 0) X(true, true, EPI_GLU, CACHE_BF16, 64, 2)
 #define CPT_NT16_INST_GLU_B(X)                                               \
-  X(true, true, EPI_GLU, CACHE_INT8, 32) X(true, true, EPI_GLU, CACHE_INT8, 64) \
-  X(true, true, EPI_GLU, CACHE_INT8, 128)
-#define CPT_NT16_INST_ALL(X) CPT_NT16_INST_STORE(X) CPT_NT16_INST_GLU_A(X) CPT_NT16_INST_GLU_B(X)
-#define CPT_NT16_DEFINE(AK, BK, EPI, CACHE, GS) \
-  template int launch_nt16<AK, BK, EPI, CACHE, GS>(const KArgs&, hipStream_t);
-#define CPT_NT16_DECLARE(AK, BK, EPI, CACHE, GS) \
-  extern template int launch_nt16<AK, BK, EPI, CACHE, GS>(const KArgs&, hipStream_t);
+  X(true, true, EPI_GLU, CACHE_INT8, 32, 0) X(true, true, EPI_GLU, CACHE_INT8, 32, 2) \
+  X(true, true, EPI_GLU, CACHE_INT8, 64, 0) X(true, true, EPI_GLU, CACHE_INT8, 64, 2) \
+  X(true, true, EPI_GLU, CACHE_INT8, 128, 0) X(true, true, EPI_GLU, CACHE_INT8, 128, 2)
+#define CPT_NT16_INST_GLU_C(X)                                               \
+  X(true, true, EPI_GLU, CACHE_INT4, 32, 0) X(true, true, EPI_GLU, CACHE_INT4, 32, 2) \
+  X(true, true, EPI_GLU, CACHE_INT4, 64, 0) X(true, true, EPI_GLU, CACHE_INT4, 64, 2) \
+  X(true, true, EPI_GLU, CACHE_INT4, 128, 0) X(true, true, EPI_GLU, CACHE_INT4, 128, 2)
+#define CPT_NT16_INST_ALL(X)                                                 \
+  CPT_NT16_INST_STORE(X) CPT_NT16_INST_GLU_A(X) CPT_NT16_INST_GLU_B(X) CPT_NT16_INST_GLU_C(X)
+#define CPT_NT16_DEFINE(AK, BK, EPI, CACHE, GS, LT) \
+  template int launch_nt16<AK, BK, EPI, CACHE, GS, LT>(const KArgs&, hipStream_t);
+#define CPT_NT16_DECLARE(AK, BK, EPI, CACHE, GS, LT) \
+  extern template int launch_nt16<AK, BK, EPI, CACHE, GS, LT>(const KArgs&, hipStream_t);
 #define CPT_GEMM_DEFINE(AK, BKM, EPI, CACHE, GS, LT) \
   template int launch<AK, BKM, EPI, CACHE, GS, LT>(KArgs&, hipStream_t);
 #define CPT_GEMM_DECLARE(AK, BKM, EPI, CACHE, GS, LT) \

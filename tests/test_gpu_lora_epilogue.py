@@ -50,9 +50,10 @@ def bits16(t):
 @pytest.mark.parametrize("bk", [True, False])
 @pytest.mark.parametrize("q_kmajor", [True, False])
 @pytest.mark.parametrize("nterms", [1, 2])
-def test_mm2_lora_terms(device, rank, bk, q_kmajor, nterms):
+@pytest.mark.parametrize("mnk", [(300, 264, 136), (512, 768, 128)])   # engine, 16x16x32 loop
+def test_mm2_lora_terms(device, rank, bk, q_kmajor, nterms, mnk):
     _, G, _ = _cpt()
-    m, n, k = 300, 264, 136
+    m, n, k = mnk
     a = rnd((m, k), 1, device)
     b = rnd((n, k), 2, device).t() if bk else rnd((k, n), 2, device)
     terms = []
@@ -74,15 +75,34 @@ def test_mm2_lora_terms(device, rank, bk, q_kmajor, nterms):
     assert diff.float().mean().item() < 1e-3, int(diff.sum())
 
 
+def plain_like_f1(G, x, w):
+    """x . w^T in the summation order of F1: the 16x16x32 loop on whole
+    256-token x 128-column tiles (ffn_nt16_fits in gemm.hip), else the
+    engine.  The plain product reaches that loop on whole 256 x 256 tiles:
+    zero rows pad w (the other columns' sums are unchanged)."""
+    n, k = x.shape
+    d = w.shape[0]
+    if n % 256 == 0 and d % 128 == 0 and k % 64 == 0:
+        dp = -(-d // 256) * 256
+        assert k < 1024 or (n // 256) * (dp // 256) >= 128, "mm would split K"
+        wp = torch.nn.functional.pad(w, (0, 0, 0, dp - d))
+        return G.linear(x, wp)[:, :d].contiguous()
+    return G.mm_engine(x, w.t())
+
+
 @pytest.mark.parametrize("cache,bits,group", [("int4", 4, 64), ("int8", 8, 128), ("bf16", 0, 64),
                                               ("none", 0, 64)])
 @pytest.mark.parametrize("which", ["both", "gate", "up"])
 @pytest.mark.parametrize("rank", [8, 16])
-def test_gate_up_lora_fused_equals_composed(device, cache, bits, group, which, rank):
+@pytest.mark.parametrize("n_tok,hid,inter", [(300, 128, 384), (512, 128, 512)])
+def test_gate_up_lora_fused_equals_composed(device, cache, bits, group, which, rank, n_tok, hid,
+                                            inter):
+    """F1 with adapter terms equals the plain product of the same main loop
+    (the engine for 300 tokens, the 16x16x32 loop for 512) with the same
+    terms, then K1, bit for bit."""
     cpt, G, _lib = _cpt()
     code = {"int4": _lib.CACHE_INT4, "int8": _lib.CACHE_INT8, "bf16": _lib.CACHE_BF16,
             "none": _lib.CACHE_NONE}[cache]
-    n_tok, hid, inter = 300, 128, 384
     x = rnd((n_tok, hid), 30, device)
     wg, wu = rnd((inter, hid), 31, device, 0.05), rnd((inter, hid), 32, device, 0.05)
     xa_g, xa_u = rnd((n_tok, rank), 33, device), rnd((n_tok, rank), 34, device)
@@ -90,8 +110,8 @@ def test_gate_up_lora_fused_equals_composed(device, cache, bits, group, which, r
     lg = (xa_g, bg, 2.0) if which in ("both", "gate") else None
     lu = (xa_u, bu, 2.0) if which in ("both", "up") else None
     hm, hg, hu, qg, sg, qu, su = G.ffn_gate_up(x, wg, wu, code, group, lora_gate=lg, lora_up=lu)
-    hg_ref = G.mm2(x, wg.t(), lora=[(xa_g, bg.t(), 2.0)]) if lg else G.mm_engine(x, wg.t())
-    hu_ref = G.mm2(x, wu.t(), lora=[(xa_u, bu.t(), 2.0)]) if lu else G.mm_engine(x, wu.t())
+    hg_ref = G.mm2(x, wg.t(), lora=[(xa_g, bg.t(), 2.0)]) if lg else plain_like_f1(G, x, wg)
+    hu_ref = G.mm2(x, wu.t(), lora=[(xa_u, bu.t(), 2.0)]) if lu else plain_like_f1(G, x, wu)
     assert torch.equal(bits16(hm), bits16(cpt.silu_mul(hg_ref, hu_ref)))
     if cache == "bf16":
         assert torch.equal(bits16(hg), bits16(hg_ref))
