@@ -80,7 +80,7 @@ def test_measured_traffic_reads_profiles():
     # the committed HBM-traffic summary carries the figure bench.py reports;
     # a pair no summary covers gives None
     assert bench.measured_traffic("ffn_gate_up", "c2") == 2573700000
-    assert bench.measured_traffic("ffn_gate_up", "c3") == 2554300000
+    assert bench.measured_traffic("ffn_gate_up", "c3") == 2554500000
     assert bench.measured_traffic("ffn_gate_up", "no_such_workload") is None
 
 
