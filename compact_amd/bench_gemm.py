@@ -1,6 +1,7 @@
-"""Per-GEMM comparison on the C2 FFN shapes: this build's MFMA engine (and
-its fused FlashFFN kernels) against the library GEMM torch calls (hipBLASLt)
-with the standalone codec kernels.
+"""Per-GEMM comparison on the C2 FFN shapes: this build's dispatch (the
+16x16x32 loop at these shapes, with its fused FlashFFN kernels), the 32x32x16
+engine where a plain product can be forced onto it, and the library GEMM torch
+calls (hipBLASLt) with the standalone codec kernels.
 
     python -m compact_amd.bench_gemm [--iters 20] [--json out.json]
 
@@ -56,20 +57,30 @@ def main():
     def lib_dgrad():
         return K.dequant_swiglu_backward(gy @ wd, qg, sg, qu, su, 8, gs, want_h_mid=True)
 
+    # arms: this build's dispatch (the 16x16x32 loop at these shapes), the
+    # 32x32x16 engine where one plain product can be forced onto it
+    # (gemm.mm_engine), and hipBLASLt (+ the standalone codec kernels)
     cases = [
-        ("fwd gate/up + GLU + int8 codec", lambda: G.ffn_gate_up(x, wg, wu, 8, gs), lib_gate_up, 2 * fl),
-        ("fwd down  h_mid @ Wd^T", lambda: G.linear(hm, wd), lambda: hm @ wd.t(), fl),
-        ("bwd gy @ Wd + dequant + SwiGLU bwd", lambda: G.ffn_down_dgrad(gy, wd, 8, gs, qg, sg, qu, su, True), lib_dgrad, fl),
-        ("bwd dWd = gy^T @ h_mid", lambda: G.mm(gy.t(), hm), lambda: gy.t() @ hm, fl),
-        ("bwd dx = dg @ Wg + du @ Wu", lambda: G.mm2(hm, wg, hm, wu), lambda: hm @ wg + hm @ wu, 2 * fl),
-        ("bwd dWg = dg^T @ x", lambda: G.mm(hm.t(), x), lambda: hm.t() @ x, fl),
+        ("fwd gate/up + GLU + int8 codec", lambda: G.ffn_gate_up(x, wg, wu, 8, gs), None, lib_gate_up, 2 * fl),
+        ("fwd down  h_mid @ Wd^T", lambda: G.linear(hm, wd), lambda: G.mm_engine(hm, wd.t()),
+         lambda: hm @ wd.t(), fl),
+        ("bwd gy @ Wd + dequant + SwiGLU bwd", lambda: G.ffn_down_dgrad(gy, wd, 8, gs, qg, sg, qu, su, True),
+         None, lib_dgrad, fl),
+        ("bwd gy @ Wd", lambda: G.mm(gy, wd), lambda: G.mm_engine(gy, wd), lambda: gy @ wd, fl),
+        ("bwd dWd = gy^T @ h_mid", lambda: G.mm(gy.t(), hm), lambda: G.mm_engine(gy.t(), hm),
+         lambda: gy.t() @ hm, fl),
+        ("bwd dx = dg @ Wg + du @ Wu", lambda: G.mm2(hm, wg, hm, wu), None, lambda: hm @ wg + hm @ wu, 2 * fl),
+        ("bwd dWg = dg^T @ x", lambda: G.mm(hm.t(), x), lambda: G.mm_engine(hm.t(), x), lambda: hm.t() @ x, fl),
     ]
     out = {}
-    for name, mine, lib, flops in cases:
+    for name, mine, eng, lib, flops in cases:
         a, b = _time(mine, args.iters), _time(lib, args.iters)
-        out[name] = {"engine_ms": a, "library_ms": b, "engine_tflops": flops / a / 1e9,
+        e = _time(eng, args.iters) if eng is not None else None
+        out[name] = {"build_ms": a, "engine_ms": e, "library_ms": b, "build_tflops": flops / a / 1e9,
+                     "engine_tflops": flops / e / 1e9 if e else None,
                      "library_tflops": flops / b / 1e9}
-        print(f"{name:38s} engine {a:7.3f} ms {flops / a / 1e9:7.1f} TF/s | "
+        es = f"engine {e:7.3f} ms {flops / e / 1e9:7.1f} TF/s" if e else f"{'engine -':30s}"
+        print(f"{name:38s} build {a:7.3f} ms {flops / a / 1e9:7.1f} TF/s | {es} | "
               f"library {b:7.3f} ms {flops / b / 1e9:7.1f} TF/s", flush=True)
     # The down projection's weight gradient, both routes of this build: K2
     # writing h_mid^ and the plain TN GEMM, against K2 without h_mid^ and the

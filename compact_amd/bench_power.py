@@ -3,8 +3,9 @@
     python -m compact_amd.bench_power [--secs 3]
 
 Runs every GEMM of a C2 fwd+bwd step (8192 tokens, d_model 4096, d_ff 11008,
-bf16) on this build's engine and through torch's `@` (hipBLASLt), each in a
-loop for --secs seconds, while a thread reads the GPU's metrics table through
+bf16) on this build's dispatch (the 16x16x32 loop at these shapes), on the
+32x32x16 engine where one plain product can be forced onto it, and through
+torch's `@` (hipBLASLt), each in a loop for --secs seconds, while a thread reads the GPU's metrics table through
 amdsmi (read-only queries: socket power, current gfx clock) every 10 ms.
 The first two lines are the register-only MFMA probe (v_mfma_f32_32x32x16_bf16,
 then v_mfma_f32_16x16x32_bf16, on every SIMD, no memory traffic): the MFMA
@@ -130,18 +131,24 @@ def main():
         print(f"{'idle':40s} {'':>9s} {'':>12s} {pw:7.0f} W {ck:6.0f} MHz", flush=True)
     p32, p32_fl = mfma_probe(0)
     p16, p16_fl = mfma_probe(1)
+    # arms: this build's dispatch (the 16x16x32 loop at these shapes), the
+    # 32x32x16 engine for the single-pair products (gemm.mm_engine), hipBLASLt
     cases = [
-        ("MFMA 32x32x16 only, registers", p32, None, p32_fl),
-        ("MFMA 16x16x32 only, registers", p16, None, p16_fl),
-        ("NT x.Wg^T, K 4096", lambda: G.linear(x, wg), lambda: x @ wg.t(), fl),
-        ("NT h_mid.Wd^T, K 11008", lambda: G.linear(hm, wd), lambda: hm @ wd.t(), fl),
-        ("NN gy.Wd, K 4096", lambda: G.mm(gy, wd), lambda: gy @ wd, fl),
-        ("NN dg.Wg + du.Wu, K 2 x 11008", lambda: G.mm2(hm, wg, hm, wu), lambda: hm @ wg + hm @ wu, 2 * fl),
-        ("TN gy^T.h_mid, K 8192", lambda: G.mm(gy.t(), hm), lambda: gy.t() @ hm, fl),
-        ("F1 gate/up + GLU + int8 codec", lambda: G.ffn_gate_up(x, wg, wu, 8, 128), None, 2 * fl),
+        ("MFMA 32x32x16 only, registers", p32, None, None, p32_fl),
+        ("MFMA 16x16x32 only, registers", p16, None, None, p16_fl),
+        ("NT x.Wg^T, K 4096", lambda: G.linear(x, wg), lambda: G.mm_engine(x, wg.t()),
+         lambda: x @ wg.t(), fl),
+        ("NT h_mid.Wd^T, K 11008", lambda: G.linear(hm, wd), lambda: G.mm_engine(hm, wd.t()),
+         lambda: hm @ wd.t(), fl),
+        ("NN gy.Wd, K 4096", lambda: G.mm(gy, wd), lambda: G.mm_engine(gy, wd), lambda: gy @ wd, fl),
+        ("NN dg.Wg + du.Wu, K 2 x 11008", lambda: G.mm2(hm, wg, hm, wu), None,
+         lambda: hm @ wg + hm @ wu, 2 * fl),
+        ("TN gy^T.h_mid, K 8192", lambda: G.mm(gy.t(), hm), lambda: G.mm_engine(gy.t(), hm),
+         lambda: gy.t() @ hm, fl),
+        ("F1 gate/up + GLU + int8 codec", lambda: G.ffn_gate_up(x, wg, wu, 8, 128), None, None, 2 * fl),
     ]
-    for name, mine, lib, flops in cases:
-        for arm, fn in (("engine", mine), ("hipBLASLt", lib)):
+    for name, mine, eng, lib, flops in cases:
+        for arm, fn in (("build", mine), ("engine", eng), ("hipBLASLt", lib)):
             if fn is None:
                 continue
             ms, pw, ck = sustained(fn, args.secs, sampler)
