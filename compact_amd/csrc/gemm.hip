@@ -253,9 +253,9 @@ int gemm_bf16_impl(const void* a, int64_t lda, int a_kmajor, const void* b, int6
   int terms = 0;
   if (const int rc = set_lora(A, L, M, N, terms)) return rc;
   hipStream_t st = (hipStream_t)stream;
-  // whole 256 x 256 tiles, K of each pair a multiple of 64: the 16x16x32 loop
-  // (another fp32 summation order than the engine's; cpt_gemm_bf16_ex mode 0
-  // keeps the engine's)
+  // K of each pair a multiple of 64, N of 8: the 16x16x32 loop (another fp32
+  // summation order than the engine's; cpt_gemm_bf16_ex mode 0 keeps the
+  // engine's)
   const bool nt16 =
       nt16_fits(M, N, K, c, ldc) && (!two || (K2 > 0 && K2 % 64 == 0 && K2 <= 0x7FFFFFFF));
   if (terms) {
@@ -285,12 +285,13 @@ int gemm_bf16_impl(const void* a, int64_t lda, int a_kmajor, const void* b, int6
   return launch<false, true, EPI_STORE, 0, 0>(A, st);
 }
 
-// F1 on the 16x16x32 loop: whole 256-token x 128-column tiles, K of 64
+// F1 on the 16x16x32 loop: d_model a multiple of 64 (d_ff is one of 8 and
+// the token count free, as for the engine)
 inline bool ffn_nt16_fits(int64_t n_tok, int64_t inter, int64_t hidden) {
   constexpr int64_t kIntMax = 0x7FFFFFFF;
   return n_tok > 0 && inter > 0 && hidden > 0 && n_tok <= kIntMax && inter <= kIntMax &&
-         hidden <= kIntMax && n_tok % 256 == 0 && inter % 128 == 0 && hidden % 64 == 0 &&
-         (n_tok / 256) * (inter / 128) <= kIntMax;
+         hidden <= kIntMax && inter % 8 == 0 && hidden % 64 == 0 &&
+         ((n_tok + 255) / 256) * ((inter + 127) / 128) <= kIntMax;
 }
 
 int ffn_gate_up_impl(const void* x, const void* w_gate, const void* w_up, int64_t n_tok,
@@ -340,8 +341,8 @@ int ffn_gate_up_impl(const void* x, const void* w_gate, const void* w_up, int64_
   int terms = 0;
   if (const int rc = set_lora(A, L, n_tok, inter, terms)) return rc;
   hipStream_t st = (hipStream_t)stream;
-  // whole 256-token x 128-column tiles: the 16x16x32 loop (its summation
-  // order is that of cpt_gemm_bf16's products on whole tiles, not of
+  // d_model a multiple of 64: the 16x16x32 loop (its summation order is that
+  // of cpt_gemm_bf16's products with K a multiple of 64, not of
   // cpt_gemm_bf16_ex mode 0); the dual kernel carries both adapter terms
   if (ffn_nt16_fits(n_tok, inter, hidden)) {
 #define CPT_F1_NT16(CACHE, GS) \

@@ -1,12 +1,14 @@
 // NT bf16 GEMM on v_mfma_f32_16x16x32_bf16 with direct-to-LDS operand loads:
 //   C[M, N] = A[M, K] . B[N, K]^T, both operands K-major, fp32 accumulate.
 // Two epilogues:
-//   EPI_STORE  C = bf16(acc): the plain NT product of cpt_gemm_bf16 when M and
-//              N are multiples of 256 and K of 64 (the forward down
-//              projection h_mid . W_d^T and other nn.Linear products);
+//   EPI_STORE  C = bf16(acc): the plain products of cpt_gemm_bf16 in every
+//              operand layout (N a multiple of 8, K of 64);
 //   EPI_GLU    F1 (x . [W_gate; W_up]^T, the GLU and the cache codec of
-//              glu_finish) when M is a multiple of 256, d_ff of 128, K of 64
-//              and no adapter terms ride in the epilogue.
+//              glu_finish; d_ff a multiple of 8, K of 64).
+// M and N are free: the last tile row and column are masked at the store, and
+// operand loads past the edge read zeros through the buffer range check (rows
+// of a K-major operand past its end, 8-column chunks of an MN-major one past
+// its edge).
 // Adapter terms (LT = 1, 2) are added in either epilogue.  Every other product
 // runs on the 32x32x16 engine in gemm_kernel.h.  The instantiations live in
 // gemm16*.hip.
@@ -255,6 +257,10 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
   //            16-byte k chunk (l % 8) ^ (row & 6) (DUAL B: source row per block as above);
   //   MN-major: k-rows 2 q, 2 q + 1; lane l k-row 2 q + l / 32, mn chunk
   //            (l % 32) ^ mn_swz(k-row).
+  // Out of range is always decided by this VGPR offset, never by the
+  // soffset delta below (the raw-buffer range check covers the VGPR offset):
+  // K-major rows past the operand's end lie past num_records; MN-major
+  // 8-column chunks past the edge (M, N multiples of 8 there) get kOOB.
   uint32_t oa[8], ob[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
@@ -264,12 +270,16 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
     const int kr = 2 * q + (lane >> 5);
     const int cm = (lane & 31) ^ mn_swz(kr);
     const int rw = DUAL ? 64 * (i >> 2) + 8 * (4 * (i & 1) + wave) + (lane >> 3) : r;
-    oa[i] = AK ? (uint32_t)(((int64_t)r * lda + ck * 8) * 2) : (uint32_t)(((int64_t)kr * lda + cm * 8) * 2);
-    ob[i] = BK ? (uint32_t)(((int64_t)rw * ldb + ck * 8) * 2) : (uint32_t)(((int64_t)kr * ldb + cm * 8) * 2);
+    oa[i] = AK ? (uint32_t)(((int64_t)r * lda + ck * 8) * 2)
+               : m0 + cm * 8 < A.M ? (uint32_t)(((int64_t)kr * lda + cm * 8) * 2) : kOOB;
+    ob[i] = BK ? (uint32_t)(((int64_t)rw * ldb + ck * 8) * 2)
+               : n0 + cm * 8 < A.N ? (uint32_t)(((int64_t)kr * ldb + cm * 8) * 2) : kOOB;
   }
   // per k-tile: the pair's buffers and each operand's byte delta (k0 * 2 for a
-  // K-major operand, k0 * ld * 2 for an MN-major one); past the last tile a
-  // delta beyond num_records (the loads return zeros and read no memory)
+  // K-major operand, k0 * ld * 2 for an MN-major one), passed as soffset.  The
+  // two tiles the loop loads past the last one re-read the last tile (valid
+  // memory; their stage is never read): soffset is outside the range check,
+  // so an out-of-range delta there would be a real access.
   struct TileLd {
     i32x4 a, b;
     uint32_t da, db;
@@ -280,10 +290,10 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
   const uint32_t stepa = AK ? (uint32_t)(kBK * 2) : (uint32_t)(kBK * lda * 2);
   const uint32_t stepb = BK ? (uint32_t)(kBK * 2) : (uint32_t)(kBK * ldb * 2);
   auto tile = [&](int kt) -> TileLd {
-    const bool p1 = kt >= nk0;
-    const uint32_t lk = (uint32_t)(kt - (p1 ? nk0 : 0));
-    const bool in = kt < nk;
-    return TileLd{p1 ? ra1 : ra0, p1 ? rb1 : rb0, in ? lk * stepa : kOOB, in ? lk * stepb : kOOB};
+    const int kc = kt < nk ? kt : nk - 1;
+    const bool p1 = kc >= nk0;
+    const uint32_t lk = (uint32_t)(kc - (p1 ? nk0 : 0));
+    return TileLd{p1 ? ra1 : ra0, p1 ? rb1 : rb0, lk * stepa, lk * stepb};
   };
   // load p (0..15) of a tile into stage st: even p -> A block p / 2, odd -> B
   auto issue = [&](int p, int st, const TileLd& T) {
@@ -392,12 +402,15 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
             make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
       }
     __syncthreads();
+    // ragged M and N: rows past M and 8-column pieces past N (N % 8 == 0) stay
+    // unwritten; the operand loads read zeros or discarded values there
     const int cl = (tid & 31) * 8;
+    const bool nok = n0 + cl < A.N;
 #pragma unroll 4
     for (int p = 0; p < 32; ++p) {
       const int r = p * 8 + (tid >> 5);
       const uint4 w = *reinterpret_cast<const uint4*>(lds + r * kLdOut + cl);
-      *reinterpret_cast<uint4*>(A.C + (m0 + r) * A.ldc + n0 + cl) = w;
+      if (nok && m0 + r < A.M) *reinterpret_cast<uint4*>(A.C + (m0 + r) * A.ldc + n0 + cl) = w;
     }
   } else {
     // F1: blocks i < 4 are gate columns d = 64 wn + 16 i + ..., i >= 4 the

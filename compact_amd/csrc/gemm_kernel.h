@@ -1177,9 +1177,9 @@ int launch(KArgs& A, hipStream_t st) {
 
 // Products on the 16x16x32 direct-to-LDS main loop (gemm16_kernel.h), K of
 // each pair a multiple of 64, adapter terms (LT) with a K-major A: EPI_STORE
-// in every operand layout with M, N multiples of 256 and C rows 16-byte
-// aligned (nt16_fits); EPI_GLU (F1, both operands K-major, one pair) with M a
-// multiple of 256 and d_ff of 128.
+// in every operand layout with N a multiple of 8 and C rows 16-byte aligned
+// (nt16_fits); EPI_GLU (F1, both operands K-major, one pair).  M, N and d_ff
+// need not fill whole tiles.
 bool nt16_fits(int64_t M, int64_t N, int64_t K, const void* c, int64_t ldc);
 template <bool AK, bool BK, int EPI, int CACHE, int GS, int LT>
 int launch_nt16(const KArgs& A, hipStream_t st);

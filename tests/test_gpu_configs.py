@@ -136,13 +136,8 @@ def test_c2_full_size(device):
     # codes and scales of sampled rows, bit for bit
     rows = _rows(N7)
     rd = rows.to(device)
-    # the Function's F1 (8192 tokens, no adapter terms) ran on the 16x16x32
-    # loop: recompute the rows there too (their count padded with row 0 to a
-    # whole 256-token tile; rows are independent)
-    rpad = torch.cat([rd, rd.new_zeros(-len(rd) % 256)])
-    _, hg, hu, *_ = G.ffn_gate_up(x[rpad].contiguous(), wg, wu, L.CACHE_BF16, 128,
+    _, hg, hu, *_ = G.ffn_gate_up(x[rd].contiguous(), wg, wu, L.CACHE_BF16, 128,
                                   want_h_mid=False)
-    hg, hu = hg[:len(rd)], hu[:len(rd)]
     for h, q, s in ((hg, qs[0], ss[0]), (hu, qs[1], ss[1])):
         rq, rs = codec.quantize_group_absmax(R.to_f32(h.cpu()), 8, 128)
         assert np.array_equal(q[rd].cpu().numpy(), rq)
@@ -231,15 +226,11 @@ def test_c3_full_size(device):
     xa_u = G.mm(x, ps["a_up"].t())
 
     def h_rows(rd):
-        # the Function's F1 (8192 tokens) ran on the 16x16x32 loop: recompute
-        # the rows there too, their count padded with row 0 to whole 256-token
-        # tiles (rows are independent)
-        rpad = torch.cat([rd, rd.new_zeros(-len(rd) % 256)])
         _, hg, hu, *_ = G.ffn_gate_up(
-            x[rpad].contiguous(), ps["w_gate"], ps["w_up"], L.CACHE_BF16, 64, want_h_mid=False,
-            lora_gate=(xa_g[rpad].contiguous(), ps["b_gate"], 2.0),
-            lora_up=(xa_u[rpad].contiguous(), ps["b_up"], 2.0))
-        return hg[:len(rd)].cpu(), hu[:len(rd)].cpu()
+            x[rd].contiguous(), ps["w_gate"], ps["w_up"], L.CACHE_BF16, 64, want_h_mid=False,
+            lora_gate=(xa_g[rd].contiguous(), ps["b_gate"], 2.0),
+            lora_up=(xa_u[rd].contiguous(), ps["b_up"], 2.0))
+        return hg.cpu(), hu.cpu()
 
     # outlier channels: ranked on the first sequence's 1024 rows, bit for bit
     hg1, hu1 = h_rows(torch.arange(1024, device=device))

@@ -6,9 +6,10 @@ reference); the bar is the bf16 rounding of the output: elementwise
 |got - ref| <= 1e-2 |ref| + 1e-3 max|ref|.  Fused kernels must equal their
 unfused composition (the same GEMM engine with a plain bf16 store, then the
 standalone K1 / K2 kernel) bit for bit: the accumulation order is the same.
-NT products on whole tiles (and F1 on whole 256-token tiles) run on a second
-main loop (16x16x32 MFMAs, another fp32 summation order); each composition
-uses the plain product of the same loop (plain_like_f1, G.mm_engine).
+Products with K a multiple of 64 (F1 with d_model a multiple of 64) run on a
+second main loop (16x16x32 MFMAs, another fp32 summation order); each
+composition uses the plain product of the same loop (plain_like_f1,
+G.mm_engine).
 """
 
 import pytest
@@ -69,15 +70,18 @@ def test_mm_deterministic_and_k_tail(device):
     assert_gemm_close(c1, ref_mm(a, b))
 
 
-# NT products on whole 256 x 256 tiles (M, N multiples of 256, K of 64) run
-# on the 16x16x32 direct-to-LDS loop (mm sends products of < 128 tiles with
-# K >= 1024 to split-K instead): one k-tile, two (the prologue's pair only),
-# odd tile counts, a last group of fewer than 4 tile rows (M 2560), and
-# operands whose rows are longer than K (sub-views of wider tensors).
+# Products with K a multiple of 64 and N of 8 run on the 16x16x32 direct-to-LDS
+# loop (mm sends products of < 128 tiles with K >= 1024 to split-K instead):
+# one k-tile, two (the prologue's pair only), odd tile counts, a last group of
+# fewer than 4 tile rows (M 2560), ragged M and N (the last tile row and column
+# masked at the store), and operands whose rows are longer than their extent
+# (sub-views of wider tensors).
 @pytest.mark.parametrize("ak", [True, False])
 @pytest.mark.parametrize("bk", [True, False])
 @pytest.mark.parametrize("m,n,k,pad", [(256, 256, 64, 0), (256, 512, 128, 0), (768, 256, 192, 8),
-                                       (2560, 2304, 960, 0), (4096, 2048, 4096, 64)])
+                                       (2560, 2304, 960, 0), (4096, 2048, 4096, 64),
+                                       (300, 264, 128, 0), (8, 520, 64, 8), (1000, 96, 192, 0),
+                                       (257, 1032, 256, 16)])
 def test_mm_nt16_loop(device, ak, bk, m, n, k, pad):
     """Every operand layout (K-major: rows of K; MN-major: rows of M or N,
     transposing LDS reads); pad > 0 makes rows longer than their extent."""
@@ -121,17 +125,14 @@ def test_mm2_nt16_two_pairs(device, ak, bk, k1, k2):
 
 def plain_like_f1(G, x, w):
     """x . w^T in the summation order of F1 without adapter terms: the
-    16x16x32 loop when F1 runs on it (ffn_nt16_fits in gemm.hip: tokens a
-    multiple of 256, d_ff of 128, d_model of 64), else the engine.  The plain
-    NT product reaches that loop on whole 256-column tiles, so zero rows pad
-    w (the other columns' sums are unchanged)."""
+    16x16x32 loop when F1 runs on it (ffn_nt16_fits in gemm.hip: d_model a
+    multiple of 64), which is also where the plain product runs then (nt16_fits:
+    K a multiple of 64, N of 8; these shapes stay off split-K and the skinny
+    kernel); else the engine."""
     n, k = x.shape
-    d = w.shape[0]
-    if n % 256 == 0 and d % 128 == 0 and k % 64 == 0:
-        dp = -(-d // 256) * 256
-        assert k < 1024 or (n // 256) * (dp // 256) >= 128, "mm would split K"
-        wp = torch.nn.functional.pad(w, (0, 0, 0, dp - d))
-        return G.linear(x, wp)[:, :d].contiguous()
+    if k % 64 == 0:
+        assert k < 1024 and w.shape[0] > 32, "mm would leave the 16x16x32 loop"
+        return G.linear(x, w)
     return G.mm_engine(x, w.t())
 
 

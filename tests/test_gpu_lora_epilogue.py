@@ -76,17 +76,12 @@ def test_mm2_lora_terms(device, rank, bk, q_kmajor, nterms, mnk):
 
 
 def plain_like_f1(G, x, w):
-    """x . w^T in the summation order of F1: the 16x16x32 loop on whole
-    256-token x 128-column tiles (ffn_nt16_fits in gemm.hip), else the
-    engine.  The plain product reaches that loop on whole 256 x 256 tiles:
-    zero rows pad w (the other columns' sums are unchanged)."""
-    n, k = x.shape
-    d = w.shape[0]
-    if n % 256 == 0 and d % 128 == 0 and k % 64 == 0:
-        dp = -(-d // 256) * 256
-        assert k < 1024 or (n // 256) * (dp // 256) >= 128, "mm would split K"
-        wp = torch.nn.functional.pad(w, (0, 0, 0, dp - d))
-        return G.linear(x, wp)[:, :d].contiguous()
+    """x . w^T in the summation order of F1: the 16x16x32 loop when d_model is
+    a multiple of 64 (ffn_nt16_fits in gemm.hip), where the plain product then
+    runs too (nt16_fits); else the engine."""
+    if x.shape[1] % 64 == 0:
+        assert x.shape[1] < 1024 and w.shape[0] > 32, "mm would leave the 16x16x32 loop"
+        return G.linear(x, w)
     return G.mm_engine(x, w.t())
 
 
@@ -94,11 +89,11 @@ def plain_like_f1(G, x, w):
                                               ("none", 0, 64)])
 @pytest.mark.parametrize("which", ["both", "gate", "up"])
 @pytest.mark.parametrize("rank", [8, 16])
-@pytest.mark.parametrize("n_tok,hid,inter", [(300, 128, 384), (512, 128, 512)])
+@pytest.mark.parametrize("n_tok,hid,inter", [(300, 128, 384), (512, 128, 512), (300, 136, 384)])
 def test_gate_up_lora_fused_equals_composed(device, cache, bits, group, which, rank, n_tok, hid,
                                             inter):
     """F1 with adapter terms equals the plain product of the same main loop
-    (the engine for 300 tokens, the 16x16x32 loop for 512) with the same
+    (the 16x16x32 loop for d_model 128, the engine for 136) with the same
     terms, then K1, bit for bit."""
     cpt, G, _lib = _cpt()
     code = {"int4": _lib.CACHE_INT4, "int8": _lib.CACHE_INT8, "bf16": _lib.CACHE_BF16,
