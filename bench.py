@@ -434,24 +434,25 @@ _ACHIEVABLE = {}
 
 
 def achievable_mfma_peak(launches: int = 200) -> dict:
-    """The bf16 MFMA rate this part sustains with nothing else running:
-    cpt_probe_mfma_rate (v_mfma_f32_32x32x16_bf16 back to back on register
-    operands, one wavefront per SIMD, no memory traffic), timed over
-    `launches` back-to-back launches of about 1.2 ms.  Measured once per
-    process; the spec peak (2.5 PF/s) assumes a clock this part does not hold
-    under MFMA load."""
+    """The bf16 MFMA rate this part sustains with nothing else running, for
+    the instruction the FFN's GEMMs issue: cpt_probe_mfma_rate with
+    v_mfma_f32_16x16x32_bf16 back to back on register operands (no memory
+    traffic), timed over `launches` back-to-back launches of about 1 ms.
+    Measured once per process; the spec peak (2.5 PF/s) assumes a clock this
+    part does not hold under MFMA load."""
     if "v" in _ACHIEVABLE:
         return _ACHIEVABLE["v"]
     import torch
     from compact_amd import _lib
     from compact_amd._lib import check
-    blocks, iters = 256, 4096
+    # shape 1: 16x16x32, 768 blocks (three per CU) x 2730 iterations x 64 MFMAs
+    shape, blocks, iters, per = 1, 768, 2730, 16384
     out = torch.empty(blocks * 4, dtype=torch.float32, device="cuda")
     stream = torch.cuda.current_stream()
     lib = _lib.lib()
 
     def launch():
-        check(lib.cpt_probe_mfma_rate(0, blocks, iters, 0.5, out.data_ptr(), stream.cuda_stream),
+        check(lib.cpt_probe_mfma_rate(shape, blocks, iters, 0.5, out.data_ptr(), stream.cuda_stream),
               "probe_mfma_rate")
     for _ in range(20):
         launch()
@@ -462,10 +463,11 @@ def achievable_mfma_peak(launches: int = 200) -> dict:
     e1.record(stream)
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / launches
-    flops = blocks * iters * 64 * 32768
+    flops = blocks * iters * 64 * per
     _ACHIEVABLE["v"] = {"value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s",
-                        "source": "cpt_probe_mfma_rate: v_mfma_f32_32x32x16_bf16 back to back on "
-                                  "register operands, no memory traffic, timed in this run"}
+                        "source": "cpt_probe_mfma_rate: v_mfma_f32_16x16x32_bf16 (the instruction "
+                                  "the FFN's GEMMs issue) back to back on register operands, no "
+                                  "memory traffic, timed in this run"}
     return _ACHIEVABLE["v"]
 
 
