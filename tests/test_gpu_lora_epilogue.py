@@ -50,7 +50,8 @@ def bits16(t):
 @pytest.mark.parametrize("bk", [True, False])
 @pytest.mark.parametrize("q_kmajor", [True, False])
 @pytest.mark.parametrize("nterms", [1, 2])
-@pytest.mark.parametrize("mnk", [(300, 264, 136), (512, 768, 128)])   # engine, 16x16x32 loop
+@pytest.mark.parametrize("mnk", [(300, 264, 136), (512, 768, 128), (300, 264, 128)])
+# the engine (K 136), the 16x16x32 loop on whole tiles and on ragged ones
 def test_mm2_lora_terms(device, rank, bk, q_kmajor, nterms, mnk):
     _, G, _ = _cpt()
     m, n, k = mnk
