@@ -1,5 +1,7 @@
-// NT bf16 GEMM on v_mfma_f32_16x16x32_bf16 with direct-to-LDS operand loads:
-//   C[M, N] = A[M, K] . B[N, K]^T, both operands K-major, fp32 accumulate.
+// bf16 GEMM on v_mfma_f32_16x16x32_bf16 with direct-to-LDS operand loads:
+//   C[M, N] = A[M, K] . B[K, N] (+ A2 . B2 over a second K range), fp32
+//   accumulate, each operand K-major (rows of K) or MN-major (rows of M or N;
+//   fragments through transposing LDS reads).
 // Two epilogues:
 //   EPI_STORE  C = bf16(acc): the plain products of cpt_gemm_bf16 in every
 //              operand layout (N a multiple of 8, K of 64);
@@ -44,10 +46,11 @@
 //   t = 96 + 2q  F0 reads of tile kt + 1 from stage s ^ 1.
 // Spreading the 16 loads over 90 slots matters: issued in one burst after a
 // single barrier the loop ran at 0.57 TF/GHz, spread this way at 0.82-0.85
-// (the engine 0.81-0.86), and at the board's power cap 8-9% faster than the
-// engine at K 11008 and 0-4% at K 4096.  Both barriers are plain s_barrier:
-// __syncthreads()'s release fence makes the compiler wait for every load in
-// flight, the direct-to-LDS ones included, which drains the pipeline.
+// (the engine 0.81-0.86).  At the board's power cap the loop spends 8-12% less
+// energy per FLOP than the engine and runs the C2 products 8-14% faster.  Both
+// barriers are plain s_barrier: __syncthreads()'s release fence makes the
+// compiler wait for every load in flight, the direct-to-LDS ones included,
+// which drains the pipeline.
 
 #pragma once
 
