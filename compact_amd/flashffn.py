@@ -77,7 +77,7 @@ _FUSED_WGRAD_GLU = False
 
 
 def _mfma(*ts) -> bool:
-    """The bf16 MFMA engine takes bf16 matrices with 16-byte aligned rows: the
+    """The bf16 MFMA GEMMs take bf16 matrices with 16-byte aligned rows: the
     base address 16-byte aligned, the contiguous extent and the row stride
     multiples of 8.  The other extent (the token count of an activation, or
     of a transposed one) is free: the kernels mask rows and k past the edge.
@@ -97,7 +97,7 @@ def _mfma(*ts) -> bool:
 
 
 def _mm(a, b, name):
-    """a @ b: the bf16 MFMA engine, or the general-layout kernel for other
+    """a @ b: the bf16 MFMA GEMMs, or the general-layout kernel for other
     dtypes and layouts."""
     if _mfma(a, b) and a.shape[0] > 0:
         return G.mm(a, b, name)

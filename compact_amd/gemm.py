@@ -280,7 +280,8 @@ def _min_splits(K: int, lda: int, ak: int, ldb: int, bk: int) -> int:
 
 
 def mm(a: torch.Tensor, b: torch.Tensor, name: str = "gemm") -> torch.Tensor:
-    """a [M, K] @ b [K, N] -> bf16 [M, N] on the MFMA engine.  Tall products
+    """a [M, K] @ b [K, N] -> bf16 [M, N] on the MFMA GEMM loops (16x16x32 when
+    K is a multiple of 64 and N of 8, else the 32x32x16 engine).  Tall products
     with N <= 32 (the adapter terms' x A^T, grad_y B, ...) go to the skinny
     kernel; other products with too few 256x256 output tiles to fill the chip
     (N or M = rank) split K across blocks instead, as do products whose
