@@ -1,8 +1,12 @@
-"""torch-facing wrappers of the MFMA GEMM engine (libcompact_amd.so).
+"""torch-facing wrappers of the MFMA GEMMs (libcompact_amd.so): the 16x16x32
+direct-to-LDS loop for products whose K is a multiple of 64, the 32x32x16
+engine otherwise.
 
 mm(a, b)        a @ b for 2-D bf16 tensors; each operand may be row-major or
                 a transposed view (K-major / MN-major on the device side).
 mm2(a, b, a2, b2)  a @ b + a2 @ b2 in one fp32 accumulation.
+mm_engine(a, b) a @ b on the 32x32x16 engine whatever the shape (the fused
+                kernels' summation order).
 linear(x, w)    x @ w.T (F.linear without bias).
 ffn_gate_up     fused dual GEMM + GLU + codec (forward of gate/up + K1).
 ffn_down_dgrad  fused grad_y @ w_down + dequantise + SwiGLU backward (+ K2).
@@ -84,8 +88,10 @@ LORA_MAX_RANK = 16
 
 
 def lora_fusable(rank: int) -> bool:
-    """Adapter terms of this rank ride in the GEMM epilogues: one
-    v_mfma_f32_32x32x16_bf16 per 32 x 32 block and term covers ranks up to 16."""
+    """Adapter terms of this rank ride in the GEMM epilogues: one MFMA per
+    output block and term over k = 16 (v_mfma_f32_16x16x16_bf16 per 16 x 16
+    block on the 16x16x32 loop, v_mfma_f32_32x32x16_bf16 per 32 x 32 block on
+    the engine) covers ranks up to 16."""
     return 1 <= rank <= LORA_MAX_RANK
 
 
