@@ -28,6 +28,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -112,15 +113,56 @@ def saved_bytes(fn, exclude_ptrs):
 
 
 def cpu_model() -> str:
-    """The host CPU's model name (what lscpu prints as 'Model name')."""
+    """The host CPU's model name as lscpu prints it ('Model name'), with the
+    family / model / stepping numbers from /proc/cpuinfo, which identify the
+    part where a virtualised host shortens the name."""
+    name = ""
+    try:
+        r = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10)
+        for line in r.stdout.splitlines():
+            if line.strip().lower().startswith("model name"):
+                name = line.split(":", 1)[1].strip()
+                break
+    except (OSError, subprocess.SubprocessError):
+        pass
+    info = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.lower().startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                if ":" in line:
+                    k, v = (t.strip() for t in line.split(":", 1))
+                    info.setdefault(k.lower(), v)
+                elif info:
+                    break
     except OSError:
         pass
-    return "unknown"
+    name = name or info.get("model name", "unknown")
+    ids = [f"{k} {info[k]}" for k in ("cpu family", "model", "stepping") if k in info]
+    return f"{name} ({', '.join(ids)})" if ids else name
+
+
+def usable_cores() -> tuple:
+    """(cores to use, os.cpu_count(), how it was bounded): os.cpu_count()
+    bounded by this process's CPU affinity and its cgroup CPU quota, so the
+    baseline's threads are the host cores it may actually run on."""
+    n = os.cpu_count() or 1
+    use, why = n, "os.cpu_count()"
+    try:
+        aff = len(os.sched_getaffinity(0))
+        if aff < use:
+            use, why = aff, "CPU affinity"
+    except (AttributeError, OSError):
+        pass
+    try:
+        with open("/sys/fs/cgroup/cpu.max") as f:
+            quota, period = f.read().split()[:2]
+        if quota != "max":
+            q = max(1, int(int(quota) // int(period)))
+            if q < use:
+                use, why = q, "cgroup CPU quota"
+    except (OSError, ValueError):
+        pass
+    return use, n, why
 
 
 def _oracle_median(ps, x, gy, mode, group, reps=3):
@@ -138,8 +180,9 @@ def _oracle_median(ps, x, gy, mode, group, reps=3):
 
 def cpu_baseline(c2_tokens=2048):
     """The CPU oracle's FlashFFNv3Function (the reference's algorithm restated;
-    the reference itself cannot run on a CPU) on the host's threads as the
-    environment sets them (torch's default, OMP_NUM_THREADS):
+    the reference itself cannot run on a CPU) on every host core this process
+    may run on: torch.set_num_threads(os.cpu_count()), bounded by the CPU
+    affinity and cgroup quota (usable_cores):
       value   C2's shape (H 4096, D 11008, int8 g128, full-FT) on a bounded
               sample of `c2_tokens` tokens, in fp32 (CPU bf16 GEMM support
               varies by host);
@@ -148,6 +191,9 @@ def cpu_baseline(c2_tokens=2048):
     1 warmup + 3 timed reps each, median; tokens/s = tokens / median."""
     import torch
     from oracle import flashffn_ref as R
+    cores, n_cpu, bound = usable_cores()
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(cores)
     out = {}
     for key, (n, h, d) in (("c2", (c2_tokens, HID, INTER)), ("c1", (2048, 2048, 5632))):
         ps = R.synthetic_param_set("fullft", h, d, 0, 0.0, seed=0, dtype=torch.float32)
@@ -156,8 +202,9 @@ def cpu_baseline(c2_tokens=2048):
         gy = torch.randn(n, h, generator=g)
         out[key] = (n, _oracle_median(ps, x, gy, "int8", 128))
     (n2, t2), (n1, t1) = out["c2"], out["c1"]
-    return {"value": n2 / t2, "unit": "tokens/s", "cores": torch.get_num_threads(),
-            "kind": "port", "cpu": cpu_model(),
+    torch.set_num_threads(prev_threads)
+    return {"value": n2 / t2, "unit": "tokens/s", "cores": cores, "os_cpu_count": n_cpu,
+            "cores_bounded_by": bound, "kind": "port", "cpu": cpu_model(),
             "sample": f"{n2} tokens of C2 (H={HID}, D={INTER}), fp32, int8 g128, full-FT "
                       "fwd+bwd; oracle FlashFFNv3Function on CPU, median of 3",
             "median_s": t2,

@@ -31,7 +31,6 @@ SIGNATURES = {
     "cpt_outlier_select": [_P, _I, _L, _L, _L, _P, _P, _P, _P, _P],
     "cpt_outlier_select_pair": [_P, _P, _I, _L, _L, _L, _P, _P, _P, _P, _P, _P, _P],
     "cpt_probe_mfma_rate": [_I, _I, _I, ctypes.c_float, _P, _P],
-    "cpt_probe_lds_pattern": [_P, _I, _I, _I, _P, _P],
     "cpt_v3_quantize_outlier": [_P, _I, _L, _L, _I, _L, _P, _L, _P, _P, _P, _P],
     "cpt_v3_dequantize_outlier": [_P, _P, _P, _L, _P, _L, _L, _I, _L, _P, _P],
     "cpt_silu_mul_quant_outlier": [_P, _P, _L, _L, _I, _L, _P, _P, _L, _P, _P, _P, _P, _P, _P,

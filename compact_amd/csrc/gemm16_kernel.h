@@ -382,8 +382,8 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
       __builtin_amdgcn_sched_barrier(0);
     });
   }
-  // the loads past the last tile write zeros into LDS: land them (every wave)
-  // before the output is staged there
+  // the loads past the last tile (re-reads of tile nk - 1) are still landing
+  // in LDS: wait for them (every wave) before the output is staged there
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
   // lane holds tile column (n side) 128 wn + 16 i + 4 (lane / 16) + 0..3 of

@@ -81,53 +81,6 @@ __global__ __launch_bounds__(256, 1) void mfma_rate_kernel(int iters, float seed
   if (lane == 0) out[blockIdx.x * 4 + (threadIdx.x >> 6)] = s;
 }
 
-// One wavefront per block reads (write == 0) or writes (1) 16 bytes per lane
-// at LDS byte offset offs[lane] & 0xfff0 (inside the 64 KiB array), or reads
-// 8 bytes at offs[lane] & 0xfff8 with ds_read_b64 (2) or ds_read_b64_tr_b16
-// (3), `iters` times, each access waited for before the next.  Under a PMC run
-// (SQ_LDS_BANK_CONFLICT / SQ_INSTS_LDS) this gives the bank-conflict cycles
-// of one 128-bit access pattern.
-__global__ __launch_bounds__(64) void lds_pattern_kernel(const int* __restrict__ offs, int write,
-                                                         int iters, float* __restrict__ out) {
-  __shared__ __attribute__((aligned(16))) uint32_t buf[16384];
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  const int lane = threadIdx.x;
-  for (int i = lane; i < 16384; i += 64) buf[i] = (uint32_t)i;
-  __syncthreads();
-  // buf is the kernel's only LDS object, so its LDS address is 0
-  const uint32_t a = (uint32_t)offs[lane] & 0xfff0u;
-  u32x4 acc = {0u, 0u, 0u, 0u};
-  if (write == 2 || write == 3) {
-    // 64-bit reads at offs[lane] & 0xfff8: plain (2) or the transposing
-    // ds_read_b64_tr_b16 (3)
-    const uint32_t a8 = (uint32_t)offs[lane] & 0xfff8u;
-    for (int it = 0; it < iters; ++it) {
-      uint64_t v;
-      if (write == 2)
-        asm volatile("ds_read_b64 %0, %1\n s_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a8) : "memory");
-      else
-        asm volatile("ds_read_b64_tr_b16 %0, %1\n s_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a8) : "memory");
-      acc[0] += (uint32_t)v;
-      acc[1] += (uint32_t)(v >> 32);
-    }
-  } else if (!write) {
-    for (int it = 0; it < iters; ++it) {
-      u32x4 v;
-      asm volatile("ds_read_b128 %0, %1\n s_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(a) : "memory");
-      acc += v;
-    }
-  } else {
-    u32x4 v = {(uint32_t)lane, 1u, 2u, 3u};
-    for (int it = 0; it < iters; ++it) {
-      asm volatile("ds_write_b128 %0, %1\n s_waitcnt lgkmcnt(0)" ::"v"(a), "v"(v) : "memory");
-      v[1] += 1u;
-    }
-    __syncthreads();
-    acc = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(buf) + a);
-  }
-  out[blockIdx.x * 64 + lane] = (float)(acc[0] + acc[1] + acc[2] + acc[3]);
-}
-
 }  // namespace probe
 }  // namespace cpt
 
@@ -142,13 +95,5 @@ extern "C" int cpt_probe_mfma_rate(int shape, int blocks, int iters, float seed,
                        (hipStream_t)stream, iters, seed, (float*)out);
   else
     return cpt::kErrShape;
-  return hipGetLastError() == hipSuccess ? cpt::kOk : cpt::kErrLaunch;
-}
-
-extern "C" int cpt_probe_lds_pattern(const void* offs, int write, int blocks, int iters, void* out,
-                                     void* stream) {
-  if (!offs || !out || blocks <= 0 || iters <= 0) return cpt::kErrShape;
-  hipLaunchKernelGGL(cpt::probe::lds_pattern_kernel, dim3((unsigned)blocks), dim3(64), 0,
-                     (hipStream_t)stream, (const int*)offs, write, iters, (float*)out);
   return hipGetLastError() == hipSuccess ? cpt::kOk : cpt::kErrLaunch;
 }

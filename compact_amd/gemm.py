@@ -13,8 +13,9 @@ ffn_down_dgrad  fused grad_y @ w_down + dequantise + SwiGLU backward (+ K2).
 
 LoRA adapter terms (`lora=` / `lora_gate=`, `lora_up=`): PEFT's
 `h + s * B(A(x))` applied in the GEMM epilogue, each step rounded to bf16 as
-the reference does (src/flashffn.py:1414,1420,1439,1529,1558-1566), for ranks
-8 and 16.
+the reference does (src/flashffn.py:1414,1420,1439,1529,1558-1566), for every
+rank from 1 to 16 (`lora_fusable`; a rank that is not a multiple of 8 is
+zero-padded to 8 or 16).
 
 mm_any          any dtype and any strides (cpt_gemm_any, fp32 MFMA): float32
                 (config C1), float16, unaligned bf16 views, rank-1 factors.
@@ -367,8 +368,9 @@ def mm_engine(a: torch.Tensor, b: torch.Tensor, name: str = "gemm_engine") -> to
     """a [M, K] @ b [K, N] -> bf16 [M, N] on the 32x32x16 engine loop for
     every shape: the fp32 summation order of the fused FFN kernels, so a
     fused kernel equals its unfused composition through this product bit for
-    bit.  mm runs NT products on whole 256 x 256 tiles on the 16x16x32 loop
-    instead (same bf16 rounding of the fp32 sum, another summation order)."""
+    bit.  mm runs every layout on the 16x16x32 loop instead whenever K is a
+    multiple of 64 and N of 8 (same bf16 rounding of the fp32 sum, another
+    summation order)."""
     _require_device(a, b)
     _check_bf16(a, b)
     M, K = a.shape

@@ -158,11 +158,12 @@ int cpt_dequant_swiglu_backward_outlier(const void* grad_h_mid, const void* q_ga
  * b_kmajor: B stored [N][ldb] (1, the nn.Linear weight) or [K][ldb] (0).
  * Pointers 16-byte aligned, leading dims multiples of 8, the contiguous
  * extent of each operand a multiple of 8, N and ldc multiples of 4.
- * One NT pair (both operands K-major) with M, N multiples of 256, K of 64
- * and ldc of 8 runs on a 16x16x32 MFMA loop; every other product on the
- * 32x32x16 loop of the fused FFN kernels.  Both round the fp32 sum to bf16
- * once; their summation orders differ (cpt_gemm_bf16_ex mode 0 is always
- * the 32x32x16 loop). */
+ * A product whose K (and K2, for a second pair) is a multiple of 64, with N
+ * and ldc multiples of 8 and C 16-byte aligned, runs on the 16x16x32 MFMA
+ * loop: any M, every operand layout, one pair or two.  Every other product
+ * runs on the 32x32x16 loop of the fused FFN kernels.  Both round the fp32
+ * sum to bf16 once; their summation orders differ (cpt_gemm_bf16_ex mode 0
+ * always uses the 32x32x16 loop). */
 int cpt_gemm_bf16(const void* a, int64_t lda, int a_kmajor, const void* b, int64_t ldb,
                   int b_kmajor, const void* a2, int64_t lda2, const void* b2, int64_t ldb2,
                   int64_t K2, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream);
@@ -397,16 +398,6 @@ int cpt_topk_scatter(const void* values, const void* indices, int dtype, int64_t
  * partial sum per wavefront.  FLOPs per launch = blocks * iters * 64 *
  * (FLOPs per MFMA). */
 int cpt_probe_mfma_rate(int shape, int blocks, int iters, float seed, void* out, void* stream);
-
-/* No counterpart in the reference: a probe for the LDS bank-conflict cost of
- * one 128-bit access pattern, which the GEMM's LDS layouts are chosen by.
- * `blocks` blocks of one wavefront each read (write == 0) or write (write ==
- * 1) 16 bytes per lane at LDS byte offset offs[lane] & 0xfff0 (offs: 64
- * int32 on the device), or read 8 bytes at offs[lane] & 0xfff8 with
- * ds_read_b64 (write == 2) or ds_read_b64_tr_b16 (write == 3), `iters` times.  out [blocks * 64] fp32 receives one
- * value per lane.  Read SQ_LDS_BANK_CONFLICT / SQ_INSTS_LDS under a PMC run. */
-int cpt_probe_lds_pattern(const void* offs, int write, int blocks, int iters, void* out,
-                          void* stream);
 
 #ifdef __cplusplus
 }

@@ -18,10 +18,14 @@ Every gradient is also checked at full size against float32 autograd of the
 plain FFN on the device (the reference's V2 cosine gates,
 src/verify_flashffn_v3.py:456-467), and saved bytes against the closed form
 (src/verify_flashffn_v3.py:594-605).
-C4 / C5 run the whole-model training step at full size and check properties:
-every MLP ran FlashFFN v3, the MLPs saved exactly the closed form per layer,
-the loss is finite and within 1e-2 of the unpatched model's on the same
-weights and tokens, and every trainable gradient is finite.
+C4 / C5 run the whole-model training step at full size.  Each MLP's input,
+output, upstream gradient and input gradient are recorded in the patched
+step, and every layer is checked against float32 autograd of the stock MLP on
+its own recorded inputs (y rel-Frobenius 1e-2, gradients by the V2 cosine
+gates), its trainable gradients also against the unpatched model's step on
+the same weights and tokens; C5's layer-0 outlier channels against the
+oracle's ranking of that layer's first sequence; saved bytes against the
+closed form per layer.
 
 Tolerances (north star: rel <= 1e-2 in bf16, <= 1e-5 in fp32):
   bf16  y rel-Frobenius 1e-2; gradients 2e-2 where the oracle derives its
@@ -327,50 +331,135 @@ def test_c1_full_size_fp32(device):
 # C4 / C5: whole-model training steps at full size
 # --------------------------------------------------------------------------
 
+def _mlp_params(mlp):
+    """(w, a, b, s) of each projection of a stock LlamaMLP, plain or LoRA."""
+    from compact_amd.flashffn import _v3_extract_proj
+    ps = {}
+    for key in R.PROJ:
+        w, a, b, s = _v3_extract_proj(getattr(mlp, f"{key}_proj"))
+        ps[f"w_{key}"], ps[f"a_{key}"], ps[f"b_{key}"], ps[f"s_{key}"] = w, a, b, s
+    ps["train_w"] = ps["w_gate"].requires_grad
+    return ps
+
+
+def _mlp_trainables(mlp):
+    """{oracle grad name: parameter} of one MLP's trainable tensors."""
+    ps = _mlp_params(mlp)
+    return {k: ps[k] for k in ps if isinstance(ps[k], torch.Tensor) and ps[k].requires_grad}
+
+
 @pytest.mark.parametrize("name", ["c4", "c5"])
 def test_model_step_full_size(device, name):
+    """The whole-model step at full size, every MLP checked on its own inputs:
+      - the unpatched model's step on the same weights and tokens gives the
+        reference gradients (bf16 autograd, stock MLPs);
+      - in the patched step every MLP's input x_l, output y_l, upstream
+        gradient gy_l and input gradient gx_l are recorded;
+      - per layer, float32 autograd of the stock MLP on (x_l, gy_l) must give
+        y_l (rel-Frobenius 1e-2), gx_l and the MLP's trainable gradients
+        under the reference's V2 cosine gates (src/verify_flashffn_v3.py:456-467:
+        0.999 for an int8 cache; int4: adapter factors 0.98, grad_x 0.99);
+      - the MLP trainables of the patched step must also match the unpatched
+        model's gradients.  With an int8 cache (C4) every layer meets the
+        0.999 gate.  With an int4 cache (C5) each layer's codec error in its
+        grad_x (cos 0.99 against exact, the V2 gate) reaches every layer below
+        it through the residual stream, so against the unpatched model only
+        the last layer, which no other codec feeds, is held to the V2 gates,
+        and the rest to 0.9 (measured 0.95-0.96 at layer 0).  To show that
+        this gap is the codec's and not the model plumbing's, C5 also runs the
+        patched model with the lossless bf16 cache (same fused LoRA kernels),
+        whose MLP gradients must meet 0.995 against the unpatched model in
+        every layer (measured 0.9975).  The unpatched model is itself a bf16
+        computation with its own roundings: C4's last layer measures 0.9993
+        against it and 0.99997 against float32 on the same inputs, so the
+        float32 per-layer gates above are the precise ones;
+      - C5: the outlier channels of layer 0 are the oracle's ranking of that
+        layer's first sequence (2048 rows) of the engine's own h_gate / h_up;
+      - every MLP ran FlashFFN v3 and saved exactly the closed form."""
     from compact_amd import e2e
     from compact_amd.kernels import _V3_COUNTERS, v3_reset_counters
     from compact_amd.model_patch import apply_flash_ffn_v3, inject_lora
+    _, L, G = _mods()
     cfg = e2e.CONFIGS[name]
     model = e2e.build_llama(cfg, device, seed=0)
     if cfg.get("lora"):
         inject_lora(model, cfg["lora"], cfg["lora_r"], cfg["lora_alpha"], b_std=0.01)
     model.train()
     ids = e2e.random_batch(cfg, device)
-    with torch.no_grad(), e2e.fused_attention_only():
-        loss_ref = float(model(input_ids=ids, labels=ids).loss)
+    mlps = [layer.mlp for layer in model.model.layers]
+    int4 = cfg["cache_mode"] == "int4"
+
+    def floor(k):
+        return (0.99 if k == "grad_x" else 0.98) if int4 else 0.999
+
+    # the unpatched step: reference gradients of every MLP trainable
+    with e2e.fused_attention_only():
+        model(input_ids=ids, labels=ids).loss.backward()
+    ref_whole = [{k: p.grad.detach().clone() for k, p in _mlp_trainables(m).items()}
+                 for m in mlps]
+    model.zero_grad(set_to_none=True)
+
+    def whole_cos(li, m):
+        return {kk: R.tensor_cos(p.grad.float(), ref_whole[li][kk].float())
+                for kk, p in _mlp_trainables(m).items()}
+
+    if int4:
+        # the same patched model with the lossless bf16 cache
+        assert apply_flash_ffn_v3(model, "bf16", cfg["group"]) == cfg["layers"]
+        with e2e.fused_attention_only():
+            model(input_ids=ids, labels=ids).loss.backward()
+        lossless = min(min(whole_cos(li, m).values()) for li, m in enumerate(mlps))
+        print(name, "bf16 cache, whole-model min cos", round(lossless, 6))
+        assert lossless >= 0.995, lossless
+        model.zero_grad(set_to_none=True)
+
     assert apply_flash_ffn_v3(model, cfg["cache_mode"], cfg["group"],
                               outlier_ratio=cfg["outlier_ratio"]) == cfg["layers"]
 
-    mlps = [layer.mlp for layer in model.model.layers]
-    inside = [False]
+    rec = [dict() for _ in mlps]
+    inside = [-1]
     params = {p.data_ptr() for p in model.parameters()}
-    seen, total = set(), [0]
+    seen, total, saved0 = set(), [0], []
 
     def pack(t):
-        if inside[0]:
+        if inside[0] >= 0:
             key = (t.data_ptr(), t.nbytes)
             if t.data_ptr() not in params and key not in seen:
                 seen.add(key)
                 total[0] += t.nbytes
+            if inside[0] == 0:
+                saved0.append(t)
         return t
+
+    def pre(li):
+        def f(mod, args):
+            inside[0] = li
+            x = args[0]
+            rec[li]["x"] = x.detach()
+            x.register_hook(lambda g: rec[li].__setitem__("gx", g.detach()))
+        return f
+
+    def post(li):
+        def f(mod, args, out):
+            inside[0] = -1
+            rec[li]["y"] = out.detach()
+            out.register_hook(lambda g: rec[li].__setitem__("gy", g.detach()))
+        return f
     hooks = []
-    for m in mlps:
-        hooks.append(m.register_forward_pre_hook(lambda mod, a: inside.__setitem__(0, True)))
-        hooks.append(m.register_forward_hook(lambda mod, a, o: inside.__setitem__(0, False)))
+    for li, m in enumerate(mlps):
+        hooks.append(m.register_forward_pre_hook(pre(li)))
+        hooks.append(m.register_forward_hook(post(li)))
     v3_reset_counters()
     with torch.autograd.graph.saved_tensors_hooks(pack, lambda t: t), e2e.fused_attention_only():
         loss = model(input_ids=ids, labels=ids).loss
+    loss.backward()
     for hk in hooks:
         hk.remove()
-    loss.backward()
     assert _V3_COUNTERS["forward"] == cfg["layers"] and _V3_COUNTERS["backward"] == cfg["layers"]
-    loss = float(loss.detach())
-    assert np.isfinite(loss) and abs(loss - loss_ref) / abs(loss_ref) < 1e-2, (loss, loss_ref)
+    assert np.isfinite(float(loss.detach()))
 
     n_tok, h, d = cfg["batch"] * cfg["seq"], cfg["hidden"], cfg["inter"]
-    bits = 4 if cfg["cache_mode"] == "int4" else 8
+    bits = 4 if int4 else 8
     k = int(d * cfg["outlier_ratio"])
     lora_mlp = cfg.get("lora") and "gate_proj" in cfg["lora"]
     per_layer = R.saved_bytes_closed_form(n_tok, h, d, bits, cfg["group"],
@@ -381,3 +470,53 @@ def test_model_step_full_size(device, name):
     trainable = [p for p in model.parameters() if p.requires_grad]
     assert trainable and all(p.grad is not None and torch.isfinite(p.grad).all()
                              for p in trainable)
+
+    # every layer against float32 autograd of the stock MLP on its own inputs,
+    # and against the unpatched model's gradients
+    worst = {}
+    for li, m in enumerate(mlps):
+        r = rec[li]
+        x2, y2 = r["x"].reshape(n_tok, h), r["y"].reshape(n_tok, h)
+        ps = _mlp_params(m)
+        ref, y_ref = _fp32_ref(ps, x2, r["gy"].reshape(n_tok, h))
+        got = {"grad_x": r["gx"].reshape(n_tok, h)}
+        got.update({kk: p.grad for kk, p in _mlp_trainables(m).items()})
+        assert set(got) == set(ref), (li, set(got), set(ref))
+        checks = {"y_rel": R.rel_frob(y2, y_ref)}
+        for kk, g in got.items():
+            checks[kk] = R.tensor_cos(g.float(), ref[kk])
+        wc = whole_cos(li, m)
+        if li in (0, len(mlps) // 2, len(mlps) - 1):
+            print(name, "layer", li, "whole-model cos",
+                  {kk: round(v, 6) for kk, v in wc.items()})
+        last = li == len(mlps) - 1
+        for kk, v in wc.items():
+            assert v >= (floor(kk) if (last or not int4) else 0.9), (li, kk, v)
+        for kk, v in checks.items():
+            worst[kk] = max(worst.get(kk, v), v) if kk == "y_rel" else min(worst.get(kk, v), v)
+        del ref, y_ref
+    print(name, "per-layer worst", {kk: round(v, 6) for kk, v in worst.items()})
+    assert worst["y_rel"] < 1e-2, worst
+    for kk, v in worst.items():
+        if kk != "y_rel":
+            assert v >= floor(kk), (kk, v)
+
+    if k:
+        # layer 0's outlier channels: the oracle's ranking of its first sequence
+        slots = _of(saved0, torch.int16, (d,))
+        assert len(slots) == 2
+        ps = _mlp_params(mlps[0])
+        # the Function's own x A^T terms, then the first sequence's rows
+        x0 = rec[0]["x"].reshape(n_tok, h)
+        s1 = cfg["seq"]
+        xa_g = G.mm(x0, ps["a_gate"].t())[:s1].contiguous()
+        xa_u = G.mm(x0, ps["a_up"].t())[:s1].contiguous()
+        _, hg, hu, *_ = G.ffn_gate_up(x0[:s1].contiguous(), ps["w_gate"], ps["w_up"],
+                                      L.CACHE_BF16, cfg["group"], want_h_mid=False,
+                                      lora_gate=(xa_g, ps["b_gate"], ps["s_gate"]),
+                                      lora_up=(xa_u, ps["b_up"], ps["s_up"]))
+        for hh, slot in ((hg, slots[0]), (hu, slots[1])):
+            ref_idx = np.asarray(R.outlier_select(hh.cpu(), cfg["outlier_ratio"], cfg["seq"]))
+            got_idx = torch.nonzero(slot >= 0).flatten().cpu().numpy()
+            assert np.array_equal(np.sort(ref_idx), got_idx)
+            assert np.array_equal(slot[slot >= 0].cpu().numpy(), np.arange(k))

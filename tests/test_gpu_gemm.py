@@ -167,6 +167,18 @@ def test_gate_up_fused_equals_unfused(device, cache, bits, group, n_tok, hid, in
         assert torch.equal(su.view(torch.int16), rsu.view(torch.int16))
 
 
+@pytest.mark.parametrize("cache,bits,group,inter", [("bf16", 0, 64, 264), ("none", 0, 64, 264),
+                                                    ("int8", 8, 64, 320), ("int4", 4, 32, 320),
+                                                    ("int8", 8, 32, 288)])
+@pytest.mark.parametrize("n_tok,hid", [(300, 128), (7, 64)])
+def test_gate_up_fused_ragged_dff(device, cache, bits, group, inter, n_tok, hid):
+    """F1 with a partial last d_ff tile (d_ff not a multiple of the 128 gate
+    columns a tile holds): the interleaved gate/up source rows past d_ff read
+    zero and glu_finish masks those columns; the result equals the plain
+    product of the same loop, then K1, bit for bit."""
+    test_gate_up_fused_equals_unfused(device, cache, bits, group, n_tok, hid, inter)
+
+
 @pytest.mark.parametrize("cache,bits,group", [("int4", 4, 64), ("int8", 8, 128), ("int4", 4, 32),
                                               ("bf16", 0, 64)])
 @pytest.mark.parametrize("want_h_mid", [True, False])
@@ -322,33 +334,3 @@ def test_mfma_probe_runs_and_scales_with_iters(device, shape):
     assert lib.cpt_probe_mfma_rate(shape, 0, 1, 0.5, out1.data_ptr(), s) != 0
     assert lib.cpt_probe_mfma_rate(shape, 8, 0, 0.5, out1.data_ptr(), s) != 0
     assert lib.cpt_probe_mfma_rate(2, 8, 1, 0.5, out1.data_ptr(), s) != 0
-
-
-def test_lds_pattern_probe_reads_what_it_addresses(device):
-    """The LDS probe behind the layout measurements: lane l reads the four
-    dwords at offs[l] & 0xfff0 of an array holding i at dword i, `iters` times,
-    so its value is iters * (offs[l] + 6); a write pass reads back its own last
-    store (lane, iters, 2, 3)."""
-    from compact_amd import _lib
-    lib = _lib.lib()
-    s = torch.cuda.current_stream().cuda_stream
-    offs = torch.tensor([(16 * l * 37) % 65536 for l in range(64)], dtype=torch.int32, device=device)
-    out = torch.empty(2 * 64, dtype=torch.float32, device=device)
-    assert lib.cpt_probe_lds_pattern(offs.data_ptr(), 0, 2, 3, out.data_ptr(), s) == 0
-    torch.cuda.synchronize()
-    want = (3 * (offs.cpu().double() + 6)).float()
-    assert torch.equal(out.cpu()[:64], want) and torch.equal(out.cpu()[64:], want)
-    assert lib.cpt_probe_lds_pattern(offs.data_ptr(), 1, 2, 3, out.data_ptr(), s) == 0
-    torch.cuda.synchronize()
-    lane = torch.arange(64, dtype=torch.float32)
-    assert torch.equal(out.cpu()[:64], lane + 3 + 2 + 3)
-    # 64-bit plain read: dwords a / 4 and a / 4 + 1 (a = offs & 0xfff8), each summed iters times
-    assert lib.cpt_probe_lds_pattern(offs.data_ptr(), 2, 2, 3, out.data_ptr(), s) == 0
-    torch.cuda.synchronize()
-    a8 = (offs.cpu().double() // 8) * 8
-    assert torch.equal(out.cpu()[:64], (3 * (a8 / 2 + 1)).float())
-    # the transposing read runs (its values are a 4 x 16 transpose across lanes)
-    assert lib.cpt_probe_lds_pattern(offs.data_ptr(), 3, 2, 3, out.data_ptr(), s) == 0
-    torch.cuda.synchronize()
-    assert torch.isfinite(out).all()
-    assert lib.cpt_probe_lds_pattern(offs.data_ptr(), 0, 0, 3, out.data_ptr(), s) != 0

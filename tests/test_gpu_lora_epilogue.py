@@ -120,6 +120,17 @@ def test_gate_up_lora_fused_equals_composed(device, cache, bits, group, which, r
         assert torch.equal(bits16(su), bits16(rsu))
 
 
+@pytest.mark.parametrize("cache,bits,group,inter", [("bf16", 0, 64, 264), ("none", 0, 64, 264),
+                                                    ("int8", 8, 64, 320), ("int4", 4, 32, 320)])
+@pytest.mark.parametrize("which", ["both", "gate"])
+@pytest.mark.parametrize("rank", [8, 16])
+def test_gate_up_lora_ragged_dff(device, cache, bits, group, inter, which, rank):
+    """The adapter terms on a partial last d_ff tile: the Q rows (B's rows)
+    past d_ff read zero and those columns are never stored."""
+    test_gate_up_lora_fused_equals_composed(device, cache, bits, group, which, rank, 300, 128,
+                                            inter)
+
+
 def test_absent_term_is_a_no_op(device):
     """Adapter on gate only: h_up must equal the adapter-free kernel's bit for
     bit (zero rows of x included)."""
