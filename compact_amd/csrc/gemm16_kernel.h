@@ -387,9 +387,13 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
   // lane holds tile column (n side) 128 wn + 16 i + 4 (lane / 16) + 0..3 of
-  // tile row (m side) 128 wm + 16 j + lane % 16 in acc[i][j]
+  // tile row (m side) 128 wm + 16 j + lane % 16 in acc[i][j].  The epilogue
+  // takes its thread index afresh (epi_tid), so no prologue value has to stay
+  // live across the main loop.
+  const int etid = epi_tid();
+  const int elane = etid & 63;
   Lora16 F;
-  if constexpr (LT > 0) lora16_load<DUAL, LT>(A, m0, n0, wm, wn, lane, F);
+  if constexpr (LT > 0) lora16_load<DUAL, LT>(A, m0, n0, wm, wn, elane, F);
   if constexpr (EPI == EPI_STORE) {
     // bf16(acc) is staged as a row-major tile (rows kLdOut apart: 32 lanes of
     // one 8-byte write cover the 64 banks once), then 32 threads store each
@@ -398,20 +402,23 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
     for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int ml = wm * 128 + 16 * j + (lane & 15);
-        const int nl = wn * 128 + 16 * i + 4 * (lane >> 4);
-        const f32x4 v = LT > 0 ? acc16<false, LT>(A, acc[i][j], F, i, j) : acc[i][j];
+        const int ml = wm * 128 + 16 * j + (elane & 15);
+        const int nl = wn * 128 + 16 * i + 4 * (elane >> 4);
+        f32x4 v = LT > 0 ? acc16<false, LT>(A, acc[i][j], F, i, j) : acc[i][j];
+        // one block's accumulators at a time: read all at once, the 256
+        // accumulator copies spilled the values that live across the loop
+        asm volatile("" : "+v"(v));
         *reinterpret_cast<uint2*>(lds + ml * kLdOut + nl) =
             make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
       }
     __syncthreads();
     // ragged M and N: rows past M and 8-column pieces past N (N % 8 == 0) stay
     // unwritten; the operand loads read zeros or discarded values there
-    const int cl = (tid & 31) * 8;
+    const int cl = (etid & 31) * 8;
     const bool nok = n0 + cl < A.N;
 #pragma unroll 4
     for (int p = 0; p < 32; ++p) {
-      const int r = p * 8 + (tid >> 5);
+      const int r = p * 8 + (etid >> 5);
       const uint4 w = *reinterpret_cast<const uint4*>(lds + r * kLdOut + cl);
       if (nok && m0 + r < A.M) *reinterpret_cast<uint4*>(A.C + (m0 + r) * A.ldc + n0 + cl) = w;
     }
@@ -425,9 +432,10 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
     for (int i = 0; i < 8; ++i)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const int ml = wm * 128 + 16 * j + (lane & 15);
-        const int dl = wn * 64 + 16 * (i & 3) + 4 * (lane >> 4);
-        const f32x4 v = LT > 0 ? acc16<true, LT>(A, acc[i][j], F, i, j) : acc[i][j];
+        const int ml = wm * 128 + 16 * j + (elane & 15);
+        const int dl = wn * 64 + 16 * (i & 3) + 4 * (elane >> 4);
+        f32x4 v = LT > 0 ? acc16<true, LT>(A, acc[i][j], F, i, j) : acc[i][j];
+        asm volatile("" : "+v"(v));
         *reinterpret_cast<uint2*>((i < 4 ? sg : su) + ml * kGluLd + dl) =
             make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
       }

@@ -642,6 +642,15 @@ __device__ __forceinline__ bf16x8 lora_frag_mn(__amdgpu_buffer_rsrc_t rs, int64_
   return __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
 }
 
+// threadIdx.x for an epilogue, as a value the compiler cannot match with the
+// prologue's: index arithmetic shared with the prologue would otherwise stay
+// live across the main loop, which holds every VGPR, and spill to scratch.
+__device__ __forceinline__ int epi_tid() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 // The adapter fragments of one wave, loaded once per tile ahead of the
 // epilogue: p[t][j] the m-side rows of P_t (block j), q[t][i] the n-side rows
 // of Q_t (block i; in the dual GEMM only the blocks of term t's columns).
@@ -652,7 +661,8 @@ struct LoraFr {
 
 template <bool DUAL, int LT>
 __device__ __forceinline__ void lora_load(const KArgs& A, int64_t m0, int64_t n0, LoraFr& F) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = epi_tid();
+  const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave & 1, wm = wave >> 1;
   const int r = A.lrank;
 #pragma unroll
@@ -720,7 +730,7 @@ __device__ __forceinline__ void epi_store(const KArgs& A, const Acc& acc, int64_
                                           uint16_t* lds) {
   constexpr int LD = 264;
   static_assert(BM * LD * 2 <= LDS_BYTES, "the staged tile must fit the main loop's LDS");
-  const int tid = threadIdx.x;
+  const int tid = epi_tid();
   const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave & 1, wm = wave >> 1;
   LoraFr F;
@@ -767,7 +777,7 @@ __device__ __forceinline__ void epi_add(const KArgs& A, const Acc& acc, int64_t 
   // threads then own one row (8 columns each), so C is read and written back
   // in contiguous row segments
   constexpr int LD = 264;
-  const int tid = threadIdx.x;
+  const int tid = epi_tid();
   const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave & 1, wm = wave >> 1;
   static_for<0, 4>([&](auto j) {
@@ -818,7 +828,8 @@ __device__ __forceinline__ void epi_add(const KArgs& A, const Acc& acc, int64_t 
 // epilogue F32: fp32 partial of this split into ws[split][M][N]
 __device__ __forceinline__ void epi_f32(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0,
                                         int split) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int tid = epi_tid();
+  const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave & 1, wm = wave >> 1;
   float* base = A.ws + (int64_t)split * A.M * A.N;
   static_for<0, 4>([&](auto j) {
@@ -863,7 +874,7 @@ __device__ __forceinline__ void glu_finish(const KArgs& A, int64_t m0, int64_t n
   constexpr int BITS = CACHE == CACHE_INT4 ? 4 : 8;
   constexpr bool QUANT = CACHE == CACHE_INT4 || CACHE == CACHE_INT8;
   constexpr int LD = kGluLd;
-  const int tid = threadIdx.x;
+  const int tid = epi_tid();
   const uint16_t* sg = lds;
   const uint16_t* su = lds + 256 * LD;
   const int64_t D = A.D;
@@ -943,7 +954,7 @@ __device__ __forceinline__ void epi_glu(const KArgs& A, const Acc& acc, int64_t 
   // through LDS (glu_finish's layout), then glu_finish writes the outputs.
   static_assert(BM * kGluLd * 2 * 2 <= LDS_BYTES, "the staged tiles must fit the main loop's LDS");
   constexpr int LD = kGluLd;
-  const int tid = threadIdx.x;
+  const int tid = epi_tid();
   const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave & 1, wm = wave >> 1;
   const int half = lane >> 5;
@@ -985,7 +996,7 @@ __device__ __forceinline__ void epi_dglu(const KArgs& A, const Acc& acc, int64_t
   // over 32 rows per instruction).
   constexpr int BITS = CACHE == CACHE_INT4 ? 4 : 8;
   constexpr int LD = 264;   // LDS row stride in bf16 (528 bytes)
-  const int tid = threadIdx.x;
+  const int tid = epi_tid();
   const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave & 1, wm = wave >> 1;
   LoraFr F;
