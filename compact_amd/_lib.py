@@ -61,12 +61,14 @@ SIGNATURES = {
     "cpt_dora_col_norm": [_P, _P, _P, _L, _L, _L, ctypes.c_double, _I, _P, _P, _I, _P],
     "cpt_topk_abs": [_P, _I, _L, _L, _L, _P, _P, _P],
     "cpt_topk_scatter": [_P, _P, _I, _L, _L, _L, _P, _P],
+    "cpt_gemm_stream_k_workspace": [_P, _L],
 }
 
 # size queries: name -> argument types (restype int64)
 SIZE_QUERIES = {
     "cpt_col_dot_workspace_bytes": [_L, _L],
     "cpt_dora_col_norm_workspace_bytes": [_L, _L],
+    "cpt_gemm_stream_k_bytes": [],
 }
 
 CACHE_NONE, CACHE_BF16, CACHE_INT4, CACHE_INT8 = 0, 1, 4, 8

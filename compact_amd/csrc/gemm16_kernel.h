@@ -216,23 +216,57 @@ __device__ __forceinline__ f32x4 acc16(const KArgs& A, const f32x4& a, const Lor
   return v;
 }
 
-template <bool AK, bool BK, int EPI, int CACHE, int GS, int LT>
-__global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
+// ---------------------------------------------------------------------------
+// Stream-K (plain-store products).  A product whose tile count T is not a
+// multiple of the CU count S leaves its last wave of tiles part-empty.  The
+// host then runs T' = T - (T mod S) - S tiles data-parallel (one block each)
+// and shares the k-iterations of the other (T mod S) + S tiles evenly over S
+// more blocks: block s owns global iterations [s I / S, (s + 1) I / S) of
+// those tiles (I = their tile count x k-tiles per tile), i.e. one to two
+// tiles' worth, and walks its tiles from the last to the first.
+//   - A tile it covers whole it finishes alone.
+//   - A tile whose k-range continues past its range (its last tile, taken
+//     first) it leaves as a partial: fp32 accumulators to slot s of the
+//     workspace, then a ready flag.
+//   - A tile whose k-range began in lower blocks (its first tile, taken last)
+//     it finishes: it waits for those blocks' flags, adds their partials in a
+//     fixed order (nearest block first), clears the flags and runs the
+//     epilogue.  The result is deterministic for a given shape and CU count.
+// A block only ever waits on lower-numbered blocks, which the hardware
+// dispatches first, so every wait ends whatever the grid's residency; the
+// wait is bounded anyway (kSkSpin polls), and a wait that runs out counts an
+// error in the word after the flags and goes on.
+// ---------------------------------------------------------------------------
+constexpr int kRoleWhole = 0, kRolePartial = 1, kRoleFinish = 2;
+// 0 as a value the compiler cannot hoist: a flag address built from it does
+// not pin a zero VGPR across the main loop (which spilled it)
+__device__ __forceinline__ int fresh_zero() {
+  int z = 0;
+  asm volatile("" : "+v"(z));
+  return z;
+}
+constexpr int kSc1 = 16;                          // buffer cache policy: agent-coherent (sc1)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+constexpr int64_t kSkSlot = 256 * 256;            // floats per partial (one tile)
+constexpr int kSkSpin = 1 << 22;
+
+template <bool AK, bool BK, int EPI, int CACHE, int GS, int LT, bool SK>
+__device__ __forceinline__ void nt16_tile(const KArgs& A, uint16_t* lds, int tm, int tn, int kb,
+                                          int ke, int role, int sk_s) {
   static_assert(LT == 0 || AK, "adapter terms ride with a K-major A (P's rows are tokens)");
   static_assert(EPI == EPI_STORE || EPI == EPI_GLU, "epilogues of the 16x16x32 loop");
   constexpr bool DUAL = EPI == EPI_GLU;
   static_assert(!DUAL || (AK && BK), "F1's operands are K-major");
-  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
-  const int tid = threadIdx.x;
+  // per-lane values are derived afresh for each tile of a stream-K block:
+  // hoisted out of its tile loop they would stay live across the main loop
+  const int tid = epi_tid();
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wn = wave & 1, wm = wave >> 1;
-  int tm, tn;
-  tile_coords(A.tiles_m, A.tiles_n, tm, tn);
   const int64_t m0 = (int64_t)tm * 256, n0 = (int64_t)tn * 256;
-  // k-tiles [0, nk0) come from pair 0, [nk0, nk) from pair 1 (K-concatenated)
+  // k-tiles [kb, ke) of the tile; [0, nk0) come from pair 0, the rest from
+  // pair 1 (K-concatenated)
   const int nk0 = (int)(A.K[0] / kBK);
-  const int nk = nk0 + (A.npairs == 2 ? (int)(A.K[1] / kBK) : 0);
   const int64_t lda = A.a[0].ld, ldb = A.b[0].ld;   // pair 1 shares them (host check)
 
   // Buffers: a K-major operand at the tile's first row (257 rows < 2 GiB), an
@@ -293,7 +327,7 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
   const uint32_t stepa = AK ? (uint32_t)(kBK * 2) : (uint32_t)(kBK * lda * 2);
   const uint32_t stepb = BK ? (uint32_t)(kBK * 2) : (uint32_t)(kBK * ldb * 2);
   auto tile = [&](int kt) -> TileLd {
-    const int kc = kt < nk ? kt : nk - 1;
+    const int kc = kt < ke ? kt : ke - 1;
     const bool p1 = kc >= nk0;
     const uint32_t lk = (uint32_t)(kc - (p1 ? nk0 : 0));
     return TileLd{p1 ? ra1 : ra0, p1 ? rb1 : rb0, lk * stepa, lk * stepb};
@@ -341,9 +375,9 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
     return __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   };
 
-  // prologue: tile 0 -> stage 0, tile 1 -> stage 1; tile 0 landed; F0 of tile 0
+  // prologue: k-tile kb -> stage 0, kb + 1 -> stage 1; kb landed; F0 of kb
   {
-    const TileLd T0 = tile(0), T1 = tile(1);
+    const TileLd T0 = tile(kb), T1 = tile(kb + 1);
 #pragma unroll
     for (int p = 0; p < 16; ++p) issue(p, 0, T0);
 #pragma unroll
@@ -359,8 +393,8 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
   }
 
   constexpr Order ord;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int stage = kt & 1;
+  for (int kt = kb; kt < ke; ++kt) {
+    const int stage = (kt - kb) & 1;
     const TileLd T2 = tile(kt + 2);
     static_for<0, 128>([&](auto tc) {
       constexpr int t = decltype(tc)::value;
@@ -382,9 +416,56 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
       __builtin_amdgcn_sched_barrier(0);
     });
   }
-  // the loads past the last tile (re-reads of tile nk - 1) are still landing
+  // the loads past the last tile (re-reads of tile ke - 1) are still landing
   // in LDS: wait for them (every wave) before the output is staged there
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  if constexpr (SK) {
+    if (role == kRolePartial) {
+      // this block's share of a tile that a higher block finishes
+      // agent-coherent (sc1) stores write through to memory, so no cache
+      // writeback is needed before the flag; waiting for them is enough
+      const int ptid = epi_tid();
+      const __amdgpu_buffer_rsrc_t rw = make_rsrc(A.sk_ws + (int64_t)sk_s * kSkSlot, kSkSlot * 4);
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          f32x4 v = acc[i][j];
+          asm volatile("" : "+v"(v));
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rw,
+                                                 ((i * 8 + j) * 256 + ptid) * 16, 0, kSc1);
+        }
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (ptid == 0) __hip_atomic_store(A.sk_flags + sk_s + fresh_zero(), 1, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    if (role == kRoleFinish) {
+      // wait for the partial of block sk_s - 1, the tile's only other
+      // contributor (each stream-K block owns more than one tile's
+      // k-iterations); the epilogue adds it to the accumulators
+      if (epi_tid() == 0) {
+        int* const flag = A.sk_flags + (sk_s - 1) + fresh_zero();
+        int spin = 0;
+        while (__hip_atomic_load(flag, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT) == 0 &&
+               ++spin < kSkSpin)
+          __builtin_amdgcn_s_sleep(2);
+        if (spin >= kSkSpin)
+          __hip_atomic_fetch_add(A.sk_flags + A.sk_blocks + fresh_zero(), 1, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(flag, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+    }
+  }
+  // the partial this tile's epilogue adds (stream-K finisher), read with
+  // agent-coherent (sc1) loads: no cache invalidation needed
+  const bool part = SK && role == kRoleFinish;
+  const __amdgpu_buffer_rsrc_t rpart =
+      make_rsrc(part ? A.sk_ws + (int64_t)(sk_s - 1) * kSkSlot : nullptr, part ? kSkSlot * 4 : 0);
 
   // lane holds tile column (n side) 128 wn + 16 i + 4 (lane / 16) + 0..3 of
   // tile row (m side) 128 wm + 16 j + lane % 16 in acc[i][j].  The epilogue
@@ -399,18 +480,29 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
     // one 8-byte write cover the 64 banks once), then 32 threads store each
     // 512-byte row.
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 8; ++i) {
+      // a stream-K finisher adds the other block's partial, 8 blocks at a time
+      f32x4 pv[8];
+      if (part) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          pv[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                 rpart, ((i * 8 + j) * 256 + etid) * 16, 0, kSc1));
+      }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int ml = wm * 128 + 16 * j + (elane & 15);
         const int nl = wn * 128 + 16 * i + 4 * (elane >> 4);
-        f32x4 v = LT > 0 ? acc16<false, LT>(A, acc[i][j], F, i, j) : acc[i][j];
+        f32x4 base = acc[i][j];
         // one block's accumulators at a time: read all at once, the 256
         // accumulator copies spilled the values that live across the loop
-        asm volatile("" : "+v"(v));
+        asm volatile("" : "+v"(base));
+        if (part) base += pv[j];
+        const f32x4 v = LT > 0 ? acc16<false, LT>(A, base, F, i, j) : base;
         *reinterpret_cast<uint2*>(lds + ml * kLdOut + nl) =
             make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
       }
+    }
     __syncthreads();
     // ragged M and N: rows past M and 8-column pieces past N (N % 8 == 0) stay
     // unwritten; the operand loads read zeros or discarded values there
@@ -444,14 +536,63 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
   }
 }
 
+// SK: the stream-K schedule (plain store with a K-major A only); without it
+// one whole tile per block.  Two kernels, so the one-tile-per-block kernel
+// keeps its own register allocation.
+template <bool AK, bool BK, int EPI, int CACHE, int GS, int LT, bool SK>
+__global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
+  static_assert(!SK || (EPI == EPI_STORE && AK), "stream-K: plain store, K-major A");
+  extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
+  const int nk = (int)(A.K[0] / kBK) + (A.npairs == 2 ? (int)(A.K[1] / kBK) : 0);
+  const int b = blockIdx.x;
+  if constexpr (!SK) {
+    int tm, tn;
+    tile_coords_of(b, gridDim.x, A.tiles_m, A.tiles_n, tm, tn);
+    nt16_tile<AK, BK, EPI, CACHE, GS, LT, SK>(A, lds, tm, tn, 0, nk, kRoleWhole, 0);
+    return;
+  }
+  // A data-parallel block (b < sk_dp) has one item, its whole tile.  Stream-K
+  // block s has the global iterations [lo, hi) of the logical tiles sk_dp ..
+  // T - 1: sk_q each, one more for s < sk_r (32-bit: the host keeps their
+  // count below 2^31), taken from its last tile to its first.
+  const bool dp = b < A.sk_dp;
+  // rank of the stream-K block: the blocks an XCD runs (every 8th) take
+  // consecutive ranks, so an XCD's blocks share operand panels in its L2
+  const int sb = b - A.sk_dp;
+  const int s = (A.sk_blocks & 7) == 0 ? (sb & 7) * (A.sk_blocks >> 3) + (sb >> 3) : sb;
+  const int lo = dp ? 0 : s * A.sk_q + min(s, A.sk_r);
+  const int hi = dp ? nk : lo + A.sk_q + (s < A.sk_r ? 1 : 0);
+  const int t_top = (hi - 1) / nk, t_bot = lo / nk;
+  for (int t = t_top; t >= t_bot; --t) {
+    const int ts = t * nk;
+    const int kb = max(lo, ts) - ts;
+    const int ke = min(hi, ts + nk) - ts;
+    const int role = (kb == 0 && ke == nk) ? kRoleWhole
+                     : ke < nk             ? kRolePartial
+                                           : kRoleFinish;
+    int tm, tn;
+    if (dp) tile_coords_of(b, A.sk_dp, A.tiles_m, A.tiles_n, tm, tn);
+    else logical_coords(A.sk_dp + t, A.tiles_m, A.tiles_n, tm, tn);
+    if (t != t_top) __syncthreads();   // the last item's epilogue read LDS
+    nt16_tile<AK, BK, EPI, CACHE, GS, LT, SK>(A, lds, tm, tn, kb, ke, role, s);
+  }
+}
+
 }  // namespace nt16
 
 template <bool AK, bool BK, int EPI, int CACHE, int GS, int LT>
 int launch_nt16(const KArgs& A, hipStream_t st) {
-  auto kern = nt16::nt16_kernel<AK, BK, EPI, CACHE, GS, LT>;
+  // stream-K only where it measured faster: plain stores with a K-major A
+  // (gy W_d, x W^T); with an MN-major A (the weight gradients) the shared
+  // tail ran 10-25% slower than one tile per block
+  constexpr bool kSkOk = EPI == EPI_STORE && AK;
+  auto kern = nt16::nt16_kernel<AK, BK, EPI, CACHE, GS, LT, false>;
+  auto kern_sk = nt16::nt16_kernel<AK, BK, EPI, CACHE, GS, LT, kSkOk>;
   static bool attr_set = false;   // per instantiation
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            nt16::kLds) != hipSuccess ||
+        hipFuncSetAttribute((const void*)kern_sk, hipFuncAttributeMaxDynamicSharedMemorySize,
                             nt16::kLds) != hipSuccess)
       return kErrLaunch;
     attr_set = true;
@@ -459,7 +600,25 @@ int launch_nt16(const KArgs& A, hipStream_t st) {
   const int64_t tiles = (int64_t)A.tiles_m * A.tiles_n;
   if (tiles <= 0) return kOk;
   if (tiles > 0x7FFFFFFF) return kErrTooLarge;
-  hipLaunchKernelGGL(kern, dim3((unsigned)tiles), dim3(nt16::kThreads), nt16::kLds, st, A);
+  KArgs B = A;
+  B.sk_dp = (int)tiles;
+  B.sk_blocks = 0;
+  if constexpr (kSkOk) {
+    const int nk = (int)(A.K[0] / nt16::kBK) + (A.npairs == 2 ? (int)(A.K[1] / nt16::kBK) : 0);
+    StreamK sk;
+    if (stream_k_plan(tiles, nk, sk)) {
+      B.sk_dp = (int)(tiles - sk.tiles);
+      B.sk_blocks = sk.blocks;
+      const int64_t iters = sk.tiles * nk;   // < 2^31 (stream_k_plan)
+      B.sk_q = (int)(iters / sk.blocks);
+      B.sk_r = (int)(iters % sk.blocks);
+      B.sk_ws = sk.ws;
+      B.sk_flags = sk.flags;
+    }
+  }
+  const int64_t grid = (int64_t)B.sk_dp + B.sk_blocks;
+  hipLaunchKernelGGL(B.sk_blocks ? kern_sk : kern, dim3((unsigned)grid), dim3(nt16::kThreads),
+                     nt16::kLds, st, B);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 

@@ -168,6 +168,17 @@ struct KArgs {
   int64_t lldp, lldq;
   int lrank;
   int lq_km;
+  // stream-K schedule of the 16x16x32 loop (gemm16_kernel.h): blocks
+  // [0, sk_dp) take one whole tile each (logical tiles 0 .. sk_dp - 1), blocks
+  // sk_dp .. sk_dp + sk_blocks - 1 share the k-iterations of the other tiles
+  // evenly; fp32 partials of shared tiles go to sk_ws, one slot of 256 x 256
+  // floats per block, with a ready flag per block in sk_flags (zero between
+  // launches).  sk_blocks == 0: every block takes one whole tile.
+  int sk_dp;
+  int sk_blocks;
+  int sk_q, sk_r;          // iterations per stream-K block: sk_q, +1 for the first sk_r
+  float* sk_ws;
+  int* sk_flags;
 };
 
 enum Epi { EPI_STORE = 0, EPI_GLU = 1, EPI_DGLU = 2, EPI_ADD = 3, EPI_F32 = 4 };
@@ -176,11 +187,32 @@ enum Cache { CACHE_NONE = 0, CACHE_BF16 = 1, CACHE_INT4 = 4, CACHE_INT8 = 8 };
 // ---------------------------------------------------------------------------
 // tile scheduling
 // ---------------------------------------------------------------------------
+// logical tile -> (tile row, tile column): GROUP_ROWS tile-rows at a time,
+// column by column, so consecutive logical tiles share operand panels
+__device__ __forceinline__ void logical_coords(int logical, int tiles_m, int tiles_n, int& tm,
+                                               int& tn) {
+  const int per_group = GROUP_ROWS * tiles_n;
+  const int g = logical / per_group;
+  const int first = g * GROUP_ROWS;
+  const int rows = min(GROUP_ROWS, tiles_m - first);
+  const int in = logical - g * per_group;
+  tm = first + in % rows;
+  tn = in / rows;
+}
+
+// block b of nb -> its tile.  Blocks are dispatched round-robin over the 8
+// XCDs: each XCD gets a contiguous range of logical tiles so co-resident
+// tiles share L2 panels.
+__device__ __forceinline__ void tile_coords_of(int b, int nb, int tiles_m, int tiles_n, int& tm,
+                                               int& tn) {
+  const int xcd = b & 7, idx = b >> 3;
+  const int base = nb >> 3, extra = nb & 7;
+  logical_coords(xcd * base + min(xcd, extra) + idx, tiles_m, tiles_n, tm, tn);
+}
+
 __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
   const int nb = gridDim.x;
   const int b = blockIdx.x;
-  // blocks are dispatched round-robin over the 8 XCDs: give each XCD a
-  // contiguous range of logical tiles so co-resident tiles share L2 panels
   const int xcd = b & 7, idx = b >> 3;
   const int base = nb >> 3, extra = nb & 7;
   const int logical = xcd * base + min(xcd, extra) + idx;
@@ -1192,6 +1224,19 @@ int launch(KArgs& A, hipStream_t st) {
 // (nt16_fits); EPI_GLU (F1, both operands K-major, one pair).  M, N and d_ff
 // need not fill whole tiles.
 bool nt16_fits(int64_t M, int64_t N, int64_t K, const void* c, int64_t ldc);
+
+// Stream-K plan of a plain-store product on the 16x16x32 loop (gemm16.hip):
+// true when the current device has a stream-K workspace attached and `tiles`
+// tiles of `nk` k-tiles leave a part-empty last wave.  Then the last `tiles`
+// of the plan's logical tiles go to `blocks` stream-K blocks.
+struct StreamK {
+  int64_t tiles;
+  int blocks;
+  float* ws;
+  int* flags;
+};
+bool stream_k_plan(int64_t tiles, int nk, StreamK& sk);
+int64_t stream_k_bytes(int cus);
 template <bool AK, bool BK, int EPI, int CACHE, int GS, int LT>
 int launch_nt16(const KArgs& A, hipStream_t st);
 

@@ -308,6 +308,48 @@ def mm(a: torch.Tensor, b: torch.Tensor, name: str = "gemm") -> torch.Tensor:
     return mm2(a, b, None, None, name)
 
 
+# Stream-K workspace per device (cpt_gemm_stream_k_workspace): attached at
+# the first product on a device while stream-K is on.
+_STREAM_K = {"on": True}
+_sk_attached: dict = {}      # device index -> workspace tensor, or None if detached
+
+
+def set_stream_k(on: bool) -> None:
+    """Turn the stream-K schedule of the 16x16x32 loop on or off for later
+    products on every device (on by default).  Results are deterministic
+    either way; the two summation orders differ in the last bits of the
+    tiles the schedule shares."""
+    _STREAM_K["on"] = bool(on)
+    for idx in list(_sk_attached):
+        with torch.cuda.device(idx):
+            check(_lib.lib().cpt_gemm_stream_k_workspace(None, 0), "stream_k_workspace")
+        del _sk_attached[idx]
+
+
+def _stream_k(dev: torch.device) -> None:
+    """Attach a zero-filled stream-K workspace to `dev` once (the kernels
+    leave it zero-filled)."""
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    if idx in _sk_attached or not _STREAM_K["on"]:
+        return
+    with torch.cuda.device(idx):
+        nbytes = int(_lib.lib().cpt_gemm_stream_k_bytes())
+        assert nbytes > 0, "stream-K workspace size"
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+        torch.cuda.synchronize(idx)
+        check(_lib.lib().cpt_gemm_stream_k_workspace(ws.data_ptr(), nbytes), "stream_k_workspace")
+    _sk_attached[idx] = ws
+
+
+def stream_k_errors(dev: torch.device) -> int:
+    """Waits for a partial that ran out of polls on `dev` since its workspace
+    was attached (the word after the flags); 0 unless the schedule broke."""
+    ws = _sk_attached.get(dev.index if dev.index is not None else torch.cuda.current_device())
+    if ws is None:
+        return 0
+    return int(ws[-4:].view(torch.int32).item())
+
+
 def mm2(a, b, a2=None, b2=None, name: str = "gemm", lora=None) -> torch.Tensor:
     """a @ b (+ a2 @ b2) in one fp32 accumulation -> bf16 [M, N], then the
     adapter terms `lora` = [(p [M, r], q [r, N], alpha), ...] (at most two),
@@ -343,6 +385,7 @@ def mm2(a, b, a2=None, b2=None, name: str = "gemm", lora=None) -> torch.Tensor:
         p_a2, p_b2 = a2.data_ptr(), b2.data_ptr()
     ldc = (N + 7) // 8 * 8
     c = torch.empty((M, ldc), dtype=torch.bfloat16, device=a.device)
+    _stream_k(a.device)
     if lora:
         if ak != 1:
             a = a.contiguous()

@@ -168,6 +168,27 @@ int cpt_gemm_bf16(const void* a, int64_t lda, int a_kmajor, const void* b, int64
                   int b_kmajor, const void* a2, int64_t lda2, const void* b2, int64_t ldb2,
                   int64_t K2, void* c, int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream);
 
+/* Stream-K workspace of the 16x16x32 loop.  The reference's GEMMs come from
+ * cuBLAS, which picks its own split of K (src/flashffn.py:1410-1439,
+ * 1503-1587); this is the same choice made explicit, in the manner of
+ * cublasSetWorkspace.  A product of cpt_gemm_bf16 or cpt_gemm_bf16_lora on
+ * the 16x16x32 loop whose tile count T (256 x 256 tiles) is above the CU
+ * count S and not a multiple of it, with at least 4 k-tiles of 64, leaves
+ * its last wave part-empty; with a workspace attached to the device it runs
+ * T - (T mod S) - S tiles one per block and shares the k-iterations of the
+ * other (T mod S) + S tiles evenly over S more blocks, which finish shared
+ * tiles in a fixed order: the result is deterministic for a given shape and
+ * CU count, and differs from the unshared summation order in the last bits.
+ * cpt_gemm_stream_k_bytes() is the size the current device needs (-1 without
+ * a device).  cpt_gemm_stream_k_workspace(ws, bytes) attaches caller-owned
+ * device memory of at least that size, 256-byte aligned and zero-filled, to
+ * the current device for every later call on it (the kernels leave it
+ * zero-filled again); NULL detaches it (one tile per block).  The memory
+ * must stay valid while attached, and products that run at the same time on
+ * one device (several streams) must not share it. */
+int64_t cpt_gemm_stream_k_bytes(void);
+int cpt_gemm_stream_k_workspace(void* workspace, int64_t bytes);
+
 /* Skinny product of the adapter terms: C[M, R] = bf16(alpha * A[M, K] . Q^T)
  * with A [M][lda] and Q [R][ldq] both K-contiguous, R <= 32 (the rank), bf16
  * in and out, fp32 accumulate.  Replaces the thin F.linear / @ of the LoRA

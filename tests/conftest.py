@@ -19,3 +19,14 @@ def device():
     if not torch.cuda.is_available():
         pytest.skip("no HIP device")
     return torch.device("cuda:0")
+
+
+@pytest.fixture
+def no_stream_k():
+    """One whole tile per block for every product (no stream-K): for checks
+    that a row's bits do not depend on where the row lies, which the shared
+    tiles of the stream-K schedule give up (they sum k in another order)."""
+    from compact_amd import gemm
+    gemm.set_stream_k(False)
+    yield
+    gemm.set_stream_k(True)

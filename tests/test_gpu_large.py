@@ -8,7 +8,9 @@ Inputs repeat one block of rows R times, so the checks need no CPU pass over
 the full size:
 - row-wise outputs (GEMM rows, y, grad_x, codes) of the last block, which lie
   past 2 GiB, equal the first block's bit for bit (same row content, same
-  kernel, same accumulation order);
+  kernel, same accumulation order: these tests run without the stream-K
+  schedule, whose shared tiles sum k in another order; one test repeats its
+  product with it and checks the last block within a bf16 rounding);
 - reductions over the tokens (weight and adapter gradients) equal R times
   the oracle's value on one block, within the bf16 / fp32 split-sum
   tolerance written in each test.
@@ -19,7 +21,8 @@ import torch
 
 from oracle import flashffn_ref as R
 
-pytestmark = pytest.mark.gpu
+# the bitwise row checks need every row summed in one order: no stream-K
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("no_stream_k")]
 
 BLOCK = 512
 REPS = 196                    # 100352 tokens
@@ -54,7 +57,14 @@ def test_kmajor_operand_over_2gib(device):
     ref = ab.float().cpu() @ w.float().cpu().t()
     got = c[:BLOCK].float().cpu()
     assert ((got - ref).abs() <= 2 ** -7 * ref.abs() + 1e-3).all()
-    del a, c
+    # with stream-K (784 tiles: the last 272 share their k-iterations)
+    G.set_stream_k(True)
+    c_sk = G.linear(a, w)
+    G.set_stream_k(False)
+    last = c_sk[-BLOCK:].float().cpu()
+    assert ((last - ref).abs() <= 2 ** -7 * ref.abs() + 1e-3).all()
+    assert ((c_sk.float() - c.float()).abs() <= 2 ** -7 * c.float().abs() + 1e-3).all()
+    del a, c, c_sk
 
 
 @pytest.mark.parametrize("m", [4096, 256])
