@@ -294,6 +294,15 @@ inline bool ffn_nt16_fits(int64_t n_tok, int64_t inter, int64_t hidden) {
          ((n_tok + 255) / 256) * ((inter + 127) / 128) <= kIntMax;
 }
 
+// B1 on the 16x16x32 loop: d_model (the k of gy . W_d) a multiple of 64;
+// d_ff is one of 8 and the token count free, as for the engine
+inline bool dgrad_nt16_fits(int64_t n_tok, int64_t inter, int64_t hidden) {
+  constexpr int64_t kIntMax = 0x7FFFFFFF;
+  return n_tok > 0 && inter > 0 && hidden > 0 && n_tok <= kIntMax && inter <= kIntMax &&
+         hidden <= kIntMax && inter % 8 == 0 && hidden % 64 == 0 &&
+         ((n_tok + 255) / 256) * ((inter + 255) / 256) <= kIntMax;
+}
+
 int ffn_gate_up_impl(const void* x, const void* w_gate, const void* w_up, int64_t n_tok,
                      int64_t hidden, int64_t inter, int cache, int64_t group_size, void* h_mid,
                      void* h_gate, void* h_up, void* q_gate, void* s_gate, void* q_up,
@@ -453,6 +462,25 @@ int ffn_down_dgrad_impl(const void* grad_y, const void* w_down, int64_t n_tok, i
   if (const int rc = set_lora(A, L, n_tok, inter, terms)) return rc;
   if (terms > 1) return kErrShape;
   hipStream_t st = (hipStream_t)stream;
+  if (dgrad_nt16_fits(n_tok, inter, hidden)) {
+    // the 16x16x32 loop: d_model a multiple of 64 (its summation order is
+    // that of cpt_gemm_bf16's product gy . W_d on the same loop)
+#define CPT_B1_NT16(CACHE, GS) \
+  (terms ? launch_nt16<true, false, EPI_DGLU, CACHE, GS, 1>(A, st) \
+         : launch_nt16<true, false, EPI_DGLU, CACHE, GS, 0>(A, st))
+    switch (cache) {
+      case CACHE_BF16: return CPT_B1_NT16(CACHE_BF16, 64);
+      case CACHE_INT4:
+        return group_size == 32   ? CPT_B1_NT16(CACHE_INT4, 32)
+               : group_size == 64 ? CPT_B1_NT16(CACHE_INT4, 64)
+                                  : CPT_B1_NT16(CACHE_INT4, 128);
+      default:
+        return group_size == 32   ? CPT_B1_NT16(CACHE_INT8, 32)
+               : group_size == 64 ? CPT_B1_NT16(CACHE_INT8, 64)
+                                  : CPT_B1_NT16(CACHE_INT8, 128);
+    }
+#undef CPT_B1_NT16
+  }
   switch (cache) {
     case CACHE_BF16:
       return terms ? launch<true, false, EPI_DGLU, CACHE_BF16, 64, 1>(A, st)

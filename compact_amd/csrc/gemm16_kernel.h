@@ -254,7 +254,9 @@ template <bool AK, bool BK, int EPI, int CACHE, int GS, int LT, bool SK>
 __device__ __forceinline__ void nt16_tile(const KArgs& A, uint16_t* lds, int tm, int tn, int kb,
                                           int ke, int role, int sk_s) {
   static_assert(LT == 0 || AK, "adapter terms ride with a K-major A (P's rows are tokens)");
-  static_assert(EPI == EPI_STORE || EPI == EPI_GLU, "epilogues of the 16x16x32 loop");
+  static_assert(EPI == EPI_STORE || EPI == EPI_GLU || EPI == EPI_DGLU,
+                "epilogues of the 16x16x32 loop");
+  static_assert(EPI != EPI_DGLU || (AK && !BK), "B1: gy (K-major) . W_d (MN-major)");
   constexpr bool DUAL = EPI == EPI_GLU;
   static_assert(!DUAL || (AK && BK), "F1's operands are K-major");
   // per-lane values are derived afresh for each tile of a stream-K block:
@@ -475,10 +477,12 @@ __device__ __forceinline__ void nt16_tile(const KArgs& A, uint16_t* lds, int tm,
   const int elane = etid & 63;
   Lora16 F;
   if constexpr (LT > 0) lora16_load<DUAL, LT>(A, m0, n0, wm, wn, elane, F);
-  if constexpr (EPI == EPI_STORE) {
+  if constexpr (EPI == EPI_STORE || EPI == EPI_DGLU) {
     // bf16(acc) is staged as a row-major tile (rows kLdOut apart: 32 lanes of
     // one 8-byte write cover the 64 banks once), then 32 threads store each
-    // 512-byte row.
+    // 512-byte row, or (B1) dglu_finish runs the dequantise + SwiGLU backward
+    // on it row by row.
+    static_assert(kLdOut == kDgluLd, "B1's staged tile layout");
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       // a stream-K finisher adds the other block's partial, 8 blocks at a time
@@ -504,6 +508,10 @@ __device__ __forceinline__ void nt16_tile(const KArgs& A, uint16_t* lds, int tm,
       }
     }
     __syncthreads();
+    if constexpr (EPI == EPI_DGLU) {
+      dglu_finish<CACHE, GS>(A, m0, n0, lds);
+      return;
+    }
     // ragged M and N: rows past M and 8-column pieces past N (N % 8 == 0) stay
     // unwritten; the operand loads read zeros or discarded values there
     const int cl = (etid & 31) * 8;

@@ -1018,16 +1018,19 @@ __device__ __forceinline__ void epi_glu(const KArgs& A, const Acc& acc, int64_t 
 // read the bf16 cache); SwiGLU backward -> grad_h_gate, grad_h_up, h_mid^.
 // n-side = d: d = n0 + 128 wn + 32 i + 8 q + 4 (lane/32) + e.
 // ---------------------------------------------------------------------------
+constexpr int kDgluLd = 264;   // B1's staged tile: LDS row stride in bf16 (528 bytes)
+template <int CACHE, int GS>
+__device__ __forceinline__ void dglu_finish(const KArgs& A, int64_t m0, int64_t n0,
+                                            const uint16_t* lds);
+
 template <int CACHE, int GS, int LT>
 __device__ __forceinline__ void epi_dglu(const KArgs& A, const Acc& acc, int64_t m0, int64_t n0,
                                          uint16_t* lds) {
   // B1: grad_h_mid = bf16(acc) is staged through LDS as a row-major
-  // 256 x 256 bf16 tile, then each row is processed by 32 consecutive threads
-  // owning 8 columns each, so every cache load and output store is a
-  // contiguous, coalesced row segment (the MFMA layout would scatter them
-  // over 32 rows per instruction).
-  constexpr int BITS = CACHE == CACHE_INT4 ? 4 : 8;
-  constexpr int LD = 264;   // LDS row stride in bf16 (528 bytes)
+  // 256 x 256 bf16 tile, then dglu_finish processes it row by row (the MFMA
+  // layout would scatter the cache loads and stores over 32 rows per
+  // instruction).
+  constexpr int LD = kDgluLd;
   const int tid = epi_tid();
   const int lane = tid & 63, wave = tid >> 6;
   const int wn = wave & 1, wm = wave >> 1;
@@ -1045,6 +1048,20 @@ __device__ __forceinline__ void epi_dglu(const KArgs& A, const Acc& acc, int64_t
     });
   });
   __syncthreads();
+  dglu_finish<CACHE, GS>(A, m0, n0, lds);
+}
+
+// B1's second half, shared by both main loops: grad_h_mid (a row-major
+// 256 x 256 bf16 tile in LDS, rows kDgluLd apart) -> dequantised cache ->
+// SwiGLU backward -> grad_h_gate, grad_h_up (and h_mid^).  Each row is
+// processed by 32 consecutive threads owning 8 columns each, so every cache
+// load and output store is a contiguous, coalesced row segment.
+template <int CACHE, int GS>
+__device__ __forceinline__ void dglu_finish(const KArgs& A, int64_t m0, int64_t n0,
+                                            const uint16_t* lds) {
+  constexpr int BITS = CACHE == CACHE_INT4 ? 4 : 8;
+  constexpr int LD = kDgluLd;
+  const int tid = epi_tid();
   const int64_t D = A.D;
   const int64_t G = D / GS;
   const int cl = (tid & 31) * 8;
@@ -1298,8 +1315,18 @@ int launch_nt16(const KArgs& A, hipStream_t st);
   X(true, true, EPI_GLU, CACHE_INT4, 32, 0) X(true, true, EPI_GLU, CACHE_INT4, 32, 2) \
   X(true, true, EPI_GLU, CACHE_INT4, 64, 0) X(true, true, EPI_GLU, CACHE_INT4, 64, 2) \
   X(true, true, EPI_GLU, CACHE_INT4, 128, 0) X(true, true, EPI_GLU, CACHE_INT4, 128, 2)
+#define CPT_NT16_INST_DGLU_A(X)                                              \
+  X(true, false, EPI_DGLU, CACHE_BF16, 64, 0) X(true, false, EPI_DGLU, CACHE_BF16, 64, 1) \
+  X(true, false, EPI_DGLU, CACHE_INT4, 32, 0) X(true, false, EPI_DGLU, CACHE_INT4, 32, 1) \
+  X(true, false, EPI_DGLU, CACHE_INT4, 64, 0) X(true, false, EPI_DGLU, CACHE_INT4, 64, 1) \
+  X(true, false, EPI_DGLU, CACHE_INT4, 128, 0) X(true, false, EPI_DGLU, CACHE_INT4, 128, 1)
+#define CPT_NT16_INST_DGLU_B(X)                                              \
+  X(true, false, EPI_DGLU, CACHE_INT8, 32, 0) X(true, false, EPI_DGLU, CACHE_INT8, 32, 1) \
+  X(true, false, EPI_DGLU, CACHE_INT8, 64, 0) X(true, false, EPI_DGLU, CACHE_INT8, 64, 1) \
+  X(true, false, EPI_DGLU, CACHE_INT8, 128, 0) X(true, false, EPI_DGLU, CACHE_INT8, 128, 1)
 #define CPT_NT16_INST_ALL(X)                                                 \
-  CPT_NT16_INST_STORE(X) CPT_NT16_INST_GLU_A(X) CPT_NT16_INST_GLU_B(X) CPT_NT16_INST_GLU_C(X)
+  CPT_NT16_INST_STORE(X) CPT_NT16_INST_GLU_A(X) CPT_NT16_INST_GLU_B(X) CPT_NT16_INST_GLU_C(X) \
+  CPT_NT16_INST_DGLU_A(X) CPT_NT16_INST_DGLU_B(X)
 #define CPT_NT16_DEFINE(AK, BK, EPI, CACHE, GS, LT) \
   template int launch_nt16<AK, BK, EPI, CACHE, GS, LT>(const KArgs&, hipStream_t);
 #define CPT_NT16_DECLARE(AK, BK, EPI, CACHE, GS, LT) \

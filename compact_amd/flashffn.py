@@ -60,12 +60,14 @@ _FUSED_GROUPS = (32, 64, 128)
 # speed).
 _F1_CODEC_CACHES = ("int8",)
 # Group sizes whose dequantise + SwiGLU backward runs in the dgrad GEMM's
-# epilogue (G.ffn_down_dgrad) instead of the dgrad GEMM followed by the K2
-# kernel.  Empty: on MI355X the fused epilogue (VALU work and 540 MB of writes
-# while the block's MFMAs idle, one wavefront per SIMD) costs more than the
-# standalone K2 at full occupancy: C2 step 5.84 -> 5.77 ms, C3 4.83 -> 4.69 ms
-# unfused.  The fused kernel stays available and tested; add group sizes here
-# to route the Function through it.
+# epilogue (G.ffn_down_dgrad, on the 16x16x32 loop when d_model is a multiple
+# of 64) instead of the dgrad GEMM followed by the K2 kernel.  Empty: on
+# MI355X the fused epilogue (VALU work and 540 MB of writes while the block's
+# MFMAs idle, one wavefront per SIMD) costs more than the standalone K2 at
+# full occupancy.  On the 16x16x32 loop, inside the step: C2 0.816 ms fused
+# against 0.555 + 0.148 ms (step 5.11 against 5.01 ms), C3 0.966 against
+# 0.590 + 0.157 ms (step 4.11 against 3.89 ms).  The fused kernel stays
+# available and tested; add group sizes here to route the Function through it.
 _FUSED_DGRAD_GROUPS = ()
 # The weight gradient of the down projection with the GLU decompressed in the
 # GEMM's operand staging (G.wgrad_glu: h^ formed from the int cache as the TN

@@ -179,10 +179,22 @@ def test_gate_up_fused_ragged_dff(device, cache, bits, group, inter, n_tok, hid)
     test_gate_up_fused_equals_unfused(device, cache, bits, group, n_tok, hid, inter)
 
 
+def plain_like_b1(G, gy, wd):
+    """gy . W_d in the summation order of B1 (the dgrad GEMM with the K2
+    epilogue): the 16x16x32 loop when d_model is a multiple of 64
+    (dgrad_nt16_fits in gemm.hip), where the plain product also runs then
+    (these shapes stay off split-K, the skinny kernel and stream-K), else the
+    engine."""
+    if gy.shape[1] % 64 == 0:
+        assert gy.shape[1] < 1024, "mm would leave the 16x16x32 loop"
+        return G.mm(gy, wd)
+    return G.mm_engine(gy, wd)
+
+
 @pytest.mark.parametrize("cache,bits,group", [("int4", 4, 64), ("int8", 8, 128), ("int4", 4, 32),
                                               ("bf16", 0, 64)])
 @pytest.mark.parametrize("want_h_mid", [True, False])
-@pytest.mark.parametrize("n_tok,hid,inter", [(512, 256, 512), (300, 128, 384)])
+@pytest.mark.parametrize("n_tok,hid,inter", [(512, 256, 512), (300, 128, 384), (300, 136, 384)])
 def test_down_dgrad_fused_equals_unfused(device, cache, bits, group, want_h_mid, n_tok, hid,
                                          inter):
     cpt, G = _cpt()
@@ -195,12 +207,12 @@ def test_down_dgrad_fused_equals_unfused(device, cache, bits, group, want_h_mid,
     if bits:
         _, qg, sg, qu, su = cpt.silu_mul_quant(hg, hu, bits, group)
         dg, du, hm = G.ffn_down_dgrad(gy, wd, code, group, qg, sg, qu, su, want_h_mid)
-        gmid = G.mm_engine(gy, wd)   # B1 runs on the engine
+        gmid = plain_like_b1(G, gy, wd)
         rdg, rdu, rhm = cpt.dequant_swiglu_backward(gmid, qg, sg, qu, su, bits, group,
                                                     want_h_mid=want_h_mid)
     else:
         dg, du, hm = G.ffn_down_dgrad(gy, wd, code, group, hg, None, hu, None, want_h_mid)
-        gmid = G.mm_engine(gy, wd)   # B1 runs on the engine
+        gmid = plain_like_b1(G, gy, wd)
         rdg, rdu, rhm = cpt.swiglu_backward_glu(gmid, hg, hu, want_h_mid)
     assert_gemm_close(gmid, ref_mm(gy, wd))
     assert torch.equal(dg.view(torch.int16), rdg.view(torch.int16))
@@ -209,6 +221,15 @@ def test_down_dgrad_fused_equals_unfused(device, cache, bits, group, want_h_mid,
         assert torch.equal(hm.view(torch.int16), rhm.view(torch.int16))
     else:
         assert hm is None
+
+
+@pytest.mark.parametrize("cache,bits,group,inter", [("bf16", 0, 64, 264), ("int8", 8, 64, 320),
+                                                    ("int4", 4, 32, 320)])
+@pytest.mark.parametrize("want_h_mid", [True, False])
+def test_down_dgrad_fused_ragged_dff(device, cache, bits, group, inter, want_h_mid):
+    """B1 with a partial last d_ff tile: the W_d columns past d_ff read zero
+    and dglu_finish masks them."""
+    test_down_dgrad_fused_equals_unfused(device, cache, bits, group, want_h_mid, 300, 128, inter)
 
 
 def test_c2_shapes_gemm_numerics(device):

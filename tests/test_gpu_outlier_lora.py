@@ -158,7 +158,8 @@ def test_outlier_fused_dgrad_equals_unfused(device, bits, group, with_lora, want
         lora = (gyb, a_d, 2.0)
     dg, du, hm = G.ffn_down_dgrad(gy, wd, bits, group, qg, sg, qu, su, want_h_mid, lora=lora,
                                   outliers=(sg_, og, su_, ou))
-    gmid = G.mm2(gy, wd, lora=[lora]) if with_lora else G.mm_engine(gy, wd)   # B1: the engine
+    # B1 runs on the 16x16x32 loop at d_model 256, as G.mm2 does
+    gmid = G.mm2(gy, wd, lora=[lora]) if with_lora else G.mm2(gy, wd)
     rdg, rdu, rhm = cpt.dequant_swiglu_backward_outlier(gmid, qg, sg, og, sg_, qu, su, ou, su_,
                                                         bits, group, want_h_mid=want_h_mid)
     assert torch.equal(dg.view(torch.int16), rdg.view(torch.int16))
