@@ -47,6 +47,9 @@ SIGNATURES = {
                            _L, _L, _I, _L, _P, _P, ctypes.c_float, _P, _P, ctypes.c_float, _P],
     "cpt_ffn_gate_up_lora": [_P, _P, _P, _L, _L, _L, _I, _L, _P, _P, _P, _P, _P, _P, _P,
                              _L, _L, _P, _P, ctypes.c_float, _P, _P, ctypes.c_float, _P],
+    "cpt_ffn_gate_up_outlier": [_P, _P, _P, _L, _L, _L, _I, _L, _P, _P, _P, _P, _P, _P, _P, _P,
+                                _P, _L, _L, _L, _P, _P, ctypes.c_float, _P, _P, ctypes.c_float,
+                                _P],
     "cpt_ffn_down_dgrad_lora": [_P, _P, _L, _L, _L, _I, _L, _P, _P, _P, _P, _P, _P, _P,
                                 _L, _L, _P, _P, ctypes.c_float, _P],
     "cpt_gemm_bf16_skinny": [_P, _L, _P, _L, _P, _L, _L, _L, _L, ctypes.c_float, _I, _P, _P],

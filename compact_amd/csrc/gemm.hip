@@ -303,10 +303,19 @@ inline bool dgrad_nt16_fits(int64_t n_tok, int64_t inter, int64_t hidden) {
          ((n_tok + 255) / 256) * ((inter + 255) / 256) <= kIntMax;
 }
 
+// outlier channels of the F1 and B1 epilogues (k == 0: none)
+struct OutlierArgs {
+  const void* slot_gate = nullptr;
+  const void* o_gate = nullptr;
+  const void* slot_up = nullptr;
+  const void* o_up = nullptr;
+  int64_t k = 0;
+};
+
 int ffn_gate_up_impl(const void* x, const void* w_gate, const void* w_up, int64_t n_tok,
                      int64_t hidden, int64_t inter, int cache, int64_t group_size, void* h_mid,
                      void* h_gate, void* h_up, void* q_gate, void* s_gate, void* q_up,
-                     void* s_up, const LoraTerms& L, void* stream) {
+                     void* s_up, const LoraTerms& L, const OutlierArgs& O, void* stream) {
   if (n_tok < 0 || hidden < 0 || inter < 0) return kErrShape;
   if (cache != CACHE_NONE && cache != CACHE_BF16 && cache != CACHE_INT4 && cache != CACHE_INT8)
     return kErrBits;
@@ -350,6 +359,30 @@ int ffn_gate_up_impl(const void* x, const void* w_gate, const void* w_up, int64_
   int terms = 0;
   if (const int rc = set_lora(A, L, n_tok, inter, terms)) return rc;
   hipStream_t st = (hipStream_t)stream;
+  if (O.k > 0) {
+    // the outlier channels ride in the codec epilogue of the 16x16x32 loop
+    if (!quant || !ffn_nt16_fits(n_tok, inter, hidden)) return kErrShape;
+    if (!O.slot_gate || !O.slot_up || !O.o_gate || !O.o_up || !al16(O.slot_gate) ||
+        !al16(O.slot_up) || O.k >= 32768 || O.k > inter)
+      return kErrAlign;
+    if (n_tok * O.k >= ((int64_t)1 << 31)) return kErrTooLarge;
+    A.slot_g = (const int16_t*)O.slot_gate;
+    A.slot_u = (const int16_t*)O.slot_up;
+    A.o_g = (uint16_t*)O.o_gate;
+    A.o_u = (uint16_t*)O.o_up;
+    A.k_out = O.k;
+#define CPT_F1O_NT16(CACHE, GS) \
+  (terms ? launch_nt16<true, true, EPI_GLUO, CACHE, GS, 2>(A, st) \
+         : launch_nt16<true, true, EPI_GLUO, CACHE, GS, 0>(A, st))
+    if (cache == CACHE_INT4)
+      return group_size == 32   ? CPT_F1O_NT16(CACHE_INT4, 32)
+             : group_size == 64 ? CPT_F1O_NT16(CACHE_INT4, 64)
+                                : CPT_F1O_NT16(CACHE_INT4, 128);
+    return group_size == 32   ? CPT_F1O_NT16(CACHE_INT8, 32)
+           : group_size == 64 ? CPT_F1O_NT16(CACHE_INT8, 64)
+                              : CPT_F1O_NT16(CACHE_INT8, 128);
+#undef CPT_F1O_NT16
+  }
   // d_model a multiple of 64: the 16x16x32 loop (its summation order is that
   // of cpt_gemm_bf16's products with K a multiple of 64, not of
   // cpt_gemm_bf16_ex mode 0); the dual kernel carries both adapter terms
@@ -387,15 +420,6 @@ int ffn_gate_up_impl(const void* x, const void* w_gate, const void* w_up, int64_
                    : dispatch_gs<EPI_GLU, CACHE_INT8, 0>(group_size, A, st);
   }
 }
-
-// outlier channels of the B1 epilogue (k == 0: none)
-struct OutlierArgs {
-  const void* slot_gate = nullptr;
-  const void* o_gate = nullptr;
-  const void* slot_up = nullptr;
-  const void* o_up = nullptr;
-  int64_t k = 0;
-};
 
 int ffn_down_dgrad_impl(const void* grad_y, const void* w_down, int64_t n_tok, int64_t hidden,
                         int64_t inter, int cache, int64_t group_size, const void* c_gate,
@@ -454,8 +478,8 @@ int ffn_down_dgrad_impl(const void* grad_y, const void* w_down, int64_t n_tok, i
     if (n_tok * O.k >= ((int64_t)1 << 31)) return kErrTooLarge;
     A.slot_g = (const int16_t*)O.slot_gate;
     A.slot_u = (const int16_t*)O.slot_up;
-    A.o_g = (const uint16_t*)O.o_gate;
-    A.o_u = (const uint16_t*)O.o_up;
+    A.o_g = (uint16_t*)O.o_gate;
+    A.o_u = (uint16_t*)O.o_up;
     A.k_out = O.k;
   }
   int terms = 0;
@@ -670,7 +694,7 @@ int cpt_ffn_gate_up(const void* x, const void* w_gate, const void* w_up, int64_t
                     void* h_gate, void* h_up, void* q_gate, void* s_gate, void* q_up,
                     void* s_up, void* stream) {
   return ffn_gate_up_impl(x, w_gate, w_up, n_tok, hidden, inter, cache, group_size, h_mid, h_gate,
-                          h_up, q_gate, s_gate, q_up, s_up, LoraTerms{}, stream);
+                          h_up, q_gate, s_gate, q_up, s_up, LoraTerms{}, OutlierArgs{}, stream);
 }
 
 int cpt_ffn_gate_up_lora(const void* x, const void* w_gate, const void* w_up, int64_t n_tok,
@@ -685,7 +709,27 @@ int cpt_ffn_gate_up_lora(const void* x, const void* w_gate, const void* w_up, in
   L.p[0] = p_gate; L.q[0] = b_gate; L.alpha[0] = alpha_gate;
   L.p[1] = p_up; L.q[1] = b_up; L.alpha[1] = alpha_up;
   return ffn_gate_up_impl(x, w_gate, w_up, n_tok, hidden, inter, cache, group_size, h_mid, h_gate,
-                          h_up, q_gate, s_gate, q_up, s_up, L, stream);
+                          h_up, q_gate, s_gate, q_up, s_up, L, OutlierArgs{}, stream);
+}
+
+int cpt_ffn_gate_up_outlier(const void* x, const void* w_gate, const void* w_up, int64_t n_tok,
+                            int64_t hidden, int64_t inter, int cache, int64_t group_size,
+                            void* h_mid, void* q_gate, void* s_gate, void* q_up, void* s_up,
+                            const void* slot_gate, void* o_gate, const void* slot_up, void* o_up,
+                            int64_t k, int64_t rank, int64_t ldp, const void* p_gate,
+                            const void* b_gate, float alpha_gate, const void* p_up,
+                            const void* b_up, float alpha_up, void* stream) {
+  if (k <= 0 || rank < 0) return kErrShape;
+  LoraTerms L;
+  if (rank > 0) {
+    L.rank = (int)rank; L.ldp = ldp; L.q_kmajor = 1;
+    L.p[0] = p_gate; L.q[0] = b_gate; L.alpha[0] = alpha_gate;
+    L.p[1] = p_up; L.q[1] = b_up; L.alpha[1] = alpha_up;
+  }
+  OutlierArgs O;
+  O.slot_gate = slot_gate; O.o_gate = o_gate; O.slot_up = slot_up; O.o_up = o_up; O.k = k;
+  return ffn_gate_up_impl(x, w_gate, w_up, n_tok, hidden, inter, cache, group_size, h_mid,
+                          nullptr, nullptr, q_gate, s_gate, q_up, s_up, L, O, stream);
 }
 
 int cpt_ffn_down_dgrad(const void* grad_y, const void* w_down, int64_t n_tok, int64_t hidden,

@@ -254,10 +254,10 @@ template <bool AK, bool BK, int EPI, int CACHE, int GS, int LT, bool SK>
 __device__ __forceinline__ void nt16_tile(const KArgs& A, uint16_t* lds, int tm, int tn, int kb,
                                           int ke, int role, int sk_s) {
   static_assert(LT == 0 || AK, "adapter terms ride with a K-major A (P's rows are tokens)");
-  static_assert(EPI == EPI_STORE || EPI == EPI_GLU || EPI == EPI_DGLU,
+  static_assert(EPI == EPI_STORE || EPI == EPI_GLU || EPI == EPI_DGLU || EPI == EPI_GLUO,
                 "epilogues of the 16x16x32 loop");
   static_assert(EPI != EPI_DGLU || (AK && !BK), "B1: gy (K-major) . W_d (MN-major)");
-  constexpr bool DUAL = EPI == EPI_GLU;
+  constexpr bool DUAL = EPI == EPI_GLU || EPI == EPI_GLUO;
   static_assert(!DUAL || (AK && BK), "F1's operands are K-major");
   // per-lane values are derived afresh for each tile of a stream-K block:
   // hoisted out of its tile loop they would stay live across the main loop
@@ -540,7 +540,7 @@ __device__ __forceinline__ void nt16_tile(const KArgs& A, uint16_t* lds, int tm,
             make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
       }
     __syncthreads();
-    glu_finish<CACHE, GS>(A, m0, n0, lds);
+    glu_finish<CACHE, GS, EPI == EPI_GLUO>(A, m0, n0, lds);
   }
 }
 

@@ -156,8 +156,8 @@ struct KArgs {
   // value o[m * k_out + slot] after the dequantisation (slot_g null: none)
   const int16_t* slot_g;
   const int16_t* slot_u;
-  const uint16_t* o_g;
-  const uint16_t* o_u;
+  uint16_t* o_g;           // (F1 with outliers writes them, B1 reads them)
+  uint16_t* o_u;
   int64_t k_out;
   int64_t lgs;             // group size of the int cache a BQ operand is the GLU of
   // low-rank adapter terms applied as the epilogue reads the accumulators
@@ -181,7 +181,8 @@ struct KArgs {
   int* sk_flags;
 };
 
-enum Epi { EPI_STORE = 0, EPI_GLU = 1, EPI_DGLU = 2, EPI_ADD = 3, EPI_F32 = 4 };
+// EPI_GLUO: F1 with the outlier channels in its codec (16x16x32 loop only)
+enum Epi { EPI_STORE = 0, EPI_GLU = 1, EPI_DGLU = 2, EPI_ADD = 3, EPI_F32 = 4, EPI_GLUO = 5 };
 enum Cache { CACHE_NONE = 0, CACHE_BF16 = 1, CACHE_INT4 = 4, CACHE_INT8 = 8 };
 
 // ---------------------------------------------------------------------------
@@ -899,12 +900,17 @@ __device__ __forceinline__ void epi_f32(const KArgs& A, const Acc& acc, int64_t 
 constexpr int kGluLd = 136;               // LDS row stride in bf16 (272 bytes)
 constexpr int kGluLdsBytes = 2 * 256 * kGluLd * 2;
 
-template <int CACHE, int GS>
+// OUTL (int caches): the outlier channels of config C3 (A.slot_g / slot_u,
+// A.o_g / o_u, A.k_out): a column with slot >= 0 is copied out as bf16 to
+// o[m * k_out + slot] and zeroed before the group absmax, after h_mid took
+// its value (the standalone K1 with outliers, HyC-LoRA's zero-and-store).
+template <int CACHE, int GS, bool OUTL = false>
 __device__ __forceinline__ void glu_finish(const KArgs& A, int64_t m0, int64_t n0,
                                            const uint16_t* lds) {
   static_assert(GS >= 8 && GS <= 128 && 128 % GS == 0, "group must divide the 128-column tile");
   constexpr int BITS = CACHE == CACHE_INT4 ? 4 : 8;
   constexpr bool QUANT = CACHE == CACHE_INT4 || CACHE == CACHE_INT8;
+  static_assert(!OUTL || QUANT, "outlier channels ride with an int cache");
   constexpr int LD = kGluLd;
   const int tid = epi_tid();
   const uint16_t* sg = lds;
@@ -914,6 +920,24 @@ __device__ __forceinline__ void glu_finish(const KArgs& A, int64_t m0, int64_t n
   const int cl = (tid & 15) * 8;
   const int64_t d = (n0 >> 1) + cl;        // D % 8 == 0: 8 columns all in or all out
   const bool dok = d < D;
+  // this thread's 8 columns are the same in every row: their slots once
+  int slg[8], slu[8];
+  uint32_t mkg = 0, mku = 0;
+  if constexpr (OUTL) {
+    uint4 wg = make_uint4(0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu), wu = wg;
+    if (dok) {
+      wg = *reinterpret_cast<const uint4*>(A.slot_g + d);
+      wu = *reinterpret_cast<const uint4*>(A.slot_u + d);
+    }
+    const uint32_t ag[4] = {wg.x, wg.y, wg.z, wg.w}, au[4] = {wu.x, wu.y, wu.z, wu.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      slg[e] = (int16_t)((ag[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+      slu[e] = (int16_t)((au[e >> 1] >> (16 * (e & 1))) & 0xFFFFu);
+      mkg |= (slg[e] >= 0 ? 1u : 0u) << e;
+      mku |= (slu[e] >= 0 ? 1u : 0u) << e;
+    }
+  }
 #pragma unroll 2
   for (int p = 0; p < 16; ++p) {
     const int r = p * 16 + (tid >> 4);
@@ -942,6 +966,22 @@ __device__ __forceinline__ void glu_finish(const KArgs& A, int64_t m0, int64_t n
       if (ok) {
         *reinterpret_cast<uint4*>(A.h_gate + off) = wg;
         *reinterpret_cast<uint4*>(A.h_up + off) = wu;
+      }
+    }
+    if constexpr (OUTL) {
+      if (ok && (mkg | mku)) {
+        uint16_t* og = A.o_g + m * A.k_out;
+        uint16_t* ou = A.o_u + m * A.k_out;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if ((mkg >> e) & 1u) og[slg[e]] = (uint16_t)f32_to_bf16_bits(g[e]);
+          if ((mku >> e) & 1u) ou[slu[e]] = (uint16_t)f32_to_bf16_bits(u[e]);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        g[e] = ((mkg >> e) & 1u) ? 0.0f : g[e];
+        u[e] = ((mku >> e) & 1u) ? 0.0f : u[e];
       }
     }
     if constexpr (QUANT) {
@@ -1324,9 +1364,16 @@ int launch_nt16(const KArgs& A, hipStream_t st);
   X(true, false, EPI_DGLU, CACHE_INT8, 32, 0) X(true, false, EPI_DGLU, CACHE_INT8, 32, 1) \
   X(true, false, EPI_DGLU, CACHE_INT8, 64, 0) X(true, false, EPI_DGLU, CACHE_INT8, 64, 1) \
   X(true, false, EPI_DGLU, CACHE_INT8, 128, 0) X(true, false, EPI_DGLU, CACHE_INT8, 128, 1)
+#define CPT_NT16_INST_GLUO(X)                                                \
+  X(true, true, EPI_GLUO, CACHE_INT4, 32, 0) X(true, true, EPI_GLUO, CACHE_INT4, 32, 2) \
+  X(true, true, EPI_GLUO, CACHE_INT4, 64, 0) X(true, true, EPI_GLUO, CACHE_INT4, 64, 2) \
+  X(true, true, EPI_GLUO, CACHE_INT4, 128, 0) X(true, true, EPI_GLUO, CACHE_INT4, 128, 2) \
+  X(true, true, EPI_GLUO, CACHE_INT8, 32, 0) X(true, true, EPI_GLUO, CACHE_INT8, 32, 2) \
+  X(true, true, EPI_GLUO, CACHE_INT8, 64, 0) X(true, true, EPI_GLUO, CACHE_INT8, 64, 2) \
+  X(true, true, EPI_GLUO, CACHE_INT8, 128, 0) X(true, true, EPI_GLUO, CACHE_INT8, 128, 2)
 #define CPT_NT16_INST_ALL(X)                                                 \
   CPT_NT16_INST_STORE(X) CPT_NT16_INST_GLU_A(X) CPT_NT16_INST_GLU_B(X) CPT_NT16_INST_GLU_C(X) \
-  CPT_NT16_INST_DGLU_A(X) CPT_NT16_INST_DGLU_B(X)
+  CPT_NT16_INST_DGLU_A(X) CPT_NT16_INST_DGLU_B(X) CPT_NT16_INST_GLUO(X)
 #define CPT_NT16_DEFINE(AK, BK, EPI, CACHE, GS, LT) \
   template int launch_nt16<AK, BK, EPI, CACHE, GS, LT>(const KArgs&, hipStream_t);
 #define CPT_NT16_DECLARE(AK, BK, EPI, CACHE, GS, LT) \

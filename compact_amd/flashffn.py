@@ -59,6 +59,19 @@ _FUSED_GROUPS = (32, 64, 128)
 # code stores cost more inside the power-limited GEMM than K1 does at HBM
 # speed).
 _F1_CODEC_CACHES = ("int8",)
+# Outlier channels (config C3) with a bf16 activation and d_model a multiple
+# of 64.  True: the first sequence (which ranks the channels) runs the dual
+# GEMM with a bf16 output, the selection and K1 with outliers, and every
+# later row the dual GEMM with the outlier codec in its epilogue
+# (G.ffn_gate_up_outlier), so only h_mid and the compressed cache of those
+# rows reach HBM.  False (the default): the dual GEMM with a bf16 output for
+# every row, then the selection and K1 with outliers.  The caches, outputs
+# and gradients are bit-identical.  Measured at C3 on MI355X: forward 1.99
+# against 1.89 ms, step 4.11 against 4.01 ms (the two dual GEMMs 1.347 ms
+# against 1.089 + 0.137 for one dual GEMM and K1): the int4 outlier codec
+# inside the power-limited GEMM, and the first sequence's 1.34 waves of
+# tiles, cost more than the 720 MB bf16 round trip at HBM speed.
+_F1_OUTLIER_FUSED = False
 # Group sizes whose dequantise + SwiGLU backward runs in the dgrad GEMM's
 # epilogue (G.ffn_down_dgrad, on the 16x16x32 loop when d_model is a multiple
 # of 64) instead of the dgrad GEMM followed by the K2 kernel.  Empty: on
@@ -248,6 +261,41 @@ class FlashFFNv3Function(torch.autograd.Function):
             h_mid, _, _, c_gate, qs_gate, c_up, qs_up = G.ffn_gate_up(
                 x_2d, w_gate, w_up, _CACHE_CODE[cache_mode], group_size, **lkw)
             _V3_COUNTERS["triton_quant_fwd"] += 1
+        elif (fusable and fused_quant and k_out > 0 and _F1_OUTLIER_FUSED
+              and group_size in _FUSED_GROUPS and G.ffn_gate_up_outlier_fits(hidden_dim)
+              and outlier_stat_rows(orig_shape) < x_2d.shape[0]):
+            # outlier channels: the first sequence ranks them, so its rows get
+            # the dual GEMM with a bf16 epilogue, the selection and K1 with
+            # outliers; every later row runs the dual GEMM with the outlier
+            # codec in its epilogue (only h_mid and the compressed cache reach
+            # HBM for them)
+            rows = outlier_stat_rows(orig_shape)
+            n_all = x_2d.shape[0]
+            lk_first, lk_rest = {}, {}
+            for key, term in lkw.items():
+                lk_first[key] = None if term is None else (term[0][:rows], term[1], term[2])
+                lk_rest[key] = None if term is None else (term[0][rows:], term[1], term[2])
+            _, hg1, hu1, *_ = G.ffn_gate_up(x_2d[:rows], w_gate, w_up, _lib.CACHE_BF16,
+                                            group_size, want_h_mid=False, **lk_first)
+            (slot_gate, _), (slot_up, _) = K.outlier_select_pair(hg1, hu1, k_out, rows)
+            bits = _bits(cache_mode)
+            dev = x.device
+            qshape = (n_all, inter // 2) if bits == 4 else (n_all, inter)
+            qdt = torch.uint8 if bits == 4 else torch.int8
+            h_mid = torch.empty((n_all, inter), dtype=x.dtype, device=dev)
+            c_gate = torch.empty(qshape, dtype=qdt, device=dev)
+            c_up = torch.empty(qshape, dtype=qdt, device=dev)
+            qs_gate = torch.empty((n_all, inter // group_size), dtype=torch.float16, device=dev)
+            qs_up = torch.empty((n_all, inter // group_size), dtype=torch.float16, device=dev)
+            o_gate = torch.empty((n_all, k_out), dtype=torch.bfloat16, device=dev)
+            o_up = torch.empty((n_all, k_out), dtype=torch.bfloat16, device=dev)
+            bufs = (h_mid, c_gate, qs_gate, o_gate, c_up, qs_up, o_up)
+            K.silu_mul_quant_outlier(hg1, hu1, bits, group_size, slot_gate, slot_up, k_out,
+                                     out=tuple(t[:rows] for t in bufs))
+            del hg1, hu1
+            G.ffn_gate_up_outlier(x_2d[rows:], w_gate, w_up, _CACHE_CODE[cache_mode], group_size,
+                                  slot_gate, slot_up, k_out, tuple(t[rows:] for t in bufs),
+                                  **lk_rest)
         elif fusable and not fused_quant and k_out == 0:
             # h_gate/h_up are needed (bf16 cache, eager codec) or not (recompute)
             keep = cache_mode != "recompute"

@@ -494,6 +494,54 @@ def ffn_gate_up(x, w_gate, w_up, cache: int, group_size: int, want_h_mid: bool =
     return h_mid, hg, hu, qg, sg, qu, su
 
 
+def ffn_gate_up_outlier_fits(hidden: int) -> bool:
+    """The outlier-codec epilogue runs on the 16x16x32 loop: d_model a
+    multiple of 64."""
+    return hidden > 0 and hidden % 64 == 0
+
+
+def ffn_gate_up_outlier(x, w_gate, w_up, cache: int, group_size: int, slot_gate, slot_up,
+                        k: int, out, lora_gate=None, lora_up=None):
+    """Fused dual GEMM + GLU + int codec with config C3's outlier channels
+    (cpt_ffn_gate_up_outlier): writes into `out` = (h_mid, q_gate, s_gate,
+    o_gate, q_up, s_up, o_up), preallocated (row slices of the Function's
+    buffers are fine); the slot maps come from an outlier selection."""
+    _require_device(x, w_gate, w_up, slot_gate, slot_up)
+    _check_bf16(x, w_gate, w_up)
+    n, hdim = x.shape
+    d = w_gate.shape[0]
+    assert w_gate.shape == (d, hdim) and w_up.shape == (d, hdim)
+    assert cache in (_lib.CACHE_INT4, _lib.CACHE_INT8) and k > 0
+    x, w_gate, w_up = x.contiguous(), w_gate.contiguous(), w_up.contiguous()
+    h_mid, qg, sg, og, qu, su, ou = out
+    for t, shape in ((h_mid, (n, d)), (sg, (n, d // group_size)), (su, (n, d // group_size)),
+                     (og, (n, k)), (ou, (n, k)),
+                     (qg, (n, d // 2) if cache == _lib.CACHE_INT4 else (n, d)),
+                     (qu, (n, d // 2) if cache == _lib.CACHE_INT4 else (n, d))):
+        assert tuple(t.shape) == shape and t.is_contiguous(), (tuple(t.shape), shape)
+    assert slot_gate.dtype == torch.int16 and slot_gate.shape == (d,) and slot_up.shape == (d,)
+    rank = ldp = 0
+    t = [(None, None, 0.0), (None, None, 0.0)]
+    keep = None
+    if lora_gate is not None or lora_up is not None:
+        present = [tt for tt in (lora_gate, lora_up) if tt is not None]
+        rank, ldp, qk, _, t, keep = _lora_args([(xa, bw.t(), sc) for xa, bw, sc in present], d)
+        assert qk == 1, "the gate/up adapter B factors go K-major"
+        if lora_gate is None:
+            t = [(None, None, 0.0), t[0]]
+        elif lora_up is None:
+            t = [t[0], (None, None, 0.0)]
+    with _timed("ffn_gate_up"):
+        rc = _lib.lib().cpt_ffn_gate_up_outlier(
+            x.data_ptr(), w_gate.data_ptr(), w_up.data_ptr(), n, hdim, d, cache, group_size,
+            h_mid.data_ptr(), qg.data_ptr(), sg.data_ptr(), qu.data_ptr(), su.data_ptr(),
+            slot_gate.data_ptr(), og.data_ptr(), slot_up.data_ptr(), ou.data_ptr(), k, rank, ldp,
+            t[0][0], t[0][1], t[0][2], t[1][0], t[1][1], t[1][2], _stream(x))
+    del keep
+    check(rc, "ffn_gate_up_outlier")
+    return out
+
+
 def ffn_down_dgrad(grad_y, w_down, cache: int, group_size: int, c_gate, s_gate, c_up, s_up,
                    want_h_mid: bool, lora=None, outliers=None, inplace: bool = False):
     """Fused grad_y @ w_down + dequantise + SwiGLU backward.

@@ -394,20 +394,29 @@ def v3_dequantize_outlier(payload, scales, outliers, slot, bits, group_size):
     return out
 
 
-def silu_mul_quant_outlier(h_gate, h_up, bits, group_size, slot_gate, slot_up, k):
+def silu_mul_quant_outlier(h_gate, h_up, bits, group_size, slot_gate, slot_up, k, out=None):
     """K1 with outlier channels.  Returns
-    (h_mid, q_gate, s_gate, o_gate, q_up, s_up, o_up)."""
+    (h_mid, q_gate, s_gate, o_gate, q_up, s_up, o_up), written into `out`
+    (the same seven, preallocated and contiguous) when given."""
     _require_device(h_gate, h_up, slot_gate, slot_up)
     n, d, g = _check_quant_shapes(h_gate, bits, group_size)
     assert h_up.shape == h_gate.shape and h_up.is_contiguous()
     dev = h_gate.device
-    h_mid = torch.empty_like(h_gate)
     shape = (n, d // 2) if bits == 4 else (n, d)
     qdt = torch.uint8 if bits == 4 else torch.int8
-    qg, qu = torch.empty(shape, dtype=qdt, device=dev), torch.empty(shape, dtype=qdt, device=dev)
-    sg = torch.empty((n, g), dtype=torch.float16, device=dev)
-    su = torch.empty((n, g), dtype=torch.float16, device=dev)
-    og, ou = _outlier_buf(n, k, dev), _outlier_buf(n, k, dev)
+    if out is not None:
+        h_mid, qg, sg, og, qu, su, ou = out
+        for t, shp, dt in ((h_mid, (n, d), h_gate.dtype), (qg, shape, qdt), (qu, shape, qdt),
+                           (sg, (n, g), torch.float16), (su, (n, g), torch.float16),
+                           (og, (n, k), torch.bfloat16), (ou, (n, k), torch.bfloat16)):
+            assert tuple(t.shape) == shp and t.dtype == dt and t.is_contiguous()
+    else:
+        h_mid = torch.empty_like(h_gate)
+        qg = torch.empty(shape, dtype=qdt, device=dev)
+        qu = torch.empty(shape, dtype=qdt, device=dev)
+        sg = torch.empty((n, g), dtype=torch.float16, device=dev)
+        su = torch.empty((n, g), dtype=torch.float16, device=dev)
+        og, ou = _outlier_buf(n, k, dev), _outlier_buf(n, k, dev)
     with _timed("silu_mul_quant_outlier"):
         rc = _lib.lib().cpt_silu_mul_quant_outlier(
             h_gate.data_ptr(), h_up.data_ptr(), n, d, bits, group_size, slot_gate.data_ptr(),

@@ -305,6 +305,25 @@ int cpt_ffn_gate_up_lora(const void* x, const void* w_gate, const void* w_up, in
                          const void* b_gate, float alpha_gate, const void* p_up,
                          const void* b_up, float alpha_up, void* stream);
 
+/* cpt_ffn_gate_up (with LoRA terms when rank > 0, as cpt_ffn_gate_up_lora)
+ * for an int4/int8 cache with config C3's outlier channels in the codec:
+ * the forward half of K1 with outliers (cpt_silu_mul_quant_outlier, the
+ * reference's HyC-LoRA extraction, hyclora/operators/compress_function.py:
+ * 111-143) fused into the dual GEMM's epilogue, so only h_mid, codes, scales
+ * and the [n_tok, k] bf16 outlier blocks reach HBM.  slot_gate / slot_up:
+ * int16 [inter] slot maps (-1 for ordinary columns, 16-byte aligned) from
+ * cpt_outlier_select; a column with slot s >= 0 is copied to o[m * k + s]
+ * and zeroed before the group absmax.  Bit-equal to the dual GEMM with a bf16
+ * output followed by cpt_silu_mul_quant_outlier.  d_model a multiple of 64
+ * (the 16x16x32 loop), else CPT_ERR_SHAPE. */
+int cpt_ffn_gate_up_outlier(const void* x, const void* w_gate, const void* w_up, int64_t n_tok,
+                            int64_t hidden, int64_t inter, int cache, int64_t group_size,
+                            void* h_mid, void* q_gate, void* s_gate, void* q_up, void* s_up,
+                            const void* slot_gate, void* o_gate, const void* slot_up, void* o_up,
+                            int64_t k, int64_t rank, int64_t ldp, const void* p_gate,
+                            const void* b_gate, float alpha_gate, const void* p_up,
+                            const void* b_up, float alpha_up, void* stream);
+
 /* Weight gradient of the down projection with the GLU decompressed in the
  * GEMM's operand staging (replaces K2's h_mid^ output and gy^T @ h_mid_hat,
  * src/flashffn.py:1538-1543): C[hidden, inter] (bf16, rows ldc apart) =

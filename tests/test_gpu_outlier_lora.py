@@ -287,3 +287,79 @@ def test_stacked_adapter_products_bitwise(device, monkeypatch, ratio, rank, s_up
     assert set(got) == set(want)
     for k in want:
         assert torch.equal(got[k].view(torch.int16), want[k].view(torch.int16)), k
+
+
+@pytest.mark.parametrize("bits,group", [(4, 64), (4, 32), (8, 128)])
+@pytest.mark.parametrize("with_lora", [False, True])
+@pytest.mark.parametrize("n,hdim,d", [(384, 256, 1024), (300, 128, 320)])
+def test_gate_up_outlier_epilogue_equals_k1(device, bits, group, with_lora, n, hdim, d):
+    """F1 with the outlier channels in its codec epilogue equals the dual GEMM
+    with a bf16 output (same loop, same accumulators) followed by K1 with
+    outliers, bit for bit: h_mid, codes, scales and outlier blocks.  The
+    (300, 128, 320) case has ragged token and d_ff tiles."""
+    if d % group:
+        pytest.skip("d_ff not a multiple of the group")
+    cpt, G = _cpt()
+    from compact_amd import _lib
+    gen = torch.Generator(device=device).manual_seed(21)
+    x = torch.randn(n, hdim, device=device, generator=gen).to(torch.bfloat16)
+    wg = (torch.randn(d, hdim, device=device, generator=gen) * 0.05).to(torch.bfloat16)
+    wu = (torch.randn(d, hdim, device=device, generator=gen) * 0.05).to(torch.bfloat16)
+    wg[7] *= 30
+    wu[(d * 3) // 4] *= 25            # hot channels, as in a trained model
+    lk = {}
+    if with_lora:
+        xa_g = (torch.randn(n, 16, device=device, generator=gen) * 0.3).to(torch.bfloat16)
+        xa_u = (torch.randn(n, 16, device=device, generator=gen) * 0.3).to(torch.bfloat16)
+        bg = (torch.randn(d, 16, device=device, generator=gen) * 0.05).to(torch.bfloat16)
+        bu = (torch.randn(d, 16, device=device, generator=gen) * 0.05).to(torch.bfloat16)
+        lk = dict(lora_gate=(xa_g, bg, 2.0), lora_up=(xa_u, bu, 2.0))
+    k = max(1, int(d * 0.01))
+    _, hg, hu, *_ = G.ffn_gate_up(x, wg, wu, _lib.CACHE_BF16, group, want_h_mid=False, **lk)
+    (slot_g, _), (slot_u, _) = cpt.outlier_select_pair(hg, hu, k)
+    ref = cpt.silu_mul_quant_outlier(hg, hu, bits, group, slot_g, slot_u, k)
+    out = tuple(torch.empty_like(t) for t in ref)
+    code = _lib.CACHE_INT4 if bits == 4 else _lib.CACHE_INT8
+    G.ffn_gate_up_outlier(x, wg, wu, code, group, slot_g, slot_u, k, out, **lk)
+    for got, want in zip(out, ref):
+        assert torch.equal(got.view(torch.uint8), want.view(torch.uint8))
+
+
+@pytest.mark.parametrize("mode,group", [("int4", 64), ("int8", 128)])
+def test_function_outlier_epilogue_route(device, mode, group):
+    """The Function's two routes for outlier channels (the rows after the
+    first sequence through the outlier-codec epilogue, or every row through a
+    bf16 dual GEMM + K1) give the same y, gradients and saved cache bit for
+    bit, with LoRA on gate/up/down and a [4, 96, 256] input (first sequence:
+    96 rows)."""
+    cpt, _ = _cpt()
+    from compact_amd import flashffn as FF
+    default = FF._F1_OUTLIER_FUSED
+    ps = R.synthetic_param_set("all", 256, 512, 16, 2.0, seed=23, dtype=torch.bfloat16,
+                               device=device, peft_init=True, b_std=0.01)
+    gen = torch.Generator(device=device).manual_seed(24)
+    x = torch.randn(4, 96, 256, device=device, generator=gen).to(torch.bfloat16)
+    gy = torch.randn(4, 96, 256, device=device, generator=gen).to(torch.bfloat16)
+    res = {}
+    for fused in (True, False):
+        FF._F1_OUTLIER_FUSED = fused
+        saved = []
+
+        def pack(t):
+            saved.append(t.detach().clone())
+            return t
+        with torch.autograd.graph.saved_tensors_hooks(pack, lambda t: t):
+            got, y = R.run_function_grads(cpt.FlashFFNv3Function.apply, ps, x, gy, mode, group,
+                                          True, 0.01)
+        res[fused] = (got, y, saved)
+    FF._F1_OUTLIER_FUSED = default
+    (g1, y1, s1), (g0, y0, s0) = res[True], res[False]
+    assert torch.equal(y1.view(torch.int16), y0.view(torch.int16))
+    assert set(g1) == set(g0)
+    for kk in g1:
+        assert torch.equal(g1[kk].view(torch.int16), g0[kk].view(torch.int16)), kk
+    assert len(s1) == len(s0)
+    for a, b in zip(s1, s0):
+        assert a.shape == b.shape and a.dtype == b.dtype
+        assert torch.equal(a.view(torch.uint8) if a.dtype != torch.bool else a,
+                           b.view(torch.uint8) if b.dtype != torch.bool else b)
