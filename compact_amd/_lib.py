@@ -65,6 +65,8 @@ SIGNATURES = {
     "cpt_topk_abs": [_P, _I, _L, _L, _L, _P, _P, _P],
     "cpt_topk_scatter": [_P, _P, _I, _L, _L, _L, _P, _P],
     "cpt_gemm_stream_k_workspace": [_P, _L],
+    "cpt_gemm_bf16_skinny_dual": [_P, _L, _P, _L, _P, _L, _P, _L, ctypes.c_float, _P, _L, _I,
+                                  ctypes.c_float, _L, _L, _L, _I, _P, _P],
 }
 
 # size queries: name -> argument types (restype int64)
@@ -72,6 +74,7 @@ SIZE_QUERIES = {
     "cpt_col_dot_workspace_bytes": [_L, _L],
     "cpt_dora_col_norm_workspace_bytes": [_L, _L],
     "cpt_gemm_stream_k_bytes": [],
+    "cpt_gemm_bf16_skinny_dual_workspace_bytes": [_L, _L, _L, _I],
 }
 
 CACHE_NONE, CACHE_BF16, CACHE_INT4, CACHE_INT8 = 0, 1, 4, 8

@@ -335,6 +335,148 @@ __global__ __launch_bounds__(256) void skinny_red_reduce_kernel(const float* __r
   out[trans ? r * ldo + n : n * ldo + r] = (uint16_t)f32_to_bf16_bits(alpha * sum);
 }
 
+// ---------------------------------------------------------------------------
+// Both adapter products of one token-major operand in one pass over it:
+//   C[T, R] = X[T, N] . Q^T  (Q [R, N]: the projection, X B)
+//   Z[N, R] = X^T . P        (P [T, R]: the token reduction, X^T (x A^T))
+// The backward of a LoRA projection needs both of one tensor: grad_h_gate B_g
+// and s grad_h_gate^T (x A_g^T) (src/flashffn.py:1556-1557,1575-1582), likewise
+// grad_h_up, and grad_y B_d with s grad_y^T (h_mid A_d^T) (:1521,1538-1545).
+// Apart they read the [T, N] operand (up to 180 MB) twice.
+//
+// Block (column block cb, token split ts): 512 columns and the split's
+// tokens, 64 at a time.  Each piece [64 tokens x 512 columns] goes through LDS
+// once (rows kDualLd apart) and feeds
+//   - the projection: wavefront w takes the piece's tokens 16 w .. 16 w + 15
+//     over all 512 columns (Q's fragments for them loaded once: the block's
+//     columns are fixed), a [16, R] partial written as the column block's
+//     partial of those C rows (ws_c[cb][t][r]);
+//   - the reduction: wavefront w takes columns 128 w .. 128 w + 127 (8 blocks
+//     of 16) over the piece's 64 tokens, accumulated over every piece of the
+//     split (fragments through ds_read_b64_tr_b16, as skinny_red_kernel) and
+//     written once as the split's partial of Z (ws_z[ts][n][r]).
+// The next piece loads into registers while this one is used.  The partials
+// are then summed in split order (deterministic) by the two reduce kernels.
+// ---------------------------------------------------------------------------
+constexpr int kDualCols = 512;   // X columns per block
+constexpr int kDualTok = 64;     // tokens per piece (16 per wavefront for the projection)
+constexpr int kDualLd = 520;     // LDS row stride of the X piece (elements)
+constexpr int kDualLdP = 40;     // LDS row stride of the P piece (elements)
+
+template <int NB>
+__global__ __launch_bounds__(256) void skinny_dual_kernel(
+    const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ q, int64_t ldq,
+    const uint16_t* __restrict__ p, int64_t ldp, int64_t T, int64_t N, int R, int64_t tchunk,
+    float* __restrict__ ws_c, float* __restrict__ ws_z) {
+  __shared__ __attribute__((aligned(16))) uint16_t xs[kDualTok * kDualLd];
+  __shared__ __attribute__((aligned(16))) uint16_t ps[kDualTok * kDualLdP];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cb = blockIdx.x, ts = blockIdx.y;
+  const int64_t n0 = (int64_t)cb * kDualCols;
+  const int64_t t_begin = (int64_t)ts * tchunk;
+  const int64_t t_end = min(T, t_begin + tchunk);
+  // X and P from the split's first token (32-bit offsets: the host checks the
+  // split plus one piece stays below 2 GiB); tokens past t_end and columns
+  // past N read zero (offsets past the records)
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + t_begin * ldx, (T - t_begin) * ldx * 2);
+  const __amdgpu_buffer_rsrc_t rp = make_rsrc(p + t_begin * ldp, (T - t_begin) * ldp * 2);
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(q, (int64_t)R * ldq * 2);
+  // X piece loads: 16 per thread, row 4 i + tid / 64, 16-byte chunk tid % 64
+  const int xr = tid >> 6, xc = (tid & 63) * 8;
+  const bool xok = n0 + xc < N;
+  // P piece: row tid / 4, chunk tid % 4 (R <= 32)
+  const int pr = tid >> 2, pc = (tid & 3) * 8;
+  const bool pok = pc < R;
+  // Q fragments of the block's 512 columns: k-step st (32 columns), term t
+  bf16x8 qf[16][NB];
+#pragma unroll
+  for (int st = 0; st < 16; ++st)
+#pragma unroll
+    for (int t = 0; t < NB; ++t) {
+      const int64_t col = n0 + st * 32 + 8 * (lane >> 4);
+      const int r = t * 16 + (lane & 15);
+      qf[st][t] = bload(rq, col < N && r < R ? (uint32_t)(((int64_t)r * ldq + col) * 2) : kOOB);
+    }
+  f32x4 az[8][NB];
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+#pragma unroll
+    for (int t = 0; t < NB; ++t) az[c][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  uint4 vx[16], vp;
+  auto load = [&](int64_t t0) {
+    const int64_t tr = t0 - t_begin;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int row = 4 * i + xr;
+      const bool ok = xok && t0 + row < t_end;
+      vx[i] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                     rx, ok ? (uint32_t)(((tr + row) * ldx + n0 + xc) * 2) : kOOB, 0, 0));
+    }
+    const bool okp = pok && t0 + pr < t_end;
+    vp = __builtin_bit_cast(
+        uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                   rp, okp ? (uint32_t)(((tr + pr) * ldp + pc) * 2) : kOOB, 0, 0));
+  };
+  load(t_begin);
+  for (int64_t t0 = t_begin; t0 < t_end; t0 += kDualTok) {
+    __syncthreads();   // the previous piece's reads are done
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      *reinterpret_cast<uint4*>(&xs[(4 * i + xr) * kDualLd + xc]) = vx[i];
+    *reinterpret_cast<uint4*>(&ps[pr * kDualLdP + pc]) = vp;
+    __syncthreads();
+    load(t0 + kDualTok);   // in flight during this piece
+    // projection: tokens 16 w .. + 15 of the piece over the 512 columns
+    f32x4 ac[NB];
+#pragma unroll
+    for (int t = 0; t < NB; ++t) ac[t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int st = 0; st < 16; ++st) {
+      const bf16x8 a = *reinterpret_cast<const bf16x8*>(
+          &xs[(16 * wave + (lane & 15)) * kDualLd + st * 32 + 8 * (lane >> 4)]);
+#pragma unroll
+      for (int t = 0; t < NB; ++t)
+        ac[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[st][t], ac[t], 0, 0, 0);
+    }
+    // reduction: 8 column blocks of 16 over the piece's 64 tokens
+#pragma unroll
+    for (int kk = 0; kk < kDualTok; kk += 32)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const bf16x8 a = red_frag<kDualLd>(xs, kk, wave * 128 + c * 16, lane);
+#pragma unroll
+        for (int t = 0; t < NB; ++t) {
+          const bf16x8 bq = red_frag<kDualLdP>(ps, kk, t * 16, lane);
+          az[c][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bq, az[c][t], 0, 0, 0);
+        }
+      }
+    // lane holds C rows 16 w + 4 (lane / 16) + i, rank t * 16 + lane % 16
+#pragma unroll
+    for (int t = 0; t < NB; ++t) {
+      const int col = t * 16 + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t tk = t0 + 16 * wave + 4 * (lane >> 4) + i;
+        if (tk < t_end && col < R) ws_c[((int64_t)cb * T + tk) * R + col] = ac[t][i];
+      }
+    }
+  }
+  float* wz = ws_z + (int64_t)ts * N * R;
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+#pragma unroll
+    for (int t = 0; t < NB; ++t) {
+      const int col = t * 16 + (lane & 15);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t n = n0 + wave * 128 + c * 16 + 4 * (lane >> 4) + i;
+        if (n < N && col < R) wz[n * R + col] = az[c][t][i];
+      }
+    }
+}
+
 inline bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // ---------------------------------------------------------------------------
@@ -488,3 +630,63 @@ int skinny_t_impl(const void* x, int64_t ldx, const void* p, int64_t ldp, void* 
 
 }  // namespace skinny
 }  // namespace cpt
+
+extern "C" {
+
+int64_t cpt_gemm_bf16_skinny_dual_workspace_bytes(int64_t T, int64_t N, int64_t R, int splits) {
+  if (T < 0 || N < 0 || R < 0 || splits < 1) return -1;
+  const int64_t csplits = (N + kDualCols - 1) / kDualCols;
+  return (csplits * T * R + (int64_t)splits * N * R) * 4;
+}
+
+int cpt_gemm_bf16_skinny_dual(const void* x, int64_t ldx, const void* q, int64_t ldq,
+                              const void* p, int64_t ldp, void* c, int64_t ldc, float alpha_c,
+                              void* z, int64_t ldz, int z_trans, float alpha_z, int64_t T,
+                              int64_t N, int64_t R, int splits, void* workspace, void* stream) {
+  if (T < 0 || N < 0 || R < 0 || splits < 1 || R > 32) return kErrShape;
+  if (N == 0 || R == 0) return kOk;
+  if (!x || !q || !p || !c || !z || !workspace || !al16(x) || !al16(q) || !al16(p) ||
+      (ldx & 7) || (ldq & 7) || (ldp & 7) || (N & 7) || (R & 7) || ldx < N || ldq < N ||
+      ldp < R || ldc < R || ldz < (z_trans ? N : R) || ((uintptr_t)workspace & 3))
+    return kErrAlign;
+  const int64_t tchunk =
+      ((T + splits - 1) / splits + kDualTok - 1) / kDualTok * kDualTok;
+  splits = (int)(tchunk > 0 ? (T + tchunk - 1) / tchunk : 1);
+  if (splits < 1) splits = 1;
+  // 32-bit buffer offsets from each split's first token: its tokens plus the
+  // prefetched piece past its end
+  if ((tchunk + 2 * kDualTok) * ldx * 2 >= ((int64_t)1 << 31) ||
+      (tchunk + 2 * kDualTok) * ldp * 2 >= ((int64_t)1 << 31) || 32 * ldq * 2 >= ((int64_t)1 << 31))
+    return kErrTooLarge;
+  const int64_t csplits = (N + kDualCols - 1) / kDualCols;
+  if (csplits > 0x7FFFFFFF || splits > 65535) return kErrTooLarge;
+  float* ws_c = (float*)workspace;
+  float* ws_z = ws_c + csplits * T * R;
+  hipStream_t st = (hipStream_t)stream;
+  const dim3 grid((unsigned)csplits, (unsigned)splits);
+  if (T > 0) {
+    if (R <= 16)
+      hipLaunchKernelGGL(skinny_dual_kernel<1>, grid, dim3(256), 0, st, (const uint16_t*)x, ldx,
+                         (const uint16_t*)q, ldq, (const uint16_t*)p, ldp, T, N, (int)R, tchunk,
+                         ws_c, ws_z);
+    else
+      hipLaunchKernelGGL(skinny_dual_kernel<2>, grid, dim3(256), 0, st, (const uint16_t*)x, ldx,
+                         (const uint16_t*)q, ldq, (const uint16_t*)p, ldp, T, N, (int)R, tchunk,
+                         ws_c, ws_z);
+    if (hipGetLastError() != hipSuccess) return kErrLaunch;
+    const int64_t tc = T * R;
+    hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((tc + 255) / 256)), dim3(256), 0, st,
+                       (const float*)ws_c, (uint16_t*)c, T, (int)R, ldc, (int)csplits, alpha_c);
+    if (hipGetLastError() != hipSuccess) return kErrLaunch;
+  } else {
+    // no tokens: C has no rows and Z is the empty sum (zero partials summed)
+    splits = 0;
+  }
+  const int64_t tz = N * R;
+  hipLaunchKernelGGL(skinny_red_reduce_kernel, dim3((unsigned)((tz + 255) / 256)), dim3(256), 0,
+                     st, (const float*)ws_z, (uint16_t*)z, N, (int)R, ldz, z_trans ? 1 : 0, splits,
+                     alpha_z);
+  return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
+}
+
+}  // extern "C"

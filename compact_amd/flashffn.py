@@ -89,6 +89,11 @@ _FUSED_DGRAD_GROUPS = ()
 # so the kernel is VALU-bound and measures slower than K2's h_mid^ plus the
 # plain GEMM.  Both are bit-equal; set True to route the Function through it.
 _FUSED_WGRAD_GLU = False
+# The LoRA backward's two thin products of one tensor (grad_h B and
+# s grad_h^T (x A^T); grad_y B_d and s grad_y^T (h_mid A_d^T)) in one pass
+# over it (G.skinny_dual) instead of a projection and a token reduction that
+# each read it.
+_DUAL_SKINNY = True
 
 
 def _mfma(*ts) -> bool:
@@ -137,6 +142,17 @@ def _mm_scaled(a, b, s, name):
     if _mfma(a, b) and a.shape[1] > 0:
         return G.mm_splitk(a, b, s, name=name)
     return G.mm_any(a, b, s, G.ANY_SCALE, name=name)
+
+
+def _dual_ok(x, b, p) -> bool:
+    """The projection x B and the reduction x^T p of one tensor go through
+    G.skinny_dual (one pass over x): bf16 x [T, N] and B [N, r], p [T, r],
+    rank a multiple of 8 up to 32, N a multiple of 8, at least one 512-column
+    block of x (thinner tensors keep the separate kernels), when
+    _DUAL_SKINNY is on."""
+    return (_DUAL_SKINNY and x is not None and b is not None and p is not None
+            and x.dim() == 2 and x.shape[1] >= 512 and x.shape[0] > 0
+            and G.skinny_dual_ok(x, b.t(), p))
 
 
 def _mm_sum(a, b, a2, b2, name):
@@ -417,7 +433,13 @@ class FlashFFNv3Function(torch.autograd.Function):
         grad_w_down = grad_a_down = grad_b_down = None
         gyB_d = None
         if a_down is not None and (need_gate_path or need_ad):
-            gyB_d = _mm(gy, b_down, "gemm_gyB_down")                      # :1521
+            if need_bd and _dual_ok(gy, b_down, ha_d):
+                # grad_y B_d and s grad_y^T (h_mid A_d^T) in one pass over
+                # grad_y (:1521,1545)
+                gyB_d, grad_b_down = G.skinny_dual(gy, b_down.t(), ha_d, 1.0, s_down,
+                                                   name="gemm_gyB_grad_b_down")
+            else:
+                gyB_d = _mm(gy, b_down, "gemm_gyB_down")                  # :1521
 
         # the down projection's LoRA term of grad_h_mid (:1527-1529) rides in
         # the dgrad GEMM's epilogue
@@ -477,7 +499,7 @@ class FlashFFNv3Function(torch.autograd.Function):
             if need_ad:
                 grad_a_down = _mm_scaled(gyB_d.t(), h_mid_hat, s_down, "gemm_grad_a_down")
             del h_mid_hat
-        if need_bd:
+        if need_bd and grad_b_down is None:
             grad_b_down = _mm_scaled(gy.t(), ha_d, s_down, "gemm_grad_b_down")   # :1545
 
         grad_x = None
@@ -496,14 +518,32 @@ class FlashFFNv3Function(torch.autograd.Function):
                 r = b_gate.shape[1]
                 ghB = torch.empty((grad_h_gate.shape[0], r + b_up.shape[1]),
                                   dtype=grad_h_gate.dtype, device=grad_h_gate.device)
-                G.skinny(grad_h_gate, b_gate.t(), 1.0, "gemm_ghgB", out=ghB[:, :r])
-                G.skinny(grad_h_up, b_up.t(), 1.0, "gemm_ghuB", out=ghB[:, r:])
+                # with the B gradient, both products of grad_h in one pass
+                # (:1556-1557 with :1575-1582)
+                if need_bg and _dual_ok(grad_h_gate, b_gate, xa_g):
+                    _, grad_b_gate = G.skinny_dual(grad_h_gate, b_gate.t(), xa_g, 1.0, s_gate,
+                                                   out_c=ghB[:, :r], name="gemm_ghgB_grad_b_gate")
+                else:
+                    G.skinny(grad_h_gate, b_gate.t(), 1.0, "gemm_ghgB", out=ghB[:, :r])
+                if need_bu and _dual_ok(grad_h_up, b_up, xa_u):
+                    _, grad_b_up = G.skinny_dual(grad_h_up, b_up.t(), xa_u, 1.0, s_up,
+                                                 out_c=ghB[:, r:], name="gemm_ghuB_grad_b_up")
+                else:
+                    G.skinny(grad_h_up, b_up.t(), 1.0, "gemm_ghuB", out=ghB[:, r:])
                 ghgB, ghuB = ghB[:, :r], ghB[:, r:]
             else:
                 if a_gate is not None and (need_x or need_ag):
-                    ghgB = _mm(grad_h_gate, b_gate, "gemm_ghgB")
+                    if need_bg and _dual_ok(grad_h_gate, b_gate, xa_g):
+                        ghgB, grad_b_gate = G.skinny_dual(grad_h_gate, b_gate.t(), xa_g, 1.0,
+                                                          s_gate, name="gemm_ghgB_grad_b_gate")
+                    else:
+                        ghgB = _mm(grad_h_gate, b_gate, "gemm_ghgB")
                 if a_up is not None and (need_x or need_au):
-                    ghuB = _mm(grad_h_up, b_up, "gemm_ghuB")
+                    if need_bu and _dual_ok(grad_h_up, b_up, xa_u):
+                        ghuB, grad_b_up = G.skinny_dual(grad_h_up, b_up.t(), xa_u, 1.0, s_up,
+                                                        name="gemm_ghuB_grad_b_up")
+                    else:
+                        ghuB = _mm(grad_h_up, b_up, "gemm_ghuB")
             if need_x:
                 xl = [(ghgB, a_gate, s_gate) if a_gate is not None else None,
                       (ghuB, a_up, s_up) if a_up is not None else None]
@@ -518,7 +558,7 @@ class FlashFFNv3Function(torch.autograd.Function):
                         grad_x = _addmm(grad_x, ghgB, a_gate, s_gate, "gemm_dgrad_x_lora_gate")
                     if a_up is not None:
                         grad_x = _addmm(grad_x, ghuB, a_up, s_up, "gemm_dgrad_x_lora_up")
-            if need_bg:
+            if need_bg and grad_b_gate is None:
                 grad_b_gate = _mm_scaled(grad_h_gate.t(), xa_g, s_gate, "gemm_grad_b_gate")
             if ghB is not None and need_ag and need_au and s_gate == s_up:
                 # s [dg B_g | du B_u]^T x: its row halves equal the two
@@ -530,7 +570,7 @@ class FlashFFNv3Function(torch.autograd.Function):
                     grad_a_gate = _mm_scaled(ghgB.t(), x_2d, s_gate, "gemm_grad_a_gate")
                 if need_au:
                     grad_a_up = _mm_scaled(ghuB.t(), x_2d, s_up, "gemm_grad_a_up")
-            if need_bu:
+            if need_bu and grad_b_up is None:
                 grad_b_up = _mm_scaled(grad_h_up.t(), xa_u, s_up, "gemm_grad_b_up")
             if need_wg:
                 grad_w_gate = _mm(grad_h_gate.t(), x_2d, "gemm_wgrad_gate")

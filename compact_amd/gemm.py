@@ -232,6 +232,61 @@ def skinny_t(x: torch.Tensor, p: torch.Tensor, alpha: float = 1.0, trans: bool =
     return out
 
 
+SKINNY_DUAL_BLOCKS = 256
+
+
+def skinny_dual_ok(x: torch.Tensor, q: torch.Tensor, p: torch.Tensor) -> bool:
+    """skinny_dual takes bf16 x [T, N] with N a multiple of 8 and a rank
+    (q [R, N], p [T, R]) that is a multiple of 8 up to 32."""
+    T, N = x.shape
+    R = q.shape[0]
+    return (x.dtype == q.dtype == p.dtype == torch.bfloat16 and x.is_cuda and N % 8 == 0
+            and R % 8 == 0 and 0 < R <= SKINNY_MAX_RANK and q.shape[1] == N
+            and tuple(p.shape) == (T, R))
+
+
+def skinny_dual(x: torch.Tensor, q: torch.Tensor, p: torch.Tensor, alpha_c: float = 1.0,
+                alpha_z: float = 1.0, out_c: torch.Tensor | None = None,
+                name: str = "gemm_skinny_dual"):
+    """(bf16(alpha_c * x @ q.T) [T, R], bf16(alpha_z * x.T @ p) [N, R]) in one
+    pass over x [T, N] (cpt_gemm_bf16_skinny_dual): the projection and the
+    token reduction a LoRA backward takes of one tensor (grad_h B and
+    s grad_h^T (x A^T)).  out_c: a bf16 [T, R] view with unit column stride
+    and 16-byte aligned rows to write C into."""
+    _require_device(x, q, p)
+    assert skinny_dual_ok(x, q, p), "skinny_dual operands"
+    T, N = x.shape
+    R = q.shape[0]
+    if not _row_major(x) or x.stride(0) < N:
+        x = x.contiguous()
+    if not _row_major(q) or q.stride(0) < N:
+        q = q.contiguous()
+    if not _row_major(p) or p.stride(0) < R:
+        p = p.contiguous()
+    # blocks of 512 columns x T / splits tokens: ~SKINNY_DUAL_BLOCKS of them
+    csplits = (N + 511) // 512
+    splits = max(1, min(max(T // 256, 1), (SKINNY_DUAL_BLOCKS + csplits - 1) // csplits))
+    per = (_SPAN_BYTES // (2 * max(x.stride(0), p.stride(0))) - 129) // 64 * 64
+    assert per >= 64, "operand rows too long for 32-bit buffer offsets"
+    splits = max(splits, (T + per - 1) // per)
+    if out_c is None:
+        c = torch.empty((T, R), dtype=torch.bfloat16, device=x.device)
+    else:
+        c = out_c
+        assert (tuple(c.shape) == (T, R) and c.dtype == torch.bfloat16 and c.stride(1) == 1
+                and c.stride(0) % 8 == 0 and c.data_ptr() % 16 == 0), "skinny_dual out layout"
+    z = torch.empty((N, R), dtype=torch.bfloat16, device=x.device)
+    nbytes = int(_lib.lib().cpt_gemm_bf16_skinny_dual_workspace_bytes(T, N, R, splits))
+    ws = torch.empty((max(nbytes, 4) // 4,), dtype=torch.float32, device=x.device)
+    with _timed(name):
+        rc = _lib.lib().cpt_gemm_bf16_skinny_dual(
+            x.data_ptr(), x.stride(0), q.data_ptr(), q.stride(0), p.data_ptr(), p.stride(0),
+            c.data_ptr(), c.stride(0), float(alpha_c), z.data_ptr(), z.stride(0), 0,
+            float(alpha_z), T, N, R, splits, ws.data_ptr(), _stream(x))
+    check(rc, name)
+    return c, z
+
+
 def skinny_t_splits(T: int, N: int) -> int:
     """Token splits of the token-reduction kernel: ~768 blocks of 64 columns."""
     blocks = (N + 63) // 64
