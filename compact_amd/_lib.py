@@ -65,7 +65,7 @@ SIGNATURES = {
     "cpt_topk_abs": [_P, _I, _L, _L, _L, _P, _P, _P],
     "cpt_topk_scatter": [_P, _P, _I, _L, _L, _L, _P, _P],
     "cpt_gemm_stream_k_workspace": [_P, _L],
-    "cpt_gemm_bf16_skinny_dual": [_P, _L, _P, _L, _P, _L, _P, _L, ctypes.c_float, _P, _L, _I,
+    "cpt_gemm_bf16_skinny_dual": [_P, _L, _P, _L, _I, _P, _L, _P, _L, ctypes.c_float, _P, _L, _I,
                                   ctypes.c_float, _L, _L, _L, _I, _P, _P],
 }
 

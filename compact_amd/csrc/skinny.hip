@@ -367,7 +367,7 @@ template <int NB>
 __global__ __launch_bounds__(256) void skinny_dual_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ q, int64_t ldq,
     const uint16_t* __restrict__ p, int64_t ldp, int64_t T, int64_t N, int R, int64_t tchunk,
-    float* __restrict__ ws_c, float* __restrict__ ws_z) {
+    float* __restrict__ ws_c, float* __restrict__ ws_z, int q_nr) {
   __shared__ __attribute__((aligned(16))) uint16_t xs[kDualTok * kDualLd];
   __shared__ __attribute__((aligned(16))) uint16_t ps[kDualTok * kDualLdP];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -381,7 +381,9 @@ __global__ __launch_bounds__(256) void skinny_dual_kernel(
   // past N read zero (offsets past the records)
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + t_begin * ldx, (T - t_begin) * ldx * 2);
   const __amdgpu_buffer_rsrc_t rp = make_rsrc(p + t_begin * ldp, (T - t_begin) * ldp * 2);
-  const __amdgpu_buffer_rsrc_t rq = make_rsrc(q, (int64_t)R * ldq * 2);
+  // Q as [R][ldq] (rank rows, q_nr == 0) or [N][ldq] (the B factor itself,
+  // q_nr == 1: 8 two-byte loads per fragment, once per block)
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(q, (q_nr ? N : (int64_t)R) * ldq * 2);
   // X piece loads: 16 per thread, row 4 i + tid / 64, 16-byte chunk tid % 64
   const int xr = tid >> 6, xc = (tid & 63) * 8;
   const bool xok = n0 + xc < N;
@@ -396,7 +398,19 @@ __global__ __launch_bounds__(256) void skinny_dual_kernel(
     for (int t = 0; t < NB; ++t) {
       const int64_t col = n0 + st * 32 + 8 * (lane >> 4);
       const int r = t * 16 + (lane & 15);
-      qf[st][t] = bload(rq, col < N && r < R ? (uint32_t)(((int64_t)r * ldq + col) * 2) : kOOB);
+      if (!q_nr) {
+        qf[st][t] = bload(rq, col < N && r < R ? (uint32_t)(((int64_t)r * ldq + col) * 2) : kOOB);
+      } else {
+        uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t off =
+              col + e < N && r < R ? (uint32_t)(((col + e) * ldq + r) * 2) : kOOB;
+          w[e >> 1] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rq, off, 0, 0)
+                       << ((e & 1) * 16);
+        }
+        qf[st][t] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
+      }
     }
   f32x4 az[8][NB];
 #pragma unroll
@@ -639,16 +653,18 @@ int64_t cpt_gemm_bf16_skinny_dual_workspace_bytes(int64_t T, int64_t N, int64_t 
   return (csplits * T * R + (int64_t)splits * N * R) * 4;
 }
 
-int cpt_gemm_bf16_skinny_dual(const void* x, int64_t ldx, const void* q, int64_t ldq,
+int cpt_gemm_bf16_skinny_dual(const void* x, int64_t ldx, const void* q, int64_t ldq, int q_nr,
                               const void* p, int64_t ldp, void* c, int64_t ldc, float alpha_c,
                               void* z, int64_t ldz, int z_trans, float alpha_z, int64_t T,
                               int64_t N, int64_t R, int splits, void* workspace, void* stream) {
   if (T < 0 || N < 0 || R < 0 || splits < 1 || R > 32) return kErrShape;
   if (N == 0 || R == 0) return kOk;
   if (!x || !q || !p || !c || !z || !workspace || !al16(x) || !al16(q) || !al16(p) ||
-      (ldx & 7) || (ldq & 7) || (ldp & 7) || (N & 7) || (R & 7) || ldx < N || ldq < N ||
-      ldp < R || ldc < R || ldz < (z_trans ? N : R) || ((uintptr_t)workspace & 3))
+      (ldx & 7) || (ldp & 7) || (N & 7) || (R & 7) || ldx < N || ldq < (q_nr ? R : N) ||
+      (!q_nr && (ldq & 7)) || ldp < R || ldc < R || ldz < (z_trans ? N : R) ||
+      ((uintptr_t)workspace & 3))
     return kErrAlign;
+  if ((q_nr ? N : 32) * ldq * 2 >= ((int64_t)1 << 31)) return kErrTooLarge;
   const int64_t tchunk =
       ((T + splits - 1) / splits + kDualTok - 1) / kDualTok * kDualTok;
   splits = (int)(tchunk > 0 ? (T + tchunk - 1) / tchunk : 1);
@@ -656,7 +672,7 @@ int cpt_gemm_bf16_skinny_dual(const void* x, int64_t ldx, const void* q, int64_t
   // 32-bit buffer offsets from each split's first token: its tokens plus the
   // prefetched piece past its end
   if ((tchunk + 2 * kDualTok) * ldx * 2 >= ((int64_t)1 << 31) ||
-      (tchunk + 2 * kDualTok) * ldp * 2 >= ((int64_t)1 << 31) || 32 * ldq * 2 >= ((int64_t)1 << 31))
+      (tchunk + 2 * kDualTok) * ldp * 2 >= ((int64_t)1 << 31))
     return kErrTooLarge;
   const int64_t csplits = (N + kDualCols - 1) / kDualCols;
   if (csplits > 0x7FFFFFFF || splits > 65535) return kErrTooLarge;
@@ -668,11 +684,11 @@ int cpt_gemm_bf16_skinny_dual(const void* x, int64_t ldx, const void* q, int64_t
     if (R <= 16)
       hipLaunchKernelGGL(skinny_dual_kernel<1>, grid, dim3(256), 0, st, (const uint16_t*)x, ldx,
                          (const uint16_t*)q, ldq, (const uint16_t*)p, ldp, T, N, (int)R, tchunk,
-                         ws_c, ws_z);
+                         ws_c, ws_z, q_nr ? 1 : 0);
     else
       hipLaunchKernelGGL(skinny_dual_kernel<2>, grid, dim3(256), 0, st, (const uint16_t*)x, ldx,
                          (const uint16_t*)q, ldq, (const uint16_t*)p, ldp, T, N, (int)R, tchunk,
-                         ws_c, ws_z);
+                         ws_c, ws_z, q_nr ? 1 : 0);
     if (hipGetLastError() != hipSuccess) return kErrLaunch;
     const int64_t tc = T * R;
     hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((tc + 255) / 256)), dim3(256), 0, st,

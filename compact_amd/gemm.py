@@ -259,8 +259,14 @@ def skinny_dual(x: torch.Tensor, q: torch.Tensor, p: torch.Tensor, alpha_c: floa
     R = q.shape[0]
     if not _row_major(x) or x.stride(0) < N:
         x = x.contiguous()
-    if not _row_major(q) or q.stride(0) < N:
+    # Q as rank rows [R][ld], or its transpose B [N][ld] as stored (no copy)
+    if q.stride(1) == 1 and q.stride(0) % 8 == 0 and q.stride(0) >= N and q.data_ptr() % 16 == 0:
+        q_nr, ldq = 0, q.stride(0)
+    elif q.stride(0) == 1 and q.stride(1) >= R and q.data_ptr() % 16 == 0:
+        q_nr, ldq = 1, q.stride(1)
+    else:
         q = q.contiguous()
+        q_nr, ldq = 0, q.stride(0)
     if not _row_major(p) or p.stride(0) < R:
         p = p.contiguous()
     # blocks of 512 columns x T / splits tokens: ~SKINNY_DUAL_BLOCKS of them
@@ -280,7 +286,7 @@ def skinny_dual(x: torch.Tensor, q: torch.Tensor, p: torch.Tensor, alpha_c: floa
     ws = torch.empty((max(nbytes, 4) // 4,), dtype=torch.float32, device=x.device)
     with _timed(name):
         rc = _lib.lib().cpt_gemm_bf16_skinny_dual(
-            x.data_ptr(), x.stride(0), q.data_ptr(), q.stride(0), p.data_ptr(), p.stride(0),
+            x.data_ptr(), x.stride(0), q.data_ptr(), ldq, q_nr, p.data_ptr(), p.stride(0),
             c.data_ptr(), c.stride(0), float(alpha_c), z.data_ptr(), z.stride(0), 0,
             float(alpha_z), T, N, R, splits, ws.data_ptr(), _stream(x))
     check(rc, name)

@@ -214,8 +214,9 @@ int cpt_gemm_bf16_skinny_t(const void* x, int64_t ldx, const void* p, int64_t ld
                            float alpha, int splits, void* workspace, void* stream);
 
 /* Both adapter products of one token-major operand X [T, N] in one pass over
- * it: C[T, R] = bf16(alpha_c * X . Q^T) (Q [R, N], K-contiguous: the
- * projection of cpt_gemm_bf16_skinny) and Z = bf16(alpha_z * X^T . P) (P
+ * it: C[T, R] = bf16(alpha_c * X . Q^T) (Q [R, N] rows ldq apart, or with
+ * q_nr the B factor itself, [N, R] rows ldq apart: the projection of
+ * cpt_gemm_bf16_skinny) and Z = bf16(alpha_z * X^T . P) (P
  * [T, R]: the token reduction of cpt_gemm_bf16_skinny_t, written [N, R] or,
  * with z_trans, [R, N]).  Replaces the pairs the reference issues on one
  * tensor in the LoRA backward (src/flashffn.py:1556-1557 with :1575-1582:
@@ -227,7 +228,7 @@ int cpt_gemm_bf16_skinny_t(const void* x, int64_t ldx, const void* p, int64_t ld
  * bytes.  R <= 32 and a multiple of 8, N a multiple of 8, pointers 16-byte
  * aligned. */
 int64_t cpt_gemm_bf16_skinny_dual_workspace_bytes(int64_t T, int64_t N, int64_t R, int splits);
-int cpt_gemm_bf16_skinny_dual(const void* x, int64_t ldx, const void* q, int64_t ldq,
+int cpt_gemm_bf16_skinny_dual(const void* x, int64_t ldx, const void* q, int64_t ldq, int q_nr,
                               const void* p, int64_t ldp, void* c, int64_t ldc, float alpha_c,
                               void* z, int64_t ldz, int z_trans, float alpha_z, int64_t T,
                               int64_t N, int64_t R, int splits, void* workspace, void* stream);

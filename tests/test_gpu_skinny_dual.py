@@ -28,12 +28,17 @@ def _close(got, ref, scale):
     return bool(((got - ref).abs() <= tol).all()), float((got - ref).abs().max())
 
 
+@pytest.mark.parametrize("q_as_b", [False, True])
 @pytest.mark.parametrize("T,N,R", [(8192, 11008, 16), (300, 520, 8), (1000, 4096, 32),
                                    (64, 1024, 24), (33, 512, 16)])
-def test_skinny_dual_against_fp32(device, T, N, R):
+def test_skinny_dual_against_fp32(device, T, N, R, q_as_b):
+    """q_as_b: Q given as the transposed view of a B factor [N, R] (read in
+    place) instead of rank rows [R, N]; same bits either way."""
     G = _G()
     x = rnd((T, N), 1, device)
     q = rnd((R, N), 2, device, 0.05)
+    if q_as_b:
+        q = q.t().contiguous().t()
     p = rnd((T, R), 3, device, 0.5)
     c, z = G.skinny_dual(x, q, p, 1.0, 2.0)
     c2, z2 = G.skinny_dual(x, q, p, 1.0, 2.0)
