@@ -29,21 +29,10 @@ constexpr int kBlock = 256;
 // int4 -> 4 bytes of (code+8) nibbles, even column low (src/flashffn.py:1081-1085).
 template <int BITS>
 __device__ __forceinline__ void store_codes8(uint8_t* q, int64_t c, const float v[8], float safe) {
-  const float rs = __builtin_amdgcn_rcpf(safe);
-  if (BITS == 8) {
-    uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      w0 |= ((uint32_t)quant_code<8>(v[j], safe, rs) & 0xFFu) << (8 * j);
-      w1 |= ((uint32_t)quant_code<8>(v[4 + j], safe, rs) & 0xFFu) << (8 * j);
-    }
-    reinterpret_cast<uint2*>(q)[c] = make_uint2(w0, w1);
-  } else {
-    uint32_t w = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) w |= (uint32_t)(quant_code<4>(v[j], safe, rs) + 8) << (4 * j);
-    reinterpret_cast<uint32_t*>(q)[c] = w;
-  }
+  float r[8];
+  quant_rint8<BITS>(v, safe, __builtin_amdgcn_rcpf(safe), r);
+  if (BITS == 8) reinterpret_cast<uint2*>(q)[c] = pack_codes8_int8(r);
+  else reinterpret_cast<uint32_t*>(q)[c] = pack_codes8_int4(r);
 }
 
 // Codes of 8 consecutive elements as floats.
@@ -87,9 +76,6 @@ __device__ __forceinline__ void quant_chunk(const float v[8], bool valid, int64_
 // out as bf16 into out[row * k + slot] and zeroed before the codec sees them
 // (HyC-LoRA's outlier extraction, hyclora/operators/compress_function.py:111-143,
 // on the v3 per-group codec).  v holds 8 consecutive elements of one row.
-// Outlier counts up to this take the one-block-per-row K2 kernel (its [2][k]
-// bf16 LDS block stays at 32 KiB or less).
-constexpr int64_t kRowOutliersMax = 8192;
 
 struct Outliers {
   const int16_t* slot;   // [D], -1 for ordinary columns
@@ -207,21 +193,13 @@ __global__ __launch_bounds__(kBlock) void quantize_fast_kernel(
 // ---------------------------------------------------------------------------
 // K1: h_mid = SiLU(g)*u (bf16) + codec of g and u, fast path
 // ---------------------------------------------------------------------------
-template <int BITS, int LPG, bool OUTL>
+template <int BITS, int LPG>
 __global__ __launch_bounds__(kBlock) void silu_mul_quant_kernel(
     const uint16_t* __restrict__ g, const uint16_t* __restrict__ u, uint16_t* __restrict__ hm,
     uint8_t* __restrict__ qg, uint16_t* __restrict__ sg, uint8_t* __restrict__ qu,
-    uint16_t* __restrict__ su, int64_t nchunk, int64_t d, Outliers og, Outliers ou) {
+    uint16_t* __restrict__ su, int64_t nchunk) {
   const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   const bool valid = c < nchunk;
-  // the slot maps first: a small cached read, in flight with the payload
-  int64_t row = 0, col = 0;
-  ChunkSlots csg, csu;
-  if (OUTL) {
-    if (valid) chunk_rc(c, d, og, row, col);
-    csg = load_slots8(og, col, valid);
-    csu = load_slots8(ou, col, valid);
-  }
   float gv[8] = {0, 0, 0, 0, 0, 0, 0, 0}, uv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
   if (valid) {
     Vec8<kBF16>::ld(g, c, gv);
@@ -230,10 +208,6 @@ __global__ __launch_bounds__(kBlock) void silu_mul_quant_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) h[j] = silu_mul1(gv[j], uv[j]);  // src/flashffn.py:1212-1215
     Vec8<kBF16>::st(hm, c, h);
-  }
-  if (OUTL) {
-    extract_outliers8(gv, row, csg, og);
-    extract_outliers8(uv, row, csu, ou);
   }
   quant_chunk<BITS, LPG>(gv, valid, c, qg, sg);
   quant_chunk<BITS, LPG>(uv, valid, c, qu, su);
@@ -337,26 +311,14 @@ __global__ __launch_bounds__(kBlock) void dequantize_generic_kernel(
 // each thread reads its 8 elements of gmid before it stores the same 8 of
 // dg, so gmid, dg, du and hm carry no __restrict__.
 // ---------------------------------------------------------------------------
-template <int BITS, bool WANT_HM, bool OUTL>
+template <int BITS, bool WANT_HM>
 __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_kernel(
     const uint16_t* gmid, const uint8_t* __restrict__ qg, const uint16_t* __restrict__ sg,
     const uint8_t* __restrict__ qu, const uint16_t* __restrict__ su, uint16_t* dg, uint16_t* du,
-    uint16_t* hm, int64_t nchunk, int gs_shift, int64_t d, Outliers outg, Outliers outu) {
+    uint16_t* hm, int64_t nchunk, int gs_shift) {
   const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   if (c >= nchunk) return;
   float cg[8], cu[8], dh[8], og[8], ou[8], oh[8], hg[8], hu[8];
-  // outlier values first: their loads depend on the slot maps, so they are
-  // issued ahead of the payload loads and overlap them
-  float ovg[8], ovu[8];
-  ChunkSlots csg, csu;
-  if (OUTL) {
-    int64_t row, col;
-    chunk_rc(c, d, outg, row, col);
-    csg = load_slots8(outg, col, true);
-    csu = load_slots8(outu, col, true);
-    fetch_outliers8(ovg, row, csg, outg);
-    fetch_outliers8(ovu, row, csu, outu);
-  }
   load_codes8<BITS>(qg, c, cg);
   load_codes8<BITS>(qu, c, cu);
   Vec8<kBF16>::ld(gmid, c, dh);
@@ -368,10 +330,6 @@ __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_kernel(
     // bf16 round trip of the dequantised cache (src/flashffn.py:1251-1253)
     hg[j] = round_bf16(cg[j] * scg);
     hu[j] = round_bf16(cu[j] * scu);
-  }
-  if (OUTL) {
-    restore_outliers8(hg, ovg, csg);
-    restore_outliers8(hu, ovu, csu);
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
@@ -411,76 +369,162 @@ __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_generic_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// K2 with outlier channels, one block per row.  The block reads the row's
-// [k] outlier values into LDS in one coalesced pass before its threads
-// restore from it, so no thread issues an HBM load that waits on the slot
-// map (0.173 against 0.185 ms for the chunk-per-thread kernel at C3).  Thread
-// t owns chunks t, t + 256, ... of the row (D / 8 chunks).  The same layout
-// for K1 (outliers collected in LDS, written once per row) measured slower
-// than the chunk-per-thread K1 (0.153-0.175 against 0.137 ms), so K1 keeps
-// the per-chunk extraction.
+// K1 and K2 with outlier channels on packed bf16 pairs.  Thread c owns chunk
+// c (8 consecutive columns of one row) as in the plain kernels.  A slot word
+// holds the int16 slots of two adjacent columns, the payload word their two
+// bf16 values, so the outlier work runs on words: an arithmetic shift of each
+// 16-bit slot by 15 gives the pair's keep mask (0xFFFF for an ordinary column,
+// slot -1; 0 for an outlier column), which zeroes (K1) or replaces (K2) the
+// outlier halves with one AND or bit-select per word.  Only lanes whose chunk
+// holds an outlier column (a 4-word AND of the slot words differs from all
+// ones) store or load outlier values.  At C3 (8192 x 11008, int4 g64, 110
+// outlier columns) these measured 135 / 169 us against 139-141 / 173 us for
+// the same work on floats with 8-bit column masks (K1 / K2).
 // ---------------------------------------------------------------------------
-// Chunks each thread has in flight per step of the row loop (loads of all of
-// them issued before any is used).
-constexpr int kRowUnroll = 2;
+typedef short short2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t keep_mask2(uint32_t slot_word) {
+  const short2_t v = __builtin_bit_cast(short2_t, slot_word) >> (short2_t){15, 15};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+__device__ __forceinline__ uint4 load_slot_words(const Outliers& o, uint32_t j, bool ok) {
+  uint4 w = make_uint4(0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu, 0xFFFFFFFFu);
+  if (ok) w = *reinterpret_cast<const uint4*>(o.slot + (int64_t)j * 8);
+  return w;
+}
+
+__device__ __forceinline__ bool any_outlier(const uint4& w) {
+  return (w.x & w.y & w.z & w.w) != 0xFFFFFFFFu;
+}
+
+// Copy the outlier columns of one chunk (raw bf16 words `p`) to out[row][slot].
+__device__ __forceinline__ void store_outlier_words(const uint4& w, const uint4& p, uint32_t row,
+                                                    const Outliers& o) {
+  uint16_t* dst = o.out + (int64_t)row * o.k;
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w}, ps[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int lo = (int16_t)(ws[i] & 0xFFFFu), hi = (int32_t)ws[i] >> 16;
+    if (lo >= 0) dst[lo] = (uint16_t)(ps[i] & 0xFFFFu);
+    if (hi >= 0) dst[hi] = (uint16_t)(ps[i] >> 16);
+  }
+}
+
+// The stored bf16 values of one chunk's outlier columns as packed pairs
+// (0 in the ordinary halves).
+__device__ __forceinline__ uint4 load_outlier_words(const uint4& w, uint32_t row,
+                                                    const Outliers& o) {
+  const uint16_t* src = o.out + (int64_t)row * o.k;
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  uint32_t r[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int lo = (int16_t)(ws[i] & 0xFFFFu), hi = (int32_t)ws[i] >> 16;
+    uint32_t a = 0, b = 0;
+    if (lo >= 0) a = src[lo];
+    if (hi >= 0) b = src[hi];
+    r[i] = a | (b << 16);
+  }
+  return make_uint4(r[0], r[1], r[2], r[3]);
+}
+
+__device__ __forceinline__ void unpack_bf16x8(const uint4& p, float v[8]) {
+  const uint32_t ps[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = __uint_as_float(ps[i] << 16);
+    v[2 * i + 1] = __uint_as_float(ps[i] & 0xFFFF0000u);
+  }
+}
+
+__device__ __forceinline__ uint4 and_words(const uint4& p, const uint4& slots) {
+  return make_uint4(p.x & keep_mask2(slots.x), p.y & keep_mask2(slots.y),
+                    p.z & keep_mask2(slots.z), p.w & keep_mask2(slots.w));
+}
+
+template <int BITS, int LPG>
+__global__ __launch_bounds__(kBlock) void silu_mul_quant_outlier_kernel(
+    const uint16_t* __restrict__ g, const uint16_t* __restrict__ u, uint16_t* __restrict__ hm,
+    uint8_t* __restrict__ qg, uint16_t* __restrict__ sg, uint8_t* __restrict__ qu,
+    uint16_t* __restrict__ su, int64_t nchunk, Outliers og, Outliers ou) {
+  const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  const bool valid = c < nchunk;
+  uint32_t row = 0, j = 0;
+  if (valid) {
+    row = og.rows.div((uint32_t)c);
+    j = (uint32_t)c - row * og.rows.d;
+  }
+  const uint4 wg = load_slot_words(og, j, valid);
+  const uint4 wu = load_slot_words(ou, j, valid);
+  uint4 pg = make_uint4(0, 0, 0, 0), pu = pg;
+  if (valid) {
+    pg = reinterpret_cast<const uint4*>(g)[c];
+    pu = reinterpret_cast<const uint4*>(u)[c];
+  }
+  float gv[8], uv[8];
+  unpack_bf16x8(pg, gv);
+  unpack_bf16x8(pu, uv);
+  if (valid) {
+    float h[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e] = silu_mul1(gv[e], uv[e]);  // src/flashffn.py:1212-1215
+    Vec8<kBF16>::st(hm, c, h);
+  }
+  // zero-and-store (compress_function.py:111-143): the codec sees 0 in the
+  // outlier columns
+  if (any_outlier(wg)) store_outlier_words(wg, pg, row, og);
+  if (any_outlier(wu)) store_outlier_words(wu, pu, row, ou);
+  unpack_bf16x8(and_words(pg, wg), gv);
+  unpack_bf16x8(and_words(pu, wu), uv);
+  quant_chunk<BITS, LPG>(gv, valid, c, qg, sg);
+  quant_chunk<BITS, LPG>(uv, valid, c, qu, su);
+}
 
 template <int BITS, bool WANT_HM>
-__global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_outlier_rows_kernel(
+__global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_outlier_kernel(
     const uint16_t* gmid, const uint8_t* __restrict__ qg, const uint16_t* __restrict__ sg,
     const uint8_t* __restrict__ qu, const uint16_t* __restrict__ su, uint16_t* dg, uint16_t* du,
-    uint16_t* hm, int64_t cpr, int gs_shift, Outliers og, Outliers ou) {
-  extern __shared__ uint16_t so[];   // [2][k] bf16: gate, up
-  const int64_t row = blockIdx.x;
-  const int k = (int)og.k;
-  for (int i = threadIdx.x; i < k; i += kBlock) {
-    so[i] = og.out[row * k + i];
-    so[k + i] = ou.out[row * k + i];
+    uint16_t* hm, int64_t nchunk, int gs_shift, Outliers og, Outliers ou) {
+  const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  if (c >= nchunk) return;
+  const uint32_t row = og.rows.div((uint32_t)c);
+  const uint32_t j = (uint32_t)c - row * og.rows.d;
+  const uint4 wg = load_slot_words(og, j, true);
+  const uint4 wu = load_slot_words(ou, j, true);
+  float cg[8], cu[8], dh[8];
+  load_codes8<BITS>(qg, c, cg);
+  load_codes8<BITS>(qu, c, cu);
+  Vec8<kBF16>::ld(gmid, c, dh);
+  const int64_t si = (c * 8) >> gs_shift;
+  const float scg = f16_bits_to_f32(sg[si]);
+  const float scu = f16_bits_to_f32(su[si]);
+  uint4 og4 = make_uint4(0, 0, 0, 0), ou4 = og4;
+  if (any_outlier(wg)) og4 = load_outlier_words(wg, row, og);
+  if (any_outlier(wu)) ou4 = load_outlier_words(wu, row, ou);
+  const uint32_t wgs[4] = {wg.x, wg.y, wg.z, wg.w}, wus[4] = {wu.x, wu.y, wu.z, wu.w};
+  const uint32_t ogs[4] = {og4.x, og4.y, og4.z, og4.w}, ous[4] = {ou4.x, ou4.y, ou4.z, ou4.w};
+  uint32_t hgw[4], huw[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    // bf16 round trip of the dequantised cache (src/flashffn.py:1251-1253), then
+    // the stored value of an outlier column (compress_function.py:147-174)
+    const uint32_t kg = keep_mask2(wgs[i]), ku = keep_mask2(wus[i]);
+    hgw[i] = (pack_bf16x2(cg[2 * i] * scg, cg[2 * i + 1] * scg) & kg) | (ogs[i] & ~kg);
+    huw[i] = (pack_bf16x2(cu[2 * i] * scu, cu[2 * i + 1] * scu) & ku) | (ous[i] & ~ku);
   }
-  __syncthreads();
-  for (int64_t j0 = 0; j0 < cpr; j0 += kBlock * kRowUnroll) {
-    ChunkSlots csg[kRowUnroll], csu[kRowUnroll];
-    float cg[kRowUnroll][8], cu[kRowUnroll][8], dh[kRowUnroll][8], scg[kRowUnroll],
-        scu[kRowUnroll];
+  float hg[8], hu[8], ogr[8], our[8], oh[8];
+  unpack_bf16x8(make_uint4(hgw[0], hgw[1], hgw[2], hgw[3]), hg);
+  unpack_bf16x8(make_uint4(huw[0], huw[1], huw[2], huw[3]), hu);
 #pragma unroll
-    for (int t = 0; t < kRowUnroll; ++t) {
-      const int64_t jc = j0 + t * kBlock + threadIdx.x;
-      // a chunk past the row reads chunk 0 of the row again and stores nothing
-      const int64_t c = row * cpr + (jc < cpr ? jc : 0);
-      csg[t] = load_slots8(og, (jc < cpr ? jc : 0) * 8, true);
-      csu[t] = load_slots8(ou, (jc < cpr ? jc : 0) * 8, true);
-      load_codes8<BITS>(qg, c, cg[t]);
-      load_codes8<BITS>(qu, c, cu[t]);
-      Vec8<kBF16>::ld(gmid, c, dh[t]);
-      const int64_t si = (c * 8) >> gs_shift;
-      scg[t] = f16_bits_to_f32(sg[si]);
-      scu[t] = f16_bits_to_f32(su[si]);
-    }
-#pragma unroll
-    for (int t = 0; t < kRowUnroll; ++t) {
-      const int64_t jc = j0 + t * kBlock + threadIdx.x;
-      if (jc >= cpr) continue;
-      const int64_t c = row * cpr + jc;
-      float ogr[8], our[8], oh[8], hg[8], hu[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        // bf16 round trip of the dequantised cache (src/flashffn.py:1251-1253),
-        // then the stored value of an outlier column (compress_function.py:147-174)
-        hg[j] = round_bf16(cg[t][j] * scg[t]);
-        hu[j] = round_bf16(cu[t][j] * scu[t]);
-        if ((csg[t].mask >> j) & 1u) hg[j] = bf16_to_f32(so[csg[t].slot(j)]);
-        if ((csu[t].mask >> j) & 1u) hu[j] = bf16_to_f32(so[k + csu[t].slot(j)]);
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float hact;
-        swiglu_bwd1(dh[t][j], hg[j], hu[j], ogr[j], our[j], hact);
-        oh[j] = hact * hu[j];  // src/flashffn.py:1298-1300
-      }
-      Vec8<kBF16>::st(dg, c, ogr);
-      Vec8<kBF16>::st(du, c, our);
-      if (WANT_HM) Vec8<kBF16>::st(hm, c, oh);
-    }
+  for (int e = 0; e < 8; ++e) {
+    float hact;
+    swiglu_bwd1(dh[e], hg[e], hu[e], ogr[e], our[e], hact);
+    oh[e] = hact * hu[e];  // src/flashffn.py:1298-1300
   }
+  Vec8<kBF16>::st(dg, c, ogr);
+  Vec8<kBF16>::st(du, c, our);
+  if (WANT_HM) Vec8<kBF16>::st(hm, c, oh);
 }
 
 // ---------------------------------------------------------------------------
@@ -626,26 +670,31 @@ void launch_quant_generic(int dt, bool glu, const void* g, const void* u, void* 
   }
 }
 
+// K1, plain or with outlier channels (OUTL: og, ou used)
 template <int BITS, int LPG, bool OUTL>
 void launch_k1(const uint16_t* g, const uint16_t* u, uint16_t* hm, uint8_t* qg, uint16_t* sg,
-               uint8_t* qu, uint16_t* su, int64_t nchunk, int64_t d, Outliers og, Outliers ou,
+               uint8_t* qu, uint16_t* su, int64_t nchunk, const Outliers& og, const Outliers& ou,
                hipStream_t st) {
-  silu_mul_quant_kernel<BITS, LPG, OUTL>
-      <<<grid_for(nchunk), kBlock, 0, st>>>(g, u, hm, qg, sg, qu, su, nchunk, d, og, ou);
+  if (OUTL)
+    silu_mul_quant_outlier_kernel<BITS, LPG>
+        <<<grid_for(nchunk), kBlock, 0, st>>>(g, u, hm, qg, sg, qu, su, nchunk, og, ou);
+  else
+    silu_mul_quant_kernel<BITS, LPG>
+        <<<grid_for(nchunk), kBlock, 0, st>>>(g, u, hm, qg, sg, qu, su, nchunk);
 }
 
 template <int BITS, bool OUTL>
 void launch_k1_lpg(int lpg, const uint16_t* g, const uint16_t* u, uint16_t* hm, uint8_t* qg,
-                   uint16_t* sg, uint8_t* qu, uint16_t* su, int64_t nchunk, int64_t d,
-                   Outliers og, Outliers ou, hipStream_t st) {
+                   uint16_t* sg, uint8_t* qu, uint16_t* su, int64_t nchunk, const Outliers& og,
+                   const Outliers& ou, hipStream_t st) {
   switch (lpg) {
-    case 1: launch_k1<BITS, 1, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, d, og, ou, st); break;
-    case 2: launch_k1<BITS, 2, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, d, og, ou, st); break;
-    case 4: launch_k1<BITS, 4, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, d, og, ou, st); break;
-    case 8: launch_k1<BITS, 8, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, d, og, ou, st); break;
-    case 16: launch_k1<BITS, 16, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, d, og, ou, st); break;
-    case 32: launch_k1<BITS, 32, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, d, og, ou, st); break;
-    default: launch_k1<BITS, 64, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, d, og, ou, st); break;
+    case 1: launch_k1<BITS, 1, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, og, ou, st); break;
+    case 2: launch_k1<BITS, 2, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, og, ou, st); break;
+    case 4: launch_k1<BITS, 4, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, og, ou, st); break;
+    case 8: launch_k1<BITS, 8, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, og, ou, st); break;
+    case 16: launch_k1<BITS, 16, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, og, ou, st); break;
+    case 32: launch_k1<BITS, 32, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, og, ou, st); break;
+    default: launch_k1<BITS, 64, OUTL>(g, u, hm, qg, sg, qu, su, nchunk, og, ou, st); break;
   }
 }
 
@@ -1033,8 +1082,8 @@ int cpt_silu_mul_quant(const void* h_gate, const void* h_up, int64_t n, int64_t 
                     aligned16(hm) && ((uintptr_t)qg & 7u) == 0 && ((uintptr_t)qu & 7u) == 0;
   if (fast) {
     const int lpg = (int)(group_size / 8);
-    if (bits == 4) launch_k1_lpg<4, false>(lpg, g, u, hm, qg, sg, qu, su, n_el / 8, d, Outliers{}, Outliers{}, st);
-    else launch_k1_lpg<8, false>(lpg, g, u, hm, qg, sg, qu, su, n_el / 8, d, Outliers{}, Outliers{}, st);
+    if (bits == 4) launch_k1_lpg<4, false>(lpg, g, u, hm, qg, sg, qu, su, n_el / 8, Outliers{}, Outliers{}, st);
+    else launch_k1_lpg<8, false>(lpg, g, u, hm, qg, sg, qu, su, n_el / 8, Outliers{}, Outliers{}, st);
   } else {
     if (bits == 4) launch_quant_generic<4>(kBF16, true, g, u, hm, qg, sg, qu, su, n_el, group_size, st);
     else launch_quant_generic<8>(kBF16, true, g, u, hm, qg, sg, qu, su, n_el, group_size, st);
@@ -1068,7 +1117,7 @@ int cpt_dequant_swiglu_backward(const void* grad_h_mid, const void* q_gate, cons
     const int64_t nchunk = n_el / 8;
     const unsigned grid = grid_for(nchunk);
     const int sh = log2_exact(group_size);
-#define CPT_K2(B, W) dequant_swiglu_bwd_kernel<B, W, false><<<grid, kBlock, 0, st>>>(gm, qg, sg, qu, su, og, ou, oh, nchunk, sh, d, Outliers{}, Outliers{})
+#define CPT_K2(B, W) dequant_swiglu_bwd_kernel<B, W><<<grid, kBlock, 0, st>>>(gm, qg, sg, qu, su, og, ou, oh, nchunk, sh)
     if (bits == 4) { if (oh) CPT_K2(4, true); else CPT_K2(4, false); }
     else { if (oh) CPT_K2(8, true); else CPT_K2(8, false); }
 #undef CPT_K2
@@ -1211,11 +1260,11 @@ int cpt_silu_mul_quant_outlier(const void* h_gate, const void* h_up, int64_t n, 
   if (bits == 4)
     launch_k1_lpg<4, true>(lpg, (const uint16_t*)h_gate, (const uint16_t*)h_up, (uint16_t*)h_mid,
                            (uint8_t*)q_gate, (uint16_t*)s_gate, (uint8_t*)q_up, (uint16_t*)s_up,
-                           n * d / 8, d, og, ou, st);
+                           n * d / 8, og, ou, st);
   else
     launch_k1_lpg<8, true>(lpg, (const uint16_t*)h_gate, (const uint16_t*)h_up, (uint16_t*)h_mid,
                            (uint8_t*)q_gate, (uint16_t*)s_gate, (uint8_t*)q_up, (uint16_t*)s_up,
-                           n * d / 8, d, og, ou, st);
+                           n * d / 8, og, ou, st);
   return launch_status();
 }
 
@@ -1251,17 +1300,7 @@ int cpt_dequant_swiglu_backward_outlier(const void* grad_h_mid, const void* q_ga
   uint16_t* dg = (uint16_t*)grad_h_gate;
   uint16_t* du = (uint16_t*)grad_h_up;
   uint16_t* hm = (uint16_t*)h_mid_hat;
-  if (k <= kRowOutliersMax && n <= 0x7FFFFFFF) {
-    // one block per row, the row's outliers staged in LDS
-    const size_t lds = (size_t)(2 * k) * sizeof(uint16_t);
-    const int64_t cpr = d / 8;
-#define CPT_K2R(B, W) dequant_swiglu_bwd_outlier_rows_kernel<B, W><<<(unsigned)n, kBlock, lds, st>>>(gm, qg, sg, qu, su, dg, du, hm, cpr, sh, og, ou)
-    if (bits == 4) { if (hm) CPT_K2R(4, true); else CPT_K2R(4, false); }
-    else { if (hm) CPT_K2R(8, true); else CPT_K2R(8, false); }
-#undef CPT_K2R
-    return launch_status();
-  }
-#define CPT_K2O(B, W) dequant_swiglu_bwd_kernel<B, W, true><<<grid, kBlock, 0, st>>>(gm, qg, sg, qu, su, dg, du, hm, nchunk, sh, d, og, ou)
+#define CPT_K2O(B, W) dequant_swiglu_bwd_outlier_kernel<B, W><<<grid, kBlock, 0, st>>>(gm, qg, sg, qu, su, dg, du, hm, nchunk, sh, og, ou)
   if (bits == 4) { if (hm) CPT_K2O(4, true); else CPT_K2O(4, false); }
   else { if (hm) CPT_K2O(8, true); else CPT_K2O(8, false); }
 #undef CPT_K2O

@@ -998,22 +998,12 @@ __device__ __forceinline__ void glu_finish(const KArgs& A, int64_t m0, int64_t n
         if (!ok) continue;
         if ((tid & (GS / 8 - 1)) == 0) (t ? A.s_up : A.s_gate)[m * G + d / GS] = sh;
         uint8_t* qp = t ? A.q_up : A.q_gate;
-        int code[8];
-        quant_codes8<BITS>(v, safe, rs, code);
-        if constexpr (BITS == 8) {
-          uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            w0 |= ((uint32_t)code[e] & 0xFFu) << (8 * e);
-            w1 |= ((uint32_t)code[e + 4] & 0xFFu) << (8 * e);
-          }
-          *reinterpret_cast<uint2*>(qp + off) = make_uint2(w0, w1);
-        } else {
-          uint32_t w = 0;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) w |= (uint32_t)(code[e] + 8) << (4 * e);
-          *reinterpret_cast<uint32_t*>(qp + m * (D >> 1) + (d >> 1)) = w;
-        }
+        float r[8];
+        quant_rint8<BITS>(v, safe, rs, r);
+        if constexpr (BITS == 8)
+          *reinterpret_cast<uint2*>(qp + off) = pack_codes8_int8(r);
+        else
+          *reinterpret_cast<uint32_t*>(qp + m * (D >> 1) + (d >> 1)) = pack_codes8_int4(r);
       }
     }
   }

@@ -106,15 +106,14 @@ __device__ __forceinline__ int quant_code(float v, float safe, float rsafe) {
   return (int)r;
 }
 
-// quant_code for the 8 values a thread owns in one group, with one branch for
-// all eight: when any fast-path quotient lies near a half-integer, all eight
-// are recomputed from the correctly rounded division, which equals the fast
-// path wherever that one is valid.  Same codes as quant_code, element for
-// element.
+// The codes of the 8 values a thread owns in one group, as clamped integral
+// floats, with one branch for all eight: when any fast-path quotient lies
+// near a half-integer, all eight are recomputed from the correctly rounded
+// division, which equals the fast path wherever that one is valid.  Same
+// codes as quant_code, element for element.
 template <int BITS>
-__device__ __forceinline__ void quant_codes8(const float v[8], float safe, float rsafe,
-                                             int code[8]) {
-  float r[8];
+__device__ __forceinline__ void quant_rint8(const float v[8], float safe, float rsafe,
+                                            float r[8]) {
   float worst = 0.0f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -127,8 +126,32 @@ __device__ __forceinline__ void quant_codes8(const float v[8], float safe, float
     for (int e = 0; e < 8; ++e) r[e] = __builtin_rintf(v[e] / safe);
   }
 #pragma unroll
-  for (int e = 0; e < 8; ++e)
-    code[e] = (int)fminf(fmaxf(r[e], -QMax<BITS>::v), QMax<BITS>::v);
+  for (int e = 0; e < 8; ++e) r[e] = fminf(fmaxf(r[e], -QMax<BITS>::v), QMax<BITS>::v);
+}
+
+// Eight codes (quant_rint8's integral floats) packed as stored
+// (src/flashffn.py:1081-1085).  int4: byte b holds column 2b in its low
+// nibble and 2b + 1 in its high one, each as code + 8; the byte's value
+// r[2b] + 16 r[2b+1] + 136 is a small integer, exact in fp32, and
+// v_cvt_pk_u8_f32 writes it into byte b.  int8: code + 128 as an unsigned
+// byte, then XOR 0x80 turns it into the two's complement byte of the code.
+__device__ __forceinline__ uint32_t pack_codes8_int4(const float r[8]) {
+  uint32_t w = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+    w = __builtin_amdgcn_cvt_pk_u8_f32(__builtin_fmaf(r[2 * b + 1], 16.0f, r[2 * b]) + 136.0f,
+                                       b, w);
+  return w;
+}
+
+__device__ __forceinline__ uint2 pack_codes8_int8(const float r[8]) {
+  uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    w0 = __builtin_amdgcn_cvt_pk_u8_f32(r[b] + 128.0f, b, w0);
+    w1 = __builtin_amdgcn_cvt_pk_u8_f32(r[4 + b] + 128.0f, b, w1);
+  }
+  return make_uint2(w0 ^ 0x80808080u, w1 ^ 0x80808080u);
 }
 
 }  // namespace cpt
