@@ -221,21 +221,23 @@ __device__ __forceinline__ f32x4 acc16(const KArgs& A, const f32x4& a, const Lor
 // multiple of the CU count S leaves its last wave of tiles part-empty.  The
 // host then runs T' = T - (T mod S) - S tiles data-parallel (one block each)
 // and shares the k-iterations of the other (T mod S) + S tiles evenly over S
-// more blocks: block s owns global iterations [s I / S, (s + 1) I / S) of
-// those tiles (I = their tile count x k-tiles per tile), i.e. one to two
-// tiles' worth, and walks its tiles from the last to the first.
+// more blocks: the block of rank s owns global iterations [s I / S,
+// (s + 1) I / S) of those tiles (I = their tile count x k-tiles per tile),
+// one to two tiles' worth, so a tile spans at most two ranks.  Ranks are
+// dealt so that the blocks of one XCD hold consecutive ranks.  A block walks
+// its tiles from the last to the first.
 //   - A tile it covers whole it finishes alone.
 //   - A tile whose k-range continues past its range (its last tile, taken
 //     first) it leaves as a partial: fp32 accumulators to slot s of the
 //     workspace, then a ready flag.
-//   - A tile whose k-range began in lower blocks (its first tile, taken last)
-//     it finishes: it waits for those blocks' flags, adds their partials in a
-//     fixed order (nearest block first), clears the flags and runs the
-//     epilogue.  The result is deterministic for a given shape and CU count.
-// A block only ever waits on lower-numbered blocks, which the hardware
-// dispatches first, so every wait ends whatever the grid's residency; the
-// wait is bounded anyway (kSkSpin polls), and a wait that runs out counts an
-// error in the word after the flags and goes on.
+//   - A tile whose k-range began in rank s - 1 (its first tile, taken last)
+//     it finishes: it waits for that rank's flag, adds its partial, clears
+//     the flag and runs the epilogue.  The result is deterministic for a
+//     given shape and CU count.
+// The S stream-K blocks fit on the chip at once (one block per CU) and the
+// data-parallel blocks ahead of them never wait, so every wait ends; it is
+// bounded anyway (kSkSpin polls), and a wait that runs out counts an error in
+// the word after the flags and goes on.
 // ---------------------------------------------------------------------------
 constexpr int kRoleWhole = 0, kRolePartial = 1, kRoleFinish = 2;
 // 0 as a value the compiler cannot hoist: a flag address built from it does
