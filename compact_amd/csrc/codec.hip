@@ -29,8 +29,10 @@ constexpr int kBlock = 256;
 // int4 -> 4 bytes of (code+8) nibbles, even column low (src/flashffn.py:1081-1085).
 template <int BITS>
 __device__ __forceinline__ void store_codes8(uint8_t* q, int64_t c, const float v[8], float safe) {
+  const float rs = __builtin_amdgcn_rcpf(safe);
   float r[8];
-  quant_rint8<BITS>(v, safe, __builtin_amdgcn_rcpf(safe), r);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = quant_rint<BITS>(v[e], safe, rs);
   if (BITS == 8) reinterpret_cast<uint2*>(q)[c] = pack_codes8_int8(r);
   else reinterpret_cast<uint32_t*>(q)[c] = pack_codes8_int4(r);
 }
@@ -70,6 +72,42 @@ __device__ __forceinline__ void quant_chunk(const float v[8], bool valid, int64_
   if (!valid) return;
   if ((c & (LPG - 1)) == 0) s[c / LPG] = sh;
   store_codes8<BITS>(q, c, v, safe_scale(sh));
+}
+
+// quant_chunk split in two, so that a kernel can form every output before it
+// stores any: on gfx950 a wait for a load also waits for the stores issued
+// before it (one counter for both), so loads consumed after a store stall on
+// that store.
+struct QuantChunk {
+  uint16_t sh;      // fp16 scale bits of the group
+  uint32_t w0, w1;  // packed codes (int4: w0; int8: w0, w1)
+};
+
+template <int BITS, int LPG>
+__device__ __forceinline__ QuantChunk quant_form(const float v[8]) {
+  QuantChunk r;
+  r.sh = scale_bits<BITS>(group_absmax8<LPG>(v));
+  const float safe = safe_scale(r.sh), rs = __builtin_amdgcn_rcpf(safe);
+  float code[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) code[e] = quant_rint<BITS>(v[e], safe, rs);
+  if (BITS == 8) {
+    const uint2 w = pack_codes8_int8(code);
+    r.w0 = w.x;
+    r.w1 = w.y;
+  } else {
+    r.w0 = pack_codes8_int4(code);
+    r.w1 = 0;
+  }
+  return r;
+}
+
+template <int BITS, int LPG>
+__device__ __forceinline__ void quant_store(const QuantChunk& r, int64_t c, uint8_t* q,
+                                            uint16_t* s) {
+  if ((c & (LPG - 1)) == 0) s[c / LPG] = r.sh;
+  if (BITS == 8) reinterpret_cast<uint2*>(q)[c] = make_uint2(r.w0, r.w1);
+  else reinterpret_cast<uint32_t*>(q)[c] = r.w0;
 }
 
 // Outlier channels (zero-and-store): columns with slot[col] >= 0 are copied
@@ -200,17 +238,20 @@ __global__ __launch_bounds__(kBlock) void silu_mul_quant_kernel(
     uint16_t* __restrict__ su, int64_t nchunk) {
   const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   const bool valid = c < nchunk;
-  float gv[8] = {0, 0, 0, 0, 0, 0, 0, 0}, uv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-  if (valid) {
-    Vec8<kBF16>::ld(g, c, gv);
-    Vec8<kBF16>::ld(u, c, uv);
-    float h[8];
+  // lanes past the end load the last chunk and store nothing (they form
+  // whole groups: nchunk is a multiple of the lanes per group)
+  const int64_t cl = valid ? c : nchunk - 1;
+  float gv[8], uv[8], h[8];
+  Vec8<kBF16>::ld(g, cl, gv);
+  Vec8<kBF16>::ld(u, cl, uv);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) h[j] = silu_mul1(gv[j], uv[j]);  // src/flashffn.py:1212-1215
-    Vec8<kBF16>::st(hm, c, h);
-  }
-  quant_chunk<BITS, LPG>(gv, valid, c, qg, sg);
-  quant_chunk<BITS, LPG>(uv, valid, c, qu, su);
+  for (int j = 0; j < 8; ++j) h[j] = silu_mul1(gv[j], uv[j]);  // src/flashffn.py:1212-1215
+  const QuantChunk rg = quant_form<BITS, LPG>(gv);
+  const QuantChunk ru = quant_form<BITS, LPG>(uv);
+  if (!valid) return;
+  Vec8<kBF16>::st(hm, c, h);
+  quant_store<BITS, LPG>(rg, c, qg, sg);
+  quant_store<BITS, LPG>(ru, c, qu, su);
 }
 
 // ---------------------------------------------------------------------------
@@ -411,22 +452,24 @@ __device__ __forceinline__ void store_outlier_words(const uint4& w, const uint4&
   }
 }
 
-// The stored bf16 values of one chunk's outlier columns as packed pairs
-// (0 in the ordinary halves).
+// The stored bf16 values of one chunk's outlier columns as packed pairs; the
+// ordinary halves hold the row's slot-0 value, which the caller's keep mask
+// discards.  The 8 loads go out unconditionally, one after the other, so the
+// lane waits for them once: loads under per-column branches were each
+// followed by their own wait.
 __device__ __forceinline__ uint4 load_outlier_words(const uint4& w, uint32_t row,
                                                     const Outliers& o) {
   const uint16_t* src = o.out + (int64_t)row * o.k;
   const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-  uint32_t r[4];
+  uint32_t v[8];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int lo = (int16_t)(ws[i] & 0xFFFFu), hi = (int32_t)ws[i] >> 16;
-    uint32_t a = 0, b = 0;
-    if (lo >= 0) a = src[lo];
-    if (hi >= 0) b = src[hi];
-    r[i] = a | (b << 16);
+    v[2 * i] = src[max(lo, 0)];
+    v[2 * i + 1] = src[max(hi, 0)];
   }
-  return make_uint4(r[0], r[1], r[2], r[3]);
+  return make_uint4(v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16),
+                    v[6] | (v[7] << 16));
 }
 
 __device__ __forceinline__ void unpack_bf16x8(const uint4& p, float v[8]) {
@@ -450,58 +493,114 @@ __global__ __launch_bounds__(kBlock) void silu_mul_quant_outlier_kernel(
     uint16_t* __restrict__ su, int64_t nchunk, Outliers og, Outliers ou) {
   const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   const bool valid = c < nchunk;
-  uint32_t row = 0, j = 0;
-  if (valid) {
-    row = og.rows.div((uint32_t)c);
-    j = (uint32_t)c - row * og.rows.d;
-  }
-  const uint4 wg = load_slot_words(og, j, valid);
-  const uint4 wu = load_slot_words(ou, j, valid);
-  uint4 pg = make_uint4(0, 0, 0, 0), pu = pg;
-  if (valid) {
-    pg = reinterpret_cast<const uint4*>(g)[c];
-    pu = reinterpret_cast<const uint4*>(u)[c];
-  }
-  float gv[8], uv[8];
+  // lanes past the end work on the last chunk and store nothing (whole groups)
+  const int64_t cl = valid ? c : nchunk - 1;
+  const uint32_t row = og.rows.div((uint32_t)cl);
+  const uint32_t j = (uint32_t)cl - row * og.rows.d;
+  const uint4 wg = load_slot_words(og, j, true);
+  const uint4 wu = load_slot_words(ou, j, true);
+  const uint4 pg = reinterpret_cast<const uint4*>(g)[cl];
+  const uint4 pu = reinterpret_cast<const uint4*>(u)[cl];
+  float gv[8], uv[8], h[8];
   unpack_bf16x8(pg, gv);
   unpack_bf16x8(pu, uv);
-  if (valid) {
-    float h[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) h[e] = silu_mul1(gv[e], uv[e]);  // src/flashffn.py:1212-1215
-    Vec8<kBF16>::st(hm, c, h);
-  }
+  for (int e = 0; e < 8; ++e) h[e] = silu_mul1(gv[e], uv[e]);  // src/flashffn.py:1212-1215
   // zero-and-store (compress_function.py:111-143): the codec sees 0 in the
   // outlier columns
-  if (any_outlier(wg)) store_outlier_words(wg, pg, row, og);
-  if (any_outlier(wu)) store_outlier_words(wu, pu, row, ou);
   unpack_bf16x8(and_words(pg, wg), gv);
   unpack_bf16x8(and_words(pu, wu), uv);
-  quant_chunk<BITS, LPG>(gv, valid, c, qg, sg);
-  quant_chunk<BITS, LPG>(uv, valid, c, qu, su);
+  const QuantChunk rg = quant_form<BITS, LPG>(gv);
+  const QuantChunk ru = quant_form<BITS, LPG>(uv);
+  if (!valid) return;
+  Vec8<kBF16>::st(hm, c, h);
+  if (any_outlier(wg)) store_outlier_words(wg, pg, row, og);
+  if (any_outlier(wu)) store_outlier_words(wu, pu, row, ou);
+  quant_store<BITS, LPG>(rg, c, qg, sg);
+  quant_store<BITS, LPG>(ru, c, qu, su);
 }
 
-template <int BITS, bool WANT_HM>
+// Outlier values for the K2 kernel below, from HBM (any k) or, STAGED, from
+// the block's LDS copy of the outlier rows it touches.
+__device__ __forceinline__ uint4 lds_outlier_words(const uint4& w, const uint16_t* so) {
+  const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  uint32_t v[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int lo = (int16_t)(ws[i] & 0xFFFFu), hi = (int32_t)ws[i] >> 16;
+    v[2 * i] = so[max(lo, 0)];
+    v[2 * i + 1] = so[max(hi, 0)];
+  }
+  return make_uint4(v[0] | (v[1] << 16), v[2] | (v[3] << 16), v[4] | (v[5] << 16),
+                    v[6] | (v[7] << 16));
+}
+
+// Outlier counts the staged K2 takes: the two rows a block can touch, k values
+// each, one value per thread and tensor.
+constexpr int kStagedOutliersMax = kBlock / 2;
+
+// STAGED (k <= kStagedOutliersMax, D / 8 >= kBlock so a block's chunks lie in
+// at most two rows r0, r0 + 1): the block copies those rows' outlier values,
+// 2k contiguous elements of each [N, k] block, into LDS with loads that do not
+// wait on the slot map, so a lane's outlier values are an LDS read away once
+// its slot words arrive.  Otherwise they are loaded from HBM after them.
+template <int BITS, bool WANT_HM, bool STAGED>
 __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_outlier_kernel(
     const uint16_t* gmid, const uint8_t* __restrict__ qg, const uint16_t* __restrict__ sg,
     const uint8_t* __restrict__ qu, const uint16_t* __restrict__ su, uint16_t* dg, uint16_t* du,
-    uint16_t* hm, int64_t nchunk, int gs_shift, Outliers og, Outliers ou) {
+    uint16_t* hm, int64_t nchunk, int64_t n_rows, int gs_shift, Outliers og, Outliers ou) {
+  __shared__ uint16_t so[STAGED ? 4 * kStagedOutliersMax : 1];   // [tensor][2 rows][k]
   const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
-  if (c >= nchunk) return;
-  const uint32_t row = og.rows.div((uint32_t)c);
-  const uint32_t j = (uint32_t)c - row * og.rows.d;
+  const bool valid = c < nchunk;
+  // lanes past the end work on the last chunk and store nothing
+  const int64_t cl = valid ? c : nchunk - 1;
+  const uint32_t row = og.rows.div((uint32_t)cl);
+  const uint32_t j = (uint32_t)cl - row * og.rows.d;
+  const int k = (int)og.k;
+  uint32_t r0 = 0, sv_g = 0, sv_u = 0;
+  bool st_lane = false;
+  if constexpr (STAGED) {
+    r0 = og.rows.div(blockIdx.x * (uint32_t)kBlock);
+    const int64_t avail = (n_rows - r0 < 2 ? n_rows - r0 : 2) * k;
+    st_lane = (int)threadIdx.x < 2 * k;
+    const bool st_ok = st_lane && (int64_t)threadIdx.x < avail;
+    const int64_t off = st_ok ? (int64_t)r0 * k + threadIdx.x : 0;
+    sv_g = og.out[off];
+    sv_u = ou.out[off];
+    if (!st_ok) sv_g = sv_u = 0;
+    // issued before the payload loads, so their LDS writes wait on them alone
+    asm volatile("" ::: "memory");
+  }
   const uint4 wg = load_slot_words(og, j, true);
   const uint4 wu = load_slot_words(ou, j, true);
   float cg[8], cu[8], dh[8];
-  load_codes8<BITS>(qg, c, cg);
-  load_codes8<BITS>(qu, c, cu);
-  Vec8<kBF16>::ld(gmid, c, dh);
-  const int64_t si = (c * 8) >> gs_shift;
+  load_codes8<BITS>(qg, cl, cg);
+  load_codes8<BITS>(qu, cl, cu);
+  Vec8<kBF16>::ld(gmid, cl, dh);
+  const int64_t si = (cl * 8) >> gs_shift;
   const float scg = f16_bits_to_f32(sg[si]);
   const float scu = f16_bits_to_f32(su[si]);
   uint4 og4 = make_uint4(0, 0, 0, 0), ou4 = og4;
-  if (any_outlier(wg)) og4 = load_outlier_words(wg, row, og);
-  if (any_outlier(wu)) ou4 = load_outlier_words(wu, row, ou);
+  if constexpr (STAGED) {
+    if (st_lane) {
+      so[threadIdx.x] = (uint16_t)sv_g;
+      so[2 * k + threadIdx.x] = (uint16_t)sv_u;
+    }
+    // the stage's writes complete, then a plain barrier (one asm statement,
+    // so no LDS read moves above it): __syncthreads() would also wait for the
+    // payload loads still in flight
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    if (any_outlier(wg) || any_outlier(wu)) {
+      const uint32_t dr = row - r0;
+      og4 = lds_outlier_words(wg, so + dr * k);
+      ou4 = lds_outlier_words(wu, so + (2 + dr) * k);
+    }
+  } else {
+    if (any_outlier(wg) || any_outlier(wu)) {
+      og4 = load_outlier_words(wg, row, og);
+      ou4 = load_outlier_words(wu, row, ou);
+    }
+  }
   const uint32_t wgs[4] = {wg.x, wg.y, wg.z, wg.w}, wus[4] = {wu.x, wu.y, wu.z, wu.w};
   const uint32_t ogs[4] = {og4.x, og4.y, og4.z, og4.w}, ous[4] = {ou4.x, ou4.y, ou4.z, ou4.w};
   uint32_t hgw[4], huw[4];
@@ -522,6 +621,7 @@ __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_outlier_kernel(
     swiglu_bwd1(dh[e], hg[e], hu[e], ogr[e], our[e], hact);
     oh[e] = hact * hu[e];  // src/flashffn.py:1298-1300
   }
+  if (!valid) return;
   Vec8<kBF16>::st(dg, c, ogr);
   Vec8<kBF16>::st(du, c, our);
   if (WANT_HM) Vec8<kBF16>::st(hm, c, oh);
@@ -1300,9 +1400,15 @@ int cpt_dequant_swiglu_backward_outlier(const void* grad_h_mid, const void* q_ga
   uint16_t* dg = (uint16_t*)grad_h_gate;
   uint16_t* du = (uint16_t*)grad_h_up;
   uint16_t* hm = (uint16_t*)h_mid_hat;
-#define CPT_K2O(B, W) dequant_swiglu_bwd_outlier_kernel<B, W><<<grid, kBlock, 0, st>>>(gm, qg, sg, qu, su, dg, du, hm, nchunk, sh, og, ou)
-  if (bits == 4) { if (hm) CPT_K2O(4, true); else CPT_K2O(4, false); }
-  else { if (hm) CPT_K2O(8, true); else CPT_K2O(8, false); }
+  const bool staged = k >= 1 && k <= kStagedOutliersMax && d / 8 >= kBlock;
+#define CPT_K2O(B, W, S) dequant_swiglu_bwd_outlier_kernel<B, W, S><<<grid, kBlock, 0, st>>>(gm, qg, sg, qu, su, dg, du, hm, nchunk, n, sh, og, ou)
+  if (staged) {
+    if (bits == 4) { if (hm) CPT_K2O(4, true, true); else CPT_K2O(4, false, true); }
+    else { if (hm) CPT_K2O(8, true, true); else CPT_K2O(8, false, true); }
+  } else {
+    if (bits == 4) { if (hm) CPT_K2O(4, true, false); else CPT_K2O(4, false, false); }
+    else { if (hm) CPT_K2O(8, true, false); else CPT_K2O(8, false, false); }
+  }
 #undef CPT_K2O
   return launch_status();
 }

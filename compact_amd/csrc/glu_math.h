@@ -106,6 +106,15 @@ __device__ __forceinline__ int quant_code(float v, float safe, float rsafe) {
   return (int)r;
 }
 
+// quant_code as a clamped integral float (the form the byte packers take).
+template <int BITS>
+__device__ __forceinline__ float quant_rint(float v, float safe, float rsafe) {
+  const float q = v * rsafe;
+  float r = __builtin_rintf(q);
+  if (__builtin_fabsf(q - r) > 0.5f - 0.000244140625f) r = __builtin_rintf(v / safe);
+  return fminf(fmaxf(r, -QMax<BITS>::v), QMax<BITS>::v);
+}
+
 // The codes of the 8 values a thread owns in one group, as clamped integral
 // floats, with one branch for all eight: when any fast-path quotient lies
 // near a half-integer, all eight are recomputed from the correctly rounded

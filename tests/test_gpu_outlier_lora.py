@@ -102,16 +102,21 @@ def test_outlier_codec_bit_exact(device, bits, group):
     assert np.array_equal(deq.cpu().view(torch.int16).numpy().view(np.uint16), rdeq)
 
 
-@pytest.mark.parametrize("bits,group,n,d", [(4, 64, 256, 1024), (8, 128, 256, 1024),
-                                            (4, 64, 7, 1024), (8, 512, 258, 2048),
-                                            (4, 8, 1, 1024), (8, 32, 5, 1024)])
-def test_outlier_k1_k2_equal_standalone(device, bits, group, n, d):
-    """K1 takes kK1Rows rows per thread: row counts that are not a multiple
-    of it, one row, and groups of 1 to 64 lanes."""
+@pytest.mark.parametrize("bits,group,n,d,ratio", [
+    (4, 64, 256, 1024, 0.01), (8, 128, 256, 1024, 0.01), (4, 64, 7, 1024, 0.01),
+    (8, 512, 258, 2048, 0.01), (4, 8, 1, 1024, 0.01), (8, 32, 5, 1024, 0.01),
+    (4, 64, 300, 4096, 0.01), (4, 64, 3, 11008, 0.01), (8, 128, 513, 2048, 0.0625),
+    (4, 64, 300, 4096, 0.05), (8, 128, 130, 2048, 0.0)])
+def test_outlier_k1_k2_equal_standalone(device, bits, group, n, d, ratio):
+    """K1 / K2 with outlier channels against the standalone codec and GLU
+    kernels, bit for bit: groups of 1 to 64 lanes, one row, ragged row counts
+    (a part-empty last block), and both K2 forms: the block's outlier rows
+    staged in LDS (k <= 128 with D / 8 >= 256, k = 128 at the limit) and read
+    from HBM (k = 204; D / 8 < 256); no outliers at all (k = 0)."""
     cpt, _ = _cpt()
     a, b = _hot(n, d, 9)
     ga, gb = a.to(device), b.to(device)
-    k = int(d * 0.01)
+    k = int(d * ratio)
     sg_, _ = cpt.outlier_select(ga, k)
     su_, _ = cpt.outlier_select(gb, k)
     hm, qg, sg, og, qu, su, ou = cpt.silu_mul_quant_outlier(ga, gb, bits, group, sg_, su_, k)
