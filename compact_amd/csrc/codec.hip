@@ -25,18 +25,6 @@ namespace cpt {
 
 constexpr int kBlock = 256;
 
-// Codes of 8 consecutive elements packed as stored: int8 -> 8 bytes,
-// int4 -> 4 bytes of (code+8) nibbles, even column low (src/flashffn.py:1081-1085).
-template <int BITS>
-__device__ __forceinline__ void store_codes8(uint8_t* q, int64_t c, const float v[8], float safe) {
-  const float rs = __builtin_amdgcn_rcpf(safe);
-  float r[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = quant_rint<BITS>(v[e], safe, rs);
-  if (BITS == 8) reinterpret_cast<uint2*>(q)[c] = pack_codes8_int8(r);
-  else reinterpret_cast<uint32_t*>(q)[c] = pack_codes8_int4(r);
-}
-
 // Codes of 8 consecutive elements as floats.
 template <int BITS>
 __device__ __forceinline__ void load_codes8(const uint8_t* q, int64_t c, float code[8]) {
@@ -63,21 +51,12 @@ __device__ __forceinline__ uint32_t group_absmax8(const float v[8]) {
   return group_max_u32<LPG>(am);
 }
 
-// Quantise the 8 elements this thread owns; lane 0 of each group writes the scale.
-template <int BITS, int LPG>
-__device__ __forceinline__ void quant_chunk(const float v[8], bool valid, int64_t c,
-                                            uint8_t* q, uint16_t* s) {
-  const uint32_t am = group_absmax8<LPG>(v);
-  const uint16_t sh = scale_bits<BITS>(am);
-  if (!valid) return;
-  if ((c & (LPG - 1)) == 0) s[c / LPG] = sh;
-  store_codes8<BITS>(q, c, v, safe_scale(sh));
-}
-
-// quant_chunk split in two, so that a kernel can form every output before it
+// Quantisation of the 8 elements a thread owns (lane 0 of each group writes
+// the scale) in two steps, so that a kernel can form every output before it
 // stores any: on gfx950 a wait for a load also waits for the stores issued
 // before it (one counter for both), so loads consumed after a store stall on
-// that store.
+// that store.  Codes packed as stored: int8 -> 8 bytes, int4 -> 4 bytes of
+// (code+8) nibbles, even column low (src/flashffn.py:1081-1085).
 struct QuantChunk {
   uint16_t sh;      // fp16 scale bits of the group
   uint32_t w0, w1;  // packed codes (int4: w0; int8: w0, w1)
@@ -113,8 +92,7 @@ __device__ __forceinline__ void quant_store(const QuantChunk& r, int64_t c, uint
 // Outlier channels (zero-and-store): columns with slot[col] >= 0 are copied
 // out as bf16 into out[row * k + slot] and zeroed before the codec sees them
 // (HyC-LoRA's outlier extraction, hyclora/operators/compress_function.py:111-143,
-// on the v3 per-group codec).  v holds 8 consecutive elements of one row.
-
+// on the v3 per-group codec).
 struct Outliers {
   const int16_t* slot;   // [D], -1 for ordinary columns
   uint16_t* out;         // [N, k] bf16
@@ -157,20 +135,6 @@ __device__ __forceinline__ ChunkSlots load_slots8(const Outliers& o, int64_t col
   return cs;
 }
 
-// Copy the chunk's outlier columns out as bf16 and zero them in v.  The
-// stores run only in lanes whose chunk holds an outlier (~8% at 1% of d_ff).
-__device__ __forceinline__ void extract_outliers8(float v[8], int64_t row, const ChunkSlots& cs,
-                                                  const Outliers& o) {
-  if (cs.mask) {
-    uint16_t* dst = o.out + row * o.k;
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if ((cs.mask >> j) & 1u) dst[cs.slot(j)] = (uint16_t)f32_to_bf16_bits(v[j]);
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) v[j] = ((cs.mask >> j) & 1u) ? 0.0f : v[j];
-}
-
 // The stored bf16 values of the chunk's outlier columns (0 elsewhere),
 // fetched ahead of the dequantisation they replace.
 __device__ __forceinline__ void fetch_outliers8(float ov[8], int64_t row, const ChunkSlots& cs,
@@ -209,22 +173,36 @@ __global__ __launch_bounds__(kBlock) void quantize_fast_kernel(
 #pragma unroll
   for (int i = 0; i < kQuantCPT; ++i) {
     const int64_t c = base + i * kBlock;
+    // lanes past the end work on the last chunk and store nothing
+    const int64_t cl = c < nchunk ? c : nchunk - 1;
     if (OUTL) {
       int64_t col = 0;
-      row[i] = 0;
-      if (c < nchunk) chunk_rc(c, d, o, row[i], col);
-      cs[i] = load_slots8(o, col, c < nchunk);
+      chunk_rc(cl, d, o, row[i], col);
+      cs[i] = load_slots8(o, col, true);
     }
+    Vec8<DT>::ld(t, cl, v[i]);
+  }
+  // every output formed before the first store (a wait for a load also waits
+  // for the stores issued before it)
+  QuantChunk r[kQuantCPT];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[i][j] = 0.0f;
-    if (c < nchunk) Vec8<DT>::ld(t, c, v[i]);
+  for (int i = 0; i < kQuantCPT; ++i) {
+    float z[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) z[e] = (OUTL && ((cs[i].mask >> e) & 1u)) ? 0.0f : v[i][e];
+    r[i] = quant_form<BITS, LPG>(z);
   }
 #pragma unroll
   for (int i = 0; i < kQuantCPT; ++i) {
     const int64_t c = base + i * kBlock;
-    const bool valid = c < nchunk;
-    if (OUTL) extract_outliers8(v[i], row[i], cs[i], o);
-    quant_chunk<BITS, LPG>(v[i], valid, c, q, s);
+    if (c >= nchunk) continue;
+    if (OUTL && cs[i].mask) {
+      uint16_t* dst = o.out + row[i] * o.k;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if ((cs[i].mask >> e) & 1u) dst[cs[i].slot(e)] = (uint16_t)f32_to_bf16_bits(v[i][e]);
+    }
+    quant_store<BITS, LPG>(r[i], c, q, s);
   }
 }
 
