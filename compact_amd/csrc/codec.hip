@@ -526,7 +526,7 @@ template <int BITS, bool WANT_HM, bool STAGED>
 __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_outlier_kernel(
     const uint16_t* gmid, const uint8_t* __restrict__ qg, const uint16_t* __restrict__ sg,
     const uint8_t* __restrict__ qu, const uint16_t* __restrict__ su, uint16_t* dg, uint16_t* du,
-    uint16_t* hm, int64_t nchunk, int64_t n_rows, int gs_shift, Outliers og, Outliers ou) {
+    uint16_t* hm, int64_t nchunk, int gs_shift, Outliers og, Outliers ou) {
   __shared__ uint16_t so[STAGED ? 4 * kStagedOutliersMax : 1];   // [tensor][2 rows][k]
   const int64_t c = (int64_t)blockIdx.x * kBlock + threadIdx.x;
   const bool valid = c < nchunk;
@@ -538,8 +538,10 @@ __global__ __launch_bounds__(kBlock) void dequant_swiglu_bwd_outlier_kernel(
   uint32_t r0 = 0, sv_g = 0, sv_u = 0;
   bool st_lane = false;
   if constexpr (STAGED) {
+    // the rows of the block's first and last chunks (one row for most blocks)
+    const int64_t c_last = min((int64_t)blockIdx.x * kBlock + kBlock - 1, nchunk - 1);
     r0 = og.rows.div(blockIdx.x * (uint32_t)kBlock);
-    const int64_t avail = (n_rows - r0 < 2 ? n_rows - r0 : 2) * k;
+    const int64_t avail = (int64_t)(og.rows.div((uint32_t)c_last) - r0 + 1) * k;
     st_lane = (int)threadIdx.x < 2 * k;
     const bool st_ok = st_lane && (int64_t)threadIdx.x < avail;
     const int64_t off = st_ok ? (int64_t)r0 * k + threadIdx.x : 0;
@@ -1379,7 +1381,7 @@ int cpt_dequant_swiglu_backward_outlier(const void* grad_h_mid, const void* q_ga
   uint16_t* du = (uint16_t*)grad_h_up;
   uint16_t* hm = (uint16_t*)h_mid_hat;
   const bool staged = k >= 1 && k <= kStagedOutliersMax && d / 8 >= kBlock;
-#define CPT_K2O(B, W, S) dequant_swiglu_bwd_outlier_kernel<B, W, S><<<grid, kBlock, 0, st>>>(gm, qg, sg, qu, su, dg, du, hm, nchunk, n, sh, og, ou)
+#define CPT_K2O(B, W, S) dequant_swiglu_bwd_outlier_kernel<B, W, S><<<grid, kBlock, 0, st>>>(gm, qg, sg, qu, su, dg, du, hm, nchunk, sh, og, ou)
   if (staged) {
     if (bits == 4) { if (hm) CPT_K2O(4, true, true); else CPT_K2O(4, false, true); }
     else { if (hm) CPT_K2O(8, true, true); else CPT_K2O(8, false, true); }
