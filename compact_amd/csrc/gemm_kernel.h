@@ -1113,14 +1113,17 @@ __device__ __forceinline__ void dglu_finish(const KArgs& A, int64_t m0, int64_t 
       any_out |= sg8[e] >= 0 || su8[e] >= 0;
     }
   }
+  // Rows go UNROLL at a time, software-pipelined: the cache loads of the next
+  // rows are issued before this batch's stores.  A wait for a load also waits
+  // for the stores issued before it (one counter for both), so loads issued
+  // after a batch's stores would stall on them.
   constexpr int UNROLL = 4;
-#pragma unroll 1
-  for (int p0 = 0; p0 < 32; p0 += UNROLL) {
-    uint4 dh[UNROLL];
-    uint4 cg[UNROLL], cu[UNROLL];    // codes (low bytes used) or bf16 cache
-    float sgv[UNROLL], suv[UNROLL];
-    bool ok[UNROLL];
-    int64_t mrow[UNROLL];
+  uint4 dh[UNROLL];
+  uint4 cg[UNROLL], cu[UNROLL];    // codes (low bytes used) or bf16 cache
+  float sgv[UNROLL], suv[UNROLL];
+  bool ok[UNROLL];
+  int64_t mrow[UNROLL];
+  auto load_rows = [&](int p0) {
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
       const int r = (p0 + u) * 8 + (tid >> 5);
@@ -1149,8 +1152,17 @@ __device__ __forceinline__ void dglu_finish(const KArgs& A, int64_t m0, int64_t 
         }
       }
     }
+  };
+  load_rows(0);
+#pragma unroll 1
+  for (int p0 = 0; p0 < 32; p0 += UNROLL) {
+    uint4 og4[UNROLL], ou4[UNROLL], oh4[UNROLL];
+    bool ok_now[UNROLL];
+    int64_t off_now[UNROLL];
 #pragma unroll
     for (int u = 0; u < UNROLL; ++u) {
+      ok_now[u] = ok[u];
+      off_now[u] = mrow[u] * D + d;
       if (!ok[u]) continue;
       float hg[8], hu[8], dhf[8];
       const uint32_t dw[4] = {dh[u].x, dh[u].y, dh[u].z, dh[u].w};
@@ -1194,17 +1206,20 @@ __device__ __forceinline__ void dglu_finish(const KArgs& A, int64_t m0, int64_t 
         swiglu_bwd1(dhf[e], hg[e], hu[e], og[e], ou[e], hact);
         oh[e] = hact * hu[e];
       }
-      const int64_t off = mrow[u] * D + d;
-      *reinterpret_cast<uint4*>(A.grad_gate + off) =
-          make_uint4(pack_bf16x2(og[0], og[1]), pack_bf16x2(og[2], og[3]),
-                     pack_bf16x2(og[4], og[5]), pack_bf16x2(og[6], og[7]));
-      *reinterpret_cast<uint4*>(A.grad_up + off) =
-          make_uint4(pack_bf16x2(ou[0], ou[1]), pack_bf16x2(ou[2], ou[3]),
-                     pack_bf16x2(ou[4], ou[5]), pack_bf16x2(ou[6], ou[7]));
-      if (A.h_mid_hat)
-        *reinterpret_cast<uint4*>(A.h_mid_hat + off) =
-            make_uint4(pack_bf16x2(oh[0], oh[1]), pack_bf16x2(oh[2], oh[3]),
-                       pack_bf16x2(oh[4], oh[5]), pack_bf16x2(oh[6], oh[7]));
+      og4[u] = make_uint4(pack_bf16x2(og[0], og[1]), pack_bf16x2(og[2], og[3]),
+                          pack_bf16x2(og[4], og[5]), pack_bf16x2(og[6], og[7]));
+      ou4[u] = make_uint4(pack_bf16x2(ou[0], ou[1]), pack_bf16x2(ou[2], ou[3]),
+                          pack_bf16x2(ou[4], ou[5]), pack_bf16x2(ou[6], ou[7]));
+      oh4[u] = make_uint4(pack_bf16x2(oh[0], oh[1]), pack_bf16x2(oh[2], oh[3]),
+                          pack_bf16x2(oh[4], oh[5]), pack_bf16x2(oh[6], oh[7]));
+    }
+    if (p0 + UNROLL < 32) load_rows(p0 + UNROLL);
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      if (!ok_now[u]) continue;
+      *reinterpret_cast<uint4*>(A.grad_gate + off_now[u]) = og4[u];
+      *reinterpret_cast<uint4*>(A.grad_up + off_now[u]) = ou4[u];
+      if (A.h_mid_hat) *reinterpret_cast<uint4*>(A.h_mid_hat + off_now[u]) = oh4[u];
     }
   }
 }
