@@ -362,12 +362,13 @@ constexpr int kDualCols = 512;   // X columns per block
 constexpr int kDualTok = 64;     // tokens per piece (16 per wavefront for the projection)
 constexpr int kDualLd = 520;     // LDS row stride of the X piece (elements)
 constexpr int kDualLdP = 40;     // LDS row stride of the P piece (elements)
+constexpr int kDualQLd = 32;     // LDS row stride of the staged B slice (elements, R <= 32)
 
 template <int NB>
 __global__ __launch_bounds__(256) void skinny_dual_kernel(
     const uint16_t* __restrict__ x, int64_t ldx, const uint16_t* __restrict__ q, int64_t ldq,
     const uint16_t* __restrict__ p, int64_t ldp, int64_t T, int64_t N, int R, int64_t tchunk,
-    float* __restrict__ ws_c, float* __restrict__ ws_z, int q_nr) {
+    float* __restrict__ ws_c, float* __restrict__ ws_z, int qmode) {
   __shared__ __attribute__((aligned(16))) uint16_t xs[kDualTok * kDualLd];
   __shared__ __attribute__((aligned(16))) uint16_t ps[kDualTok * kDualLdP];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -381,9 +382,10 @@ __global__ __launch_bounds__(256) void skinny_dual_kernel(
   // past N read zero (offsets past the records)
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + t_begin * ldx, (T - t_begin) * ldx * 2);
   const __amdgpu_buffer_rsrc_t rp = make_rsrc(p + t_begin * ldp, (T - t_begin) * ldp * 2);
-  // Q as [R][ldq] (rank rows, q_nr == 0) or [N][ldq] (the B factor itself,
-  // q_nr == 1: 8 two-byte loads per fragment, once per block)
-  const __amdgpu_buffer_rsrc_t rq = make_rsrc(q, (q_nr ? N : (int64_t)R) * ldq * 2);
+  // Q as [R][ldq] (rank rows, qmode 0) or [N][ldq] (the B factor itself:
+  // qmode 1 with 16-byte rows, staged through LDS; qmode 2 otherwise, 8
+  // two-byte loads per fragment), read once per block
+  const __amdgpu_buffer_rsrc_t rq = make_rsrc(q, (qmode ? N : (int64_t)R) * ldq * 2);
   // X piece loads: 16 per thread, row 4 i + tid / 64, 16-byte chunk tid % 64
   const int xr = tid >> 6, xc = (tid & 63) * 8;
   const bool xok = n0 + xc < N;
@@ -392,26 +394,49 @@ __global__ __launch_bounds__(256) void skinny_dual_kernel(
   const bool pok = pc < R;
   // Q fragments of the block's 512 columns: k-step st (32 columns), term t
   bf16x8 qf[16][NB];
+  if (qmode == 1) {
+    // B [N][ldq] as stored, ldq % 8 == 0: the block's 512 rows x R ranks go
+    // through LDS (xs, before the first piece) in 16-byte loads, rows
+    // kDualQLd apart, and each fragment (8 consecutive rows of one rank) comes
+    // back with two transposing reads
 #pragma unroll
-  for (int st = 0; st < 16; ++st)
-#pragma unroll
-    for (int t = 0; t < NB; ++t) {
-      const int64_t col = n0 + st * 32 + 8 * (lane >> 4);
-      const int r = t * 16 + (lane & 15);
-      if (!q_nr) {
-        qf[st][t] = bload(rq, col < N && r < R ? (uint32_t)(((int64_t)r * ldq + col) * 2) : kOOB);
-      } else {
-        uint32_t w[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t off =
-              col + e < N && r < R ? (uint32_t)(((col + e) * ldq + r) * 2) : kOOB;
-          w[e >> 1] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rq, off, 0, 0)
-                       << ((e & 1) * 16);
-        }
-        qf[st][t] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
-      }
+    for (int i = 0; i < kDualCols * 4 / 256; ++i) {
+      const int e = i * 256 + tid, rb = e >> 2, ch = e & 3;
+      const bool ok = ch * 8 < R && n0 + rb < N;
+      const uint4 v = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(
+                     rq, ok ? (uint32_t)(((n0 + rb) * ldq + ch * 8) * 2) : kOOB, 0, 0));
+      *reinterpret_cast<uint4*>(&xs[rb * kDualQLd + ch * 8]) = v;
     }
+    __syncthreads();
+#pragma unroll
+    for (int st = 0; st < 16; ++st)
+#pragma unroll
+      for (int t = 0; t < NB; ++t) qf[st][t] = red_frag<kDualQLd>(xs, st * 32, t * 16, lane);
+    // the main loop's first barrier orders these reads before xs is rewritten
+  } else {
+#pragma unroll
+    for (int st = 0; st < 16; ++st)
+#pragma unroll
+      for (int t = 0; t < NB; ++t) {
+        const int64_t col = n0 + st * 32 + 8 * (lane >> 4);
+        const int r = t * 16 + (lane & 15);
+        if (qmode == 0) {
+          qf[st][t] = bload(rq, col < N && r < R ? (uint32_t)(((int64_t)r * ldq + col) * 2) : kOOB);
+        } else {
+          // B as stored with a row stride that is not a multiple of 8
+          uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const uint32_t off =
+                col + e < N && r < R ? (uint32_t)(((col + e) * ldq + r) * 2) : kOOB;
+            w[e >> 1] |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rq, off, 0, 0)
+                         << ((e & 1) * 16);
+          }
+          qf[st][t] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
+        }
+      }
+  }
   f32x4 az[8][NB];
 #pragma unroll
   for (int c = 0; c < 8; ++c)
@@ -680,15 +705,18 @@ int cpt_gemm_bf16_skinny_dual(const void* x, int64_t ldx, const void* q, int64_t
   float* ws_z = ws_c + csplits * T * R;
   hipStream_t st = (hipStream_t)stream;
   const dim3 grid((unsigned)csplits, (unsigned)splits);
+  // Q's form in the kernel: 0 rank rows, 1 B as stored with 16-byte rows
+  // (staged through LDS), 2 B as stored otherwise
+  const int qmode = !q_nr ? 0 : ((ldq & 7) == 0 && al16(q) ? 1 : 2);
   if (T > 0) {
     if (R <= 16)
       hipLaunchKernelGGL(skinny_dual_kernel<1>, grid, dim3(256), 0, st, (const uint16_t*)x, ldx,
                          (const uint16_t*)q, ldq, (const uint16_t*)p, ldp, T, N, (int)R, tchunk,
-                         ws_c, ws_z, q_nr ? 1 : 0);
+                         ws_c, ws_z, qmode);
     else
       hipLaunchKernelGGL(skinny_dual_kernel<2>, grid, dim3(256), 0, st, (const uint16_t*)x, ldx,
                          (const uint16_t*)q, ldq, (const uint16_t*)p, ldp, T, N, (int)R, tchunk,
-                         ws_c, ws_z, q_nr ? 1 : 0);
+                         ws_c, ws_z, qmode);
     if (hipGetLastError() != hipSuccess) return kErrLaunch;
     const int64_t tc = T * R;
     hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((tc + 255) / 256)), dim3(256), 0, st,
