@@ -937,16 +937,18 @@ __global__ __launch_bounds__(kPickThreads) void outlier_pick_kernel(SelectSet S,
       if (tid < 256) hist[tid] = 0;
       __syncthreads();
       for (int64_t i0 = 0; i0 < d; i0 += kPickThreads) {
-        // the two top bytes (sign, exponent) are shared by nearly all sums:
-        // there, one LDS atomic per distinct digit in the wavefront instead
-        // of 64 atomics on one bin
+        // the top byte (sign, high exponent bits) is shared by nearly all
+        // sums: there, one LDS atomic per distinct digit in the wavefront
+        // instead of 64 atomics on one bin.  From the next byte on (low
+        // exponent and mantissa bits) the digits spread over tens of bins,
+        // where a loop over distinct digits costs more than plain atomics.
         const int64_t i = i0 + tid;
         int digit = -1;
         if (i < d) {
           const unsigned long long key = (unsigned long long)__double_as_longlong(v[i]);
           if ((key & mask) == prefix) digit = (int)((key >> shift) & 0xFF);
         }
-        if (pass < 6) {                 // mantissa bytes: spread digits, plain atomics
+        if (pass < 7) {
           if (digit >= 0) atomicAdd(&hist[digit], 1);
           continue;
         }
