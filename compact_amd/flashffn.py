@@ -59,6 +59,12 @@ _FUSED_GROUPS = (32, 64, 128)
 # code stores cost more inside the power-limited GEMM than K1 does at HBM
 # speed).
 _F1_CODEC_CACHES = ("int8",)
+# ... and only from this many tokens: below about four waves of F1 tiles the
+# fused codec epilogue cannot hide behind later tiles' MFMAs, and the bf16
+# dual GEMM plus the standalone K1 is faster (int8 g128 at 2048 tokens,
+# d_model 2048, d_ff 5632: 118.8 against 110.1 us; at 8192 tokens 372.9
+# against 386.0 us).  The two routes are bit-identical.
+_F1_CODEC_MIN_TOKENS = 4096
 # Outlier channels (config C3) with a bf16 activation and d_model a multiple
 # of 64.  True: the first sequence (which ranks the channels) runs the dual
 # GEMM with a bf16 output, the selection and K1 with outliers, and every
@@ -272,7 +278,7 @@ class FlashFFNv3Function(torch.autograd.Function):
             xa_g, xa_u, lkw = _gate_up_lora(x_2d, a_gate, b_gate, s_gate, a_up, b_up, s_up)
         fused_quant = (quant and use_triton and x.dtype == torch.bfloat16)   # :1424-1426
         if (fusable and fused_quant and k_out == 0 and group_size in _FUSED_GROUPS
-                and cache_mode in _F1_CODEC_CACHES):
+                and cache_mode in _F1_CODEC_CACHES and x_2d.shape[0] >= _F1_CODEC_MIN_TOKENS):
             # dual GEMM + GLU + codec in one kernel (K1 fused into the epilogue)
             h_mid, _, _, c_gate, qs_gate, c_up, qs_up = G.ffn_gate_up(
                 x_2d, w_gate, w_up, _CACHE_CODE[cache_mode], group_size, **lkw)
@@ -842,7 +848,8 @@ class FlashFFNv3AdapterFunction(torch.autograd.Function):
 
         c_gate = qs_gate = c_up = qs_up = None
         h_gate = h_up = xa_g = xa_u = None
-        if fusable and fused_quant and group_size in _FUSED_GROUPS and cache_mode in _F1_CODEC_CACHES:
+        if (fusable and fused_quant and group_size in _FUSED_GROUPS
+                and cache_mode in _F1_CODEC_CACHES and x_2d.shape[0] >= _F1_CODEC_MIN_TOKENS):
             h_mid, _, _, c_gate, qs_gate, c_up, qs_up = G.ffn_gate_up(
                 x_2d, w_gate, w_up, _CACHE_CODE[cache_mode], group_size)
             _V3_COUNTERS["triton_quant_fwd"] += 1
