@@ -65,6 +65,7 @@ SIGNATURES = {
     "cpt_topk_abs": [_P, _I, _L, _L, _L, _P, _P, _P],
     "cpt_topk_scatter": [_P, _P, _I, _L, _L, _L, _P, _P],
     "cpt_gemm_stream_k_workspace": [_P, _L],
+    "cpt_transpose_bf16": [_P, _L, _L, _L, _P, _L, _P],
     "cpt_gemm_bf16_skinny_dual": [_P, _L, _P, _L, _I, _P, _L, _P, _L, ctypes.c_float, _P, _L, _I,
                                   ctypes.c_float, _L, _L, _L, _I, _P, _P],
 }

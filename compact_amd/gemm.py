@@ -235,6 +235,27 @@ def skinny_t(x: torch.Tensor, p: torch.Tensor, alpha: float = 1.0, trans: bool =
 SKINNY_DUAL_BLOCKS = 256
 
 
+def transpose_ok(x: torch.Tensor) -> bool:
+    """transpose takes a bf16 row-major [rows, cols] device tensor with rows,
+    cols and the row stride multiples of 8 and a 16-byte aligned base."""
+    return (x.dtype == torch.bfloat16 and x.is_cuda and x.dim() == 2 and x.stride(1) == 1
+            and x.shape[0] % 8 == 0 and x.shape[1] % 8 == 0 and x.stride(0) % 8 == 0
+            and x.data_ptr() % 16 == 0)
+
+
+def transpose(x: torch.Tensor, name: str = "transpose") -> torch.Tensor:
+    """x^T as a new row-major [cols, rows] bf16 tensor (cpt_transpose_bf16)."""
+    _require_device(x)
+    assert transpose_ok(x), "transpose operand"
+    rows, cols = x.shape
+    out = torch.empty((cols, rows), dtype=x.dtype, device=x.device)
+    with _timed(name):
+        rc = _lib.lib().cpt_transpose_bf16(x.data_ptr(), x.stride(0), rows, cols, out.data_ptr(),
+                                           out.stride(0), _stream(x))
+    check(rc, name)
+    return out
+
+
 def skinny_dual_ok(x: torch.Tensor, q: torch.Tensor, p: torch.Tensor) -> bool:
     """skinny_dual takes bf16 x [T, N] with N a multiple of 8 and a rank
     (q [R, N], p [T, R]) that is a multiple of 8 up to 32."""

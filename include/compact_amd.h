@@ -233,6 +233,14 @@ int cpt_gemm_bf16_skinny_dual(const void* x, int64_t ldx, const void* q, int64_t
                               void* z, int64_t ldz, int z_trans, float alpha_z, int64_t T,
                               int64_t N, int64_t R, int splits, void* workspace, void* stream);
 
+/* dst [cols][ld_dst] = src [rows][ld_src] transposed (bf16).  No reference
+ * counterpart: a layout helper for the weight gradients dg^T x and du^T x
+ * (src/flashffn.py:1585,1587), which then read x^T as a K-major operand with
+ * bit-identical results.  rows, cols and both strides multiples of 8,
+ * pointers 16-byte aligned. */
+int cpt_transpose_bf16(const void* src, int64_t ld_src, int64_t rows, int64_t cols, void* dst,
+                       int64_t ld_dst, void* stream);
+
 /* No counterpart in the reference.  cpt_gemm_bf16_skinny_t for callers that
  * cannot allocate (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc): the same kernels and result, with the

@@ -355,3 +355,40 @@ def test_mfma_probe_runs_and_scales_with_iters(device, shape):
     assert lib.cpt_probe_mfma_rate(shape, 0, 1, 0.5, out1.data_ptr(), s) != 0
     assert lib.cpt_probe_mfma_rate(shape, 8, 0, 0.5, out1.data_ptr(), s) != 0
     assert lib.cpt_probe_mfma_rate(2, 8, 1, 0.5, out1.data_ptr(), s) != 0
+
+
+@pytest.mark.parametrize("rows,cols", [(8, 8), (64, 64), (136, 200), (1024, 4096), (8200, 264)])
+def test_transpose_bf16(device, rows, cols):
+    """cpt_transpose_bf16 against torch's transposed copy, bit for bit:
+    whole and partial 64 x 64 tiles, and a strided source (row stride past
+    the column count)."""
+    _, G = _cpt()
+    x = rnd((rows, cols), 31, device)
+    assert torch.equal(G.transpose(x), x.t().contiguous())
+    wide = rnd((rows, cols + 24), 32, device)
+    v = wide[:, 8:8 + cols]
+    assert torch.equal(G.transpose(v), v.t().contiguous())
+
+
+@pytest.mark.parametrize("mode", ["int8", "bf16"])
+def test_wgrad_transposed_x_route_bitwise(device, monkeypatch, mode):
+    """The full fine-tune weight gradients dg^T x and du^T x read x^T as a
+    K-major operand from _XT_MIN_TOKENS tokens on: forced either way at one
+    shape, every output and gradient is bit-identical."""
+    from compact_amd import flashffn as FF
+    from oracle import flashffn_ref as R
+    cpt, _ = _cpt()
+    ps = R.synthetic_param_set("fullft", 256, 768, 16, 2.0, seed=7, dtype=torch.bfloat16)
+    ps = {k: (v.to(device) if isinstance(v, torch.Tensor) else v) for k, v in ps.items()}
+    x = rnd((520, 256), 33, device)
+    gy = rnd((520, 256), 34, device)
+    out = {}
+    for threshold in (0, 10 ** 9):
+        monkeypatch.setattr(FF, "_XT_MIN_TOKENS", threshold)
+        out[threshold] = R.run_function_grads(cpt.FlashFFNv3Function.apply, ps, x, gy, mode, 64,
+                                              True)
+    (g0, y0), (g1, y1) = out[0], out[10 ** 9]
+    assert torch.equal(y0, y1)
+    assert set(g0) == set(g1) and "w_gate" in g0 and "w_up" in g0
+    for k in g0:
+        assert torch.equal(g0[k], g1[k]), k
