@@ -62,11 +62,25 @@ struct QuantChunk {
   uint32_t w0, w1;  // packed codes (int4: w0; int8: w0, w1)
 };
 
-template <int BITS, int LPG>
+// BF16_IN: the values are bf16, so the division-free quant_snap8 applies.
+template <int BITS, int LPG, bool BF16_IN>
 __device__ __forceinline__ QuantChunk quant_form(const float v[8]) {
   QuantChunk r;
   r.sh = scale_bits<BITS>(group_absmax8<LPG>(v));
   const float safe = safe_scale(r.sh), rs = __builtin_amdgcn_rcpf(safe);
+  if constexpr (BF16_IN) {
+    float z[8];
+    quant_snap8<BITS>(v, rs, z);
+    if (BITS == 8) {
+      const uint2 w = pack_snap8_int8(z);
+      r.w0 = w.x;
+      r.w1 = w.y;
+    } else {
+      r.w0 = pack_snap8_int4(z);
+      r.w1 = 0;
+    }
+    return r;
+  }
   float code[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) code[e] = quant_rint<BITS>(v[e], safe, rs);
@@ -190,7 +204,7 @@ __global__ __launch_bounds__(kBlock) void quantize_fast_kernel(
     float z[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) z[e] = (OUTL && ((cs[i].mask >> e) & 1u)) ? 0.0f : v[i][e];
-    r[i] = quant_form<BITS, LPG>(z);
+    r[i] = quant_form<BITS, LPG, DT == kBF16>(z);
   }
 #pragma unroll
   for (int i = 0; i < kQuantCPT; ++i) {
@@ -224,8 +238,8 @@ __global__ __launch_bounds__(kBlock) void silu_mul_quant_kernel(
   Vec8<kBF16>::ld(u, cl, uv);
 #pragma unroll
   for (int j = 0; j < 8; ++j) h[j] = silu_mul1(gv[j], uv[j]);  // src/flashffn.py:1212-1215
-  const QuantChunk rg = quant_form<BITS, LPG>(gv);
-  const QuantChunk ru = quant_form<BITS, LPG>(uv);
+  const QuantChunk rg = quant_form<BITS, LPG, true>(gv);
+  const QuantChunk ru = quant_form<BITS, LPG, true>(uv);
   if (!valid) return;
   Vec8<kBF16>::st(hm, c, h);
   quant_store<BITS, LPG>(rg, c, qg, sg);
@@ -488,8 +502,8 @@ __global__ __launch_bounds__(kBlock) void silu_mul_quant_outlier_kernel(
   // outlier columns
   unpack_bf16x8(and_words(pg, wg), gv);
   unpack_bf16x8(and_words(pu, wu), uv);
-  const QuantChunk rg = quant_form<BITS, LPG>(gv);
-  const QuantChunk ru = quant_form<BITS, LPG>(uv);
+  const QuantChunk rg = quant_form<BITS, LPG, true>(gv);
+  const QuantChunk ru = quant_form<BITS, LPG, true>(uv);
   if (!valid) return;
   Vec8<kBF16>::st(hm, c, h);
   if (any_outlier(wg)) store_outlier_words(wg, pg, row, og);

@@ -998,12 +998,12 @@ __device__ __forceinline__ void glu_finish(const KArgs& A, int64_t m0, int64_t n
         if (!ok) continue;
         if ((tid & (GS / 8 - 1)) == 0) (t ? A.s_up : A.s_gate)[m * G + d / GS] = sh;
         uint8_t* qp = t ? A.q_up : A.q_gate;
-        float r[8];
-        quant_rint8<BITS>(v, safe, rs, r);
+        float z[8];
+        quant_snap8<BITS>(v, rs, z);    // v is bf16 (the staged tile)
         if constexpr (BITS == 8)
-          *reinterpret_cast<uint2*>(qp + off) = pack_codes8_int8(r);
+          *reinterpret_cast<uint2*>(qp + off) = pack_snap8_int8(z);
         else
-          *reinterpret_cast<uint32_t*>(qp + m * (D >> 1) + (d >> 1)) = pack_codes8_int4(r);
+          *reinterpret_cast<uint32_t*>(qp + m * (D >> 1) + (d >> 1)) = pack_snap8_int4(z);
       }
     }
   }

@@ -115,30 +115,75 @@ __device__ __forceinline__ float quant_rint(float v, float safe, float rsafe) {
   return fminf(fmaxf(r, -QMax<BITS>::v), QMax<BITS>::v);
 }
 
-// The codes of the 8 values a thread owns in one group, as clamped integral
-// floats, with one branch for all eight: when any fast-path quotient lies
-// near a half-integer, all eight are recomputed from the correctly rounded
-// division, which equals the fast path wherever that one is valid.  Same
-// codes as quant_code, element for element.
+// Codes of bf16 values with no division and no fallback: the same codes as
+// quant_rint, from v * rcp(safe) rounded twice.
+//   (1) y = fma(v, rs, 3072): the exact product, rounded once onto the
+//       2^-12 grid (fp32 values in [2048, 4096) are the multiples of 2^-12;
+//       |v * rs| < 256 keeps y inside).
+//   (2) z = y + (1.5 * 2^23 - 3072 + off) = 1.5 * 2^23 + off + rint(y - 3072),
+//       exactly: fp32 values in [2^23, 2^24) are the integers, and the sum is
+//       rounded to nearest even.
+// Why rint(y - 3072) = rint(fp32(v / safe)).  Write v = m_v 2^a (integer
+// m_v < 256, v bf16) and safe = m_s 2^b (integer 1 <= m_s < 2048, safe fp16
+// or 1).  For a half-integer h >= 1/2, v / safe - h = (2 m_v 2^(a-b) -
+// (2k+1) m_s) / (2 m_s).  If a - b >= -1 the numerator is an integer, so
+// v / safe is h or at least 1 / 4094 from it.  If a - b <= -2 it is a
+// multiple of 2^(a-b+1), and v / safe > 1/2 - 2^-12 forces 2^(a-b) >
+// m_s / 511, so the distance is 0 or above 1/511.  Quotients here satisfy
+// |v / safe| < 256 (at most 1.5 qmax, with fp16-subnormal scales), and rs =
+// v_rcp_f32(safe) is within 1 ulp of 1 / safe, so |v * rs - v / safe| <=
+// 2^-15.  A tie (v / safe = h) then lies within 2^-15 < 2^-13 of the grid
+// point h and (1) returns h exactly, whose rint in (2) is round-half-even,
+// as rint of the exact fp32 quotient h.  Any other quotient lies at least
+// 1/4094 - 2^-15 > 2^-13 from every h, so (1) keeps it on its side of each
+// h, as does fp32's own rounding of the quotient (at most 2^-17): both
+// rints agree.  An exhaustive check over every bf16 v and fp16 scale, with
+// rs up to 2 ulp off, is in tests/quant_snap_check.c.  Not valid for fp16 or
+// fp32 inputs (more significant bits close the gap).
+//
+// z stays an fp32, clamped to the code range; its low byte is then the
+// stored byte: int8 off = 0, the two's complement of the code (1.5 * 2^23
+// has 22 zero low bits); int4 off = 8, code + 8.
 template <int BITS>
-__device__ __forceinline__ void quant_rint8(const float v[8], float safe, float rsafe,
-                                            float r[8]) {
-  float worst = 0.0f;
+__device__ __forceinline__ void quant_snap8(const float v[8], float rs, float z[8]) {
+  constexpr float kGrid = 3072.0f;
+  constexpr float kInt = 12582912.0f;                   // 1.5 * 2^23
+  constexpr float kOff = BITS == 4 ? 8.0f : 0.0f;
+  constexpr float kLo = kInt + kOff - QMax<BITS>::v, kHi = kInt + kOff + QMax<BITS>::v;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float q = v[e] * rsafe;
-    r[e] = __builtin_rintf(q);
-    worst = fmaxf(worst, __builtin_fabsf(q - r[e]));
+    const float y = __builtin_fmaf(v[e], rs, kGrid);
+    z[e] = fminf(fmaxf(y + (kInt - kGrid + kOff), kLo), kHi);
   }
-  if (worst > 0.5f - 0.000244140625f) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) r[e] = __builtin_rintf(v[e] / safe);
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = fminf(fmaxf(r[e], -QMax<BITS>::v), QMax<BITS>::v);
 }
 
-// Eight codes (quant_rint8's integral floats) packed as stored
+// Byte 0 of each of four words, in order, as one word.
+__device__ __forceinline__ uint32_t low_bytes4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  // v_perm_b32 (S0, S1, sel): selectors 0-3 pick bytes of S1, 4-7 of S0,
+  // 0x0C gives a zero byte
+  const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0C0C0400u);
+  const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x0C0C0400u);
+  return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
+}
+
+// quant_snap8's eight values packed as stored (same bytes as pack_codes8_*).
+__device__ __forceinline__ uint2 pack_snap8_int8(const float z[8]) {
+  uint32_t b[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) b[e] = __float_as_uint(z[e]);
+  return make_uint2(low_bytes4(b[0], b[1], b[2], b[3]), low_bytes4(b[4], b[5], b[6], b[7]));
+}
+
+__device__ __forceinline__ uint32_t pack_snap8_int4(const float z[8]) {
+  // byte 0 of (odd << 4) | even: the even column's code + 8 in the low
+  // nibble, the odd one's in the high nibble
+  uint32_t p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = (__float_as_uint(z[2 * i + 1]) << 4) | __float_as_uint(z[2 * i]);
+  return low_bytes4(p[0], p[1], p[2], p[3]);
+}
+
+// Eight codes (quant_rint's integral floats) packed as stored
 // (src/flashffn.py:1081-1085).  int4: byte b holds column 2b in its low
 // nibble and 2b + 1 in its high one, each as code + 8; the byte's value
 // r[2b] + 16 r[2b+1] + 136 is a small integer, exact in fp32, and

@@ -96,3 +96,54 @@ def test_codes_at_half_integer_ties(device, bits, gs, dtype):
         hm, qg, sg, qu, su = cpt.silu_mul_quant(tv.to(device), tv.to(device), bits, gs)
         assert torch.equal(qg.cpu().view(torch.uint8), torch.from_numpy(rq.view(np.uint8)))
         assert torch.equal(qu.cpu().view(torch.uint8), torch.from_numpy(rq.view(np.uint8)))
+
+
+def _bf16_round(x):
+    """float64 -> nearest bf16 (round-half-even), as float32."""
+    f = np.asarray(x, np.float32)
+    u = f.view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16
+    return u.astype(np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("bits,gs", [(4, 64), (8, 128)])
+def test_bf16_codes_near_ties_over_scales(device, bits, gs):
+    """bf16 inputs take the division-free code rule (two roundings of v *
+    rcp(safe)).  Sweep every bf16 group maximum over 40 binades (fp16-
+    subnormal, normal and large scales), and fill each group with the bf16
+    values nearest to half-integer multiples of its scale and their bf16
+    neighbours: exact ties where representable, the closest non-ties
+    otherwise.  Codes and scales of the quantiser and of K1 (both tensors)
+    must equal the oracle's."""
+    cpt = _cpt()
+    qmax = 7 if bits == 4 else 127
+    rng = np.random.default_rng(100 + bits)
+    mant = np.arange(128, dtype=np.uint32)
+    exps = np.arange(127 - 28, 127 + 12, dtype=np.uint32)     # 2^-28 .. 2^11
+    amax = ((exps[:, None] << 23) | (mant[None, :] << 16)).reshape(-1).view(np.float32)
+    s = (amax / np.float32(qmax)).astype(np.float16).astype(np.float64)
+    safe = np.where(s > 0, s, 1.0)
+    k = rng.integers(-qmax - 1, qmax + 1, size=(amax.size, gs))
+    near = _bf16_round((k + 0.5) * safe[:, None])
+    step = rng.integers(-1, 2, size=near.shape).astype(np.int32) << 16   # bf16 neighbours
+    v = (near.view(np.int32) + step * (near != 0)).view(np.float32)
+    v = np.clip(v, -amax[:, None], amax[:, None])
+    v[:, 0] = amax
+    v[:, 1] = -amax * rng.choice([0.0, 0.5, 1.0], size=amax.size).astype(np.float32)
+    v = _bf16_round(v)
+    rows = 64
+    pad = (-v.shape[0]) % rows
+    v = np.concatenate([v, np.zeros((pad, gs), np.float32)]).reshape(rows, -1)
+    tv = torch.from_numpy(v).to(torch.bfloat16)
+    assert torch.equal(tv.float(), torch.from_numpy(v))                   # exact bf16 values
+    rq, rs = codec.quantize_group_absmax(v, bits, gs)
+    q, sc = cpt.v3_quantize_group_absmax(tv.to(device), bits, gs)
+    assert np.array_equal(sc.cpu().numpy().view(np.uint16), rs.view(np.uint16))
+    assert np.array_equal(q.cpu().numpy().view(np.uint8), rq.view(np.uint8))
+    u = torch.flip(tv, dims=[1]).contiguous()
+    rqu, rsu = codec.quantize_group_absmax(u.float().numpy(), bits, gs)
+    hm, qg, sg, qu, su = cpt.silu_mul_quant(tv.to(device), u.to(device), bits, gs)
+    assert np.array_equal(qg.cpu().numpy().view(np.uint8), rq.view(np.uint8))
+    assert np.array_equal(sg.cpu().numpy().view(np.uint16), rs.view(np.uint16))
+    assert np.array_equal(qu.cpu().numpy().view(np.uint8), rqu.view(np.uint8))
+    assert np.array_equal(su.cpu().numpy().view(np.uint16), rsu.view(np.uint16))
