@@ -50,21 +50,27 @@ _CACHE_CODE = {"int4": _lib.CACHE_INT4, "int8": _lib.CACHE_INT8, "bf16": _lib.CA
                "recompute": _lib.CACHE_NONE}
 _FUSED_GROUPS = (32, 64, 128)
 # Cache formats whose codec runs in the gate/up dual GEMM's epilogue (K1 fused,
-# only codes and h_mid leave the kernel).  The other formats take the same
-# dual GEMM with a bf16 epilogue and then the standalone K1; the two paths are
-# bit-identical.  Measured on MI355X, fused against bf16 out + K1: int8 g128
-# at C2 1256 against 1272 us (fused kept); int4 g64 1268 against 1254 us at
-# the C2 dims, 401 against 388 us at TinyLlama dims with 8192 tokens and 126
-# against 112 us with 2048 (the int4 epilogue's smaller groups and half-line
-# code stores cost more inside the power-limited GEMM than K1 does at HBM
-# speed).
-_F1_CODEC_CACHES = ("int8",)
-# ... and only from this many tokens: below about four waves of F1 tiles the
-# fused codec epilogue cannot hide behind later tiles' MFMAs, and the bf16
-# dual GEMM plus the standalone K1 is faster (int8 g128 at 2048 tokens,
-# d_model 2048, d_ff 5632: 118.8 against 110.1 us; at 8192 tokens 372.9
-# against 386.0 us).  The two routes are bit-identical.
-_F1_CODEC_MIN_TOKENS = 4096
+# only codes and h_mid leave the kernel), and from how many tokens.  Otherwise
+# the forward runs the same dual GEMM with a bf16 epilogue and then the
+# standalone K1; the two paths are bit-identical.  Measured on MI355X, fused
+# against bf16 out + K1 (us, with and without LoRA terms in the epilogue):
+#   d_model 2048, d_ff 5632:  2048 tokens int8 110.5 / 106.6, int4 109.2 / 105.6;
+#                             4096 tokens int8 178.4 / 180.1, int4 177.6 / 175.9;
+#                             8192 tokens int8 350.8 / 377.0, int4 348.7 / 366.3;
+#   d_model 4096, d_ff 11008: fused faster at every count from 1024 to 16384
+#                             (ratio 0.96-0.99; C2: 1141 / 1187 int8).
+# Below that the codec epilogue's VALU work (one wavefront per SIMD, so the
+# block's MFMAs idle meanwhile) costs more than K1 at HBM speed; a longer
+# k-loop per tile (larger d_model) and more waves of tiles amortise it.
+_F1_CODEC_MIN_TOKENS = {"int8": 4096, "int4": 8192}
+_F1_CODEC_WIDE_D_MODEL = 4096      # from here on, at any token count
+
+
+def _f1_codec_fused(cache_mode: str, tokens: int, d_model: int) -> bool:
+    m = _F1_CODEC_MIN_TOKENS.get(cache_mode)
+    return m is not None and (tokens >= m or d_model >= _F1_CODEC_WIDE_D_MODEL)
+
+
 # Outlier channels (config C3) with a bf16 activation and d_model a multiple
 # of 64.  True: the first sequence (which ranks the channels) runs the dual
 # GEMM with a bf16 output, the selection and K1 with outliers, and every
@@ -290,7 +296,7 @@ class FlashFFNv3Function(torch.autograd.Function):
             xa_g, xa_u, lkw = _gate_up_lora(x_2d, a_gate, b_gate, s_gate, a_up, b_up, s_up)
         fused_quant = (quant and use_triton and x.dtype == torch.bfloat16)   # :1424-1426
         if (fusable and fused_quant and k_out == 0 and group_size in _FUSED_GROUPS
-                and cache_mode in _F1_CODEC_CACHES and x_2d.shape[0] >= _F1_CODEC_MIN_TOKENS):
+                and _f1_codec_fused(cache_mode, x_2d.shape[0], hidden_dim)):
             # dual GEMM + GLU + codec in one kernel (K1 fused into the epilogue)
             h_mid, _, _, c_gate, qs_gate, c_up, qs_up = G.ffn_gate_up(
                 x_2d, w_gate, w_up, _CACHE_CODE[cache_mode], group_size, **lkw)
@@ -868,7 +874,7 @@ class FlashFFNv3AdapterFunction(torch.autograd.Function):
         c_gate = qs_gate = c_up = qs_up = None
         h_gate = h_up = xa_g = xa_u = None
         if (fusable and fused_quant and group_size in _FUSED_GROUPS
-                and cache_mode in _F1_CODEC_CACHES and x_2d.shape[0] >= _F1_CODEC_MIN_TOKENS):
+                and _f1_codec_fused(cache_mode, x_2d.shape[0], hidden_dim)):
             h_mid, _, _, c_gate, qs_gate, c_up, qs_up = G.ffn_gate_up(
                 x_2d, w_gate, w_up, _CACHE_CODE[cache_mode], group_size)
             _V3_COUNTERS["triton_quant_fwd"] += 1

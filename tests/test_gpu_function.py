@@ -131,19 +131,23 @@ def test_fused_equals_unfused_bitwise(device, mode, config):
 
 
 @pytest.mark.parametrize("config", ["fullft", "none"])
-def test_fused_codec_epilogue_route_at_any_token_count(device, monkeypatch, config):
-    """Below _F1_CODEC_MIN_TOKENS the int8 forward runs the bf16 dual GEMM
-    and the standalone K1 instead of the codec epilogue: forced either way at
-    the same small shape, y, the cache and every gradient are bit-identical."""
+@pytest.mark.parametrize("mode", ["int8", "int4"])
+def test_fused_codec_epilogue_route_at_any_token_count(device, monkeypatch, config, mode):
+    """Below _F1_CODEC_MIN_TOKENS (and d_model _F1_CODEC_WIDE_D_MODEL) the
+    forward runs the bf16 dual GEMM and the standalone K1 instead of the
+    codec epilogue: forced either way at the same small shape, y, the cache
+    and every gradient are bit-identical."""
     from compact_amd import flashffn as FF
     ps = _to(R.synthetic_param_set(config, H, D, RANK, S, seed=6), device)
     gen = torch.Generator().manual_seed(14)
     x = torch.randn(N, H, generator=gen).to(torch.bfloat16).to(device)
     gy = torch.randn(N, H, generator=gen).to(torch.bfloat16).to(device)
+    monkeypatch.setattr(FF, "_F1_CODEC_WIDE_D_MODEL", H + 1)
     out = {}
     for threshold in (0, N + 1):
-        monkeypatch.setattr(FF, "_F1_CODEC_MIN_TOKENS", threshold)
-        out[threshold] = _run(ps, x, gy, "int8", 128)
+        monkeypatch.setattr(FF, "_F1_CODEC_MIN_TOKENS", {"int8": threshold, "int4": threshold})
+        assert FF._f1_codec_fused(mode, N, H) == (threshold == 0)
+        out[threshold] = _run(ps, x, gy, mode, 64 if mode == "int4" else 128)
     (g0, y0), (g1, y1) = out[0], out[N + 1]
     assert torch.equal(y0, y1)
     for k in g0:
