@@ -179,6 +179,38 @@ def test_gate_up_fused_ragged_dff(device, cache, bits, group, inter, n_tok, hid)
     test_gate_up_fused_equals_unfused(device, cache, bits, group, n_tok, hid, inter)
 
 
+@pytest.mark.parametrize("cache,bits,group", [("int8", 8, 128), ("int4", 4, 64), ("int4", 4, 32)])
+def test_gate_up_codec_mixed_scale_ranges(device, cache, bits, group):
+    """F1's codec epilogue over every scale range: rows scaled by 1e-4 give
+    fp16-subnormal scales (quotients up to 1.5 qmax, which the clamp
+    decides), zero rows scale 0, and the rest normal scales, mixed within
+    wavefronts and alone in others.  Codes and scales equal the plain
+    product's through K1."""
+    cpt, G = _cpt()
+    from compact_amd import _lib
+    code = {"int4": _lib.CACHE_INT4, "int8": _lib.CACHE_INT8}[cache]
+    n_tok, hid, inter = 512, 256, 512
+    x = rnd((n_tok, hid), 13, device)
+    r = torch.arange(n_tok, device=device)
+    f = torch.where((r // 2) % 3 == 0, 1e-4, 1.0)            # mixed within wavefronts
+    f = torch.where((r >= 256) & (r < 320), 1e-4, f)          # tiny-only wavefronts
+    f = torch.where((r % 37) == 5, 0.0, f)                    # zero rows: scale 0
+    x = (x.float() * f[:, None]).to(torch.bfloat16)
+    wg = rnd((inter, hid), 14, device, 0.05)
+    wu = rnd((inter, hid), 15, device, 0.05)
+    hm, _, _, qg, sg, qu, su = G.ffn_gate_up(x, wg, wu, code, group)
+    hg_ref = plain_like_f1(G, x, wg)
+    hu_ref = plain_like_f1(G, x, wu)
+    _, rqg, rsg, rqu, rsu = cpt.silu_mul_quant(hg_ref, hu_ref, bits, group)
+    sub = ((rsg.view(torch.int16) > 0) & (rsg.view(torch.int16) < 0x0400)).sum().item()
+    zero = (rsg.view(torch.int16) == 0).sum().item()
+    assert sub > 100 and zero > 10, (sub, zero)
+    assert torch.equal(qg.view(torch.uint8), rqg.view(torch.uint8))
+    assert torch.equal(qu.view(torch.uint8), rqu.view(torch.uint8))
+    assert torch.equal(sg.view(torch.int16), rsg.view(torch.int16))
+    assert torch.equal(su.view(torch.int16), rsu.view(torch.int16))
+
+
 def plain_like_b1(G, gy, wd):
     """gy . W_d in the summation order of B1 (the dgrad GEMM with the K2
     epilogue): the 16x16x32 loop when d_model is a multiple of 64
