@@ -78,11 +78,12 @@ def _f1_codec_fused(cache_mode: str, tokens: int, d_model: int) -> bool:
 # (G.ffn_gate_up_outlier), so only h_mid and the compressed cache of those
 # rows reach HBM.  False (the default): the dual GEMM with a bf16 output for
 # every row, then the selection and K1 with outliers.  The caches, outputs
-# and gradients are bit-identical.  Measured at C3 on MI355X: forward 1.99
-# against 1.89 ms, step 4.11 against 4.01 ms (the two dual GEMMs 1.347 ms
-# against 1.089 + 0.137 for one dual GEMM and K1): the int4 outlier codec
-# inside the power-limited GEMM, and the first sequence's 1.34 waves of
-# tiles, cost more than the 720 MB bf16 round trip at HBM speed.
+# and gradients are bit-identical.  Measured at C3 on MI355X with the
+# division-free quantiser: step 3.94 against 3.82 ms (the two dual GEMMs
+# 1.286 ms plus 0.019 for the first sequence's K1, against 1.073 + 0.122 for
+# one dual GEMM and K1): the int4 outlier codec inside the power-limited
+# GEMM, and the first sequence's 1.34 waves of tiles, cost more than the
+# 720 MB bf16 round trip at HBM speed.
 _F1_OUTLIER_FUSED = False
 # Group sizes whose dequantise + SwiGLU backward runs in the dgrad GEMM's
 # epilogue (G.ffn_down_dgrad, on the 16x16x32 loop when d_model is a multiple
