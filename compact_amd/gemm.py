@@ -148,8 +148,11 @@ def _lora_args(terms, n_q):
 
 
 SKINNY_MAX_RANK = 32
-# blocks of 128 rows x one K range the skinny projection aims for
-SKINNY_BLOCKS = 512
+# blocks of 128 rows x one K range the skinny projection aims for.  In the C3
+# step on MI355X (M = 8192: 4 K ranges) h_mid A_d^T took 44.5 us and
+# x [A_g; A_u]^T 21.5 us, against 52.0 and 23.6 at 512 blocks (8 ranges) and
+# 52.4 / 24.6 at 384, including their reductions.
+SKINNY_BLOCKS = 256
 
 # Buffer offsets are 32-bit.  Every kernel's resource starts where a block's
 # reads start (a tile's first row, a split's first token or k row), so an
@@ -175,9 +178,8 @@ def skinny(a: torch.Tensor, q: torch.Tensor, alpha: float = 1.0,
         a = a.contiguous()
     if q.stride(1) != 1 or q.stride(0) % 8 or q.stride(0) < K or q.data_ptr() % 16:
         q = q.contiguous()
-    # K ranges for ~512 blocks of 128 rows (each range >= 256 of K): more
-    # ranges cost more partials than they gain in parallelism (measured at
-    # M = 8192, K = 4096 / 11008: 3.6 / 4.9 TB/s)
+    # K ranges for ~SKINNY_BLOCKS blocks of 128 rows (each range >= 256 of
+    # K): more ranges cost more partials than they gain in parallelism
     blocks = (M + 127) // 128
     splits = max(1, min(K // 256, (SKINNY_BLOCKS + blocks - 1) // blocks))
     if out is None:
@@ -232,7 +234,13 @@ def skinny_t(x: torch.Tensor, p: torch.Tensor, alpha: float = 1.0, trans: bool =
     return out
 
 
-SKINNY_DUAL_BLOCKS = 256
+# Blocks of a skinny_dual launch (column blocks x token splits).  In the C3
+# step on MI355X, 176 (8 token splits over d_ff 11008, 22 over d_model 4096)
+# against 256: 64.6 / 62.7 / 37.1 us against 66.6 / 68.8 / 44.5 us for the
+# gate, up and down passes including their reductions (128, 352, 512 and 704
+# blocks were no better).  Fewer, longer token splits also cut the Z partials
+# by a third.
+SKINNY_DUAL_BLOCKS = 176
 
 
 def transpose_ok(x: torch.Tensor) -> bool:
