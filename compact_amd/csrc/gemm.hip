@@ -192,7 +192,7 @@ inline int set_lora(KArgs& A, const LoraTerms& L, int64_t m_p, int64_t n_q, int&
   terms = 0;
   A.lalpha[0] = A.lalpha[1] = -0.0f;
   if (L.rank == 0) return kOk;
-  if (L.rank != 8 && L.rank != 16) return kErrShape;
+  if (L.rank != 8 && L.rank != 16 && L.rank != 24 && L.rank != 32) return kErrShape;
   if (L.ldp < L.rank || (L.ldp & 7)) return kErrAlign;
   if (!L.q_kmajor && L.ldq < n_q) return kErrShape;
   if (!L.p[0] && !L.p[1]) return kErrShape;
@@ -267,6 +267,8 @@ int gemm_bf16_impl(const void* a, int64_t lda, int a_kmajor, const void* b, int6
     if (nt16)
       return b_kmajor ? launch_nt16<true, true, EPI_STORE, 0, 0, 2>(A, st)
                       : launch_nt16<true, false, EPI_STORE, 0, 0, 2>(A, st);
+    // the engine carries adapter ranks up to 16
+    if (L.rank > 16) return kErrShape;
     if (terms == 1)
       return b_kmajor ? launch<true, true, EPI_STORE, 0, 0, 1>(A, st)
                       : launch<true, false, EPI_STORE, 0, 0, 1>(A, st);
@@ -404,6 +406,8 @@ int ffn_gate_up_impl(const void* x, const void* w_gate, const void* w_up, int64_
     }
 #undef CPT_F1_NT16
   }
+  // the engine carries adapter ranks up to 16
+  if (L.rank > 16) return kErrShape;
   // the dual kernel carries both terms (gate, up); an absent one is a no-op
   switch (cache) {
     case CACHE_NONE:
@@ -505,6 +509,7 @@ int ffn_down_dgrad_impl(const void* grad_y, const void* w_down, int64_t n_tok, i
     }
 #undef CPT_B1_NT16
   }
+  if (L.rank > 16) return kErrShape;   // the engine carries adapter ranks up to 16
   switch (cache) {
     case CACHE_BF16:
       return terms ? launch<true, false, EPI_DGLU, CACHE_BF16, 64, 1>(A, st)

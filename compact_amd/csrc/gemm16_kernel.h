@@ -136,7 +136,8 @@ __device__ __forceinline__ int mn_swz(int k) { return 2 * ((k & 3) | ((k & 8) >>
 // ---------------------------------------------------------------------------
 // Adapter (LoRA) terms in the epilogue: out = bf16(bf16(acc) + bf16(alpha *
 // bf16(P_t Q_t^T))) per term, PEFT's order.  The rank-sized product of each
-// 16 x 16 block is one v_mfma_f32_16x16x16_bf16: lane l supplies k
+// 16 x 16 block is one v_mfma_f32_16x16x16_bf16 over k 0..15 (and, for a rank
+// above 16, a second over k 16..31 accumulated onto it): lane l supplies k
 // 4 (l / 16) .. + 3 of row l % 16 of a block (Q for the n side, P for the m
 // side); k past the rank, rows past an operand's end and an absent term's null
 // P read zero through the buffer range check.  An absent term also has
@@ -145,16 +146,16 @@ __device__ __forceinline__ int mn_swz(int k) { return 2 * ((k & 3) | ((k & 8) >>
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ s16x4 lora4_km(__amdgpu_buffer_rsrc_t rs, int64_t ld, int64_t row, int r,
-                                          int lane) {
-  const int k0 = (lane >> 4) * 4;
+                                          int lane, int kb = 0) {
+  const int k0 = kb + (lane >> 4) * 4;
   const uint32_t off = k0 < r ? (uint32_t)((row * ld + k0) * 2) : kOOB;
   return __builtin_bit_cast(s16x4, __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0));
 }
 
 // Q stored [r][ld] (n contiguous): 4 k of column n, one 2-byte load each
 __device__ __forceinline__ s16x4 lora4_mn(__amdgpu_buffer_rsrc_t rs, int64_t ld, int64_t n, int r,
-                                          int lane) {
-  const int k0 = (lane >> 4) * 4;
+                                          int lane, int kb = 0) {
+  const int k0 = kb + (lane >> 4) * 4;
   s16x4 v;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
@@ -166,15 +167,25 @@ __device__ __forceinline__ s16x4 lora4_mn(__amdgpu_buffer_rsrc_t rs, int64_t ld,
 
 // One wave's adapter fragments: p[t][j] the m-side rows of P_t (block j),
 // q[t][i] the n-side rows of Q_t (block i; DUAL: term t's blocks only, gate
-// i < 4 and up i >= 4).
+// i < 4 and up i >= 4), over k 0..15.  HI (ranks 17..32, kernels of their
+// own, so the rank-16 kernels keep their code and registers): ph / qh the
+// same over k 16..31, which a second MFMA accumulates.
+template <bool HI>
 struct Lora16 {
   s16x4 p[2][8];
   s16x4 q[2][8];
 };
+template <>
+struct Lora16<true> {
+  s16x4 p[2][8];
+  s16x4 q[2][8];
+  s16x4 ph[2][8];
+  s16x4 qh[2][8];
+};
 
-template <bool DUAL, int LT>
+template <bool DUAL, int LT, bool HI>
 __device__ __forceinline__ void lora16_load(const KArgs& A, int64_t m0, int64_t n0, int wm, int wn,
-                                            int lane, Lora16& F) {
+                                            int lane, Lora16<HI>& F) {
   const int r = A.lrank;
 #pragma unroll
   for (int t = 0; t < LT; ++t) {
@@ -182,11 +193,22 @@ __device__ __forceinline__ void lora16_load(const KArgs& A, int64_t m0, int64_t 
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       F.p[t][j] = lora4_km(rp, A.lldp, m0 + wm * 128 + 16 * j + (lane & 15), r, lane);
+    if constexpr (HI) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        F.ph[t][j] = lora4_km(rp, A.lldp, m0 + wm * 128 + 16 * j + (lane & 15), r, lane, 16);
+    }
     if constexpr (DUAL) {
       const __amdgpu_buffer_rsrc_t rq = make_rsrc(A.lq[t], A.lq[t] ? A.D * r * 2 : 0);
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii)
         F.q[t][4 * t + ii] = lora4_km(rq, r, (n0 >> 1) + wn * 64 + 16 * ii + (lane & 15), r, lane);
+      if constexpr (HI) {
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii)
+          F.qh[t][4 * t + ii] =
+              lora4_km(rq, r, (n0 >> 1) + wn * 64 + 16 * ii + (lane & 15), r, lane, 16);
+      }
     } else {
       const int64_t qbytes = A.lq_km ? A.N * r * 2 : (int64_t)r * A.lldq * 2;
       const __amdgpu_buffer_rsrc_t rq = make_rsrc(A.lq[t], qbytes);
@@ -194,21 +216,26 @@ __device__ __forceinline__ void lora16_load(const KArgs& A, int64_t m0, int64_t 
       for (int i = 0; i < 8; ++i) {
         const int64_t n = n0 + wn * 128 + 16 * i + (lane & 15);
         F.q[t][i] = A.lq_km ? lora4_km(rq, r, n, r, lane) : lora4_mn(rq, A.lldq, n, r, lane);
+        if constexpr (HI)
+          F.qh[t][i] = A.lq_km ? lora4_km(rq, r, n, r, lane, 16)
+                               : lora4_mn(rq, A.lldq, n, r, lane, 16);
       }
     }
   }
 }
 
 // accumulator block (i, j) with the kernel's LT adapter terms applied
-template <bool DUAL, int LT>
-__device__ __forceinline__ f32x4 acc16(const KArgs& A, const f32x4& a, const Lora16& F, int i,
+template <bool DUAL, int LT, bool HI>
+__device__ __forceinline__ f32x4 acc16(const KArgs& A, const f32x4& a, const Lora16<HI>& F, int i,
                                        int j) {
   f32x4 v = a;
 #pragma unroll
   for (int t = 0; t < LT; ++t) {
     if (DUAL && (i >> 2) != t) continue;
-    const f32x4 l = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(F.q[t][i], F.p[t][j],
-                                                             f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    f32x4 l = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(F.q[t][i], F.p[t][j],
+                                                       f32x4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+    if constexpr (HI)   // k 16..31 onto the fp32 sum of k 0..15
+      l = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(F.qh[t][i], F.ph[t][j], l, 0, 0, 0);
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       v[r] = round_bf16(round_bf16(v[r]) + round_bf16(A.lalpha[t] * round_bf16(l[r])));
@@ -252,7 +279,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int64_t kSkSlot = 256 * 256;            // floats per partial (one tile)
 constexpr int kSkSpin = 1 << 22;
 
-template <bool AK, bool BK, int EPI, int CACHE, int GS, int LT, bool SK>
+template <bool AK, bool BK, int EPI, int CACHE, int GS, int LT, bool SK, bool HI>
 __device__ __forceinline__ void nt16_tile(const KArgs& A, uint16_t* lds, int tm, int tn, int kb,
                                           int ke, int role, int sk_s) {
   static_assert(LT == 0 || AK, "adapter terms ride with a K-major A (P's rows are tokens)");
@@ -477,8 +504,8 @@ __device__ __forceinline__ void nt16_tile(const KArgs& A, uint16_t* lds, int tm,
   // live across the main loop.
   const int etid = epi_tid();
   const int elane = etid & 63;
-  Lora16 F;
-  if constexpr (LT > 0) lora16_load<DUAL, LT>(A, m0, n0, wm, wn, elane, F);
+  Lora16<HI> F;
+  if constexpr (LT > 0) lora16_load<DUAL, LT, HI>(A, m0, n0, wm, wn, elane, F);
   if constexpr (EPI == EPI_STORE || EPI == EPI_DGLU) {
     // bf16(acc) is staged as a row-major tile (rows kLdOut apart: 32 lanes of
     // one 8-byte write cover the 64 banks once), then 32 threads store each
@@ -504,7 +531,7 @@ __device__ __forceinline__ void nt16_tile(const KArgs& A, uint16_t* lds, int tm,
         // accumulator copies spilled the values that live across the loop
         asm volatile("" : "+v"(base));
         if (part) base += pv[j];
-        const f32x4 v = LT > 0 ? acc16<false, LT>(A, base, F, i, j) : base;
+        const f32x4 v = LT > 0 ? acc16<false, LT, HI>(A, base, F, i, j) : base;
         *reinterpret_cast<uint2*>(lds + ml * kLdOut + nl) =
             make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
       }
@@ -536,7 +563,7 @@ __device__ __forceinline__ void nt16_tile(const KArgs& A, uint16_t* lds, int tm,
       for (int j = 0; j < 8; ++j) {
         const int ml = wm * 128 + 16 * j + (elane & 15);
         const int dl = wn * 64 + 16 * (i & 3) + 4 * (elane >> 4);
-        f32x4 v = LT > 0 ? acc16<true, LT>(A, acc[i][j], F, i, j) : acc[i][j];
+        f32x4 v = LT > 0 ? acc16<true, LT, HI>(A, acc[i][j], F, i, j) : acc[i][j];
         asm volatile("" : "+v"(v));
         *reinterpret_cast<uint2*>((i < 4 ? sg : su) + ml * kGluLd + dl) =
             make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
@@ -548,17 +575,19 @@ __device__ __forceinline__ void nt16_tile(const KArgs& A, uint16_t* lds, int tm,
 
 // SK: the stream-K schedule (plain store with a K-major A only); without it
 // one whole tile per block.  Two kernels, so the one-tile-per-block kernel
-// keeps its own register allocation.
-template <bool AK, bool BK, int EPI, int CACHE, int GS, int LT, bool SK>
+// keeps its own register allocation.  HI: adapter ranks 17..32 (a third
+// kernel, one tile per block).
+template <bool AK, bool BK, int EPI, int CACHE, int GS, int LT, bool SK, bool HI = false>
 __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
   static_assert(!SK || (EPI == EPI_STORE && AK), "stream-K: plain store, K-major A");
+  static_assert(!HI || (LT > 0 && !SK), "ranks above 16: adapter kernels, one tile per block");
   extern __shared__ __attribute__((aligned(16))) uint16_t lds[];
   const int nk = (int)(A.K[0] / kBK) + (A.npairs == 2 ? (int)(A.K[1] / kBK) : 0);
   const int b = blockIdx.x;
   if constexpr (!SK) {
     int tm, tn;
     tile_coords_of(b, gridDim.x, A.tiles_m, A.tiles_n, tm, tn);
-    nt16_tile<AK, BK, EPI, CACHE, GS, LT, SK>(A, lds, tm, tn, 0, nk, kRoleWhole, 0);
+    nt16_tile<AK, BK, EPI, CACHE, GS, LT, SK, HI>(A, lds, tm, tn, 0, nk, kRoleWhole, 0);
     return;
   }
   // A data-parallel block (b < sk_dp) has one item, its whole tile.  Stream-K
@@ -584,7 +613,7 @@ __global__ __launch_bounds__(kThreads, 1) void nt16_kernel(const KArgs A) {
     if (dp) tile_coords_of(b, A.sk_dp, A.tiles_m, A.tiles_n, tm, tn);
     else logical_coords(A.sk_dp + t, A.tiles_m, A.tiles_n, tm, tn);
     if (t != t_top) __syncthreads();   // the last item's epilogue read LDS
-    nt16_tile<AK, BK, EPI, CACHE, GS, LT, SK>(A, lds, tm, tn, kb, ke, role, s);
+    nt16_tile<AK, BK, EPI, CACHE, GS, LT, SK, false>(A, lds, tm, tn, kb, ke, role, s);
   }
 }
 
@@ -598,15 +627,20 @@ int launch_nt16(const KArgs& A, hipStream_t st) {
   constexpr bool kSkOk = EPI == EPI_STORE && AK;
   auto kern = nt16::nt16_kernel<AK, BK, EPI, CACHE, GS, LT, false>;
   auto kern_sk = nt16::nt16_kernel<AK, BK, EPI, CACHE, GS, LT, kSkOk>;
+  // adapter ranks 17..32 (LT == 0: the same kernel as kern)
+  auto kern_hi = nt16::nt16_kernel<AK, BK, EPI, CACHE, GS, LT, false, (LT > 0)>;
   static bool attr_set = false;   // per instantiation
   if (!attr_set) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                             nt16::kLds) != hipSuccess ||
         hipFuncSetAttribute((const void*)kern_sk, hipFuncAttributeMaxDynamicSharedMemorySize,
+                            nt16::kLds) != hipSuccess ||
+        hipFuncSetAttribute((const void*)kern_hi, hipFuncAttributeMaxDynamicSharedMemorySize,
                             nt16::kLds) != hipSuccess)
       return kErrLaunch;
     attr_set = true;
   }
+  const bool hi = LT > 0 && A.lrank > 16;
   const int64_t tiles = (int64_t)A.tiles_m * A.tiles_n;
   if (tiles <= 0) return kOk;
   if (tiles > 0x7FFFFFFF) return kErrTooLarge;
@@ -616,7 +650,8 @@ int launch_nt16(const KArgs& A, hipStream_t st) {
   if constexpr (kSkOk) {
     const int nk = (int)(A.K[0] / nt16::kBK) + (A.npairs == 2 ? (int)(A.K[1] / nt16::kBK) : 0);
     StreamK sk;
-    if (stream_k_plan(tiles, nk, sk)) {
+    // the stream-K kernels carry adapter ranks up to 16
+    if (!hi && stream_k_plan(tiles, nk, sk)) {
       B.sk_dp = (int)(tiles - sk.tiles);
       B.sk_blocks = sk.blocks;
       const int64_t iters = sk.tiles * nk;   // < 2^31 (stream_k_plan)
@@ -627,8 +662,8 @@ int launch_nt16(const KArgs& A, hipStream_t st) {
     }
   }
   const int64_t grid = (int64_t)B.sk_dp + B.sk_blocks;
-  hipLaunchKernelGGL(B.sk_blocks ? kern_sk : kern, dim3((unsigned)grid), dim3(nt16::kThreads),
-                     nt16::kLds, st, B);
+  hipLaunchKernelGGL(hi ? kern_hi : B.sk_blocks ? kern_sk : kern, dim3((unsigned)grid),
+                     dim3(nt16::kThreads), nt16::kLds, st, B);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 

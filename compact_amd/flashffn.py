@@ -189,12 +189,13 @@ def _mm_sum(a, b, a2, b2, name):
     return G.mm_any(a2, b2, 1.0, G.ANY_ADD, out=out, name=name)
 
 
-def _lora_ok(*pairs) -> bool:
-    """The adapter terms (a, b) present ride in the GEMM epilogues: bf16
-    factors of one shared rank up to 16 (G.lora_fusable; the GEMM wrapper
-    re-lays and zero-pads them for the kernel's 8-wide k chunks)."""
+def _lora_ok(*pairs, dims) -> bool:
+    """The adapter terms (a, b) present ride in the epilogues of the GEMMs
+    with the (k, n) `dims`: bf16 factors of one shared rank up to 16, or up to
+    32 where those GEMMs run on the 16x16x32 loop (G.lora_fusable; the GEMM
+    wrapper re-lays and zero-pads them for the kernel's 8-wide k chunks)."""
     ranks = {a.shape[0] for a, b in pairs if a is not None}
-    return (len(ranks) <= 1 and all(G.lora_fusable(r) for r in ranks)
+    return (len(ranks) <= 1 and all(G.lora_fusable(r, *dims) for r in ranks)
             and all(t.dtype == torch.bfloat16 and t.dim() == 2
                     for a, b in pairs if a is not None for t in (a, b)))
 
@@ -216,7 +217,8 @@ def outlier_stat_rows(shape) -> int:
 def _proj(x_2d, w, a, b, s, name):
     """out = x W^T (+ s * (x A^T) B^T) in PEFT op order (src/flashffn.py:1410-1420).
     Returns (out, xA | None)."""
-    if a is not None and _mfma(x_2d, w) and _lora_ok((a, b)) and x_2d.shape[0] > 0:
+    if (a is not None and _mfma(x_2d, w) and _lora_ok((a, b), dims=((w.shape[1], w.shape[0]),))
+            and x_2d.shape[0] > 0):
         xa = _mm(x_2d, a.t(), name + "_xa")
         return G.linear_lora(x_2d, w, xa, b, s, name), xa
     h = _linear(x_2d, w, name)
@@ -285,7 +287,8 @@ class FlashFFNv3Function(torch.autograd.Function):
         k_out = int(inter * outlier_ratio) if (quant and outlier_ratio > 0) else 0
         assert k_out == 0 or x.dtype == torch.bfloat16, "outlier channels need bf16 activations"
         # the dual gate/up kernel, with the gate/up LoRA terms in its epilogue
-        fusable = (_mfma(x_2d, w_gate, w_up) and _lora_ok((a_gate, b_gate), (a_up, b_up))
+        fusable = (_mfma(x_2d, w_gate, w_up)
+                   and _lora_ok((a_gate, b_gate), (a_up, b_up), dims=((hidden_dim, inter),))
                    and x_2d.shape[0] > 0)
 
         c_gate = qs_gate = c_up = qs_up = None
@@ -423,11 +426,15 @@ class FlashFFNv3Function(torch.autograd.Function):
         use_wglu = (_FUSED_WGRAD_GLU and use_k2 and need_wd and not outl and gs in _FUSED_GROUPS
                     and _mfma(gy) and gy.shape[0] > 0)
         need_hm = need_h_mid and ((a_down is not None and need_ad) or not use_wglu)
-        lora_d = _lora_ok((a_down, b_down))
+        lora_d = _lora_ok((a_down, b_down), dims=((w_down.shape[0], w_down.shape[1]),))
         # the fused dgrad kernel restores outlier channels only for the
         # quantised caches (K2's path); bf16 / recompute caches carry none
         fusable = _mfma(gy, w_down) and lora_d and gy.shape[0] > 0 and (use_k2 or not outl)
-        fusable_gu = (_mfma(x_2d, w_gate, w_up) and _lora_ok((a_gate, b_gate), (a_up, b_up))
+        # F1's recompute (k d_model) and the K-concatenated grad_x product (k d_ff)
+        d_ff, d_model = w_gate.shape
+        fusable_gu = (_mfma(x_2d, w_gate, w_up)
+                      and _lora_ok((a_gate, b_gate), (a_up, b_up),
+                                   dims=((d_model, d_ff), (d_ff, d_model)))
                       and x_2d.shape[0] > 0)
 
         hg = hu = None

@@ -14,8 +14,9 @@ ffn_down_dgrad  fused grad_y @ w_down + dequantise + SwiGLU backward (+ K2).
 LoRA adapter terms (`lora=` / `lora_gate=`, `lora_up=`): PEFT's
 `h + s * B(A(x))` applied in the GEMM epilogue, each step rounded to bf16 as
 the reference does (src/flashffn.py:1414,1420,1439,1529,1558-1566), for every
-rank from 1 to 16 (`lora_fusable`; a rank that is not a multiple of 8 is
-zero-padded to 8 or 16).
+rank from 1 to 16, and from 17 to 32 where the product runs on the 16x16x32
+loop (`lora_fusable`; a rank that is not a multiple of 8 is zero-padded to the
+next multiple of 8).
 
 mm_any          any dtype and any strides (cpt_gemm_any, fp32 MFMA): float32
                 (config C1), float16, unaligned bf16 views, rank-1 factors.
@@ -85,28 +86,37 @@ def _check_bf16(*ts):
         assert t.dim() == 2
 
 
-LORA_MAX_RANK = 16
+LORA_MAX_RANK = 32
 
 
-def lora_fusable(rank: int) -> bool:
-    """Adapter terms of this rank ride in the GEMM epilogues: one MFMA per
+def lora_fusable(rank: int, *dims) -> bool:
+    """Adapter terms of this rank ride in the epilogue of a GEMM whose summed
+    products have the (k, n) `dims` (inner dim, output columns).  One MFMA per
     output block and term over k = 16 (v_mfma_f32_16x16x16_bf16 per 16 x 16
     block on the 16x16x32 loop, v_mfma_f32_32x32x16_bf16 per 32 x 32 block on
-    the engine) covers ranks up to 16."""
-    return 1 <= rank <= LORA_MAX_RANK
+    the engine) covers ranks up to 16 on either loop.  Ranks 17 to 32 take a
+    second MFMA accumulated onto the first, carried by the 16x16x32 loop's
+    kernels only (not the engine's, nor stream-K's): every k a positive
+    multiple of 64 and n a multiple of 8."""
+    if not 1 <= rank <= LORA_MAX_RANK:
+        return False
+    return rank <= 16 or (len(dims) > 0 and all(k > 0 and k % 64 == 0 and n % 8 == 0
+                                                for k, n in dims))
 
 
-def _lora_args(terms, n_q):
+def _lora_args(terms, n_q, dims):
     """(rank, ldp, q_kmajor, ldq, [(p, q, alpha) x 2], keep) for up to two
-    terms (p [M, r], q the logical [r, N] factor, alpha); `keep` holds any
+    terms (p [M, r], q the logical [r, N] factor, alpha) of a GEMM with the
+    (k, n) `dims` (lora_fusable); `keep` holds any
     re-laid copies alive until the launch.  The kernels fetch P and K-major Q
     in 16-byte chunks of 8 k, so a rank that is not a multiple of 8 is
-    zero-padded to the next one (8 or 16): the padded k add exact zeros to
+    zero-padded to the next one (8, 16, 24 or 32): the padded k add exact zeros to
     each fp32 dot product."""
     terms = [t for t in terms if t is not None]
     assert 1 <= len(terms) <= 2
     r = terms[0][0].shape[1]
-    assert lora_fusable(r), f"adapter rank {r} above {LORA_MAX_RANK}"
+    assert lora_fusable(r, *dims), \
+        f"adapter rank {r} not carried by a GEMM of (k, n) {tuple(dims)} (lora_fusable)"
     if r % 8:
         rp = (r + 7) // 8 * 8
         pad = torch.nn.functional.pad
@@ -481,7 +491,8 @@ def mm2(a, b, a2=None, b2=None, name: str = "gemm", lora=None) -> torch.Tensor:
             a = a.contiguous()
             a, lda, ak = _layout_a(a)
             assert a2 is None, "adapter terms with a K-concatenated MN-major A"
-        r, ldp, qk, ldq, t, keep = _lora_args(lora, N)
+        dims = ((K, N),) if a2 is None else ((K, N), (K2, N))
+        r, ldp, qk, ldq, t, keep = _lora_args(lora, N, dims)
         with _timed(name):
             rc = _lib.lib().cpt_gemm_bf16_lora(
                 a.data_ptr(), lda, ak, b.data_ptr(), ldb, bk, p_a2, lda2, p_b2, ldb2, K2,
@@ -565,7 +576,8 @@ def ffn_gate_up(x, w_gate, w_up, cache: int, group_size: int, want_h_mid: bool =
     if lora_gate is not None or lora_up is not None:
         # term 0 on the gate columns, term 1 on the up columns (absent: no-op)
         present = [t for t in (lora_gate, lora_up) if t is not None]
-        r, ldp, qk, _, t, keep = _lora_args([(xa, bw.t(), s) for xa, bw, s in present], d)
+        r, ldp, qk, _, t, keep = _lora_args([(xa, bw.t(), s) for xa, bw, s in present], d,
+                                            ((hdim, d),))
         assert qk == 1, "the gate/up adapter B factors go K-major"
         if lora_gate is None:
             t = [(None, None, 0.0), t[0]]
@@ -615,7 +627,8 @@ def ffn_gate_up_outlier(x, w_gate, w_up, cache: int, group_size: int, slot_gate,
     keep = None
     if lora_gate is not None or lora_up is not None:
         present = [tt for tt in (lora_gate, lora_up) if tt is not None]
-        rank, ldp, qk, _, t, keep = _lora_args([(xa, bw.t(), sc) for xa, bw, sc in present], d)
+        rank, ldp, qk, _, t, keep = _lora_args([(xa, bw.t(), sc) for xa, bw, sc in present], d,
+                                               ((hdim, d),))
         assert qk == 1, "the gate/up adapter B factors go K-major"
         if lora_gate is None:
             t = [(None, None, 0.0), t[0]]
@@ -673,7 +686,7 @@ def ffn_down_dgrad(grad_y, w_down, cache: int, group_size: int, c_gate, s_gate, 
         if lora is not None:
             gyb, a_down, s = lora
             a_down = a_down.contiguous()
-            rank, ldp, qk, ldq, t, keep = _lora_args([(gyb, a_down, s)], d)
+            rank, ldp, qk, ldq, t, keep = _lora_args([(gyb, a_down, s)], d, ((hdim, d),))
             assert qk == 0 and ldq == d
             pp, qq, alpha = t[0]
         with _timed("ffn_down_dgrad"):
@@ -686,7 +699,7 @@ def ffn_down_dgrad(grad_y, w_down, cache: int, group_size: int, c_gate, s_gate, 
     elif lora is not None:
         gyb, a_down, s = lora
         a_down = a_down.contiguous()          # [r, inter] rows: the MN-major factor
-        r, ldp, qk, ldq, t, keep = _lora_args([(gyb, a_down, s)], d)
+        r, ldp, qk, ldq, t, keep = _lora_args([(gyb, a_down, s)], d, ((hdim, d),))
         assert qk == 0 and ldq == d
         with _timed("ffn_down_dgrad"):
             rc = _lib.lib().cpt_ffn_down_dgrad_lora(

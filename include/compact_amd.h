@@ -289,8 +289,10 @@ int cpt_gemm_any(int dtype, const void* a, int64_t sam, int64_t sak, const void*
  * in PEFT's op order `h + s * B(A(x))` (src/flashffn.py:1414,1420,1439,1529,
  * 1558-1566):
  *   out = bf16(bf16(out) + bf16(alpha_t * bf16(P_t . Q_t)))   t = 0, then 1
- * rank in {8, 16} (a rank below 16 that is not a multiple of 8 is passed
- * zero-padded to the next one, P's extra columns and Q's extra k zero);
+ * rank in {8, 16}, or {24, 32} where the product runs on the 16x16x32 loop
+ * (every K a multiple of 64, N of 8; otherwise CPT_ERR_SHAPE); a rank that is
+ * not a multiple of 8 is passed zero-padded to the next one, P's extra
+ * columns and Q's extra k zero;
  * P_t [M, rank] (tokens x rank, e.g. x A^T or grad_y B) with
  * rows ldp apart (ldp % 8 == 0, 16-byte aligned); Q_t the [rank, N] factor,
  * given as [N, rank] contiguous (q_kmajor = 1: an nn.Linear B weight) or as

@@ -269,14 +269,15 @@ def test_function_odd_token_counts(device, n, config, mode, group):
         assert R.rel_frob(got[k].cpu(), ora[k]) < 2e-2, k
 
 
-@pytest.mark.parametrize("rank", [1, 4, 12, 32, 64])
+@pytest.mark.parametrize("rank", [1, 4, 12, 20, 32, 64])
 @pytest.mark.parametrize("mode,group", [("int4", 64), ("int8", 128), ("bf16", 64),
                                         ("recompute", 64)])
 def test_function_other_lora_ranks(device, rank, mode, group):
-    """Ranks other than 8 and 16.  Up to 16 they ride in the fused epilogues
-    zero-padded to 8 or 16 (P's extra columns, Q's extra k); above 16 the LoRA
-    terms run as separate rank-sized products and adds, in the reference's op
-    order.  Same bars as the rank-16 parity test."""
+    """Ranks other than 8 and 16.  Up to 32 they ride in the fused epilogues
+    (d_model and d_ff here are multiples of 64) zero-padded to a multiple of 8
+    (P's extra columns, Q's extra k); above 32 the LoRA terms run as separate
+    rank-sized products and adds, in the reference's op order.  Same bars as
+    the rank-16 parity test."""
     ps = R.synthetic_param_set("all", H, D, rank, S, seed=7, dtype=torch.bfloat16)
     gen = torch.Generator().manual_seed(8)
     x = torch.randn(N, H, generator=gen).to(torch.bfloat16)
@@ -292,11 +293,11 @@ def test_function_other_lora_ranks(device, rank, mode, group):
         assert c >= (0.99 if k == "grad_x" else 0.98), (k, c)
 
 
-@pytest.mark.parametrize("rank", [1, 4, 12])
+@pytest.mark.parametrize("rank", [1, 4, 12, 20, 30])
 def test_padded_rank_takes_the_fused_epilogue(device, monkeypatch, rank):
-    """A rank below 16 that is not a multiple of 8 reaches the LoRA-epilogue
-    kernels zero-padded (the GEMM wrapper's launches carry rank 8 or 16), and
-    the outputs match the unfused route's to bf16 rounding."""
+    """A rank up to 32 that is not a multiple of 8 reaches the LoRA-epilogue
+    kernels zero-padded (the GEMM wrapper's launches carry rank 8, 16, 24 or
+    32), and the outputs match the unfused route's to bf16 rounding."""
     from compact_amd import flashffn as F
     from compact_amd import gemm as G
     ps = R.synthetic_param_set("all", H, D, rank, S, seed=9, dtype=torch.bfloat16)
@@ -307,9 +308,9 @@ def test_padded_rank_takes_the_fused_epilogue(device, monkeypatch, rank):
     real = G._lora_args
     monkeypatch.setattr(G, "_lora_args", lambda *a, **k: seen.append(real(*a, **k)[0]) or real(*a, **k))
     fused, y = _run(_to(ps, device), x, gy, "int4", 64)
-    assert seen and set(seen) <= {8, 16} and max(seen) == (8 if rank <= 8 else 16)
+    assert seen and set(seen) <= {8, 16, 24, 32} and max(seen) == (rank + 7) // 8 * 8
     monkeypatch.setattr(G, "_lora_args", real)
-    monkeypatch.setattr(F.G, "lora_fusable", lambda r: False)
+    monkeypatch.setattr(F.G, "lora_fusable", lambda r, *dims: False)
     plain, y2 = _run(_to(ps, device), x, gy, "int4", 64)
     assert R.rel_frob(y.float().cpu(), y2.float().cpu()) < 1e-2
     for k in plain:

@@ -11,7 +11,10 @@
     plain GEMM with the same terms followed by the standalone K1 / K2 kernels:
     bitwise, since both apply the terms with the same instructions;
   * an absent term (adapter on gate only, or up only) leaves its columns
-    bitwise equal to the adapter-free kernel.
+    bitwise equal to the adapter-free kernel;
+  * ranks 17 to 32 (a second MFMA over k 16..31) on the 16x16x32 loop, and
+    their refusal where a product would leave it (the engine, and the
+    stream-K kernels, carry ranks up to 16).
 """
 
 import pytest
@@ -46,7 +49,7 @@ def bits16(t):
     return t.contiguous().view(torch.int16)
 
 
-@pytest.mark.parametrize("rank", [8, 16])
+@pytest.mark.parametrize("rank", [8, 16, 24, 32])
 @pytest.mark.parametrize("bk", [True, False])
 @pytest.mark.parametrize("q_kmajor", [True, False])
 @pytest.mark.parametrize("nterms", [1, 2])
@@ -55,6 +58,8 @@ def bits16(t):
 def test_mm2_lora_terms(device, rank, bk, q_kmajor, nterms, mnk):
     _, G, _ = _cpt()
     m, n, k = mnk
+    if not G.lora_fusable(rank, (k, n)):
+        pytest.skip("ranks above 16 ride on the 16x16x32 loop only (K a multiple of 64)")
     a = rnd((m, k), 1, device)
     b = rnd((n, k), 2, device).t() if bk else rnd((k, n), 2, device)
     terms = []
@@ -89,7 +94,7 @@ def plain_like_f1(G, x, w):
 @pytest.mark.parametrize("cache,bits,group", [("int4", 4, 64), ("int8", 8, 128), ("bf16", 0, 64),
                                               ("none", 0, 64)])
 @pytest.mark.parametrize("which", ["both", "gate", "up"])
-@pytest.mark.parametrize("rank", [8, 16])
+@pytest.mark.parametrize("rank", [8, 16, 24, 32])
 @pytest.mark.parametrize("n_tok,hid,inter", [(300, 128, 384), (512, 128, 512), (300, 136, 384)])
 def test_gate_up_lora_fused_equals_composed(device, cache, bits, group, which, rank, n_tok, hid,
                                             inter):
@@ -97,6 +102,8 @@ def test_gate_up_lora_fused_equals_composed(device, cache, bits, group, which, r
     (the 16x16x32 loop for d_model 128, the engine for 136) with the same
     terms, then K1, bit for bit."""
     cpt, G, _lib = _cpt()
+    if not G.lora_fusable(rank, (hid, inter)):
+        pytest.skip("ranks above 16 ride on the 16x16x32 loop only (d_model a multiple of 64)")
     code = {"int4": _lib.CACHE_INT4, "int8": _lib.CACHE_INT8, "bf16": _lib.CACHE_BF16,
             "none": _lib.CACHE_NONE}[cache]
     x = rnd((n_tok, hid), 30, device)
@@ -123,7 +130,7 @@ def test_gate_up_lora_fused_equals_composed(device, cache, bits, group, which, r
 @pytest.mark.parametrize("cache,bits,group,inter", [("bf16", 0, 64, 264), ("none", 0, 64, 264),
                                                     ("int8", 8, 64, 320), ("int4", 4, 32, 320)])
 @pytest.mark.parametrize("which", ["both", "gate"])
-@pytest.mark.parametrize("rank", [8, 16])
+@pytest.mark.parametrize("rank", [8, 16, 32])
 def test_gate_up_lora_ragged_dff(device, cache, bits, group, inter, which, rank):
     """The adapter terms on a partial last d_ff tile: the Q rows (B's rows)
     past d_ff read zero and those columns are never stored."""
@@ -147,7 +154,7 @@ def test_absent_term_is_a_no_op(device):
 
 @pytest.mark.parametrize("cache,bits,group", [("int4", 4, 64), ("int8", 8, 128), ("bf16", 0, 64)])
 @pytest.mark.parametrize("want_h_mid", [True, False])
-@pytest.mark.parametrize("rank", [8, 16])
+@pytest.mark.parametrize("rank", [8, 16, 24, 32])
 def test_down_dgrad_lora_fused_equals_composed(device, cache, bits, group, want_h_mid, rank):
     cpt, G, _lib = _cpt()
     code = {"int4": _lib.CACHE_INT4, "int8": _lib.CACHE_INT8, "bf16": _lib.CACHE_BF16}[cache]
@@ -172,13 +179,13 @@ def test_down_dgrad_lora_fused_equals_composed(device, cache, bits, group, want_
         assert torch.equal(bits16(hm), bits16(rhm))
 
 
-def test_rank_below_16_is_zero_padded(device):
+def test_rank_not_a_multiple_of_8_is_zero_padded(device):
     """A rank that is not a multiple of 8 is passed to the epilogue
-    zero-padded to 8 or 16: the extra products are exact zeros, so the
-    result equals the caller-padded call bit for bit."""
+    zero-padded to the next multiple: the extra products are exact zeros, so
+    the result equals the caller-padded call bit for bit."""
     _, G, _ = _cpt()
     a, b = rnd((64, 64), 60, device), rnd((64, 64), 61, device)
-    for r, rp in ((4, 8), (12, 16)):
+    for r, rp in ((4, 8), (12, 16), (17, 24), (30, 32)):
         p, q = rnd((64, r), 62, device), rnd((r, 64), 63, device)
         pp = torch.nn.functional.pad(p, (0, rp - r))
         qp = torch.nn.functional.pad(q, (0, 0, 0, rp - r))
@@ -190,6 +197,52 @@ def test_rank_below_16_is_zero_padded(device):
 def test_rank_outside_epilogue_set_raises(device):
     _, G, _ = _cpt()
     a, b = rnd((64, 64), 60, device), rnd((64, 64), 61, device)
-    p, q = rnd((64, 32), 62, device), rnd((32, 64), 63, device)
+    p, q = rnd((64, 40), 62, device), rnd((40, 64), 63, device)
     with pytest.raises(AssertionError):
         G.mm2(a, b, lora=[(p, q, 1.0)])
+    # rank 24 on a product the engine would run (K not a multiple of 64)
+    a = rnd((64, 72), 64, device)
+    b = rnd((72, 64), 65, device)
+    p, q = rnd((64, 24), 62, device), rnd((24, 64), 63, device)
+    with pytest.raises(AssertionError):
+        G.mm2(a, b, lora=[(p, q, 1.0)])
+
+
+@pytest.mark.parametrize("rank", [16, 24, 32])
+def test_high_rank_term_equals_two_low_rank_terms(device, rank):
+    """Ranks 17 to 32 go through two MFMAs, k 0..15 then k 16..31, accumulated
+    in fp32: the term over k 0..15 plus the term over k 16..r-1 in one fp32
+    sum.  Against the fp32 reference with PEFT's roundings (the bar of
+    test_mm2_lora_terms) and, with the first half of the factors zero, against
+    the rank-(r - 16) call bit for bit (the zero half adds exact zeros)."""
+    _, G, _ = _cpt()
+    m, n, k = 300, 264, 128
+    a, b = rnd((m, k), 70, device), rnd((k, n), 71, device)
+    p, q = rnd((m, rank), 72, device), rnd((rank, n), 73, device, 0.1)
+    got = G.mm2(a, b, lora=[(p, q, 2.0)])
+    base = G.mm(a, b)
+    ref, mag = peft_ref(base.float().cpu(), [(p, q, 2.0)])
+    assert not ((got.float().cpu() - ref).abs() > 2 ** -7 * mag + 1e-6).any()
+    if rank > 16:
+        pz, qz = p.clone(), q.clone()
+        pz[:, :16] = 0
+        qz[:16] = 0
+        lo = G.mm2(a, b, lora=[(pz, qz, 2.0)])
+        hi = G.mm2(a, b, lora=[(p[:, 16:].contiguous(), q[16:].contiguous(), 2.0)])
+        assert torch.equal(bits16(lo), bits16(hi))
+
+
+def test_high_rank_stream_k_shape(device):
+    """A product whose tile count would take the stream-K schedule: with a
+    rank-32 term it runs data-parallel (the stream-K kernels carry ranks up
+    to 16) and its rows match the same product computed in row blocks that
+    the stream-K plan leaves alone."""
+    _, G, _ = _cpt()
+    # 8 x 43 = 344 tiles of 256 x 256 on 256 CUs: a part-empty second wave
+    m, n, k = 2048, 11008, 1024
+    a, b = rnd((m, k), 80, device), rnd((n, k), 81, device, 0.05).t()
+    p, q = rnd((m, 32), 82, device), rnd((32, n), 83, device, 0.1)
+    got = G.mm2(a, b, lora=[(p, q, 0.5)])
+    for r0 in range(0, m, 256):
+        part = G.mm2(a[r0:r0 + 256], b, lora=[(p[r0:r0 + 256], q, 0.5)])
+        assert torch.equal(bits16(got[r0:r0 + 256]), bits16(part)), r0

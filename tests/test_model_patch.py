@@ -87,3 +87,31 @@ def test_mfma_layout_rule():
     assert not _mfma(torch.zeros(8, 8, dtype=torch.float32))
     assert _mfma(torch.zeros(16, 768, dtype=bf)[:4])         # a row slice of a weight
     assert not _mfma(torch.zeros(4, 264, dtype=bf)[:, 1:257])  # rows 2 bytes off 16-byte alignment
+
+
+def test_lora_fusable_rule():
+    """Adapter ranks up to 16 ride in every GEMM epilogue; 17 to 32 only where
+    every summed product runs on the 16x16x32 loop (k a positive multiple of
+    64, n of 8); above 32 none."""
+    from compact_amd import gemm as G
+    from compact_amd.flashffn import _lora_ok
+    for r in range(1, 17):
+        assert G.lora_fusable(r, (136, 12))                  # the engine's shapes too
+    assert not G.lora_fusable(0, (128, 64))
+    for r in (17, 24, 30, 32):
+        assert G.lora_fusable(r, (128, 264))
+        assert G.lora_fusable(r, (4096, 11008), (11008, 4096))
+        assert not G.lora_fusable(r, (136, 264))             # k not a multiple of 64
+        assert not G.lora_fusable(r, (128, 260))             # n not a multiple of 8
+        assert not G.lora_fusable(r, (128, 264), (136, 264))  # one product on the engine
+        assert not G.lora_fusable(r, (0, 264))
+        assert not G.lora_fusable(r)                         # no shapes given
+    assert not G.lora_fusable(33, (128, 264))
+    assert not G.lora_fusable(64, (4096, 11008))
+    bf = torch.bfloat16
+    a24, b24 = torch.zeros(24, 256, dtype=bf), torch.zeros(768, 24, dtype=bf)
+    assert _lora_ok((a24, b24), dims=((256, 768), (768, 256)))
+    assert not _lora_ok((a24, b24), dims=((264, 768),))
+    a16 = torch.zeros(16, 256, dtype=bf)
+    assert not _lora_ok((a16, torch.zeros(768, 16, dtype=bf)), (a24, b24), dims=((256, 768),))
+    assert _lora_ok((None, None), dims=((136, 12),))
