@@ -190,6 +190,24 @@ __global__ __launch_bounds__(256) void skinny_proj_kernel(
     }
 }
 
+// sum_s p[s * stride], s = 0 .. splits - 1, added in split order; the loads
+// of 8 splits are issued together (the additions stay in order, so the sum is
+// that of the one-at-a-time loop)
+__device__ __forceinline__ float sum_splits(const float* __restrict__ p, int64_t stride,
+                                            int splits) {
+  float sum = 0.0f;
+  int s = 0;
+  for (; s + 8 <= splits; s += 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = p[(int64_t)(s + j) * stride];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum += v[j];
+  }
+  for (; s < splits; ++s) sum += p[(int64_t)s * stride];
+  return sum;
+}
+
 // C[m, r] = bf16(alpha * sum_s ws[s][m][r]), splits summed in order
 __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restrict__ ws,
                                                             uint16_t* __restrict__ c, int64_t M,
@@ -197,8 +215,7 @@ __global__ __launch_bounds__(256) void skinny_reduce_kernel(const float* __restr
                                                             float alpha) {
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (e >= M * R) return;
-  float sum = 0.0f;
-  for (int s = 0; s < splits; ++s) sum += ws[(int64_t)s * M * R + e];
+  const float sum = sum_splits(ws + e, M * R, splits);
   const int64_t m = e / R, r = e - m * R;
   c[m * ldc + r] = (uint16_t)f32_to_bf16_bits(alpha * sum);
 }
@@ -330,8 +347,7 @@ __global__ __launch_bounds__(256) void skinny_red_reduce_kernel(const float* __r
   // transposed output: consecutive threads take consecutive n of one r
   const int64_t n = trans ? e % N : e / R;
   const int64_t r = trans ? e / N : e % R;
-  float sum = 0.0f;
-  for (int sp = 0; sp < splits; ++sp) sum += ws[(int64_t)sp * N * R + n * R + r];
+  const float sum = sum_splits(ws + n * R + r, N * R, splits);
   out[trans ? r * ldo + n : n * ldo + r] = (uint16_t)f32_to_bf16_bits(alpha * sum);
 }
 
