@@ -344,10 +344,12 @@ __global__ __launch_bounds__(256) void skinny_red_reduce_kernel(const float* __r
                                                                 float alpha) {
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (e >= N * R) return;
-  // transposed output: consecutive threads take consecutive n of one r
-  const int64_t n = trans ? e % N : e / R;
-  const int64_t r = trans ? e / N : e % R;
-  const float sum = sum_splits(ws + n * R + r, N * R, splits);
+  // consecutive threads read consecutive partials (r fastest); a transposed
+  // output then takes scattered 2-byte stores (N R of them, against splits N R
+  // partial reads)
+  const int64_t n = e / R;
+  const int64_t r = e % R;
+  const float sum = sum_splits(ws + e, N * R, splits);
   out[trans ? r * ldo + n : n * ldo + r] = (uint16_t)f32_to_bf16_bits(alpha * sum);
 }
 
