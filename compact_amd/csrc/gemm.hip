@@ -17,8 +17,17 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
                                                             float alpha) {
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (e >= M * N) return;
+  // splits added in order; the loads of 8 splits are issued together
   float sum = 0.0f;
-  for (int s = 0; s < splits; ++s) sum += ws[(int64_t)s * M * N + e];
+  int s = 0;
+  for (; s + 8 <= splits; s += 8) {
+    float v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = ws[(int64_t)(s + j) * M * N + e];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum += v[j];
+  }
+  for (; s < splits; ++s) sum += ws[(int64_t)s * M * N + e];
   const int64_t m = e / N, n = e - m * N;
   out[m * ldc + n] = (uint16_t)f32_to_bf16_bits(alpha * sum);
 }
