@@ -353,6 +353,27 @@ __global__ __launch_bounds__(256) void skinny_red_reduce_kernel(const float* __r
   out[trans ? r * ldo + n : n * ldo + r] = (uint16_t)f32_to_bf16_bits(alpha * sum);
 }
 
+// Both split sums of a skinny_dual pass in one launch: elements [0, T R) sum
+// the projection's column-block partials into C, the rest the reduction's
+// token-split partials into Z (each as the two kernels above)
+__global__ __launch_bounds__(256) void skinny_dual_reduce_kernel(
+    const float* __restrict__ ws_c, uint16_t* __restrict__ c, int64_t T, int64_t ldc,
+    int csplits, float alpha_c, const float* __restrict__ ws_z, uint16_t* __restrict__ z,
+    int64_t N, int64_t ldz, int z_trans, int splits, float alpha_z, int R) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e < T * R) {
+    const float sum = sum_splits(ws_c + e, T * R, csplits);
+    const int64_t m = e / R, r = e - m * R;
+    c[m * ldc + r] = (uint16_t)f32_to_bf16_bits(alpha_c * sum);
+    return;
+  }
+  const int64_t ez = e - T * R;
+  if (ez >= N * R) return;
+  const int64_t n = ez / R, r = ez % R;
+  const float sum = sum_splits(ws_z + ez, N * R, splits);
+  z[z_trans ? r * ldz + n : n * ldz + r] = (uint16_t)f32_to_bf16_bits(alpha_z * sum);
+}
+
 // ---------------------------------------------------------------------------
 // Both adapter products of one token-major operand in one pass over it:
 //   C[T, R] = X[T, N] . Q^T  (Q [R, N]: the projection, X B)
@@ -736,18 +757,16 @@ int cpt_gemm_bf16_skinny_dual(const void* x, int64_t ldx, const void* q, int64_t
                          (const uint16_t*)q, ldq, (const uint16_t*)p, ldp, T, N, (int)R, tchunk,
                          ws_c, ws_z, qmode);
     if (hipGetLastError() != hipSuccess) return kErrLaunch;
-    const int64_t tc = T * R;
-    hipLaunchKernelGGL(skinny_reduce_kernel, dim3((unsigned)((tc + 255) / 256)), dim3(256), 0, st,
-                       (const float*)ws_c, (uint16_t*)c, T, (int)R, ldc, (int)csplits, alpha_c);
-    if (hipGetLastError() != hipSuccess) return kErrLaunch;
   } else {
     // no tokens: C has no rows and Z is the empty sum (zero partials summed)
     splits = 0;
   }
-  const int64_t tz = N * R;
-  hipLaunchKernelGGL(skinny_red_reduce_kernel, dim3((unsigned)((tz + 255) / 256)), dim3(256), 0,
-                     st, (const float*)ws_z, (uint16_t*)z, N, (int)R, ldz, z_trans ? 1 : 0, splits,
-                     alpha_z);
+  // both split sums in one launch
+  const int64_t total = T * R + N * R;
+  hipLaunchKernelGGL(skinny_dual_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256),
+                     0, st, (const float*)ws_c, (uint16_t*)c, T, ldc, (int)csplits, alpha_c,
+                     (const float*)ws_z, (uint16_t*)z, N, ldz, z_trans ? 1 : 0, splits, alpha_z,
+                     (int)R);
   return hipGetLastError() == hipSuccess ? kOk : kErrLaunch;
 }
 
