@@ -139,12 +139,13 @@ def test_outlier_k1_k2_equal_standalone(device, bits, group, n, d, ratio):
 
 
 @pytest.mark.parametrize("bits,group", [(4, 64), (8, 128)])
-@pytest.mark.parametrize("with_lora", [False, True])
+@pytest.mark.parametrize("with_lora", [False, 16, 32])
 @pytest.mark.parametrize("want_h_mid", [True, False])
 def test_outlier_fused_dgrad_equals_unfused(device, bits, group, with_lora, want_h_mid):
     """The dgrad GEMM with dequantise + outlier restore + SwiGLU backward in
-    its epilogue equals the GEMM (with the down projection's LoRA term) and
-    the standalone outlier K2, bit for bit."""
+    its epilogue equals the GEMM (with the down projection's LoRA term, rank
+    16, or 32 on the kernels for ranks above 16) and the standalone outlier
+    K2, bit for bit."""
     cpt, G = _cpt()
     n, hdim, d = 384, 256, 1024
     a, b = _hot(n, d, 11)
@@ -158,8 +159,9 @@ def test_outlier_fused_dgrad_equals_unfused(device, bits, group, with_lora, want
     wd = (torch.randn(hdim, d, device=device, generator=gen) * 0.05).to(torch.bfloat16)
     lora = None
     if with_lora:
-        gyb = (torch.randn(n, 16, device=device, generator=gen) * 0.1).to(torch.bfloat16)
-        a_d = (torch.randn(16, d, device=device, generator=gen) * 0.05).to(torch.bfloat16)
+        r = with_lora
+        gyb = (torch.randn(n, r, device=device, generator=gen) * 0.1).to(torch.bfloat16)
+        a_d = (torch.randn(r, d, device=device, generator=gen) * 0.05).to(torch.bfloat16)
         lora = (gyb, a_d, 2.0)
     dg, du, hm = G.ffn_down_dgrad(gy, wd, bits, group, qg, sg, qu, su, want_h_mid, lora=lora,
                                   outliers=(sg_, og, su_, ou))
@@ -295,12 +297,13 @@ def test_stacked_adapter_products_bitwise(device, monkeypatch, ratio, rank, s_up
 
 
 @pytest.mark.parametrize("bits,group", [(4, 64), (4, 32), (8, 128)])
-@pytest.mark.parametrize("with_lora", [False, True])
+@pytest.mark.parametrize("with_lora", [False, 16, 32])
 @pytest.mark.parametrize("n,hdim,d", [(384, 256, 1024), (300, 128, 320)])
 def test_gate_up_outlier_epilogue_equals_k1(device, bits, group, with_lora, n, hdim, d):
     """F1 with the outlier channels in its codec epilogue equals the dual GEMM
     with a bf16 output (same loop, same accumulators) followed by K1 with
-    outliers, bit for bit: h_mid, codes, scales and outlier blocks.  The
+    outliers, bit for bit: h_mid, codes, scales and outlier blocks, with LoRA
+    terms of rank 16 or 32 (the kernels for ranks above 16).  The
     (300, 128, 320) case has ragged token and d_ff tiles."""
     if d % group:
         pytest.skip("d_ff not a multiple of the group")
@@ -314,10 +317,11 @@ def test_gate_up_outlier_epilogue_equals_k1(device, bits, group, with_lora, n, h
     wu[(d * 3) // 4] *= 25            # hot channels, as in a trained model
     lk = {}
     if with_lora:
-        xa_g = (torch.randn(n, 16, device=device, generator=gen) * 0.3).to(torch.bfloat16)
-        xa_u = (torch.randn(n, 16, device=device, generator=gen) * 0.3).to(torch.bfloat16)
-        bg = (torch.randn(d, 16, device=device, generator=gen) * 0.05).to(torch.bfloat16)
-        bu = (torch.randn(d, 16, device=device, generator=gen) * 0.05).to(torch.bfloat16)
+        r = with_lora
+        xa_g = (torch.randn(n, r, device=device, generator=gen) * 0.3).to(torch.bfloat16)
+        xa_u = (torch.randn(n, r, device=device, generator=gen) * 0.3).to(torch.bfloat16)
+        bg = (torch.randn(d, r, device=device, generator=gen) * 0.05).to(torch.bfloat16)
+        bu = (torch.randn(d, r, device=device, generator=gen) * 0.05).to(torch.bfloat16)
         lk = dict(lora_gate=(xa_g, bg, 2.0), lora_up=(xa_u, bu, 2.0))
     k = max(1, int(d * 0.01))
     _, hg, hu, *_ = G.ffn_gate_up(x, wg, wu, _lib.CACHE_BF16, group, want_h_mid=False, **lk)
