@@ -431,16 +431,25 @@ __device__ __forceinline__ bool any_outlier(const uint4& w) {
   return (w.x & w.y & w.z & w.w) != 0xFFFFFFFFu;
 }
 
-// Copy the outlier columns of one chunk (raw bf16 words `p`) to out[row][slot].
+// Copy the outlier columns of one chunk (raw bf16 words `p`) to out[row][slot]:
+// one store per outlier column, a loop over the set bits of the chunk's mask
+// (a chunk holds one outlier column or none nearly always, so the wavefront
+// issues one or two stores where an unrolled test of all 8 columns issued 8)
 __device__ __forceinline__ void store_outlier_words(const uint4& w, const uint4& p, uint32_t row,
                                                     const Outliers& o) {
   uint16_t* dst = o.out + (int64_t)row * o.k;
-  const uint32_t ws[4] = {w.x, w.y, w.z, w.w}, ps[4] = {p.x, p.y, p.z, p.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int lo = (int16_t)(ws[i] & 0xFFFFu), hi = (int32_t)ws[i] >> 16;
-    if (lo >= 0) dst[lo] = (uint16_t)(ps[i] & 0xFFFFu);
-    if (hi >= 0) dst[hi] = (uint16_t)(ps[i] >> 16);
+  uint32_t m = 0;   // bit j: column j's slot is >= 0
+  m |= ((~w.x >> 15) & 1u) | ((~w.x >> 30) & 2u);
+  m |= (((~w.y >> 15) & 1u) | ((~w.y >> 30) & 2u)) << 2;
+  m |= (((~w.z >> 15) & 1u) | ((~w.z >> 30) & 2u)) << 4;
+  m |= (((~w.w >> 15) & 1u) | ((~w.w >> 30) & 2u)) << 6;
+  while (m) {
+    const int j = __builtin_ctz(m);
+    m &= m - 1;
+    const int q = j >> 1, sh = (j & 1) * 16;
+    const uint32_t sw = q == 0 ? w.x : q == 1 ? w.y : q == 2 ? w.z : w.w;
+    const uint32_t pw = q == 0 ? p.x : q == 1 ? p.y : q == 2 ? p.z : p.w;
+    dst[(int16_t)((sw >> sh) & 0xFFFFu)] = (uint16_t)((pw >> sh) & 0xFFFFu);
   }
 }
 
